@@ -1,0 +1,214 @@
+// Device-side data layout shared by the HIP kernels (leo_kernels.hip) and the
+// host runtime (leo_runtime.hip). One "lane" is one independent runtime
+// trajectory: a logical story worker (training.rs:1669-1683) or the canonical
+// runtime itself. Every array is structure-of-arrays in HBM.
+#ifndef LEO_DEVICE_H
+#define LEO_DEVICE_H
+
+#include <stdint.h>
+
+#include "leo_hip_abi.h"
+
+namespace leo {
+
+constexpr uint32_t kSymbols = 258;
+constexpr uint32_t kOutputs = 257;
+constexpr uint32_t kOutStride = 260;      // neuron-major output row, padded to 16 B
+constexpr uint32_t kEndIndex = 256;
+constexpr uint32_t kRing = 9;             // delay ring: max delay 8 + 1 (runtime.rs:200-208)
+constexpr uint32_t kMaxOrder = 16;        // config.rs:452-456
+constexpr uint32_t kThreads = 256;        // threads per workgroup
+constexpr uint32_t kMaxBlockNeurons = 1024;
+constexpr uint32_t kGlobalSortCapacity = 8192;
+
+// Step flags (per scheduled step).
+enum : uint32_t {
+    kStepFrozen = 1u << 0,        // Permission::Frozen
+    kStepLearnTrace = 1u << 1,    // learning_trace_enabled (!frozen)
+    kStepContext = 1u << 2,       // context enabled (frozen, or survived dropout)
+    kStepAllocate = 1u << 3,      // context allocation allowed
+    kStepLearn = 1u << 4,         // target present and strength > 0
+    kStepOutput = 1u << 5,        // compute logits/probabilities
+};
+
+// One scheduled step, prepared by the host from the story bytes
+// (training.rs:1747-1757) -- the role of LeoPersistentStep (cuda.rs:398-406).
+struct StepParams {
+    uint32_t symbol;
+    int32_t target_index;          // dense output class or -1
+    uint32_t flags;
+    float supervised_strength;     // strength * target weight
+    float strength;                // permission strength (inhibitory homeostasis)
+    float plasticity_scale;
+};
+
+// Per-step record written by the device (the role of CudaTrainingStepRecord,
+// cuda.rs:354-370). The loss itself is -ln(max(p_target,1e-12)) on the host.
+struct StepRecord {
+    float p_target;
+    float population_inhibition;
+    uint32_t predicted;
+    uint32_t active;
+    uint32_t suprathreshold;
+    uint32_t block_selected;
+    uint32_t clipped;
+    uint32_t context_cells;
+    uint32_t context_probes;
+    uint32_t context_applied;
+    uint32_t eligible_rec;
+    uint32_t eligible_in;
+    uint32_t error_code;
+    uint32_t pad[2];
+};
+
+// Device numerical guard codes (the reference's sticky error_flag 1-7,
+// cuda_kernels.cu:3276-3588).
+enum : uint32_t {
+    kErrOutput = 1, kErrBias = 2, kErrContextProjection = 3, kErrContextEmbedding = 4,
+    kErrRecurrent = 5, kErrInput = 6, kErrInhibitory = 7, kErrCapacity = 8, kErrBarrier = 9,
+};
+
+// Device-resident scalars of a lane that persist across launches.
+struct LaneControl {
+    uint32_t tick;                   // current_tick
+    float population_inhibition;
+    uint32_t parity;                 // which eligible list is current
+    uint32_t rec_count[2];
+    uint32_t in_count[2];
+    uint32_t dest_epoch;             // learning-destination epoch
+    uint32_t history_len;
+    uint32_t history[kMaxOrder];
+    uint32_t ctx_count;
+    uint32_t ctx_probes;
+    uint32_t ctx_applied;
+    uint32_t ctx_slots[kMaxOrder];
+    float ctx_scales[kMaxOrder];
+    uint32_t block_selected;
+    uint32_t clipped;
+    float pop_cutoff;
+    uint32_t active_count;
+    uint32_t bias_dirty;
+    uint32_t ctx_out_dirty;
+    uint32_t error_code;
+    uint32_t barrier;                // lane-group barrier arrival counter
+    uint32_t abort;
+    uint32_t ring_tick[kRing];       // tick whose active set ring slot holds (UINT32_MAX = empty)
+    uint32_t ring_count[kRing];      // active count of that tick
+    uint32_t tick_touched[2];        // touched count, indexed by tick parity
+    uint32_t tick_supra[2];          // suprathreshold count, indexed by tick parity
+    uint32_t pad[2];
+};
+
+// Learned parameters of a lane (private copy for story lanes, the canonical
+// image for the canonical runtime).
+struct LaneParams {
+    float* threshold;        // N
+    float* rec_weight;       // N*S (slot = src*S + j)
+    float* in_weight;        // 258*F
+    float* out_w;            // N * kOutStride, neuron-major
+    float* bias;             // kOutStride
+    uint64_t* ctx_keys;      // slots
+    float* ctx_emb;          // slots * E
+    uint32_t* ctx_obs;       // slots
+    float* ctx_out;          // 257 * E, output-major
+};
+
+// Everything a kernel needs to run one lane.
+struct LaneDesc {
+    LaneParams p;
+    LaneControl* ctl;
+    // neuron state (N)
+    float* membrane;
+    float* activation;
+    float* fatigue;
+    uint32_t* refractory_until;
+    float* branches;         // N*4
+    uint32_t* last_tick;
+    float* adapt;            // 3*N (fast, medium, slow)
+    uint32_t* touched_epoch; // == tick+1 when touched this tick
+    uint32_t* touched_list;  // N
+    uint32_t* selected_epoch;
+    float* surrogate;
+    uint32_t* dest_epoch;
+    float* learning_signal;
+    uint32_t* bucket_count;  // N
+    uint64_t* bucket;        // 2 words per entry: delivery-order key, value bits
+    // block selection
+    uint32_t* block_winners; // blocks * max_active_per_block
+    uint32_t* block_count;   // blocks
+    float* block_cutoff;     // blocks
+    // ring: per slot, up to max_active_global active neurons, activation, and S snapshot values each
+    uint32_t* ring_active;   // kRing * cap
+    float* ring_act;         // kRing * cap
+    float* ring_value;       // kRing * cap * S
+    // recurrent traces (N*S): branch, membrane, fatigue, 3 adaptation sensitivities, eligibility
+    float* rec_trace;        // 7 * NS (SoA planes)
+    uint32_t* rec_last;      // NS
+    uint8_t* rec_mark;       // NS
+    uint32_t* rec_list;      // 2 * NS
+    // input traces (258*F)
+    float* in_trace;         // 7 * NI
+    uint32_t* in_last;
+    uint8_t* in_mark;
+    uint32_t* in_list;       // 2 * NI
+    // readout
+    float* logits;           // kOutStride
+    float* probs;            // kOutStride
+    float* errors;           // kOutStride
+    float* ctx_latent;       // E
+    // change tracking bitmaps (ParameterChanges)
+    uint32_t* ch_threshold;  // ceil(N/32)
+    uint32_t* ch_rec;        // ceil(NS/32)
+    uint32_t* ch_in;         // ceil(NI/32)
+    uint32_t* ch_out;        // ceil(N/32)
+    uint32_t* ch_ctx;        // ceil(slots/32)
+    // schedule for the current launch
+    const StepParams* steps;
+    StepRecord* records;
+    uint32_t step_count;
+    uint32_t pad;
+};
+
+// Read-only model data shared by every lane.
+struct SharedModel {
+    const float* excitability;
+    const uint8_t* neuron_type;
+    const uint32_t* rec_target;
+    const uint8_t* rec_branch;
+    const uint8_t* rec_delay;
+    const uint32_t* in_target;
+    const uint8_t* in_branch;
+    const uint64_t* bucket_offset;   // N+1
+};
+
+struct KernelArgs {
+    LeoConfig cfg;
+    SharedModel m;
+    LaneDesc* lanes;
+    uint32_t lane_count;
+    uint32_t wgs_per_lane;
+    uint32_t redundant_global;       // block_count*max_active_per_block <= max_active_global
+    uint32_t spin_limit;
+};
+
+// Batch-end mean of one fixed-parameter tensor (see leo_merge_fixed).
+enum : uint32_t { kMergeThreshold = 0, kMergeRecurrent, kMergeInput, kMergeOutput, kMergeBias, kMergeContextOut };
+
+struct MergeArgs {
+    float* canonical;
+    const float* const* lanes;   // per-lane pointer to the same tensor
+    uint32_t lane_count;
+    uint32_t kind;
+    uint64_t count;              // logical elements
+    uint32_t row;                // logical row length for padded layouts (output: 257)
+    uint32_t stride;             // physical row stride (output: kOutStride)
+    uint32_t synapses_per_neuron;
+    const uint8_t* neuron_type;
+    float weight_min, weight_max;
+    unsigned long long* updates;
+    uint32_t* error;
+};
+
+}  // namespace leo
+
+#endif

@@ -1,0 +1,1516 @@
+// Host runtime of the MI355X backend behind the C-ABI in include/leo_hip.h.
+//
+// It plays the role of the reference's GpuRuntime/CudaRuntime
+// (backend.rs:547-794, cuda.rs:1553-9355): it owns the canonical model image on
+// the device, a canonical lane (the runtime that trains in place for
+// one-worker batches and executes replay), and story lanes for logical
+// batches. The training coordinator (training.rs:1539-1954) sits on top:
+// document passes, the batch-end lane-ordered mean (device fixed-parameter
+// merge + host keyed context merge, parallel.rs:694-1113), and
+// bounded-surprise replay.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "leo_device.h"
+#include "leo_hip.h"
+#include "leo_host.h"
+
+namespace leo {
+
+__global__ void leo_lane_steps(KernelArgs args);
+__global__ void leo_reset_lanes(KernelArgs args, uint32_t set_tick, uint32_t new_tick);
+
+__global__ void leo_merge_fixed(MergeArgs m);
+
+namespace {
+
+thread_local std::string g_error;
+
+#define LEO_HIP_CHECK(expr)                                                                          \
+    do {                                                                                             \
+        hipError_t status_ = (expr);                                                                 \
+        if (status_ != hipSuccess)                                                                   \
+            throw Error(status_ == hipErrorOutOfMemory ? LEO_ERR_OUT_OF_MEMORY : LEO_ERR_DEVICE,     \
+                        std::string(#expr) + ": " + hipGetErrorString(status_));                     \
+    } while (0)
+
+constexpr uint32_t kBegin = 256, kEnd = 257;
+
+// ---------------------------------------------------------------------------
+// Device memory: one arena per lane / per image, carved into 256-byte
+// aligned arrays.
+// ---------------------------------------------------------------------------
+struct Arena {
+    char* base = nullptr;
+    size_t bytes = 0;
+    Arena() = default;
+    Arena(const Arena&) = delete;
+    Arena& operator=(const Arena&) = delete;
+    ~Arena() { release(); }
+    void release() {
+        if (base) (void)hipFree(base);
+        base = nullptr;
+        bytes = 0;
+    }
+    void allocate(size_t n) {
+        release();
+        bytes = n;
+        LEO_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&base), std::max<size_t>(n, 256)));
+    }
+};
+
+struct Layout {
+    size_t cursor = 0;
+    template <class T>
+    size_t add(size_t count) {
+        size_t at = cursor;
+        cursor += (count * sizeof(T) + 255) & ~static_cast<size_t>(255);
+        return at;
+    }
+};
+
+struct Sizes {
+    uint64_t n, s, f, ns, ni, slots, e, blocks, limit, cap, bucket_total;
+    uint64_t words(uint64_t count) const { return (count + 31) / 32; }
+};
+
+float plasticity_step(uint32_t window, uint32_t& phase, bool end_document) {  // config.rs:137-145
+    uint32_t w = std::max<uint32_t>(window, 1);
+    uint32_t step = std::min(phase, w - 1) + 1;
+    if (step == w || end_document) {
+        phase = 0;
+        return static_cast<float>(step);
+    }
+    phase = step;
+    return 0.0f;
+}
+
+bool context_survives_dropout(uint64_t seed, uint64_t tick, uint32_t symbol, float rate) {  // runtime.rs:103-116
+    if (rate <= 0.0f) return true;
+    uint64_t v = seed ^ (tick * 0x9e3779b97f4a7c15ULL) ^ (static_cast<uint64_t>(symbol) * 0xbf58476d1ce4e5b9ULL);
+    v = (v ^ (v >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    v = (v ^ (v >> 27)) * 0x94d049bb133111ebULL;
+    v ^= v >> 31;
+    float draw = static_cast<float>(static_cast<uint32_t>(v >> 40)) / static_cast<float>(1u << 24);
+    return draw >= rate;
+}
+
+float permission_strength(const LeoHostConfig& c, int32_t permission) {  // permission.rs:24-31
+    switch (permission) {
+        case LEO_FROZEN: return 0.0f;
+        case LEO_PROVISIONAL: return c.provisional_strength;
+        case LEO_TRAINING: return c.training_strength;
+        case LEO_VERIFIED: return c.verified_strength;
+        default: throw Error(LEO_ERR_INVALID_ARGUMENT, "unknown permission");
+    }
+}
+
+struct HostStep {
+    uint32_t symbol;
+    int32_t target;  // external symbol or -1
+};
+
+// Lane: transient state (+ optionally its own learned-parameter copy).
+struct Lane {
+    Arena state;
+    Arena params;
+    LaneDesc desc{};
+    Arena schedule;  // steps + records
+    uint32_t schedule_capacity = 0;
+    // host mirrors of per-runtime scalars (deterministic from the schedule)
+    uint32_t tick = 0;
+    uint32_t plasticity_phase = 0;
+    bool persistent_activity = false;
+};
+
+struct ContextDelta {
+    size_t order;
+    uint64_t key;
+    std::vector<float> emb;
+    uint32_t obs_inc;
+};
+
+}  // namespace
+
+}  // namespace leo
+
+struct LeoHipRuntime {
+    LeoHostConfig cfg{};
+    leo::Sizes z{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int cus = 0;
+    int coop_blocks_per_cu = 0;
+    leo::Arena shared;
+    leo::SharedModel sm{};
+    leo::Arena canon_params;
+    leo::LaneParams canon{};
+    std::unique_ptr<leo::Lane> canonical;
+    std::vector<std::unique_ptr<leo::Lane>> lanes;
+    uint32_t max_lanes = 0;
+    leo::Arena lane_descs;     // LaneDesc[max(1,max_lanes)]
+    leo::Arena merge_scratch;  // lane pointer table + counters
+    // host copies of the read-only topology (device copies are immutable)
+    std::vector<float> excitability;
+    std::vector<uint8_t> neuron_type, rec_branch, rec_delay, in_branch;
+    std::vector<uint32_t> rec_target, in_target;
+    // host mirrors of model scalars
+    uint64_t generation = 0, revision = 0;
+    LeoStatistics stats{};
+    bool tracking = false;
+    std::atomic<bool> busy{false};
+    uint32_t wgs_override = 0;
+};
+
+namespace leo {
+
+int32_t set_error(int32_t code, const std::string& message) {
+    g_error = message;
+    return code;
+}
+
+namespace {
+
+struct BusyGuard {
+    LeoHipRuntime* h;
+    explicit BusyGuard(LeoHipRuntime* rt) : h(rt) {
+        if (!h) throw Error(LEO_ERR_INVALID_ARGUMENT, "null runtime handle");
+        bool expected = false;
+        if (!h->busy.compare_exchange_strong(expected, true))
+            throw Error(LEO_ERR_BUSY, "concurrent call on one runtime handle");
+        LEO_HIP_CHECK(hipSetDevice(h->device));
+    }
+    ~BusyGuard() { h->busy.store(false); }
+};
+
+Sizes sizes_of(const LeoHostConfig& c) {
+    Sizes z{};
+    z.n = c.device.neuron_count;
+    z.s = c.device.synapses_per_neuron;
+    z.f = c.device.input_fanout;
+    z.ns = z.n * z.s;
+    z.ni = static_cast<uint64_t>(kSymbols) * z.f;
+    z.slots = static_cast<uint64_t>(c.device.context_max_order) * c.device.context_slots_per_order;
+    z.e = c.device.context_embedding_dim;
+    z.blocks = c.device.block_count;
+    z.limit = c.device.max_active_per_block;
+    z.cap = c.device.max_active_global;
+    return z;
+}
+
+void upload(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    if (bytes) LEO_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
+}
+void download(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    if (bytes) LEO_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s));
+}
+void sync(hipStream_t s) { LEO_HIP_CHECK(hipStreamSynchronize(s)); }
+
+// Allocate a learned-parameter image.
+LaneParams allocate_params(Arena& arena, const Sizes& z, hipStream_t stream) {
+    Layout l;
+    size_t o_th = l.add<float>(z.n), o_rw = l.add<float>(z.ns), o_iw = l.add<float>(z.ni);
+    size_t o_ow = l.add<float>(z.n * kOutStride), o_b = l.add<float>(kOutStride);
+    size_t o_ck = l.add<uint64_t>(z.slots), o_ce = l.add<float>(z.slots * z.e), o_co = l.add<uint32_t>(z.slots);
+    size_t o_cw = l.add<float>(static_cast<uint64_t>(kOutputs) * z.e);
+    arena.allocate(l.cursor);
+    LaneParams p{};
+    p.threshold = reinterpret_cast<float*>(arena.base + o_th);
+    p.rec_weight = reinterpret_cast<float*>(arena.base + o_rw);
+    p.in_weight = reinterpret_cast<float*>(arena.base + o_iw);
+    p.out_w = reinterpret_cast<float*>(arena.base + o_ow);
+    p.bias = reinterpret_cast<float*>(arena.base + o_b);
+    p.ctx_keys = reinterpret_cast<uint64_t*>(arena.base + o_ck);
+    p.ctx_emb = reinterpret_cast<float*>(arena.base + o_ce);
+    p.ctx_obs = reinterpret_cast<uint32_t*>(arena.base + o_co);
+    p.ctx_out = reinterpret_cast<float*>(arena.base + o_cw);
+    // zero on the runtime's stream: a non-blocking stream is not ordered after the null stream
+    LEO_HIP_CHECK(hipMemsetAsync(arena.base, 0, arena.bytes, stream));
+    LEO_HIP_CHECK(hipStreamSynchronize(stream));
+    return p;
+}
+
+void copy_params(const LaneParams& dst, const LaneParams& src, const Sizes& z, hipStream_t s) {
+    auto cp = [&](void* d, const void* from, size_t bytes) {
+        LEO_HIP_CHECK(hipMemcpyAsync(d, from, bytes, hipMemcpyDeviceToDevice, s));
+    };
+    cp(dst.threshold, src.threshold, z.n * 4);
+    cp(dst.rec_weight, src.rec_weight, z.ns * 4);
+    cp(dst.in_weight, src.in_weight, z.ni * 4);
+    cp(dst.out_w, src.out_w, z.n * kOutStride * 4);
+    cp(dst.bias, src.bias, kOutStride * 4);
+    cp(dst.ctx_keys, src.ctx_keys, z.slots * 8);
+    cp(dst.ctx_emb, src.ctx_emb, z.slots * z.e * 4);
+    cp(dst.ctx_obs, src.ctx_obs, z.slots * 4);
+    cp(dst.ctx_out, src.ctx_out, kOutputs * z.e * 4);
+}
+
+void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
+    Layout l;
+    size_t o_ctl = l.add<LaneControl>(1);
+    size_t o_mem = l.add<float>(z.n), o_act = l.add<float>(z.n), o_fat = l.add<float>(z.n);
+    size_t o_ref = l.add<uint32_t>(z.n), o_br = l.add<float>(4 * z.n), o_last = l.add<uint32_t>(z.n);
+    size_t o_ad = l.add<float>(3 * z.n), o_te = l.add<uint32_t>(z.n), o_tl = l.add<uint32_t>(z.n);
+    size_t o_se = l.add<uint32_t>(z.n), o_su = l.add<float>(z.n), o_de = l.add<uint32_t>(z.n);
+    size_t o_ls = l.add<float>(z.n), o_bc = l.add<uint32_t>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
+    size_t o_bw = l.add<uint32_t>(z.blocks * z.limit), o_bn = l.add<uint32_t>(z.blocks), o_bcut = l.add<float>(z.blocks);
+    size_t o_ra = l.add<uint32_t>(kRing * z.cap), o_rv = l.add<float>(kRing * z.cap), o_rval = l.add<float>(kRing * z.cap * z.s);
+    size_t o_rt = l.add<float>(7 * z.ns), o_rl = l.add<uint32_t>(z.ns), o_rm = l.add<uint8_t>(z.ns), o_rlist = l.add<uint32_t>(2 * z.ns);
+    size_t o_it = l.add<float>(7 * z.ni), o_il = l.add<uint32_t>(z.ni), o_im = l.add<uint8_t>(z.ni), o_ilist = l.add<uint32_t>(2 * z.ni);
+    size_t o_lg = l.add<float>(kOutStride), o_pr = l.add<float>(kOutStride), o_er = l.add<float>(kOutStride);
+    size_t o_lat = l.add<float>(std::max<uint64_t>(z.e, 1));
+    size_t o_cth = l.add<uint32_t>(z.words(z.n)), o_crec = l.add<uint32_t>(z.words(z.ns)), o_cin = l.add<uint32_t>(z.words(z.ni));
+    size_t o_cout = l.add<uint32_t>(z.words(z.n)), o_cctx = l.add<uint32_t>(z.words(z.slots));
+    lane.state.allocate(l.cursor);
+    char* b = lane.state.base;
+    LaneDesc& d = lane.desc;
+    d.ctl = reinterpret_cast<LaneControl*>(b + o_ctl);
+    d.membrane = reinterpret_cast<float*>(b + o_mem);
+    d.activation = reinterpret_cast<float*>(b + o_act);
+    d.fatigue = reinterpret_cast<float*>(b + o_fat);
+    d.refractory_until = reinterpret_cast<uint32_t*>(b + o_ref);
+    d.branches = reinterpret_cast<float*>(b + o_br);
+    d.last_tick = reinterpret_cast<uint32_t*>(b + o_last);
+    d.adapt = reinterpret_cast<float*>(b + o_ad);
+    d.touched_epoch = reinterpret_cast<uint32_t*>(b + o_te);
+    d.touched_list = reinterpret_cast<uint32_t*>(b + o_tl);
+    d.selected_epoch = reinterpret_cast<uint32_t*>(b + o_se);
+    d.surrogate = reinterpret_cast<float*>(b + o_su);
+    d.dest_epoch = reinterpret_cast<uint32_t*>(b + o_de);
+    d.learning_signal = reinterpret_cast<float*>(b + o_ls);
+    d.bucket_count = reinterpret_cast<uint32_t*>(b + o_bc);
+    d.bucket = reinterpret_cast<uint64_t*>(b + o_bk);
+    d.block_winners = reinterpret_cast<uint32_t*>(b + o_bw);
+    d.block_count = reinterpret_cast<uint32_t*>(b + o_bn);
+    d.block_cutoff = reinterpret_cast<float*>(b + o_bcut);
+    d.ring_active = reinterpret_cast<uint32_t*>(b + o_ra);
+    d.ring_act = reinterpret_cast<float*>(b + o_rv);
+    d.ring_value = reinterpret_cast<float*>(b + o_rval);
+    d.rec_trace = reinterpret_cast<float*>(b + o_rt);
+    d.rec_last = reinterpret_cast<uint32_t*>(b + o_rl);
+    d.rec_mark = reinterpret_cast<uint8_t*>(b + o_rm);
+    d.rec_list = reinterpret_cast<uint32_t*>(b + o_rlist);
+    d.in_trace = reinterpret_cast<float*>(b + o_it);
+    d.in_last = reinterpret_cast<uint32_t*>(b + o_il);
+    d.in_mark = reinterpret_cast<uint8_t*>(b + o_im);
+    d.in_list = reinterpret_cast<uint32_t*>(b + o_ilist);
+    d.logits = reinterpret_cast<float*>(b + o_lg);
+    d.probs = reinterpret_cast<float*>(b + o_pr);
+    d.errors = reinterpret_cast<float*>(b + o_er);
+    d.ctx_latent = reinterpret_cast<float*>(b + o_lat);
+    d.ch_threshold = reinterpret_cast<uint32_t*>(b + o_cth);
+    d.ch_rec = reinterpret_cast<uint32_t*>(b + o_crec);
+    d.ch_in = reinterpret_cast<uint32_t*>(b + o_cin);
+    d.ch_out = reinterpret_cast<uint32_t*>(b + o_cout);
+    d.ch_ctx = reinterpret_cast<uint32_t*>(b + o_cctx);
+    LEO_HIP_CHECK(hipMemsetAsync(b, 0, lane.state.bytes, stream));
+    LEO_HIP_CHECK(hipStreamSynchronize(stream));
+}
+
+void clear_changes(const Lane& lane, const Sizes& z, hipStream_t s) {
+    const LaneDesc& d = lane.desc;
+    LEO_HIP_CHECK(hipMemsetAsync(d.ch_threshold, 0, z.words(z.n) * 4, s));
+    LEO_HIP_CHECK(hipMemsetAsync(d.ch_rec, 0, z.words(z.ns) * 4, s));
+    LEO_HIP_CHECK(hipMemsetAsync(d.ch_in, 0, z.words(z.ni) * 4, s));
+    LEO_HIP_CHECK(hipMemsetAsync(d.ch_out, 0, z.words(z.n) * 4, s));
+    LEO_HIP_CHECK(hipMemsetAsync(d.ch_ctx, 0, z.words(z.slots) * 4, s));
+    LEO_HIP_CHECK(hipMemsetAsync(&d.ctl->bias_dirty, 0, 8, s));  // bias_dirty, ctx_out_dirty
+}
+
+KernelArgs kernel_args(LeoHipRuntime* h, LaneDesc* lanes, uint32_t count, uint32_t P) {
+    KernelArgs a{};
+    a.cfg = h->cfg.device;
+    a.m = h->sm;
+    a.lanes = lanes;
+    a.lane_count = count;
+    a.wgs_per_lane = P;
+    a.redundant_global = (static_cast<uint64_t>(h->z.blocks) * h->z.limit <= h->z.cap) ? 1 : 0;
+    a.spin_limit = 1u << 26;
+    return a;
+}
+
+// Reset transient state of the given lanes (runtime.rs:365-425). Descriptors
+// of these lanes must already be resident at lane_descs[0..count).
+void reset_lanes(LeoHipRuntime* h, uint32_t count, bool set_tick, uint32_t new_tick) {
+    LaneDesc* descs = reinterpret_cast<LaneDesc*>(h->lane_descs.base);
+    KernelArgs a = kernel_args(h, descs, count, 1);
+    uint32_t grid = count * 64;
+    hipLaunchKernelGGL(leo_reset_lanes, dim3(grid), dim3(kThreads), 0, h->stream, a, set_tick ? 1u : 0u, new_tick);
+    LEO_HIP_CHECK(hipGetLastError());
+}
+
+void stage_descs(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
+    std::vector<LaneDesc> host(lanes.size());
+    for (size_t i = 0; i < lanes.size(); ++i) host[i] = lanes[i]->desc;
+    upload(h->lane_descs.base, host.data(), host.size() * sizeof(LaneDesc), h->stream);
+}
+
+void reset_lane_objects(LeoHipRuntime* h, const std::vector<Lane*>& lanes, bool set_tick, uint32_t new_tick) {
+    stage_descs(h, lanes);
+    reset_lanes(h, static_cast<uint32_t>(lanes.size()), set_tick, new_tick);
+    for (Lane* l : lanes) {
+        if (set_tick) l->tick = new_tick;
+        l->plasticity_phase = 0;
+        l->persistent_activity = false;
+    }
+}
+
+uint32_t choose_wgs_per_lane(LeoHipRuntime* h, uint32_t lanes) {
+    uint32_t coop = static_cast<uint32_t>(h->cus * h->coop_blocks_per_cu);
+    uint32_t limit = std::max<uint32_t>(1, coop / std::max<uint32_t>(lanes, 1));
+    uint32_t want;
+    if (h->wgs_override) {
+        want = h->wgs_override;
+    } else {
+        uint64_t by_blocks = h->z.blocks;
+        uint64_t by_edges = h->z.ns / 8192;
+        want = static_cast<uint32_t>(std::max<uint64_t>(1, std::max(by_blocks, by_edges)));
+        want = std::min<uint32_t>(want, 64);
+    }
+    return std::max<uint32_t>(1, std::min(want, limit));
+}
+
+StepParams make_step(const LeoHostConfig& c, Lane& lane, uint32_t symbol, int32_t target, int32_t permission,
+                     uint32_t tick, bool output) {
+    if (symbol >= kSymbols) throw Error(LEO_ERR_INVALID_ARGUMENT, "invalid input symbol: " + std::to_string(symbol));
+    int32_t target_index = -1;
+    if (target >= 0) {
+        uint32_t t = static_cast<uint32_t>(target);
+        if (t < 256) target_index = static_cast<int32_t>(t);
+        else if (t == kEnd) target_index = static_cast<int32_t>(kEndIndex);
+        else throw Error(LEO_ERR_INVALID_ARGUMENT, "invalid output target: " + std::to_string(t));
+    }
+    const bool frozen = permission == LEO_FROZEN;
+    const float strength = permission_strength(c, permission);
+    StepParams sp{};
+    sp.symbol = symbol;
+    sp.target_index = target_index;
+    bool ctx = frozen || context_survives_dropout(c.seed, tick, symbol, c.context_dropout_rate);
+    sp.flags = (frozen ? kStepFrozen : kStepLearnTrace) | (ctx ? kStepContext : 0u) | ((!frozen && ctx) ? kStepAllocate : 0u);
+    const bool learn = target_index >= 0 && strength > 0.0f;
+    if (output || learn) sp.flags |= kStepOutput;
+    sp.strength = strength;
+    if (learn) {
+        sp.flags |= kStepLearn;
+        float weight = static_cast<uint32_t>(target_index) == kEndIndex ? c.end_document_weight : 1.0f;
+        sp.supervised_strength = strength * weight;
+        sp.plasticity_scale = plasticity_step(c.plasticity_window, lane.plasticity_phase,
+                                              static_cast<uint32_t>(target_index) == kEndIndex);
+    }
+    return sp;
+}
+
+struct LaneRun {
+    Lane* lane;
+    std::vector<StepParams> steps;
+    std::vector<StepRecord> records;
+};
+
+// One cooperative launch over all given lanes (each with its own schedule).
+void run_lanes(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
+    const uint32_t count = static_cast<uint32_t>(runs.size());
+    if (count == 0) return;
+    uint64_t max_tick = 0;
+    for (auto& r : runs) max_tick = std::max<uint64_t>(max_tick, static_cast<uint64_t>(r.lane->tick) + r.steps.size());
+    if (max_tick + static_cast<uint64_t>(h->cfg.device.refractory_ticks) + 2 >= 0xffffffffULL)
+        throw Error(LEO_ERR_UNSUPPORTED, "lane tick would exceed the 32-bit device tick range");
+    for (auto& r : runs) {
+        Lane& lane = *r.lane;
+        uint32_t need = static_cast<uint32_t>(std::max<size_t>(r.steps.size(), 1));
+        if (need > lane.schedule_capacity) {
+            uint32_t cap = std::max<uint32_t>(need, 256);
+            lane.schedule.allocate(static_cast<size_t>(cap) * (sizeof(StepParams) + sizeof(StepRecord)) + 512);
+            lane.schedule_capacity = cap;
+        }
+        lane.desc.steps = reinterpret_cast<const StepParams*>(lane.schedule.base);
+        lane.desc.records = reinterpret_cast<StepRecord*>(
+            lane.schedule.base + ((static_cast<size_t>(lane.schedule_capacity) * sizeof(StepParams) + 255) & ~size_t(255)));
+        lane.desc.step_count = static_cast<uint32_t>(r.steps.size());
+        upload(const_cast<StepParams*>(lane.desc.steps), r.steps.data(), r.steps.size() * sizeof(StepParams), h->stream);
+        LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->barrier, 0, 8, h->stream));  // barrier + abort
+        LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->error_code, 0, 4, h->stream));
+    }
+    std::vector<Lane*> lanes;
+    for (auto& r : runs) lanes.push_back(r.lane);
+    stage_descs(h, lanes);
+    const uint32_t P = choose_wgs_per_lane(h, count);
+    KernelArgs a = kernel_args(h, reinterpret_cast<LaneDesc*>(h->lane_descs.base), count, P);
+    void* params[] = {&a};
+    LEO_HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&leo_lane_steps), dim3(count * P),
+                                             dim3(kThreads), params, 0, h->stream));
+    std::vector<LaneControl> ctl(count);
+    for (uint32_t i = 0; i < count; ++i) {
+        runs[i].records.resize(runs[i].steps.size());
+        download(runs[i].records.data(), runs[i].lane->desc.records, runs[i].steps.size() * sizeof(StepRecord), h->stream);
+        download(&ctl[i], runs[i].lane->desc.ctl, sizeof(LaneControl), h->stream);
+    }
+    sync(h->stream);
+    for (uint32_t i = 0; i < count; ++i) {
+        runs[i].lane->tick += static_cast<uint32_t>(runs[i].steps.size());
+        if (ctl[i].error_code != 0) {
+            uint32_t code = ctl[i].error_code;
+            if (code == kErrBarrier) throw Error(LEO_ERR_DEVICE, "device lane barrier timed out");
+            if (code == kErrCapacity)
+                throw Error(LEO_ERR_UNSUPPORTED, "global selection exceeds the device sort capacity");
+            throw Error(LEO_ERR_NUMERICAL, "device numerical guard tripped (code " + std::to_string(code) + ")");
+        }
+        if (ctl[i].tick != runs[i].lane->tick) throw Error(LEO_ERR_INTERNAL, "device lane tick diverged from the host mirror");
+    }
+}
+
+// Statistics of one step (runtime.rs:1595-1622) from its device record.
+void account_step(LeoStatistics& st, const StepParams& sp, const StepRecord& rec, float loss, uint32_t synapses) {
+    if (sp.flags & kStepFrozen) return;
+    if (sp.symbol < 256) st.processed_bytes += 1;
+    if (sp.target_index >= 0) {
+        st.training_loss_sum += static_cast<double>(loss);
+        st.training_targets += 1;
+    }
+    st.active_neurons_sum += rec.active;
+    st.active_neurons_peak = std::max<uint64_t>(st.active_neurons_peak, rec.active);
+    st.synaptic_events += static_cast<uint64_t>(rec.active) * synapses;
+    st.persistent_ticks += 1;
+}
+
+float step_loss(const StepParams& sp, const StepRecord& rec) {
+    if (sp.target_index < 0) return NAN;
+    return -std::log(std::max(rec.p_target, 1.0e-12f));  // runtime.rs:471 (glibc logf)
+}
+
+LeoStepMetrics to_metrics(const StepParams& sp, const StepRecord& rec, float loss) {
+    LeoStepMetrics m{};
+    m.loss = loss;
+    m.has_loss = sp.target_index >= 0 ? 1 : 0;
+    m.predicted_symbol = rec.predicted < 256 ? rec.predicted : kEnd;
+    m.active_neurons = rec.active;
+    m.suprathreshold_neurons = rec.suprathreshold;
+    m.block_selected_neurons = rec.block_selected;
+    m.global_cap_clipped_neurons = rec.clipped;
+    m.population_inhibition = rec.population_inhibition;
+    m.context_cells = rec.context_cells;
+    m.context_probes = rec.context_probes;
+    m.context_applied = rec.context_applied;
+    m.eligible_recurrent_synapses = rec.eligible_rec;
+    m.eligible_input_synapses = rec.eligible_in;
+    m.target_probability = sp.target_index >= 0 ? rec.p_target : NAN;
+    m.error_code = rec.error_code;
+    return m;
+}
+
+// Execute steps on the canonical runtime; stats and revision update the
+// canonical mirrors exactly as Runtime::step does.
+std::vector<LeoStepMetrics> canonical_steps(LeoHipRuntime* h, const std::vector<HostStep>& steps,
+                                            const std::vector<int32_t>& permissions, bool output) {
+    Lane& lane = *h->canonical;
+    LaneRun run{&lane, {}, {}};
+    run.steps.reserve(steps.size());
+    uint32_t tick = lane.tick;
+    for (size_t i = 0; i < steps.size(); ++i)
+        run.steps.push_back(make_step(h->cfg, lane, steps[i].symbol, steps[i].target, permissions[i], tick++, output));
+    std::vector<LaneRun> runs;
+    runs.push_back(std::move(run));
+    run_lanes(h, runs);
+    std::vector<LeoStepMetrics> out;
+    out.reserve(steps.size());
+    const LaneRun& r = runs[0];
+    for (size_t i = 0; i < r.steps.size(); ++i) {
+        float loss = step_loss(r.steps[i], r.records[i]);
+        account_step(h->stats, r.steps[i], r.records[i], loss, h->cfg.device.synapses_per_neuron);
+        if (r.steps[i].flags & kStepLearn) h->revision += 1;
+        if (!(r.steps[i].flags & kStepFrozen)) lane.persistent_activity = true;
+        LeoStepMetrics m = to_metrics(r.steps[i], r.records[i], loss);
+        m.emitted_events = r.records[i].active * h->cfg.device.synapses_per_neuron;
+        out.push_back(m);
+    }
+    return out;
+}
+
+void canonical_reset(LeoHipRuntime* h) {
+    std::vector<Lane*> lanes{h->canonical.get()};
+    reset_lane_objects(h, lanes, false, 0);
+    sync(h->stream);
+}
+
+void canonical_finish_document(LeoHipRuntime* h) {  // runtime.rs:357-363
+    if (h->canonical->persistent_activity) h->stats.processed_stories += 1;
+    canonical_reset(h);
+}
+
+std::vector<HostStep> document_steps(const uint8_t* story, size_t len) {  // training.rs:1747-1757
+    std::vector<HostStep> steps;
+    steps.reserve(len + 1);
+    steps.push_back({kBegin, story[0]});
+    for (size_t i = 0; i + 1 < len; ++i) steps.push_back({story[i], story[i + 1]});
+    steps.push_back({story[len - 1], static_cast<int32_t>(kEnd)});
+    return steps;
+}
+
+// Host layouts <-> device layouts.
+void upload_model(LeoHipRuntime* h, const LeoModelView& m) {
+    const Sizes& z = h->z;
+    hipStream_t s = h->stream;
+    upload(h->canon.threshold, m.threshold, z.n * 4, s);
+    upload(h->canon.rec_weight, m.rec_weight, z.ns * 4, s);
+    upload(h->canon.in_weight, m.in_weight, z.ni * 4, s);
+    std::vector<float> rows(z.n * kOutStride, 0.0f);
+    for (uint64_t o = 0; o < kOutputs; ++o)
+        for (uint64_t n = 0; n < z.n; ++n) rows[n * kOutStride + o] = m.out_weight[o * z.n + n];
+    upload(h->canon.out_w, rows.data(), rows.size() * 4, s);
+    std::vector<float> bias(kOutStride, 0.0f);
+    std::copy(m.bias, m.bias + kOutputs, bias.begin());
+    upload(h->canon.bias, bias.data(), kOutStride * 4, s);
+    upload(h->canon.ctx_keys, m.ctx_keys, z.slots * 8, s);
+    upload(h->canon.ctx_emb, m.ctx_emb, z.slots * z.e * 4, s);
+    upload(h->canon.ctx_obs, m.ctx_obs, z.slots * 4, s);
+    upload(h->canon.ctx_out, m.ctx_out, kOutputs * z.e * 4, s);
+    sync(s);
+    h->generation = m.generation;
+    h->revision = m.parameter_revision;
+    h->stats = m.statistics;
+}
+
+void upload_topology(LeoHipRuntime* h, const LeoModelView& m) {
+    const Sizes& z = h->z;
+    h->excitability.assign(m.excitability, m.excitability + z.n);
+    h->neuron_type.assign(m.neuron_type, m.neuron_type + z.n);
+    h->rec_target.assign(m.rec_target, m.rec_target + z.ns);
+    h->rec_branch.assign(m.rec_branch, m.rec_branch + z.ns);
+    h->rec_delay.assign(m.rec_delay, m.rec_delay + z.ns);
+    h->in_target.assign(m.in_target, m.in_target + z.ni);
+    h->in_branch.assign(m.in_branch, m.in_branch + z.ni);
+    // per-target delivery bucket capacity: recurrent in-degree + the largest
+    // number of times one input row names the target
+    std::vector<uint64_t> cap(z.n, 0);
+    for (uint64_t i = 0; i < z.ns; ++i) cap[m.rec_target[i]] += 1;
+    std::vector<uint32_t> row_count(z.n, 0), row_max(z.n, 0);
+    for (uint64_t sym = 0; sym < kSymbols; ++sym) {
+        for (uint64_t i = 0; i < z.f; ++i) {
+            uint32_t t = m.in_target[sym * z.f + i];
+            row_count[t] += 1;
+            row_max[t] = std::max(row_max[t], row_count[t]);
+        }
+        for (uint64_t i = 0; i < z.f; ++i) row_count[m.in_target[sym * z.f + i]] = 0;
+    }
+    std::vector<uint64_t> offsets(z.n + 1, 0);
+    for (uint64_t n = 0; n < z.n; ++n) offsets[n + 1] = offsets[n] + cap[n] + row_max[n];
+    h->z.bucket_total = offsets[z.n];
+    Layout l;
+    size_t o_ex = l.add<float>(z.n), o_ty = l.add<uint8_t>(z.n), o_rt = l.add<uint32_t>(z.ns);
+    size_t o_rb = l.add<uint8_t>(z.ns), o_rd = l.add<uint8_t>(z.ns), o_it = l.add<uint32_t>(z.ni);
+    size_t o_ib = l.add<uint8_t>(z.ni), o_off = l.add<uint64_t>(z.n + 1);
+    h->shared.allocate(l.cursor);
+    char* b = h->shared.base;
+    h->sm.excitability = reinterpret_cast<const float*>(b + o_ex);
+    h->sm.neuron_type = reinterpret_cast<const uint8_t*>(b + o_ty);
+    h->sm.rec_target = reinterpret_cast<const uint32_t*>(b + o_rt);
+    h->sm.rec_branch = reinterpret_cast<const uint8_t*>(b + o_rb);
+    h->sm.rec_delay = reinterpret_cast<const uint8_t*>(b + o_rd);
+    h->sm.in_target = reinterpret_cast<const uint32_t*>(b + o_it);
+    h->sm.in_branch = reinterpret_cast<const uint8_t*>(b + o_ib);
+    h->sm.bucket_offset = reinterpret_cast<const uint64_t*>(b + o_off);
+    hipStream_t s = h->stream;
+    upload(b + o_ex, m.excitability, z.n * 4, s);
+    upload(b + o_ty, m.neuron_type, z.n, s);
+    upload(b + o_rt, m.rec_target, z.ns * 4, s);
+    upload(b + o_rb, m.rec_branch, z.ns, s);
+    upload(b + o_rd, m.rec_delay, z.ns, s);
+    upload(b + o_it, m.in_target, z.ni * 4, s);
+    upload(b + o_ib, m.in_branch, z.ni, s);
+    upload(b + o_off, offsets.data(), offsets.size() * 8, s);
+    sync(s);
+}
+
+void download_model(LeoHipRuntime* h, LeoModelView& m) {
+    const Sizes& z = h->z;
+    hipStream_t s = h->stream;
+    std::copy(h->excitability.begin(), h->excitability.end(), m.excitability);
+    std::copy(h->neuron_type.begin(), h->neuron_type.end(), m.neuron_type);
+    std::copy(h->rec_target.begin(), h->rec_target.end(), m.rec_target);
+    std::copy(h->rec_branch.begin(), h->rec_branch.end(), m.rec_branch);
+    std::copy(h->rec_delay.begin(), h->rec_delay.end(), m.rec_delay);
+    std::copy(h->in_target.begin(), h->in_target.end(), m.in_target);
+    std::copy(h->in_branch.begin(), h->in_branch.end(), m.in_branch);
+    download(m.threshold, h->canon.threshold, z.n * 4, s);
+    download(m.rec_weight, h->canon.rec_weight, z.ns * 4, s);
+    download(m.in_weight, h->canon.in_weight, z.ni * 4, s);
+    std::vector<float> rows(z.n * kOutStride);
+    download(rows.data(), h->canon.out_w, rows.size() * 4, s);
+    std::vector<float> bias(kOutStride);
+    download(bias.data(), h->canon.bias, kOutStride * 4, s);
+    download(m.ctx_keys, h->canon.ctx_keys, z.slots * 8, s);
+    download(m.ctx_emb, h->canon.ctx_emb, z.slots * z.e * 4, s);
+    download(m.ctx_obs, h->canon.ctx_obs, z.slots * 4, s);
+    download(m.ctx_out, h->canon.ctx_out, kOutputs * z.e * 4, s);
+    sync(s);
+    for (uint64_t o = 0; o < kOutputs; ++o)
+        for (uint64_t n = 0; n < z.n; ++n) m.out_weight[o * z.n + n] = rows[n * kOutStride + o];
+    std::copy(bias.begin(), bias.begin() + kOutputs, m.bias);
+    m.generation = h->generation;
+    m.parameter_revision = h->revision;
+    m.statistics = h->stats;
+}
+
+// ---------------------------------------------------------------------------
+// Keyed context merge on the host (parallel.rs:916-973, 1024-1113, 1226-1233).
+// ---------------------------------------------------------------------------
+struct HostContext {
+    std::vector<uint64_t> keys;
+    std::vector<uint32_t> obs;
+    std::vector<float> emb;
+};
+
+int64_t find_context_slot(const HostContext& c, const LeoHostConfig& cfg, size_t order, uint64_t key) {
+    const uint64_t spo = cfg.device.context_slots_per_order;
+    const uint64_t base = (order - 1) * spo, start = key % spo;
+    for (uint64_t off = 0; off < cfg.device.context_probe_limit; ++off) {
+        uint64_t slot = base + (start + off) % spo;
+        if (c.keys[slot] == key) return static_cast<int64_t>(slot);
+    }
+    return -1;
+}
+
+int64_t resolve_context_slot(HostContext& c, const LeoHostConfig& cfg, size_t order, uint64_t key, bool allocate,
+                             size_t E) {  // model.rs:173-221
+    const uint64_t spo = cfg.device.context_slots_per_order;
+    const uint64_t base = (order - 1) * spo, start = key % spo;
+    int64_t empty = -1;
+    uint64_t weakest = base + start;
+    uint32_t weakest_obs = UINT32_MAX;
+    for (uint64_t off = 0; off < cfg.device.context_probe_limit; ++off) {
+        uint64_t slot = base + (start + off) % spo;
+        if (c.keys[slot] == key) return static_cast<int64_t>(slot);
+        if (c.keys[slot] == 0 && empty < 0) empty = static_cast<int64_t>(slot);
+        if (c.obs[slot] < weakest_obs) {
+            weakest_obs = c.obs[slot];
+            weakest = slot;
+        }
+    }
+    if (!allocate) return -1;
+    uint64_t slot = empty >= 0 ? static_cast<uint64_t>(empty) : weakest;
+    if (c.keys[slot] != key) {
+        c.keys[slot] = key;
+        c.obs[slot] = 0;
+        std::fill(c.emb.begin() + slot * E, c.emb.begin() + (slot + 1) * E, 0.0f);
+    }
+    return static_cast<int64_t>(slot);
+}
+
+HostContext download_context(LeoHipRuntime* h, const LaneParams& p) {
+    const Sizes& z = h->z;
+    HostContext c;
+    c.keys.resize(z.slots);
+    c.obs.resize(z.slots);
+    c.emb.resize(z.slots * z.e);
+    download(c.keys.data(), p.ctx_keys, z.slots * 8, h->stream);
+    download(c.obs.data(), p.ctx_obs, z.slots * 4, h->stream);
+    download(c.emb.data(), p.ctx_emb, z.slots * z.e * 4, h->stream);
+    return c;
+}
+
+std::vector<uint32_t> download_bits(LeoHipRuntime* h, const uint32_t* bits, uint64_t count) {
+    std::vector<uint32_t> v((count + 31) / 32);
+    download(v.data(), bits, v.size() * 4, h->stream);
+    return v;
+}
+
+std::vector<uint64_t> bits_to_indices(const std::vector<uint32_t>& bits, uint64_t count) {
+    std::vector<uint64_t> out;
+    for (uint64_t w = 0; w < bits.size(); ++w) {
+        uint32_t v = bits[w];
+        while (v) {
+            int b = __builtin_ctz(v);
+            uint64_t idx = w * 32 + static_cast<uint64_t>(b);
+            if (idx < count) out.push_back(idx);
+            v &= v - 1;
+        }
+    }
+    return out;
+}
+
+size_t merge_context(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
+    const Sizes& z = h->z;
+    const size_t E = z.e;
+    const uint64_t spo = h->cfg.device.context_slots_per_order;
+    HostContext master = download_context(h, h->canon);
+    std::vector<HostContext> lane_ctx;
+    std::vector<std::vector<uint32_t>> lane_bits;
+    for (Lane* l : lanes) {
+        lane_ctx.push_back(download_context(h, l->desc.p));
+        lane_bits.push_back(download_bits(h, l->desc.ch_ctx, z.slots));
+    }
+    sync(h->stream);
+    // per-lane deltas against the pre-merge canonical (context_deltas_for_slots)
+    std::vector<std::vector<ContextDelta>> deltas(lanes.size());
+    for (size_t li = 0; li < lanes.size(); ++li) {
+        const HostContext& t = lane_ctx[li];
+        for (uint64_t slot : bits_to_indices(lane_bits[li], z.slots)) {
+            uint64_t key = t.keys[slot];
+            if (key == 0) continue;
+            size_t order = static_cast<size_t>(slot / spo + 1);
+            int64_t bslot = find_context_slot(master, h->cfg, order, key);
+            uint32_t bobs = bslot >= 0 ? master.obs[static_cast<size_t>(bslot)] : 0;
+            ContextDelta d{order, key, std::vector<float>(E), 0};
+            bool changed = false;
+            for (size_t e = 0; e < E; ++e) {
+                float before = bslot >= 0 ? master.emb[static_cast<size_t>(bslot) * E + e] : 0.0f;
+                d.emb[e] = t.emb[slot * E + e] - before;
+                changed |= d.emb[e] != 0.0f;
+            }
+            d.obs_inc = t.obs[slot] > bobs ? t.obs[slot] - bobs : 0;
+            if (changed || d.obs_inc > 0) deltas[li].push_back(std::move(d));
+        }
+        std::sort(deltas[li].begin(), deltas[li].end(), [](const ContextDelta& a, const ContextDelta& b) {
+            return std::make_pair(a.order, a.key) < std::make_pair(b.order, b.key);
+        });
+    }
+    struct Merged {
+        size_t order;
+        uint64_t key;
+        std::vector<double> sum;
+        uint64_t obs;
+    };
+    std::vector<Merged> merged;
+    std::vector<size_t> pos(lanes.size(), 0);
+    while (true) {
+        bool found = false;
+        std::pair<size_t, uint64_t> next{0, 0};
+        for (size_t li = 0; li < lanes.size(); ++li)
+            if (pos[li] < deltas[li].size()) {
+                auto k = std::make_pair(deltas[li][pos[li]].order, deltas[li][pos[li]].key);
+                if (!found || k < next) {
+                    next = k;
+                    found = true;
+                }
+            }
+        if (!found) break;
+        Merged m{next.first, next.second, std::vector<double>(E, 0.0), 0};
+        for (size_t li = 0; li < lanes.size(); ++li) {
+            if (pos[li] < deltas[li].size() && deltas[li][pos[li]].order == next.first && deltas[li][pos[li]].key == next.second) {
+                const ContextDelta& d = deltas[li][pos[li]];
+                for (size_t e = 0; e < E; ++e) {
+                    if (!std::isfinite(d.emb[e])) throw Error(LEO_ERR_INTERNAL, "invalid keyed context worker delta");
+                    m.sum[e] += static_cast<double>(d.emb[e]);
+                }
+                m.obs = m.obs + d.obs_inc;
+                pos[li] += 1;
+            }
+        }
+        merged.push_back(std::move(m));
+    }
+    std::sort(merged.begin(), merged.end(), [](const Merged& a, const Merged& b) {
+        if (a.obs != b.obs) return a.obs > b.obs;
+        return std::make_pair(a.order, a.key) < std::make_pair(b.order, b.key);
+    });
+    const double divisor = static_cast<double>(lanes.size());
+    for (const Merged& m : merged) {
+        int64_t slot = resolve_context_slot(master, h->cfg, m.order, m.key, true, E);
+        for (size_t e = 0; e < E; ++e)
+            master.emb[static_cast<size_t>(slot) * E + e] += static_cast<float>(m.sum[e] / divisor);
+        uint32_t inc = static_cast<uint32_t>(std::min<uint64_t>(m.obs, UINT32_MAX));
+        uint32_t& o = master.obs[static_cast<size_t>(slot)];
+        o = (o > UINT32_MAX - inc) ? UINT32_MAX : o + inc;
+    }
+    // projection + validation of the merged embeddings (parallel.rs:1226-1233, 1317-1333)
+    const float wmin = h->cfg.device.weight_min, wmax = h->cfg.device.weight_max;
+    for (auto& lane_deltas : deltas) {
+        for (const ContextDelta& d : lane_deltas) {
+            int64_t slot = resolve_context_slot(master, h->cfg, d.order, d.key, false, E);
+            if (slot < 0) continue;
+            for (size_t e = 0; e < E; ++e) {
+                float& w = master.emb[static_cast<size_t>(slot) * E + e];
+                if (w < wmin) w = wmin;
+                if (w > wmax) w = wmax;
+                if (!std::isfinite(w)) throw Error(LEO_ERR_INTERNAL, "merged context embedding violates canonical parameter bounds");
+            }
+        }
+    }
+    upload(h->canon.ctx_keys, master.keys.data(), z.slots * 8, h->stream);
+    upload(h->canon.ctx_obs, master.obs.data(), z.slots * 4, h->stream);
+    upload(h->canon.ctx_emb, master.emb.data(), z.slots * z.e * 4, h->stream);
+    sync(h->stream);
+    return merged.size();
+}
+
+// Device mean of every fixed-parameter tensor (parallel.rs:746-782).
+uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
+    const Sizes& z = h->z;
+    const uint32_t L = static_cast<uint32_t>(lanes.size());
+    // scratch: 6 pointer tables of L entries + 1 counter + error word
+    size_t need = 6 * L * sizeof(float*) + 256;
+    if (h->merge_scratch.bytes < need) {
+        h->merge_scratch.allocate(need);
+    }
+    std::vector<const float*> tables(6 * L);
+    for (uint32_t l = 0; l < L; ++l) {
+        const LaneParams& p = lanes[l]->desc.p;
+        tables[0 * L + l] = p.threshold;
+        tables[1 * L + l] = p.rec_weight;
+        tables[2 * L + l] = p.in_weight;
+        tables[3 * L + l] = p.out_w;
+        tables[4 * L + l] = p.bias;
+        tables[5 * L + l] = p.ctx_out;
+    }
+    char* base = h->merge_scratch.base;
+    upload(base, tables.data(), tables.size() * sizeof(float*), h->stream);
+    auto* counter = reinterpret_cast<unsigned long long*>(base + 6 * L * sizeof(float*));
+    auto* error = reinterpret_cast<uint32_t*>(counter + 1);
+    LEO_HIP_CHECK(hipMemsetAsync(counter, 0, 16, h->stream));
+    struct Job {
+        float* canonical;
+        uint32_t kind;
+        uint64_t count;
+        uint32_t row, stride;
+    };
+    const Job jobs[6] = {
+        {h->canon.threshold, 0, z.n, 0, 0},
+        {h->canon.rec_weight, 1, z.ns, 0, 0},
+        {h->canon.in_weight, 2, z.ni, 0, 0},
+        {h->canon.out_w, 3, z.n * kOutputs, kOutputs, kOutStride},
+        {h->canon.bias, 4, kOutputs, 0, 0},
+        {h->canon.ctx_out, 5, kOutputs * z.e, 0, 0},
+    };
+    for (int j = 0; j < 6; ++j) {
+        MergeArgs m{};
+        m.canonical = jobs[j].canonical;
+        m.lanes = reinterpret_cast<const float* const*>(base + static_cast<size_t>(j) * L * sizeof(float*));
+        m.lane_count = L;
+        m.kind = jobs[j].kind;
+        m.count = jobs[j].count;
+        m.row = jobs[j].row;
+        m.stride = jobs[j].stride;
+        m.synapses_per_neuron = static_cast<uint32_t>(z.s);
+        m.neuron_type = h->sm.neuron_type;
+        m.weight_min = h->cfg.device.weight_min;
+        m.weight_max = h->cfg.device.weight_max;
+        m.updates = counter;
+        m.error = error;
+        uint64_t blocks = std::min<uint64_t>((m.count + kThreads - 1) / kThreads, 4096);
+        hipLaunchKernelGGL(leo_merge_fixed, dim3(static_cast<uint32_t>(std::max<uint64_t>(blocks, 1))), dim3(kThreads), 0,
+                           h->stream, m);
+        LEO_HIP_CHECK(hipGetLastError());
+    }
+    unsigned long long updates = 0;
+    uint32_t err = 0;
+    download(&updates, counter, 8, h->stream);
+    download(&err, error, 4, h->stream);
+    sync(h->stream);
+    if (err) throw Error(LEO_ERR_INTERNAL, "merged parameter became non-finite");
+    return updates;
+}
+
+Lane& story_lane(LeoHipRuntime* h, uint32_t index) {
+    while (h->lanes.size() <= index) {
+        auto lane = std::make_unique<Lane>();
+        allocate_lane_state(*lane, h->z, h->stream);
+        lane->desc.p = allocate_params(lane->params, h->z, h->stream);
+        h->lanes.push_back(std::move(lane));
+    }
+    return *h->lanes[index];
+}
+
+void story_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets, uint32_t count, int32_t permission,
+                 float* losses_out, LeoBatchReport& rep) {
+    if (count == 0) throw Error(LEO_ERR_INVALID_ARGUMENT, "training batch cannot be empty");
+    if (count > h->max_lanes)
+        throw Error(LEO_ERR_UNSUPPORTED, "story batch exceeds the runtime's max_lanes (" + std::to_string(h->max_lanes) + ")");
+    auto t0 = std::chrono::steady_clock::now();
+    std::vector<Lane*> lanes;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (offsets[i + 1] <= offsets[i]) throw Error(LEO_ERR_UNSUPPORTED, "empty stories are not supported in a device batch");
+        Lane& l = story_lane(h, i);
+        copy_params(l.desc.p, h->canon, h->z, h->stream);  // fork(base.clone())
+        clear_changes(l, h->z, h->stream);                  // enable_parameter_tracking
+        lanes.push_back(&l);
+    }
+    reset_lane_objects(h, lanes, true, 0);  // Runtime::new (tick 0) + begin_document
+    std::vector<LaneRun> runs;
+    for (uint32_t i = 0; i < count; ++i) {
+        LaneRun r{lanes[i], {}, {}};
+        auto steps = document_steps(bytes + offsets[i], static_cast<size_t>(offsets[i + 1] - offsets[i]));
+        uint32_t tick = 0;
+        for (auto& st : steps) r.steps.push_back(make_step(h->cfg, *lanes[i], st.symbol, st.target, permission, tick++, true));
+        runs.push_back(std::move(r));
+    }
+    run_lanes(h, runs);
+    auto t1 = std::chrono::steady_clock::now();
+    // per-lane statistics deltas (parallel.rs:1115-1137) and revision increments
+    const uint32_t S = h->cfg.device.synapses_per_neuron;
+    LeoStatistics merged = h->stats;
+    uint64_t revision_increment = 0;
+    double weighted = 0.0;
+    uint64_t targets = 0;
+    size_t cursor = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        LeoStatistics st = h->stats;  // the forked worker starts from the canonical statistics
+        double loss_sum = 0.0;
+        uint64_t steps_with_loss = 0;
+        bool activity = false;
+        for (size_t k = 0; k < runs[i].steps.size(); ++k) {
+            const StepParams& sp = runs[i].steps[k];
+            const StepRecord& rec = runs[i].records[k];
+            float loss = step_loss(sp, rec);
+            account_step(st, sp, rec, loss, S);
+            if (!(sp.flags & kStepFrozen)) activity = true;
+            if (sp.flags & kStepLearn) revision_increment += 1;
+            float recorded = sp.target_index >= 0 ? loss : 0.0f;  // record_training_step
+            loss_sum += static_cast<double>(recorded);
+            steps_with_loss += 1;
+            if (losses_out) losses_out[cursor++] = recorded;
+            rep.activity_steps += 1;
+            rep.active_neurons_sum += rec.active;
+            rep.emitted_events += static_cast<uint64_t>(rec.active) * S;
+        }
+        if (activity) st.processed_stories += 1;  // finish_document
+        double mean = loss_sum / static_cast<double>(std::max<uint64_t>(steps_with_loss, 1));
+        weighted += mean * static_cast<double>(steps_with_loss);
+        targets += steps_with_loss;
+        merged.processed_bytes += st.processed_bytes - h->stats.processed_bytes;
+        merged.processed_stories += st.processed_stories - h->stats.processed_stories;
+        merged.training_loss_sum += st.training_loss_sum - h->stats.training_loss_sum;
+        merged.training_targets += st.training_targets - h->stats.training_targets;
+        merged.active_neurons_sum += st.active_neurons_sum - h->stats.active_neurons_sum;
+        merged.active_neurons_peak = std::max(merged.active_neurons_peak, st.active_neurons_peak);
+        merged.synaptic_events += st.synaptic_events - h->stats.synaptic_events;
+        merged.persistent_ticks += st.persistent_ticks - h->stats.persistent_ticks;
+    }
+    // batch-end mean (parallel.rs:715-798): fixed tensors on the device, keyed context on the host
+    uint64_t fixed = merge_fixed(h, lanes);
+    uint64_t ctx = merge_context(h, lanes);
+    h->stats = merged;
+    h->revision += revision_increment;
+    canonical_reset(h);  // runtime.reset_transient_state() after the merge
+    auto t2 = std::chrono::steady_clock::now();
+    rep.mean_loss = weighted / static_cast<double>(std::max<uint64_t>(targets, 1));
+    rep.targets = targets;
+    rep.stories = count;
+    rep.merge_workers = count;
+    rep.merge_fixed_parameter_updates = fixed;
+    rep.merge_context_keys = ctx;
+    rep.story_seconds += std::chrono::duration<double>(t1 - t0).count();
+    rep.merge_seconds += std::chrono::duration<double>(t2 - t1).count();
+}
+
+// training.rs:1782-1830
+std::vector<std::pair<size_t, size_t>> select_replay_ranges(const std::vector<float>& losses, float fraction,
+                                                            size_t segment) {
+    std::vector<std::pair<size_t, size_t>> selected;
+    const size_t n = losses.size();
+    if (n == 0 || !std::isfinite(fraction) || fraction <= 0.0f || segment == 0) return selected;
+    size_t budget = static_cast<size_t>(
+        std::max(1.0, std::ceil(static_cast<double>(n) * static_cast<double>(std::min(fraction, 1.0f)))));
+    std::vector<size_t> order(n);
+    for (size_t i = 0; i < n; ++i) order[i] = i;
+    auto key = [](float v) {
+        int32_t b;
+        std::memcpy(&b, &v, 4);
+        return b ^ static_cast<int32_t>(static_cast<uint32_t>(b >> 31) >> 1);
+    };
+    std::sort(order.begin(), order.end(), [&](size_t l, size_t r) {
+        int32_t kl = key(losses[l]), kr = key(losses[r]);
+        if (kl != kr) return kl > kr;
+        return l < r;
+    });
+    size_t chosen = 0;
+    for (size_t p : order) {
+        if (chosen >= budget) break;
+        float loss = losses[p];
+        if (!std::isfinite(loss) || loss <= 0.0f) continue;
+        size_t width = std::min(std::min(segment, budget - chosen), n);
+        size_t start = p >= width / 2 ? p - width / 2 : 0;
+        size_t end = std::min(start + width, n);
+        start = end >= width ? end - width : 0;
+        bool overlap = false;
+        for (auto& r : selected)
+            if (r.first < end && start < r.second) overlap = true;
+        if (overlap) continue;
+        chosen += end - start;
+        selected.push_back({start, end});
+    }
+    std::sort(selected.begin(), selected.end());
+    return selected;
+}
+
+// Replay on the canonical runtime (training.rs:162-255, 394-470, 1848-1954).
+void replay_story(LeoHipRuntime* h, const uint8_t* story, size_t len, const std::vector<float>& losses, int32_t permission,
+                  LeoBatchReport& rep) {
+    auto ranges = select_replay_ranges(losses, h->cfg.replay_fraction, h->cfg.replay_segment_bytes);
+    rep.replay_segments += ranges.size();
+    if (ranges.empty() || len == 0) return;
+    auto position_step = [&](size_t p, bool supervised) {
+        HostStep s{p == 0 ? kBegin : story[p - 1], -1};
+        if (supervised) s.target = p < len ? static_cast<int32_t>(story[p]) : static_cast<int32_t>(kEnd);
+        return s;
+    };
+    auto execute = [&](const std::vector<HostStep>& steps, const std::vector<int32_t>& perms) {
+        auto metrics = canonical_steps(h, steps, perms, false);
+        for (size_t i = 0; i < metrics.size(); ++i) {
+            if (perms[i] == LEO_FROZEN) continue;
+            rep.activity_steps += 1;
+            rep.active_neurons_sum += metrics[i].active_neurons;
+            rep.emitted_events += metrics[i].emitted_events;
+        }
+    };
+    if (h->cfg.replay_stateful_batch) {
+        canonical_reset(h);
+        std::vector<HostStep> steps;
+        std::vector<int32_t> perms;
+        const size_t terminal = len + 1;
+        size_t cursor = 0;
+        for (auto [rs, re] : ranges) {
+            size_t start = std::max(std::min(rs, terminal), cursor);
+            size_t end = std::max(std::min(re, terminal), start);
+            for (size_t p = cursor; p < start; ++p) {
+                steps.push_back(position_step(p, false));
+                perms.push_back(LEO_FROZEN);
+                rep.replay_prefix_steps += 1;
+            }
+            for (size_t p = start; p < end; ++p) {
+                steps.push_back(position_step(p, true));
+                perms.push_back(permission);
+                rep.replay_steps += 1;
+            }
+            cursor = end;
+        }
+        if (!steps.empty()) execute(steps, perms);
+        canonical_reset(h);
+        return;
+    }
+    for (size_t ri = 0; ri < ranges.size(); ++ri) {
+        auto [rs, re] = ranges[ri];
+        if (rs >= re || rs > len) continue;
+        size_t end = std::min(re, len + 1);
+        canonical_reset(h);  // begin_document_deferred_for_replay
+        std::vector<HostStep> steps;
+        std::vector<int32_t> perms;
+        size_t next = rs;
+        if (next > 0) {
+            steps.push_back({kBegin, -1});
+            perms.push_back(LEO_FROZEN);
+            for (size_t i = 0; i + 1 < next; ++i) {
+                steps.push_back({story[i], -1});
+                perms.push_back(LEO_FROZEN);
+            }
+            rep.replay_prefix_steps += next;
+        }
+        if (next == 0) {
+            steps.push_back({kBegin, story[0]});
+            perms.push_back(permission);
+            rep.replay_steps += 1;
+            next = 1;
+        }
+        for (size_t p = next; p < end; ++p) {
+            steps.push_back(position_step(p, true));
+            perms.push_back(permission);
+            rep.replay_steps += 1;
+        }
+        execute(steps, perms);
+        if (ri + 1 == ranges.size()) canonical_reset(h);
+    }
+}
+
+}  // namespace
+}  // namespace leo
+
+using leo::Error;
+using leo::guarded;
+
+extern "C" {
+
+int32_t leo_hip_last_error(char* buffer, size_t capacity) {
+    if (!buffer || capacity == 0) return LEO_ERR_INVALID_ARGUMENT;
+    std::snprintf(buffer, capacity, "%s", leo::g_error.c_str());
+    return LEO_OK;
+}
+
+int32_t leo_hip_abi_version(void) { return LEO_HIP_ABI_VERSION; }
+
+int32_t leo_splitmix64(uint64_t seed, uint64_t* out, uint64_t count) {
+    return guarded([&] {
+        if (!out && count) throw Error(LEO_ERR_INVALID_ARGUMENT, "null output");
+        leo::splitmix64_stream(seed, out, count);
+    });
+}
+
+int32_t leo_model_initialize(const LeoHostConfig* config, LeoModelView* out) {
+    return guarded([&] {
+        if (!config || !out) throw Error(LEO_ERR_INVALID_ARGUMENT, "null argument");
+        leo::model_initialize(*config, *out);
+    });
+}
+
+int32_t leo_model_initialize_synthetic(const LeoHostConfig* config, uint32_t topology, float exponent,
+                                       uint32_t in_degree_cap, float weight_sigma, LeoModelView* out) {
+    return guarded([&] {
+        if (!config || !out) throw Error(LEO_ERR_INVALID_ARGUMENT, "null argument");
+        leo::model_initialize_synthetic(*config, topology, exponent, in_degree_cap, weight_sigma, *out);
+    });
+}
+
+int32_t leo_model_validate(const LeoHostConfig* config, const LeoModelView* model) {
+    return guarded([&] {
+        if (!config || !model) throw Error(LEO_ERR_INVALID_ARGUMENT, "null argument");
+        leo::model_validate(*config, *model);
+    });
+}
+
+int32_t leo_synthetic_stories(uint64_t seed, uint32_t count, double mean, double stddev, uint32_t min_len,
+                              uint32_t max_len, uint8_t* bytes, uint64_t capacity, uint64_t* offsets) {
+    return guarded([&] {
+        if (!bytes || !offsets) throw Error(LEO_ERR_INVALID_ARGUMENT, "null argument");
+        leo::synthetic_stories(seed, count, mean, stddev, min_len, max_len, bytes, capacity, offsets);
+    });
+}
+
+int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, int32_t device, uint32_t max_lanes,
+                       LeoHipRuntime** out) {
+    return guarded([&] {
+        if (!config || !model || !out) throw Error(LEO_ERR_INVALID_ARGUMENT, "null argument");
+        leo::model_validate(*config, *model);
+        if (config->device.neurons_per_block > leo::kMaxBlockNeurons)
+            throw Error(LEO_ERR_UNSUPPORTED, "neurons_per_block above 1024 is not supported by the device selection");
+        int devices = 0;
+        if (hipGetDeviceCount(&devices) != hipSuccess || devices <= 0)
+            throw Error(LEO_ERR_DEVICE, "GPU backend requested, but no HIP device is available");
+        if (device < 0 || device >= devices) throw Error(LEO_ERR_DEVICE, "HIP device index out of range");
+        hipDeviceProp_t prop{};
+        LEO_HIP_CHECK(hipGetDeviceProperties(&prop, device));
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            throw Error(LEO_ERR_DEVICE, std::string("this build targets gfx950; device reports ") + prop.gcnArchName);
+        int coop = 0;
+        LEO_HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device));
+        if (!coop) throw Error(LEO_ERR_DEVICE, "device does not support cooperative launches");
+        auto h = std::make_unique<LeoHipRuntime>();
+        h->cfg = *config;
+        h->z = leo::sizes_of(*config);
+        h->device = device;
+        h->max_lanes = std::max<uint32_t>(max_lanes, 1);
+        LEO_HIP_CHECK(hipSetDevice(device));
+        LEO_HIP_CHECK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+        h->cus = prop.multiProcessorCount;
+        LEO_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&h->coop_blocks_per_cu,
+                                                                   reinterpret_cast<const void*>(&leo::leo_lane_steps),
+                                                                   leo::kThreads, 0));
+        if (h->coop_blocks_per_cu <= 0) throw Error(LEO_ERR_DEVICE, "step kernel cannot be resident");
+        if (const char* env = std::getenv("LEO_HIP_WGS_PER_LANE")) h->wgs_override = static_cast<uint32_t>(std::atoi(env));
+        leo::upload_topology(h.get(), *model);
+        h->canon = leo::allocate_params(h->canon_params, h->z, h->stream);
+        leo::upload_model(h.get(), *model);
+        h->canonical = std::make_unique<leo::Lane>();
+        leo::allocate_lane_state(*h->canonical, h->z, h->stream);
+        h->canonical->desc.p = h->canon;
+        h->lane_descs.allocate(sizeof(leo::LaneDesc) * std::max<uint32_t>(h->max_lanes, 1));
+        std::vector<leo::Lane*> lanes{h->canonical.get()};
+        leo::reset_lane_objects(h.get(), lanes, true, 0);  // Runtime::new: tick 0, empty state
+        leo::sync(h->stream);
+        *out = h.release();
+    });
+}
+
+void leo_hip_destroy(LeoHipRuntime* runtime) {
+    if (!runtime) return;
+    (void)hipSetDevice(runtime->device);
+    (void)hipStreamSynchronize(runtime->stream);
+    hipStream_t s = runtime->stream;
+    delete runtime;
+    if (s) (void)hipStreamDestroy(s);
+}
+
+int32_t leo_hip_begin_document(LeoHipRuntime* h) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        leo::canonical_reset(h);
+    });
+}
+
+int32_t leo_hip_finish_document(LeoHipRuntime* h) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        leo::canonical_finish_document(h);
+    });
+}
+
+int32_t leo_hip_reset_transient_state(LeoHipRuntime* h) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        leo::canonical_reset(h);
+    });
+}
+
+int32_t leo_hip_enable_parameter_tracking(LeoHipRuntime* h) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (h->tracking) return;
+        h->tracking = true;
+        leo::clear_changes(*h->canonical, h->z, h->stream);
+        leo::sync(h->stream);
+    });
+}
+
+int32_t leo_hip_step(LeoHipRuntime* h, uint32_t symbol, int32_t target, int32_t permission, LeoStepMetrics* out) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        auto m = leo::canonical_steps(h, {{symbol, target}}, {permission}, true);
+        if (out) *out = m[0];
+    });
+}
+
+int32_t leo_hip_training_step_batch(LeoHipRuntime* h, const uint32_t* symbols, const int32_t* targets, uint32_t count,
+                                    int32_t permission, LeoStepMetrics* out) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (count == 0) return;
+        if (!symbols || !targets) throw Error(LEO_ERR_INVALID_ARGUMENT, "null step arrays");
+        std::vector<leo::HostStep> steps(count);
+        for (uint32_t i = 0; i < count; ++i) steps[i] = {symbols[i], targets[i]};
+        auto m = leo::canonical_steps(h, steps, std::vector<int32_t>(count, permission), true);
+        if (out) std::copy(m.begin(), m.end(), out);
+    });
+}
+
+int32_t leo_hip_advance_frozen_batch(LeoHipRuntime* h, const uint32_t* symbols, uint32_t count) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (count == 0) return;
+        std::vector<leo::HostStep> steps(count);
+        for (uint32_t i = 0; i < count; ++i) steps[i] = {symbols[i], -1};
+        leo::canonical_steps(h, steps, std::vector<int32_t>(count, LEO_FROZEN), false);
+    });
+}
+
+int32_t leo_hip_training_story_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets, uint32_t count,
+                                     int32_t permission, float* losses_out, LeoBatchReport* report) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (!bytes || !offsets) throw Error(LEO_ERR_INVALID_ARGUMENT, "null story arrays");
+        LeoBatchReport rep{};
+        leo::story_batch(h, bytes, offsets, count, permission, losses_out, rep);
+        if (report) *report = rep;
+    });
+}
+
+int32_t leo_hip_train_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets, uint32_t count,
+                            int32_t permission, uint32_t replay_enabled, float* losses_out, LeoBatchReport* report) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (!bytes || !offsets) throw Error(LEO_ERR_INVALID_ARGUMENT, "null story arrays");
+        if (count == 0) throw Error(LEO_ERR_INVALID_ARGUMENT, "training batch cannot be empty");
+        LeoBatchReport rep{};
+        std::vector<std::vector<float>> losses(count);
+        auto t0 = std::chrono::steady_clock::now();
+        if (count == 1) {
+            // training.rs:1548-1582: the canonical runtime trains in place
+            size_t len = static_cast<size_t>(offsets[1] - offsets[0]);
+            if (len > 0) {
+                leo::canonical_reset(h);  // begin_document
+                auto steps = leo::document_steps(bytes + offsets[0], len);
+                auto m = leo::canonical_steps(h, steps, std::vector<int32_t>(steps.size(), permission), true);
+                double sum = 0.0;
+                for (auto& s : m) {
+                    float loss = s.has_loss ? s.loss : 0.0f;
+                    losses[0].push_back(loss);
+                    sum += static_cast<double>(loss);
+                    rep.activity_steps += 1;
+                    rep.active_neurons_sum += s.active_neurons;
+                    rep.emitted_events += s.emitted_events;
+                }
+                leo::canonical_finish_document(h);
+                rep.mean_loss = sum / static_cast<double>(std::max<size_t>(losses[0].size(), 1));
+            }
+            rep.targets = losses[0].size();
+            rep.stories = 1;
+            rep.merge_workers = 1;
+            rep.story_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        } else {
+            std::vector<float> flat(static_cast<size_t>(offsets[count] - offsets[0]) + count);
+            leo::story_batch(h, bytes, offsets, count, permission, flat.data(), rep);
+            size_t cursor = 0;
+            for (uint32_t i = 0; i < count; ++i) {
+                size_t n = static_cast<size_t>(offsets[i + 1] - offsets[i]) + 1;
+                losses[i].assign(flat.begin() + cursor, flat.begin() + cursor + n);
+                cursor += n;
+            }
+        }
+        if (losses_out) {
+            size_t cursor = 0;
+            for (auto& l : losses) {
+                std::copy(l.begin(), l.end(), losses_out + cursor);
+                cursor += l.size();
+            }
+        }
+        auto t1 = std::chrono::steady_clock::now();
+        if (replay_enabled)
+            for (uint32_t i = 0; i < count; ++i)
+                leo::replay_story(h, bytes + offsets[i], static_cast<size_t>(offsets[i + 1] - offsets[i]), losses[i],
+                                  permission, rep);
+        rep.replay_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
+        if (report) *report = rep;
+    });
+}
+
+int32_t leo_hip_download_model(LeoHipRuntime* h, LeoModelView* out) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (!out) throw Error(LEO_ERR_INVALID_ARGUMENT, "null model view");
+        leo::download_model(h, *out);
+    });
+}
+
+int32_t leo_hip_upload_model(LeoHipRuntime* h, const LeoModelView* model) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (!model) throw Error(LEO_ERR_INVALID_ARGUMENT, "null model view");
+        leo::model_validate(h->cfg, *model);
+        leo::upload_topology(h, *model);
+        leo::upload_model(h, *model);
+        // bucket capacities may have changed: story lanes are rebuilt on demand
+        h->lanes.clear();
+        leo::LaneParams p = h->canon;
+        uint32_t tick = h->canonical->tick;
+        leo::allocate_lane_state(*h->canonical, h->z, h->stream);
+        h->canonical->desc.p = p;
+        std::vector<leo::Lane*> lanes{h->canonical.get()};
+        leo::reset_lane_objects(h, lanes, true, tick);
+        if (h->tracking) leo::clear_changes(*h->canonical, h->z, h->stream);
+        leo::sync(h->stream);
+    });
+}
+
+int32_t leo_hip_parameter_changes(LeoHipRuntime* h, int32_t which, uint64_t* out, uint64_t capacity, uint64_t* count,
+                                  uint32_t* bias_dirty, uint32_t* context_output_dirty) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        const leo::LaneDesc& d = h->canonical->desc;
+        const leo::Sizes& z = h->z;
+        const uint32_t* bits = nullptr;
+        uint64_t n = 0;
+        switch (which) {
+            case LEO_CHANGED_THRESHOLD: bits = d.ch_threshold; n = z.n; break;
+            case LEO_CHANGED_RECURRENT: bits = d.ch_rec; n = z.ns; break;
+            case LEO_CHANGED_INPUT: bits = d.ch_in; n = z.ni; break;
+            case LEO_CHANGED_OUTPUT_NEURONS: bits = d.ch_out; n = z.n; break;
+            case LEO_CHANGED_CONTEXT_SLOTS: bits = d.ch_ctx; n = z.slots; break;
+            default: throw Error(LEO_ERR_INVALID_ARGUMENT, "unknown change set");
+        }
+        std::vector<uint64_t> idx;
+        uint32_t flags[2] = {0, 0};
+        if (h->tracking) {
+            auto v = leo::download_bits(h, bits, n);
+            leo::download(flags, &d.ctl->bias_dirty, 8, h->stream);
+            leo::sync(h->stream);
+            idx = leo::bits_to_indices(v, n);
+        }
+        if (count) *count = idx.size();
+        if (out)
+            for (uint64_t i = 0; i < std::min<uint64_t>(capacity, idx.size()); ++i) out[i] = idx[i];
+        if (bias_dirty) *bias_dirty = flags[0];
+        if (context_output_dirty) *context_output_dirty = flags[1];
+    });
+}
+
+int32_t leo_hip_probabilities(LeoHipRuntime* h, float* out257) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        leo::download(out257, h->canonical->desc.probs, leo::kOutputs * 4, h->stream);
+        leo::sync(h->stream);
+    });
+}
+
+int32_t leo_hip_read_list(LeoHipRuntime* h, int32_t which, uint64_t* out, uint64_t capacity, uint64_t* count) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        const leo::LaneDesc& d = h->canonical->desc;
+        leo::LaneControl ctl{};
+        leo::download(&ctl, d.ctl, sizeof(ctl), h->stream);
+        leo::sync(h->stream);
+        std::vector<uint32_t> v;
+        bool sorted = true;
+        const uint32_t last = ctl.tick - 1;
+        switch (which) {
+            case LEO_LIST_ACTIVE: {
+                uint32_t rs = last % leo::kRing;
+                uint32_t n = (ctl.tick > 0 && ctl.ring_tick[rs] == last) ? ctl.ring_count[rs] : 0;
+                v.resize(n);
+                leo::download(v.data(), d.ring_active + static_cast<uint64_t>(rs) * h->z.cap, n * 4, h->stream);
+                sorted = false;
+                break;
+            }
+            case LEO_LIST_TOUCHED: {
+                uint32_t n = ctl.tick > 0 ? ctl.tick_touched[last & 1] : 0;
+                v.resize(n);
+                leo::download(v.data(), d.touched_list, n * 4, h->stream);
+                break;
+            }
+            case LEO_LIST_ELIGIBLE_REC: {
+                uint32_t n = ctl.rec_count[ctl.parity];
+                v.resize(n);
+                leo::download(v.data(), d.rec_list + static_cast<uint64_t>(ctl.parity) * h->z.ns, n * 4, h->stream);
+                break;
+            }
+            case LEO_LIST_ELIGIBLE_IN: {
+                uint32_t n = ctl.in_count[ctl.parity];
+                v.resize(n);
+                leo::download(v.data(), d.in_list + static_cast<uint64_t>(ctl.parity) * h->z.ni, n * 4, h->stream);
+                break;
+            }
+            default: throw Error(LEO_ERR_INVALID_ARGUMENT, "unknown list");
+        }
+        leo::sync(h->stream);
+        if (sorted) std::sort(v.begin(), v.end());
+        if (count) *count = v.size();
+        if (out)
+            for (uint64_t i = 0; i < std::min<uint64_t>(capacity, v.size()); ++i) out[i] = v[i];
+    });
+}
+
+int32_t leo_hip_read_state(LeoHipRuntime* h, int32_t which, float* out, uint64_t count) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        const leo::LaneDesc& d = h->canonical->desc;
+        const leo::Sizes& z = h->z;
+        const float* src = nullptr;
+        uint64_t n = 0;
+        if (which >= LEO_STATE_REC_BS && which <= LEO_STATE_REC_E) {
+            src = d.rec_trace + static_cast<uint64_t>(which - LEO_STATE_REC_BS) * z.ns;
+            n = z.ns;
+        } else if (which >= LEO_STATE_IN_BS && which <= LEO_STATE_IN_E) {
+            src = d.in_trace + static_cast<uint64_t>(which - LEO_STATE_IN_BS) * z.ni;
+            n = z.ni;
+        } else {
+            switch (which) {
+                case LEO_STATE_MEMBRANE: src = d.membrane; n = z.n; break;
+                case LEO_STATE_ACTIVATION: src = d.activation; n = z.n; break;
+                case LEO_STATE_FATIGUE: src = d.fatigue; n = z.n; break;
+                case LEO_STATE_BRANCHES: src = d.branches; n = 4 * z.n; break;
+                case LEO_STATE_ADAPT0: src = d.adapt; n = z.n; break;
+                case LEO_STATE_ADAPT1: src = d.adapt + z.n; n = z.n; break;
+                case LEO_STATE_ADAPT2: src = d.adapt + 2 * z.n; n = z.n; break;
+                case LEO_STATE_SURROGATE: src = d.surrogate; n = z.n; break;
+                case LEO_STATE_LOGITS: src = d.logits; n = leo::kOutputs; break;
+                case LEO_STATE_PROBABILITIES: src = d.probs; n = leo::kOutputs; break;
+                case LEO_STATE_ERRORS: src = d.errors; n = leo::kOutputs; break;
+                case LEO_STATE_LEARNING_SIGNAL: src = d.learning_signal; n = z.n; break;
+                default: throw Error(LEO_ERR_INVALID_ARGUMENT, "unknown state selector");
+            }
+        }
+        if (count != n) throw Error(LEO_ERR_INVALID_ARGUMENT, "state size mismatch: expected " + std::to_string(n));
+        leo::download(out, src, n * 4, h->stream);
+        leo::sync(h->stream);
+    });
+}
+
+uint64_t leo_hip_current_tick(const LeoHipRuntime* h) { return h ? h->canonical->tick : 0; }
+
+}  // extern "C"

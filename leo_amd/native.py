@@ -1,0 +1,179 @@
+"""ctypes binding of the C-ABI in include/leo_hip.h (libleo_hip.so).
+
+The library is built in-tree by ``python -m leo_amd.build``. Loading fails
+loudly when it is missing: there is no CPU fallback behind this module.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+from typing import Optional
+
+from ._abi import LeoConfig
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libleo_hip.so"
+
+OK = 0
+ERR_INVALID_ARGUMENT = 1
+ERR_OUT_OF_MEMORY = 2
+ERR_DEVICE = 3
+ERR_NUMERICAL = 4
+ERR_UNSUPPORTED = 5
+ERR_INTERNAL = 6
+ERR_BUSY = 7
+
+FROZEN, PROVISIONAL, TRAINING, VERIFIED = 0, 1, 2, 3
+TOPOLOGY_UNIFORM, TOPOLOGY_POWER_LAW, TOPOLOGY_HEAVY_TAIL = 0, 1, 2
+
+CHANGED_THRESHOLD, CHANGED_RECURRENT, CHANGED_INPUT, CHANGED_OUTPUT_NEURONS, CHANGED_CONTEXT_SLOTS = range(5)
+LIST_ACTIVE, LIST_TOUCHED, LIST_ELIGIBLE_REC, LIST_ELIGIBLE_IN = range(4)
+STATE_NAMES = [
+    "membrane", "activation", "fatigue", "branches", "adapt0", "adapt1", "adapt2", "surrogate",
+    "rec_bs", "rec_ms", "rec_fs", "rec_as0", "rec_as1", "rec_as2", "rec_e",
+    "in_bs", "in_ms", "in_fs", "in_as0", "in_as1", "in_as2", "in_e",
+    "logits", "probabilities", "errors", "learning_signal",
+]
+STATE = {name: i for i, name in enumerate(STATE_NAMES)}
+
+
+class LeoError(RuntimeError):
+    """A failed C-ABI call: ``code`` is the LEO_ERR_* status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+        self.message = message
+
+
+class LeoHostConfig(ctypes.Structure):
+    _fields_ = [
+        ("device", LeoConfig),
+        ("seed", ctypes.c_uint64),
+        ("excitatory_fraction", ctypes.c_float),
+        ("plasticity_window", ctypes.c_uint32),
+        ("end_document_weight", ctypes.c_float),
+        ("provisional_strength", ctypes.c_float),
+        ("training_strength", ctypes.c_float),
+        ("verified_strength", ctypes.c_float),
+        ("context_dropout_rate", ctypes.c_float),
+        ("replay_fraction", ctypes.c_float),
+        ("replay_segment_bytes", ctypes.c_uint32),
+        ("replay_stateful_batch", ctypes.c_uint32),
+    ]
+
+
+class LeoStatistics(ctypes.Structure):
+    _fields_ = [
+        ("processed_bytes", ctypes.c_uint64),
+        ("processed_stories", ctypes.c_uint64),
+        ("training_loss_sum", ctypes.c_double),
+        ("training_targets", ctypes.c_uint64),
+        ("active_neurons_sum", ctypes.c_uint64),
+        ("active_neurons_peak", ctypes.c_uint64),
+        ("synaptic_events", ctypes.c_uint64),
+        ("numerical_rejections", ctypes.c_uint64),
+        ("persistent_ticks", ctypes.c_uint64),
+    ]
+
+
+_P = ctypes.c_void_p
+
+
+class LeoModelView(ctypes.Structure):
+    _fields_ = [
+        ("threshold", _P), ("excitability", _P), ("neuron_type", _P), ("rec_target", _P), ("rec_branch", _P),
+        ("rec_delay", _P), ("rec_weight", _P), ("in_target", _P), ("in_branch", _P), ("in_weight", _P),
+        ("out_weight", _P), ("bias", _P), ("ctx_keys", _P), ("ctx_emb", _P), ("ctx_obs", _P), ("ctx_out", _P),
+        ("generation", ctypes.c_uint64),
+        ("parameter_revision", ctypes.c_uint64),
+        ("statistics", LeoStatistics),
+    ]
+
+
+class LeoStepMetrics(ctypes.Structure):
+    _fields_ = [
+        ("loss", ctypes.c_float), ("has_loss", ctypes.c_uint32), ("predicted_symbol", ctypes.c_uint32),
+        ("active_neurons", ctypes.c_uint32), ("emitted_events", ctypes.c_uint32),
+        ("suprathreshold_neurons", ctypes.c_uint32), ("block_selected_neurons", ctypes.c_uint32),
+        ("global_cap_clipped_neurons", ctypes.c_uint32), ("population_inhibition", ctypes.c_float),
+        ("context_cells", ctypes.c_uint32), ("context_probes", ctypes.c_uint32),
+        ("context_applied", ctypes.c_uint32), ("eligible_recurrent_synapses", ctypes.c_uint32),
+        ("eligible_input_synapses", ctypes.c_uint32), ("target_probability", ctypes.c_float),
+        ("error_code", ctypes.c_uint32),
+    ]
+
+
+class LeoBatchReport(ctypes.Structure):
+    _fields_ = [
+        ("mean_loss", ctypes.c_double), ("targets", ctypes.c_uint64), ("stories", ctypes.c_uint64),
+        ("replay_segments", ctypes.c_uint64), ("replay_steps", ctypes.c_uint64),
+        ("replay_prefix_steps", ctypes.c_uint64), ("merge_workers", ctypes.c_uint64),
+        ("merge_fixed_parameter_updates", ctypes.c_uint64), ("merge_context_keys", ctypes.c_uint64),
+        ("activity_steps", ctypes.c_uint64), ("active_neurons_sum", ctypes.c_uint64),
+        ("emitted_events", ctypes.c_uint64), ("story_seconds", ctypes.c_double),
+        ("merge_seconds", ctypes.c_double), ("replay_seconds", ctypes.c_double),
+    ]
+
+
+# Every symbol include/leo_hip.h declares, with its ctypes signature.
+_I32, _U32, _U64, _F32, _F64, _SZ = ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, ctypes.c_double, ctypes.c_size_t
+SIGNATURES = {
+    "leo_hip_last_error": (_I32, [ctypes.c_char_p, _SZ]),
+    "leo_hip_abi_version": (_I32, []),
+    "leo_splitmix64": (_I32, [_U64, _P, _U64]),
+    "leo_model_initialize": (_I32, [_P, _P]),
+    "leo_model_initialize_synthetic": (_I32, [_P, _U32, _F32, _U32, _F32, _P]),
+    "leo_model_validate": (_I32, [_P, _P]),
+    "leo_synthetic_stories": (_I32, [_U64, _U32, _F64, _F64, _U32, _U32, _P, _U64, _P]),
+    "leo_hip_create": (_I32, [_P, _P, _I32, _U32, _P]),
+    "leo_hip_destroy": (None, [_P]),
+    "leo_hip_begin_document": (_I32, [_P]),
+    "leo_hip_finish_document": (_I32, [_P]),
+    "leo_hip_reset_transient_state": (_I32, [_P]),
+    "leo_hip_enable_parameter_tracking": (_I32, [_P]),
+    "leo_hip_step": (_I32, [_P, _U32, _I32, _I32, _P]),
+    "leo_hip_training_step_batch": (_I32, [_P, _P, _P, _U32, _I32, _P]),
+    "leo_hip_advance_frozen_batch": (_I32, [_P, _P, _U32]),
+    "leo_hip_training_story_batch": (_I32, [_P, _P, _P, _U32, _I32, _P, _P]),
+    "leo_hip_train_batch": (_I32, [_P, _P, _P, _U32, _I32, _U32, _P, _P]),
+    "leo_hip_download_model": (_I32, [_P, _P]),
+    "leo_hip_upload_model": (_I32, [_P, _P]),
+    "leo_hip_parameter_changes": (_I32, [_P, _I32, _P, _U64, _P, _P, _P]),
+    "leo_hip_probabilities": (_I32, [_P, _P]),
+    "leo_hip_read_list": (_I32, [_P, _I32, _P, _U64, _P]),
+    "leo_hip_read_state": (_I32, [_P, _I32, _P, _U64]),
+    "leo_hip_current_tick": (_U64, [_P]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load(path: Optional[pathlib.Path] = None) -> ctypes.CDLL:
+    """Load libleo_hip.so (raises when it has not been built)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    target = pathlib.Path(path) if path else LIB_PATH
+    if not target.exists():
+        raise RuntimeError(f"{target} is missing: build it with `python -m leo_amd.build` (no CPU fallback exists)")
+    lib = ctypes.CDLL(str(target))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if lib.leo_hip_abi_version() != 1:
+        raise RuntimeError("libleo_hip.so ABI version mismatch")
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def last_error(lib: ctypes.CDLL) -> str:
+    buf = ctypes.create_string_buffer(4096)
+    lib.leo_hip_last_error(buf, len(buf))
+    return buf.value.decode(errors="replace")
+
+
+def check(lib: ctypes.CDLL, status: int) -> None:
+    if status != OK:
+        raise LeoError(status, last_error(lib))

@@ -1,0 +1,142 @@
+"""GPU parity: the HIP path (through the C-ABI) against the CPU oracle on the
+same seeded inputs. Worklists, masks and model tensors are compared bit for
+bit; the HIP kernels reproduce the CPU executor's FP32 operation order."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from leo_amd import native
+from leo_amd.model import BEGIN_DOCUMENT, END_DOCUMENT, Model
+from tests.helpers import (assert_models_equal, causal_model, small_redundant_config, story, toml_test_config)
+
+pytestmark = pytest.mark.gpu
+
+
+def _runtime(model, max_lanes=8):
+    from leo_amd.runtime import HipRuntime
+
+    return HipRuntime(model, device=0, max_lanes=max_lanes)
+
+
+def _document_steps(text: bytes):
+    steps = [(BEGIN_DOCUMENT, text[0])]
+    steps += [(text[i], text[i + 1]) for i in range(len(text) - 1)]
+    steps.append((text[-1], END_DOCUMENT))
+    return steps
+
+
+STATE_COMPARE = ["membrane", "activation", "fatigue", "branches", "adapt0", "adapt1", "adapt2",
+                 "rec_bs", "rec_ms", "rec_fs", "rec_as0", "rec_as1", "rec_as2", "rec_e",
+                 "in_bs", "in_ms", "in_fs", "in_as0", "in_as1", "in_as2", "in_e", "probabilities"]
+
+
+def _compare_step_state(gpu, cpu, label):
+    for lst, name in ((native.LIST_ACTIVE, "active"), (native.LIST_TOUCHED, "touched"),
+                      (native.LIST_ELIGIBLE_REC, "eligible_rec"), (native.LIST_ELIGIBLE_IN, "eligible_in")):
+        g = gpu.read_list(lst)
+        c = cpu.read_list(name)
+        assert np.array_equal(g, c), f"{label}: {name} list differs: gpu {g[:16]} cpu {c[:16]}"
+    for name in STATE_COMPARE:
+        g = gpu.read_state(name)
+        c = cpu.read_f32(name)
+        assert np.array_equal(g, c), f"{label}: {name} differs at {np.nonzero(g != c)[0][:8]}"
+
+
+@pytest.mark.parametrize("make", ["test_toml", "small_redundant"])
+def test_step_by_step_parity(require_gpu, oracle, make):
+    cfg = toml_test_config() if make == "test_toml" else small_redundant_config()
+    model = Model.initialize(cfg)
+    if make == "test_toml":
+        model.threshold[:] = 0.12  # make the tiny model active from the first bytes
+    cpu = oracle.OracleRuntime(model)
+    gpu = _runtime(model)
+    cpu.begin_document()
+    gpu.begin_document()
+    text = story(7, 40)
+    for i, (sym, tgt) in enumerate(_document_steps(text)):
+        print(f"step {i} symbol {sym} target {tgt}", flush=True)
+        cm = cpu.step(sym, tgt, oracle.TRAINING)
+        gm = gpu.step(sym, tgt, native.TRAINING)
+        assert gm.active_neurons == cm.active_neurons, (i, gm.active_neurons, cm.active_neurons)
+        assert gm.predicted_symbol == cm.predicted_symbol, i
+        assert gm.loss == cm.loss, (i, gm.loss, cm.loss)
+        assert gm.eligible_recurrent_synapses == cm.eligible_recurrent_synapses, i
+        assert gm.context_cells == cm.context_cells and gm.context_probes == cm.context_probes, i
+        assert gm.population_inhibition == cm.population_inhibition, i
+        _compare_step_state(gpu, cpu, f"step {i}")
+    assert_models_equal(gpu.model(), cpu.model(), "after document")
+    gpu.close()
+
+
+def test_causal_model_delay_credit(require_gpu, oracle):
+    for delay in (1, 2, 4, 8):
+        model = causal_model(delay)
+        cpu = oracle.OracleRuntime(model)
+        gpu = _runtime(model)
+        for rt in (cpu, gpu):
+            rt.begin_document()
+        steps = [(ord("A"), ord("Y"))] + [(ord("B"), ord("Y"))] * delay
+        for sym, tgt in steps:
+            cpu.step(sym, tgt, oracle.TRAINING)
+        gpu.training_step_batch(steps, native.TRAINING)
+        g, c = gpu.model(), cpu.model()
+        assert g.rec_weight[0] == c.rec_weight[0] != 0.5
+        assert_models_equal(g, c, f"delay {delay}")
+        gpu.close()
+
+
+@pytest.mark.parametrize("make", ["test_toml", "small_redundant"])
+def test_document_batch_parity(require_gpu, oracle, make):
+    cfg = toml_test_config() if make == "test_toml" else small_redundant_config()
+    model = Model.initialize(cfg)
+    cpu = oracle.OracleRuntime(model)
+    gpu = _runtime(model)
+    for k in range(3):
+        text = story(100 + k, 120)
+        cpu.begin_document()
+        gpu.begin_document()
+        steps = _document_steps(text)
+        cms = [cpu.step(s, t, oracle.TRAINING) for s, t in steps]
+        gms = gpu.training_step_batch(steps, native.TRAINING)
+        assert [m.loss for m in gms] == [m.loss for m in cms]
+        assert [m.active_neurons for m in gms] == [m.active_neurons for m in cms]
+        cpu.finish_document()
+        gpu.finish_document()
+    assert_models_equal(gpu.model(), cpu.model(), make)
+    gpu.close()
+
+
+@pytest.mark.parametrize("make", ["test_toml", "small_redundant"])
+def test_story_batch_merge_parity(require_gpu, oracle, make):
+    cfg = toml_test_config() if make == "test_toml" else small_redundant_config()
+    model = Model.initialize(cfg)
+    stories = [story(200 + k, 60 + 17 * k) for k in range(4)]
+    cpu = oracle.OracleRuntime(model)
+    gpu = _runtime(model)
+    crep, closs = cpu.train_story_batch(stories, oracle.TRAINING, replay=False)
+    grep, gloss = gpu.train_batch(stories, native.TRAINING, replay=False)
+    for a, b in zip(gloss, closs):
+        assert np.array_equal(a, b)
+    assert grep.merge_fixed_parameter_updates == crep.merge_fixed_parameter_updates
+    assert grep.merge_context_keys == crep.merge_context_keys
+    assert grep.mean_loss == crep.mean_loss
+    assert_models_equal(gpu.model(), cpu.model(), make)
+    gpu.close()
+
+
+@pytest.mark.parametrize("make", ["test_toml", "small_redundant"])
+def test_train_batch_with_replay_parity(require_gpu, oracle, make):
+    cfg = toml_test_config() if make == "test_toml" else small_redundant_config()
+    model = Model.initialize(cfg)
+    cpu = oracle.OracleRuntime(model)
+    gpu = _runtime(model)
+    batches = [[story(300, 90)], [story(301 + k, 50 + 11 * k) for k in range(3)]]
+    for batch in batches:
+        crep, _ = cpu.train_story_batch(batch, oracle.TRAINING, replay=True)
+        grep, _ = gpu.train_batch(batch, native.TRAINING, replay=True)
+        assert grep.replay_segments == crep.replay_segments
+        assert grep.replay_steps == crep.replay_steps
+        assert grep.replay_prefix_steps == crep.replay_prefix_steps
+    assert_models_equal(gpu.model(), cpu.model(), make)
+    gpu.close()
