@@ -1,0 +1,160 @@
+"""Benchmark: trained bytes/s of Leo's per-byte training step on one MI355X.
+
+One benchmark step is one logical batch of the workload (L stories, one device
+lane each) through the whole training path: the lane-parallel story pass, the
+batch-end lane-ordered mean, and 30% bounded-surprise replay on the canonical
+runtime -- the reference benchmark's input_bytes_per_second definition
+(crates/leo-cli/src/main.rs:716,768: story bytes / wall seconds including
+replay and merge). Synthetic seeded stories and a seeded synthetic model of the
+workload's shape; nothing is skipped inside the timed region.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload B] [--no-replay]
+
+Prints one JSON line. The roofline object prices the step kernel's work
+counters with the per-lane-step byte model of leo_runtime.hip (step_bytes) and
+divides by the summed HIP-event time of its launches inside the timed region.
+cpu_baseline times the CPU oracle (this repository's restatement of Leo's CPU
+executor, one thread per story as in training.rs:1669-1683) on one batch of the
+same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def _device_sync() -> None:
+    hip = ctypes.CDLL("libamdhip64.so")
+    if hip.hipDeviceSynchronize() != 0:
+        raise RuntimeError("hipDeviceSynchronize failed")
+
+
+def cpu_baseline(workload, model, data, offsets, replay: bool):
+    """Time the CPU oracle on one batch of the same workload (bounded sample)."""
+    from oracle import binding
+
+    stories = [data[int(offsets[i]):int(offsets[i + 1])].tobytes() for i in range(len(offsets) - 1)]
+    rt = binding.OracleRuntime(model)
+    started = time.perf_counter()
+    rt.train_story_batch(stories, binding.TRAINING, replay=replay)
+    seconds = time.perf_counter() - started
+    nbytes = int(offsets[-1])
+    return {
+        "value": nbytes / seconds,
+        "unit": "bytes/s",
+        "cores": min(len(stories), os.cpu_count() or 1),
+        "kind": "port",
+        "sample": f"1 batch of workload {workload.name}: {len(stories)} stories, {nbytes} bytes, "
+                  f"replay {'on' if replay else 'off'}, {seconds:.1f} s",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", default="B")
+    ap.add_argument("--no-replay", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every box in this setup has one MI355X, so --gpus {args.gpus} "
+              "is not run (the lane-sharded multi-GPU design is described in DESIGN.md)", file=sys.stderr)
+        return 2
+
+    from leo_amd import native
+    from leo_amd.runtime import HipRuntime
+    from leo_amd.workload import WORKLOADS, synthetic_stories, workload_model
+
+    w = WORKLOADS[args.workload]
+    replay = not args.no_replay
+    lanes = w.lanes
+    model = workload_model(w)
+    total_batches = args.warmup + args.steps
+    data, offsets = synthetic_stories(w, total_batches * lanes)
+    runtime = HipRuntime(model, device=0, max_lanes=lanes)
+    batches = []
+    for b in range(total_batches):
+        lo, hi = b * lanes, (b + 1) * lanes
+        d = data[int(offsets[lo]):int(offsets[hi])].copy()
+        o = (offsets[lo:hi + 1] - offsets[lo]).astype("uint64")
+        batches.append((d, o))
+    for b in range(args.warmup):
+        runtime.train_batch_packed(*batches[b], native.TRAINING, replay=replay)
+    _device_sync()
+    runtime.kernel_stats(reset=True)
+    trained = 0
+    replay_steps = prefix_steps = 0
+    t0 = time.perf_counter()
+    for b in range(args.warmup, total_batches):
+        rep = runtime.train_batch_packed(*batches[b], native.TRAINING, replay=replay)
+        trained += int(batches[b][1][-1])
+        replay_steps += rep.replay_steps
+        prefix_steps += rep.replay_prefix_steps
+    _device_sync()
+    elapsed = time.perf_counter() - t0
+    ks = runtime.kernel_stats()
+    bpb = runtime.model().bits_per_byte()
+    runtime.close()
+
+    kernel_s = ks["kernel_ms"] / 1e3
+    achieved = ks["algorithmic_bytes"] / kernel_s / 1e9 if kernel_s > 0 else 0.0
+    line = {
+        "metric": "trained bytes/sec (FP32, 1 MI355X)",
+        "value": trained / elapsed,
+        "unit": "bytes/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Zipf-ASCII stories, seeded synthetic model)",
+        "config": {
+            "workload": f"{w.name}: {w.neurons} units, fan-in {w.synapses} CSR, 256x{w.fanout} input projection, "
+                        f"{lanes} story lanes, replay {'0.30' if replay else 'off'}",
+            "stories_per_step": lanes,
+            "trained_bytes": trained,
+            "replay_steps": replay_steps,
+            "replay_prefix_steps": prefix_steps,
+            "bits_per_byte": bpb,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "kernel": "leo_lane_steps",
+            "launches": ks["launches"],
+            "kernel_ms_total": ks["kernel_ms"],
+            "avg_launch_us": ks["kernel_ms"] * 1e3 / max(ks["launches"], 1),
+            "algorithmic_bytes": ks["algorithmic_bytes"],
+            "lane_steps": ks["lane_steps"],
+            "merge_ms": ks["merge_ms"],
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        d, o = batches[args.warmup]
+        line["cpu_baseline"] = cpu_baseline(w, model, d, o, replay)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

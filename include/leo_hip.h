@@ -139,6 +139,34 @@ typedef struct LeoBatchReport {
     double replay_seconds;
 } LeoBatchReport;
 
+/* Device telemetry of the step kernel (the role of the reference's sampled
+ * batch telemetry, cuda_plan.rs:67-103 / cuda.rs:8671-9022). kernel_ms is the
+ * summed HIP-event time of the step-kernel launches on the runtime's stream;
+ * algorithmic_bytes applies a per-lane-step byte model to the device's work
+ * counters (events, touched neurons, eligible slots, destinations, ...). */
+typedef struct LeoKernelStats {
+    uint64_t launches;
+    uint64_t lane_steps;
+    double kernel_ms;
+    double algorithmic_bytes;
+    uint64_t events;
+    uint64_t touched;
+    uint64_t active;
+    uint64_t scanned_rec;
+    uint64_t scanned_in;
+    uint64_t kept_rec;
+    uint64_t kept_in;
+    uint64_t destinations;
+    uint64_t active_inhibitory;
+    uint64_t merge_launches;
+    double merge_ms;
+    /* With LEO_HIP_PHASE_PROFILE=1 at creation: per step phase (deliver, fold,
+     * select, eligibility/active list, post/readout, signals, learn, extra), the
+     * microseconds workgroup 0 spent working and waiting at the phase barrier. */
+    double phase_work_us[8];
+    double phase_wait_us[8];
+} LeoKernelStats;
+
 /* Selectors for leo_hip_parameter_changes (ParameterChanges, runtime.rs:37-46). */
 enum {
     LEO_CHANGED_THRESHOLD = 0,
@@ -256,6 +284,9 @@ int32_t leo_hip_read_list(LeoHipRuntime* runtime, int32_t which, uint64_t* out,
  * equal the state's element count. */
 int32_t leo_hip_read_state(LeoHipRuntime* runtime, int32_t which, float* out, uint64_t count);
 uint64_t leo_hip_current_tick(const LeoHipRuntime* runtime);
+/* Accumulated device telemetry since creation or the last reset (reset != 0
+ * clears it after copying). */
+int32_t leo_hip_kernel_stats(LeoHipRuntime* runtime, LeoKernelStats* out, int32_t reset);
 
 #ifdef __cplusplus
 }

@@ -19,6 +19,9 @@ constexpr uint32_t kRing = 9;             // delay ring: max delay 8 + 1 (runtim
 constexpr uint32_t kMaxOrder = 16;        // config.rs:452-456
 constexpr uint32_t kThreads = 256;        // threads per workgroup
 constexpr uint32_t kMaxBlockNeurons = 1024;
+constexpr uint32_t kWaveSize = 64;
+constexpr uint32_t kWavesPerGroup = kThreads / kWaveSize;
+constexpr uint32_t kMaxWaves = 1024;     // selecting waves per lane (workgroups per lane <= 256)
 constexpr uint32_t kGlobalSortCapacity = 8192;
 
 // Step flags (per scheduled step).
@@ -58,6 +61,13 @@ struct StepRecord {
     uint32_t eligible_rec;
     uint32_t eligible_in;
     uint32_t error_code;
+    // work counters of the step (for the algorithmic byte model)
+    uint32_t events;            // recurrent events delivered
+    uint32_t touched;           // neurons touched
+    uint32_t scanned_rec;       // eligible recurrent slots updated
+    uint32_t scanned_in;        // eligible input slots updated
+    uint32_t destinations;      // learning destinations
+    uint32_t active_inhibitory; // active inhibitory sources
     uint32_t pad[2];
 };
 
@@ -96,7 +106,11 @@ struct LaneControl {
     uint32_t ring_count[kRing];      // active count of that tick
     uint32_t tick_touched[2];        // touched count, indexed by tick parity
     uint32_t tick_supra[2];          // suprathreshold count, indexed by tick parity
-    uint32_t pad[2];
+    uint32_t tick_events[2];         // delivered events, indexed by tick parity
+    uint32_t tick_dest[2];           // learning destinations, indexed by tick parity
+    uint32_t tick_ainh[2];           // active inhibitory sources, indexed by tick parity
+    uint32_t tick_scan_rec[2];       // eligible recurrent slots scanned, indexed by tick parity
+    uint32_t tick_scan_in[2];        // eligible input slots scanned, indexed by tick parity
 };
 
 // Learned parameters of a lane (private copy for story lanes, the canonical
@@ -137,6 +151,7 @@ struct LaneDesc {
     uint32_t* block_winners; // blocks * max_active_per_block
     uint32_t* block_count;   // blocks
     float* block_cutoff;     // blocks
+    uint32_t* wave_total;    // kMaxWaves: block winners per selecting wave (block-range owner)
     // ring: per slot, up to max_active_global active neurons, activation, and S snapshot values each
     uint32_t* ring_active;   // kRing * cap
     float* ring_act;         // kRing * cap
@@ -167,7 +182,12 @@ struct LaneDesc {
     StepRecord* records;
     uint32_t step_count;
     uint32_t pad;
+    // phase profile (profiling kernel only): per phase, summed wall-clock ticks of
+    // workgroup 0's own work [0..kPhases) and of its barrier wait [kPhases..2*kPhases)
+    unsigned long long* phase_profile;
 };
+
+constexpr uint32_t kPhases = 8;
 
 // Read-only model data shared by every lane.
 struct SharedModel {

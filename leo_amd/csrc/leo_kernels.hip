@@ -91,6 +91,16 @@ __device__ uint64_t context_key(const uint32_t* history, uint32_t len, uint32_t 
 __device__ __forceinline__ void set_error(LaneControl* ctl, uint32_t code) { atomicCAS(&ctl->error_code, 0u, code); }
 __device__ __forceinline__ void mark_bit(uint32_t* bits, uint32_t index) { atomicOr(&bits[index >> 5], 1u << (index & 31)); }
 
+// Workgroup-wide sum of a per-thread count, added to *global once.
+__device__ void add_count(uint32_t* global, uint32_t local) {
+    __shared__ uint32_t s_count;
+    if (threadIdx.x == 0) s_count = 0;
+    __syncthreads();
+    if (local) atomicAdd(&s_count, local);
+    __syncthreads();
+    if (threadIdx.x == 0 && s_count) atomicAdd(global, s_count);
+}
+
 // Lane-group barrier. Every thread publishes its writes with an agent-scope
 // fence, thread 0 arrives on the lane's counter and waits for all P
 // workgroups, and the acquire fence afterwards makes the other workgroups'
@@ -203,7 +213,20 @@ __device__ __forceinline__ void advance_trace(float* planes, uint64_t plane, uin
     last[slot] = tick;
 }
 
-__device__ void phase_deliver(const StepCtx& c, const StepParams& sp) {
+// Late fields of a step record: work counters complete only after the step's
+// last barrier, so the record is finished by the next step (or kernel end).
+__device__ void finalize_record(const LaneDesc& d, LaneControl* ctl, uint32_t step_index, uint32_t tick) {
+    StepRecord& rec = d.records[step_index];
+    const uint32_t k = tick & 1;
+    rec.events = ctl->tick_events[k];
+    rec.touched = ctl->tick_touched[k];
+    rec.scanned_rec = ctl->tick_scan_rec[k];
+    rec.scanned_in = ctl->tick_scan_in[k];
+    rec.destinations = ctl->tick_dest[k];
+    rec.active_inhibitory = ctl->tick_ainh[k];
+}
+
+__device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t step_index) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = *c.d;
     const LeoConfig& cfg = a.cfg;
@@ -213,10 +236,18 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp) {
     const bool trace = (sp.flags & kStepLearnTrace) != 0;
     const uint32_t tick = c.tick;
     if (c.part == 0 && threadIdx.x == 0) {
-        c.ctl->tick_touched[(tick + 1) & 1] = 0;
-        c.ctl->tick_supra[(tick + 1) & 1] = 0;
-        c.ctl->rec_count[c.parity ^ 1] = 0;
-        c.ctl->in_count[c.parity ^ 1] = 0;
+        LaneControl* ctl = c.ctl;
+        if (step_index > 0) finalize_record(d, ctl, step_index - 1, tick - 1);
+        const uint32_t n = (tick + 1) & 1;
+        ctl->tick_touched[n] = 0;
+        ctl->tick_supra[n] = 0;
+        ctl->tick_events[n] = 0;
+        ctl->tick_dest[n] = 0;
+        ctl->tick_ainh[n] = 0;
+        ctl->tick_scan_rec[n] = 0;
+        ctl->tick_scan_in[n] = 0;
+        ctl->rec_count[c.parity ^ 1] = 0;
+        ctl->in_count[c.parity ^ 1] = 0;
     }
     // previous active set (runtime.rs:544-555)
     uint32_t prev_slot = (tick + kRing - 1) % kRing;
@@ -233,6 +264,7 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp) {
         cls_off[k + 1] = cls_off[k] + cls_count[k] * S;
     }
     const uint32_t total = cls_off[4] + F;
+    uint32_t delivered = 0;
     for (uint32_t item = c.gtid; item < total; item += c.gstride) {
         if (item < prev_count) {
             uint32_t n = d.ring_active[static_cast<uint64_t>(prev_slot) * cap + item];
@@ -247,6 +279,7 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp) {
             uint32_t src = d.ring_active[rbase];
             uint64_t slot = static_cast<uint64_t>(src) * S + j;
             if (a.m.rec_delay[slot] != (8u >> k)) continue;
+            delivered += 1;
             float act = d.ring_act[rbase];
             float value = d.ring_value[rbase * S + j];
             uint32_t target = a.m.rec_target[slot];
@@ -294,6 +327,7 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp) {
             }
         }
     }
+    add_count(&c.ctl->tick_events[tick & 1], delivered);
 }
 
 // ---------------------------------------------------------------------------
@@ -659,6 +693,10 @@ __device__ void phase_eligibility(const StepCtx& c) {
     const uint64_t NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
     const uint32_t p = c.parity, q = c.parity ^ 1;
     const uint32_t rec_n = c.ctl->rec_count[p];
+    if (c.part == 0 && threadIdx.x == 0) {
+        c.ctl->tick_scan_rec[c.tick & 1] = rec_n;
+        c.ctl->tick_scan_in[c.tick & 1] = c.ctl->in_count[p];
+    }
     const uint32_t* rec_cur = d.rec_list + p * NS;
     uint32_t* rec_next = d.rec_list + q * NS;
     for (uint32_t i = c.gtid; i < rec_n; i += c.gstride) {
@@ -779,9 +817,11 @@ __device__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step
     const uint32_t total = A + A * S;
     const uint32_t N = cfg.neuron_count;
     const uint32_t refractory = c.tick + cfg.refractory_ticks + 1;
+    uint32_t inhibitory = 0;
     for (uint32_t item = c.gtid; item < total; item += c.gstride) {
         if (item < A) {
             uint32_t n = act_list[item];
+            inhibitory += a.m.neuron_type[n] != 0 ? 1u : 0u;
             float act = d.activation[n];
             d.fatigue[n] += cfg.fatigue_gain * act;
             d.adapt[n] += cfg.adaptation_fast_gain * act;
@@ -796,6 +836,7 @@ __device__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step
             d.ring_value[rb * S + j] = act_val[r] * d.p.rec_weight[static_cast<uint64_t>(act_list[r]) * S + j];
         }
     }
+    add_count(&c.ctl->tick_ainh[c.tick & 1], inhibitory);
     const uint32_t readout_wg = c.P - 1;
     if ((sp.flags & kStepOutput) && c.part == readout_wg) readout(c, sp, s_f, s_f2, s_u32, step_index);
     if (c.part == readout_wg && threadIdx.x == 0) {
@@ -837,17 +878,20 @@ __device__ void phase_signals(const StepCtx& c, float* s_err) {
     const uint32_t* rec_cur = d.rec_list + c.parity * NS;
     const uint32_t* in_cur = d.in_list + c.parity * NI;
     const uint32_t total = rec_n + in_n + A;
+    uint32_t claimed = 0;
     for (uint32_t item = c.gtid; item < total; item += c.gstride) {
         uint32_t dst;
         if (item < rec_n) dst = a.m.rec_target[rec_cur[item]];
         else if (item < rec_n + in_n) dst = a.m.in_target[in_cur[item - rec_n]];
         else dst = act_list[item - rec_n - in_n];
         if (atomicExch(&d.dest_epoch[dst], c.dest_epoch) == c.dest_epoch) continue;
+        claimed += 1;
         const float* row = d.p.out_w + static_cast<uint64_t>(dst) * kOutStride;
         float signal = 0.0f;
         for (uint32_t o = 0; o < kOutputs; ++o) signal += row[o] * s_err[o];
         d.learning_signal[dst] = signal;
     }
+    add_count(&c.ctl->tick_dest[c.tick & 1], claimed);
 }
 
 // ---------------------------------------------------------------------------
@@ -1023,7 +1067,38 @@ __device__ void phase_learn(const StepCtx& c, const StepParams& sp, float* s_err
     }
 }
 
-__global__ void __launch_bounds__(kThreads) leo_lane_steps(KernelArgs args) {
+// Phase profiler: workgroup 0 of each lane timestamps the end of its own work
+// and the end of the barrier wait of every phase (wall_clock64, constant rate).
+struct PhaseClock {
+    unsigned long long last = 0;
+    unsigned long long* out = nullptr;
+    __device__ void start(unsigned long long* profile) {
+        out = profile;
+        last = wall_clock64();
+    }
+    __device__ void arrive(uint32_t phase, unsigned long long& arrived) {
+        arrived = wall_clock64();
+        out[phase] += arrived - last;
+    }
+    __device__ void release(uint32_t phase, unsigned long long arrived) {
+        last = wall_clock64();
+        out[kPhases + phase] += last - arrived;
+    }
+};
+
+template <bool kProfile>
+__device__ __forceinline__ bool phase_barrier(const StepCtx& c, uint32_t& target, uint32_t spin_limit,
+                                              PhaseClock& clock, uint32_t phase) {
+    unsigned long long arrived = 0;
+    const bool timer = kProfile && c.part == 0 && threadIdx.x == 0;
+    if (timer) clock.arrive(phase, arrived);
+    bool ok = lane_barrier(c.ctl, c.P, target, spin_limit);
+    if (timer) clock.release(phase, arrived);
+    return ok;
+}
+
+template <bool kProfile>
+__device__ void lane_steps(const KernelArgs& args) {
     __shared__ uint64_t s_keys[kMaxBlockNeurons];
     __shared__ float s_f[kOutStride + 4];
     __shared__ float s_f2[kOutStride + kThreads + 4];
@@ -1044,22 +1119,25 @@ __global__ void __launch_bounds__(kThreads) leo_lane_steps(KernelArgs args) {
     uint32_t target = 0;
     const uint32_t steps = c.d->step_count;
     const bool redundant = args.redundant_global != 0;
+    const uint32_t spin = args.spin_limit;
+    PhaseClock clock;
+    if (kProfile && c.part == 0 && threadIdx.x == 0) clock.start(c.d->phase_profile);
     bool ok = true;
     for (uint32_t s = 0; s < steps && ok; ++s) {
         const StepParams sp = c.d->steps[s];
         const bool trace = (sp.flags & kStepLearnTrace) != 0;
-        phase_deliver(c, sp);
-        if (!(ok = lane_barrier(c.ctl, P, target, args.spin_limit))) break;
+        phase_deliver(c, sp, s);
+        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 0))) break;
         phase_fold(c, sp);
-        if (!(ok = lane_barrier(c.ctl, P, target, args.spin_limit))) break;
+        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 1))) break;
         phase_select(c, s_keys, s_u32);
-        if (!(ok = lane_barrier(c.ctl, P, target, args.spin_limit))) break;
+        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 2))) break;
         if (redundant) {
             if (c.part == 0) build_active(c, s_keys, s_u32);
             if (trace) phase_eligibility(c);
         } else {
             if (c.part == 0) build_active(c, s_keys, s_u32);
-            if (!(ok = lane_barrier(c.ctl, P, target, args.spin_limit))) break;
+            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 7))) break;
             const uint32_t touched = c.ctl->tick_touched[c.tick & 1];
             const uint32_t nb = args.cfg.neurons_per_block;
             for (uint32_t i = c.gtid; i < touched; i += c.gstride) {
@@ -1067,32 +1145,38 @@ __global__ void __launch_bounds__(kThreads) leo_lane_steps(KernelArgs args) {
                 surrogate_for(c, n, c.d->block_cutoff[n / nb], c.ctl->pop_cutoff);
             }
             if (trace) {
-                if (!(ok = lane_barrier(c.ctl, P, target, args.spin_limit))) break;
+                if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 7))) break;
                 phase_eligibility(c);
             }
         }
-        if (!(ok = lane_barrier(c.ctl, P, target, args.spin_limit))) break;
+        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 3))) break;
         if (trace) c.parity ^= 1;
         phase_post(c, sp, s, s_f, s_f2, s_u32);
         const bool learn = (sp.flags & kStepLearn) != 0;
         if (learn || !(sp.flags & kStepFrozen)) {
-            if (!(ok = lane_barrier(c.ctl, P, target, args.spin_limit))) break;
+            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 4))) break;
             if (learn && sp.plasticity_scale > 0.0f) {
                 c.dest_epoch += 1;
                 phase_signals(c, s_f);
-                if (!(ok = lane_barrier(c.ctl, P, target, args.spin_limit))) break;
+                if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 5))) break;
             }
             phase_learn(c, sp, s_f, s_f2);
+            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 6))) break;
+        } else {
+            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 4))) break;
         }
-        if (!(ok = lane_barrier(c.ctl, P, target, args.spin_limit))) break;
         c.tick += 1;
     }
     if (ok && c.part == 0 && threadIdx.x == 0) {
+        if (steps > 0) finalize_record(*c.d, c.ctl, steps - 1, c.tick - 1);
         c.ctl->tick = c.tick;
         c.ctl->parity = c.parity;
         c.ctl->dest_epoch = c.dest_epoch;
     }
 }
+
+__global__ void __launch_bounds__(kThreads) leo_lane_steps(KernelArgs args) { lane_steps<false>(args); }
+__global__ void __launch_bounds__(kThreads) leo_lane_steps_profiled(KernelArgs args) { lane_steps<true>(args); }
 
 // ---------------------------------------------------------------------------
 // reset_transient_state (runtime.rs:365-425) for every lane in args.
@@ -1158,8 +1242,10 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
             ctl->ring_tick[k] = 0xffffffffu;
             ctl->ring_count[k] = 0;
         }
-        ctl->tick_touched[0] = ctl->tick_touched[1] = 0;
-        ctl->tick_supra[0] = ctl->tick_supra[1] = 0;
+        for (int k = 0; k < 2; ++k) {
+            ctl->tick_touched[k] = ctl->tick_supra[k] = ctl->tick_events[k] = 0;
+            ctl->tick_dest[k] = ctl->tick_ainh[k] = ctl->tick_scan_rec[k] = ctl->tick_scan_in[k] = 0;
+        }
     }
 }
 

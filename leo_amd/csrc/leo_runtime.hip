@@ -31,6 +31,7 @@
 namespace leo {
 
 __global__ void leo_lane_steps(KernelArgs args);
+__global__ void leo_lane_steps_profiled(KernelArgs args);
 __global__ void leo_reset_lanes(KernelArgs args, uint32_t set_tick, uint32_t new_tick);
 
 __global__ void leo_merge_fixed(MergeArgs m);
@@ -173,6 +174,10 @@ struct LeoHipRuntime {
     bool tracking = false;
     std::atomic<bool> busy{false};
     uint32_t wgs_override = 0;
+    LeoKernelStats telemetry{};
+    bool phase_profile = false;
+    double wall_clock_khz = 0.0;
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr;
 };
 
 namespace leo {
@@ -267,6 +272,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     size_t o_se = l.add<uint32_t>(z.n), o_su = l.add<float>(z.n), o_de = l.add<uint32_t>(z.n);
     size_t o_ls = l.add<float>(z.n), o_bc = l.add<uint32_t>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
     size_t o_bw = l.add<uint32_t>(z.blocks * z.limit), o_bn = l.add<uint32_t>(z.blocks), o_bcut = l.add<float>(z.blocks);
+    size_t o_wt = l.add<uint32_t>(kMaxWaves);
     size_t o_ra = l.add<uint32_t>(kRing * z.cap), o_rv = l.add<float>(kRing * z.cap), o_rval = l.add<float>(kRing * z.cap * z.s);
     size_t o_rt = l.add<float>(7 * z.ns), o_rl = l.add<uint32_t>(z.ns), o_rm = l.add<uint8_t>(z.ns), o_rlist = l.add<uint32_t>(2 * z.ns);
     size_t o_it = l.add<float>(7 * z.ni), o_il = l.add<uint32_t>(z.ni), o_im = l.add<uint8_t>(z.ni), o_ilist = l.add<uint32_t>(2 * z.ni);
@@ -274,6 +280,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     size_t o_lat = l.add<float>(std::max<uint64_t>(z.e, 1));
     size_t o_cth = l.add<uint32_t>(z.words(z.n)), o_crec = l.add<uint32_t>(z.words(z.ns)), o_cin = l.add<uint32_t>(z.words(z.ni));
     size_t o_cout = l.add<uint32_t>(z.words(z.n)), o_cctx = l.add<uint32_t>(z.words(z.slots));
+    size_t o_prof = l.add<unsigned long long>(2 * kPhases);
     lane.state.allocate(l.cursor);
     char* b = lane.state.base;
     LaneDesc& d = lane.desc;
@@ -296,6 +303,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     d.block_winners = reinterpret_cast<uint32_t*>(b + o_bw);
     d.block_count = reinterpret_cast<uint32_t*>(b + o_bn);
     d.block_cutoff = reinterpret_cast<float*>(b + o_bcut);
+    d.wave_total = reinterpret_cast<uint32_t*>(b + o_wt);
     d.ring_active = reinterpret_cast<uint32_t*>(b + o_ra);
     d.ring_act = reinterpret_cast<float*>(b + o_rv);
     d.ring_value = reinterpret_cast<float*>(b + o_rval);
@@ -316,6 +324,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     d.ch_in = reinterpret_cast<uint32_t*>(b + o_cin);
     d.ch_out = reinterpret_cast<uint32_t*>(b + o_cout);
     d.ch_ctx = reinterpret_cast<uint32_t*>(b + o_cctx);
+    d.phase_profile = reinterpret_cast<unsigned long long*>(b + o_prof);
     LEO_HIP_CHECK(hipMemsetAsync(b, 0, lane.state.bytes, stream));
     LEO_HIP_CHECK(hipStreamSynchronize(stream));
 }
@@ -371,12 +380,14 @@ void reset_lane_objects(LeoHipRuntime* h, const std::vector<Lane*>& lanes, bool 
 uint32_t choose_wgs_per_lane(LeoHipRuntime* h, uint32_t lanes) {
     uint32_t coop = static_cast<uint32_t>(h->cus * h->coop_blocks_per_cu);
     uint32_t limit = std::max<uint32_t>(1, coop / std::max<uint32_t>(lanes, 1));
+    limit = std::min<uint32_t>(limit, kMaxWaves / kWavesPerGroup);
     uint32_t want;
     if (h->wgs_override) {
         want = h->wgs_override;
     } else {
-        uint64_t by_blocks = h->z.blocks;
-        uint64_t by_edges = h->z.ns / 8192;
+        // one selecting wave per block, and about one workgroup per 32K edges
+        uint64_t by_blocks = (h->z.blocks + kWavesPerGroup - 1) / kWavesPerGroup;
+        uint64_t by_edges = h->z.ns / 32768;
         want = static_cast<uint32_t>(std::max<uint64_t>(1, std::max(by_blocks, by_edges)));
         want = std::min<uint32_t>(want, 64);
     }
@@ -419,6 +430,61 @@ struct LaneRun {
     std::vector<StepRecord> records;
 };
 
+// Algorithmic HBM bytes of one lane-step: each DRAM-resident element a phase
+// touches counts once (read 1x, read-modify-write 2x); lane-private vectors of
+// at most 64 KB (logits, errors, bias, context projection) are on-chip and not
+// counted. FP32/u32 = 4 B, u8 = 1 B.
+//   29 per delivered event      emission snapshot 8 + slot meta/value 13 + branch RMW 8
+//   17 per injected input slot  target/branch/weight 9 + branch RMW 8
+//   72 per activated trace      last-tick RMW 16 + 6 sensitivities RMW 48 + mark/list 8
+//  172 per touched neuron       branches, ticks, membrane, fatigue, adaptation, refractory,
+//                               threshold, excitability, candidate, surrogate, homeostasis
+//  140 per eligible slot scan   meta 5 + 7 FP32 + tick RMW 72 + list/mark 12 + destination 40 + list 4 + epoch 8
+//   60 per active neuron        post-activation state RMW + ring entry
+//    8 per active edge          emission snapshot weight read + value write
+// 1028 per active neuron        readout row gather (output computed)
+// 1032 per destination          learning-signal row read + signal write
+// 2056 per active neuron        output row RMW (learning step)
+//   37 per kept eligible slot   weight RMW 8 + eligibility 4 + target 4 + signal 4 + list 4 + marks/type 13
+//   24 per inhibitory edge      target activation 4 + weight RMW 8 + target 4 + mark 8
+//    4 per context cell * E     embedding row read
+double step_bytes(const LeoHostConfig& c, const StepParams& sp, const StepRecord& r) {
+    const double S = c.device.synapses_per_neuron, F = c.device.input_fanout, E = c.device.context_embedding_dim;
+    const bool lam = (sp.flags & kStepLearnTrace) != 0;
+    const bool sig = (sp.flags & kStepLearn) != 0;
+    const bool pi = sig && sp.plasticity_scale > 0.0f;
+    const bool out = (sp.flags & kStepOutput) != 0;
+    double b = 29.0 * r.events + 17.0 * F + 172.0 * r.touched + 60.0 * r.active + 8.0 * r.active * S +
+               4.0 * r.context_cells * E;
+    if (lam) b += 72.0 * (static_cast<double>(r.events) + F) + 140.0 * (static_cast<double>(r.scanned_rec) + r.scanned_in);
+    if (out) b += 1028.0 * r.active;
+    if (pi) b += 1032.0 * r.destinations + 37.0 * (static_cast<double>(r.eligible_rec) + r.eligible_in);
+    if (sig) b += 2056.0 * r.active + 24.0 * r.active_inhibitory * S;
+    return b;
+}
+
+void account_launch(LeoHipRuntime* h, const std::vector<LaneRun>& runs, float ms) {
+    LeoKernelStats& t = h->telemetry;
+    t.launches += 1;
+    t.kernel_ms += ms;
+    for (const LaneRun& run : runs) {
+        for (size_t i = 0; i < run.steps.size(); ++i) {
+            const StepRecord& r = run.records[i];
+            t.lane_steps += 1;
+            t.algorithmic_bytes += step_bytes(h->cfg, run.steps[i], r);
+            t.events += r.events;
+            t.touched += r.touched;
+            t.active += r.active;
+            t.scanned_rec += r.scanned_rec;
+            t.scanned_in += r.scanned_in;
+            t.kept_rec += r.eligible_rec;
+            t.kept_in += r.eligible_in;
+            t.destinations += r.destinations;
+            t.active_inhibitory += r.active_inhibitory;
+        }
+    }
+}
+
 // One cooperative launch over all given lanes (each with its own schedule).
 void run_lanes(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     const uint32_t count = static_cast<uint32_t>(runs.size());
@@ -449,8 +515,13 @@ void run_lanes(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     const uint32_t P = choose_wgs_per_lane(h, count);
     KernelArgs a = kernel_args(h, reinterpret_cast<LaneDesc*>(h->lane_descs.base), count, P);
     void* params[] = {&a};
-    LEO_HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&leo_lane_steps), dim3(count * P),
-                                             dim3(kThreads), params, 0, h->stream));
+    const void* kernel = h->phase_profile ? reinterpret_cast<const void*>(&leo_lane_steps_profiled)
+                                          : reinterpret_cast<const void*>(&leo_lane_steps);
+    if (h->phase_profile)
+        for (auto& r : runs) LEO_HIP_CHECK(hipMemsetAsync(r.lane->desc.phase_profile, 0, 2 * kPhases * 8, h->stream));
+    LEO_HIP_CHECK(hipEventRecord(h->ev_start, h->stream));
+    LEO_HIP_CHECK(hipLaunchCooperativeKernel(kernel, dim3(count * P), dim3(kThreads), params, 0, h->stream));
+    LEO_HIP_CHECK(hipEventRecord(h->ev_stop, h->stream));
     std::vector<LaneControl> ctl(count);
     for (uint32_t i = 0; i < count; ++i) {
         runs[i].records.resize(runs[i].steps.size());
@@ -458,6 +529,19 @@ void run_lanes(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
         download(&ctl[i], runs[i].lane->desc.ctl, sizeof(LaneControl), h->stream);
     }
     sync(h->stream);
+    float ms = 0.0f;
+    LEO_HIP_CHECK(hipEventElapsedTime(&ms, h->ev_start, h->ev_stop));
+    account_launch(h, runs, ms);
+    if (h->phase_profile) {
+        // lane 0 of the launch is representative (lanes run the same phase sequence)
+        unsigned long long prof[2 * kPhases];
+        download(prof, runs[0].lane->desc.phase_profile, sizeof(prof), h->stream);
+        sync(h->stream);
+        for (uint32_t p = 0; p < kPhases; ++p) {
+            h->telemetry.phase_work_us[p] += static_cast<double>(prof[p]) / h->wall_clock_khz * 1e3;
+            h->telemetry.phase_wait_us[p] += static_cast<double>(prof[kPhases + p]) / h->wall_clock_khz * 1e3;
+        }
+    }
     for (uint32_t i = 0; i < count; ++i) {
         runs[i].lane->tick += static_cast<uint32_t>(runs[i].steps.size());
         if (ctl[i].error_code != 0) {
@@ -868,6 +952,7 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
     auto* counter = reinterpret_cast<unsigned long long*>(base + 6 * L * sizeof(float*));
     auto* error = reinterpret_cast<uint32_t*>(counter + 1);
     LEO_HIP_CHECK(hipMemsetAsync(counter, 0, 16, h->stream));
+    LEO_HIP_CHECK(hipEventRecord(h->ev_start, h->stream));
     struct Job {
         float* canonical;
         uint32_t kind;
@@ -902,11 +987,16 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
                            h->stream, m);
         LEO_HIP_CHECK(hipGetLastError());
     }
+    LEO_HIP_CHECK(hipEventRecord(h->ev_stop, h->stream));
     unsigned long long updates = 0;
     uint32_t err = 0;
     download(&updates, counter, 8, h->stream);
     download(&err, error, 4, h->stream);
     sync(h->stream);
+    float ms = 0.0f;
+    LEO_HIP_CHECK(hipEventElapsedTime(&ms, h->ev_start, h->ev_stop));
+    h->telemetry.merge_launches += 6;
+    h->telemetry.merge_ms += ms;
     if (err) throw Error(LEO_ERR_INTERNAL, "merged parameter became non-finite");
     return updates;
 }
@@ -1199,12 +1289,18 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         h->max_lanes = std::max<uint32_t>(max_lanes, 1);
         LEO_HIP_CHECK(hipSetDevice(device));
         LEO_HIP_CHECK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+        LEO_HIP_CHECK(hipEventCreate(&h->ev_start));
+        LEO_HIP_CHECK(hipEventCreate(&h->ev_stop));
         h->cus = prop.multiProcessorCount;
         LEO_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&h->coop_blocks_per_cu,
                                                                    reinterpret_cast<const void*>(&leo::leo_lane_steps),
                                                                    leo::kThreads, 0));
         if (h->coop_blocks_per_cu <= 0) throw Error(LEO_ERR_DEVICE, "step kernel cannot be resident");
         if (const char* env = std::getenv("LEO_HIP_WGS_PER_LANE")) h->wgs_override = static_cast<uint32_t>(std::atoi(env));
+        if (const char* env = std::getenv("LEO_HIP_PHASE_PROFILE")) h->phase_profile = std::atoi(env) != 0;
+        int clock_khz = 0;
+        LEO_HIP_CHECK(hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, device));
+        h->wall_clock_khz = clock_khz > 0 ? clock_khz : 100000.0;
         leo::upload_topology(h.get(), *model);
         h->canon = leo::allocate_params(h->canon_params, h->z, h->stream);
         leo::upload_model(h.get(), *model);
@@ -1224,7 +1320,10 @@ void leo_hip_destroy(LeoHipRuntime* runtime) {
     (void)hipSetDevice(runtime->device);
     (void)hipStreamSynchronize(runtime->stream);
     hipStream_t s = runtime->stream;
+    hipEvent_t e0 = runtime->ev_start, e1 = runtime->ev_stop;
     delete runtime;
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
     if (s) (void)hipStreamDestroy(s);
 }
 
@@ -1512,5 +1611,13 @@ int32_t leo_hip_read_state(LeoHipRuntime* h, int32_t which, float* out, uint64_t
 }
 
 uint64_t leo_hip_current_tick(const LeoHipRuntime* h) { return h ? h->canonical->tick : 0; }
+
+int32_t leo_hip_kernel_stats(LeoHipRuntime* h, LeoKernelStats* out, int32_t reset) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (out) *out = h->telemetry;
+        if (reset) h->telemetry = LeoKernelStats{};
+    });
+}
 
 }  // extern "C"

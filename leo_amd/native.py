@@ -115,6 +115,17 @@ class LeoBatchReport(ctypes.Structure):
     ]
 
 
+class LeoKernelStats(ctypes.Structure):
+    _fields_ = [
+        ("launches", ctypes.c_uint64), ("lane_steps", ctypes.c_uint64), ("kernel_ms", ctypes.c_double),
+        ("algorithmic_bytes", ctypes.c_double), ("events", ctypes.c_uint64), ("touched", ctypes.c_uint64),
+        ("active", ctypes.c_uint64), ("scanned_rec", ctypes.c_uint64), ("scanned_in", ctypes.c_uint64),
+        ("kept_rec", ctypes.c_uint64), ("kept_in", ctypes.c_uint64), ("destinations", ctypes.c_uint64),
+        ("active_inhibitory", ctypes.c_uint64), ("merge_launches", ctypes.c_uint64), ("merge_ms", ctypes.c_double),
+        ("phase_work_us", ctypes.c_double * 8), ("phase_wait_us", ctypes.c_double * 8),
+    ]
+
+
 # Every symbol include/leo_hip.h declares, with its ctypes signature.
 _I32, _U32, _U64, _F32, _F64, _SZ = ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, ctypes.c_double, ctypes.c_size_t
 SIGNATURES = {
@@ -143,6 +154,7 @@ SIGNATURES = {
     "leo_hip_read_list": (_I32, [_P, _I32, _P, _U64, _P]),
     "leo_hip_read_state": (_I32, [_P, _I32, _P, _U64]),
     "leo_hip_current_tick": (_U64, [_P]),
+    "leo_hip_kernel_stats": (_I32, [_P, _P, _I32]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

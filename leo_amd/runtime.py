@@ -240,6 +240,16 @@ class HipRuntime:
         self._call("leo_hip_read_state", native.STATE[name], out.ctypes.data, size)
         return out
 
+    def kernel_stats(self, reset: bool = False) -> Dict[str, float]:
+        """Device telemetry of the step kernel (HIP-event time, work counters, byte model)."""
+        st = native.LeoKernelStats()
+        self._call("leo_hip_kernel_stats", ctypes.byref(st), 1 if reset else 0)
+        out = {}
+        for name, _ in native.LeoKernelStats._fields_:
+            v = getattr(st, name)
+            out[name] = list(v) if name.startswith("phase_") else v
+        return out
+
     @property
     def current_tick(self) -> int:
         return int(self._lib.leo_hip_current_tick(self._handle))
