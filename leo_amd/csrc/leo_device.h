@@ -22,7 +22,15 @@ constexpr uint32_t kMaxBlockNeurons = 1024;
 constexpr uint32_t kWaveSize = 64;
 constexpr uint32_t kWavesPerGroup = kThreads / kWaveSize;
 constexpr uint32_t kMaxWaves = 1024;     // selecting waves per lane (workgroups per lane <= 256)
-constexpr uint32_t kGlobalSortCapacity = 8192;
+
+// Dynamic LDS of the step kernel: per wave a u64 candidate list and a u32
+// touched list of one block each; the binding-cap global sort (up to
+// kMaxBlockNeurons keys) reuses the front.
+inline size_t step_lds_bytes(uint32_t neurons_per_block) {
+    const size_t lists = static_cast<size_t>(kWavesPerGroup) * neurons_per_block * (8 + 4);
+    const size_t sort = static_cast<size_t>(kMaxBlockNeurons) * 8;
+    return ((lists > sort ? lists : sort) + 15) / 16 * 16;
+}
 
 // Step flags (per scheduled step).
 enum : uint32_t {

@@ -101,18 +101,57 @@ __device__ void add_count(uint32_t* global, uint32_t local) {
     if (threadIdx.x == 0 && s_count) atomicAdd(global, s_count);
 }
 
-// Lane-group barrier. Every thread publishes its writes with an agent-scope
-// fence, thread 0 arrives on the lane's counter and waits for all P
-// workgroups, and the acquire fence afterwards makes the other workgroups'
-// writes visible. The wait is bounded: on timeout the lane is aborted and
-// every workgroup leaves the step loop, so the grid always drains.
+// Wave-aggregated append: one atomic per wave instead of one per lane. Must be
+// reached by every active lane of the wave (wave-uniform control flow).
+__device__ __forceinline__ uint32_t wave_append(uint32_t* counter, bool pred) {
+    const unsigned long long mask = __ballot(pred);
+    if (mask == 0) return 0;
+    const uint32_t lane = __lane_id();
+    const uint32_t leader = static_cast<uint32_t>(__ffsll(static_cast<long long>(mask)) - 1);
+    uint32_t base = 0;
+    if (lane == leader) base = atomicAdd(counter, static_cast<uint32_t>(__popcll(mask)));
+    base = __shfl(base, static_cast<int>(leader));
+    return base + static_cast<uint32_t>(__popcll(mask & ((1ULL << lane) - 1ULL)));
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+__device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long v) {
+    for (int off = 32; off > 0; off >>= 1) {
+        unsigned long long o = __shfl_xor(v, off);
+        v = o < v ? o : v;
+    }
+    return v;
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+    for (int off = 32; off > 0; off >>= 1) {
+        unsigned long long o = __shfl_xor(v, off);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+// Orders LDS traffic between lanes of one wave (the wave executes in lockstep;
+// this keeps the compiler from moving LDS accesses across the point).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Lane-group barrier. Every thread releases its writes at agent scope, thread
+// 0 arrives on the lane's counter and waits for all P workgroups, and an
+// agent-scope acquire afterwards makes the other workgroups' writes visible.
+// The wait is bounded: on timeout the lane is aborted and every workgroup
+// leaves the step loop, so the grid always drains.
 __device__ bool lane_barrier(LaneControl* ctl, uint32_t P, uint32_t& target, uint32_t spin_limit) {
     __shared__ uint32_t s_abort;
     if (P == 1) {
         __syncthreads();
         return true;
     }
-    __threadfence();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     if (threadIdx.x == 0) {
         target += P;
@@ -124,7 +163,7 @@ __device__ bool lane_barrier(LaneControl* ctl, uint32_t P, uint32_t& target, uin
                 aborted = 1;
                 break;
             }
-            __builtin_amdgcn_s_sleep(2);
+            __builtin_amdgcn_s_sleep(1);
             if (++spins > spin_limit) {
                 __hip_atomic_store(&ctl->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 set_error(ctl, kErrBarrier);
@@ -135,7 +174,7 @@ __device__ bool lane_barrier(LaneControl* ctl, uint32_t P, uint32_t& target, uin
         s_abort = aborted;
     }
     __syncthreads();
-    __threadfence();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     return s_abort == 0;
 }
 
@@ -172,6 +211,27 @@ __device__ __forceinline__ uint64_t selection_key(float act, uint32_t tie) {
 }
 __device__ __forceinline__ float key_activation(uint64_t key) { return __uint_as_float(~static_cast<uint32_t>(key >> 32)); }
 
+// Shared memory of the step kernel, reused phase by phase.
+struct alignas(16) StepShared {
+    float err[kOutStride];                                      // errors / logits
+    float aux[kOutStride + kThreads];                           // exps, latent, gradient
+    uint32_t queue[kWavesPerGroup][2 * kWaveSize];              // per-wave destination queue
+    uint32_t scan[kThreads];
+    unsigned long long red[kWavesPerGroup];
+    float redf[kWavesPerGroup];
+    // context resolution (one thread per order)
+    uint32_t hist[kMaxOrder];
+    int64_t ctx_slot[kMaxOrder];
+    float ctx_scale[kMaxOrder];
+    uint32_t ctx_probes[kMaxOrder];
+    uint32_t hist_len;
+};
+
+// Dynamic LDS (step_lds_bytes): per wave a candidate-key list and a touched
+// list of neurons_per_block entries each; the binding-cap global sort reuses
+// the front.
+extern __shared__ __align__(16) unsigned char step_lds[];
+
 struct StepCtx {
     const KernelArgs* a;
     const LaneDesc* d;
@@ -191,15 +251,6 @@ struct StepCtx {
 // (runtime.rs:710-766) is slot-local; branch adds go to per-target buckets
 // keyed by CPU delivery order and are folded in phase 2.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void touch(const StepCtx& c, uint32_t n) {
-    const LaneDesc& d = *c.d;
-    uint32_t old = atomicExch(&d.touched_epoch[n], c.tick + 1);
-    if (old != c.tick + 1) {
-        uint32_t pos = atomicAdd(&c.ctl->tick_touched[c.tick & 1], 1u);
-        d.touched_list[pos] = n;
-    }
-}
-
 __device__ __forceinline__ void advance_trace(float* planes, uint64_t plane, uint32_t* last, uint32_t slot,
                                               uint32_t tick, const LeoConfig& cfg) {
     uint32_t e = tick - last[slot];
@@ -230,13 +281,13 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t s
     const KernelArgs& a = *c.a;
     const LaneDesc& d = *c.d;
     const LeoConfig& cfg = a.cfg;
+    LaneControl* ctl = c.ctl;
     const uint32_t S = cfg.synapses_per_neuron, F = cfg.input_fanout, cap = cfg.max_active_global;
     const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * S;
     const uint64_t NI = static_cast<uint64_t>(kSymbols) * F;
     const bool trace = (sp.flags & kStepLearnTrace) != 0;
     const uint32_t tick = c.tick;
     if (c.part == 0 && threadIdx.x == 0) {
-        LaneControl* ctl = c.ctl;
         if (step_index > 0) finalize_record(d, ctl, step_index - 1, tick - 1);
         const uint32_t n = (tick + 1) & 1;
         ctl->tick_touched[n] = 0;
@@ -250,373 +301,483 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t s
         ctl->in_count[c.parity ^ 1] = 0;
     }
     // previous active set (runtime.rs:544-555)
-    uint32_t prev_slot = (tick + kRing - 1) % kRing;
-    uint32_t prev_count = (tick > 0 && c.ctl->ring_tick[prev_slot] == tick - 1) ? c.ctl->ring_count[prev_slot] : 0;
+    const uint32_t prev_slot = (tick + kRing - 1) % kRing;
+    const uint32_t prev_count = (tick > 0 && ctl->ring_tick[prev_slot] == tick - 1) ? ctl->ring_count[prev_slot] : 0;
     // delivery classes: delay 8, 4, 2, 1 in that order (chronological by emission tick)
-    uint32_t cls_slot[4], cls_count[4], cls_off[5];
-    cls_off[0] = prev_count;
-    for (int k = 0; k < 4; ++k) {
-        uint32_t delay = 8u >> k;
-        uint32_t rs = (tick + kRing - delay) % kRing;
-        bool valid = tick >= delay && c.ctl->ring_tick[rs] == tick - delay;
-        cls_slot[k] = rs;
-        cls_count[k] = valid ? c.ctl->ring_count[rs] : 0;
-        cls_off[k + 1] = cls_off[k] + cls_count[k] * S;
-    }
-    const uint32_t total = cls_off[4] + F;
+    // (scalars, not arrays: a dynamically indexed private array lives in scratch)
+    auto class_items = [&](uint32_t delay, uint32_t& rs) {
+        rs = (tick + kRing - delay) % kRing;
+        const bool valid = tick >= delay && ctl->ring_tick[rs] == tick - delay;
+        return (valid ? ctl->ring_count[rs] : 0) * S;
+    };
+    uint32_t rs8, rs4, rs2, rs1;
+    const uint32_t off8 = prev_count;
+    const uint32_t off4 = off8 + class_items(8, rs8);
+    const uint32_t off2 = off4 + class_items(4, rs4);
+    const uint32_t off1 = off2 + class_items(2, rs2);
+    const uint32_t off_in = off1 + class_items(1, rs1);
+    const uint32_t total = off_in + F;
+    const uint32_t lane = __lane_id();
     uint32_t delivered = 0;
-    for (uint32_t item = c.gtid; item < total; item += c.gstride) {
+    for (uint32_t base = c.gtid - lane; base < total; base += c.gstride) {
+        const uint32_t item = base + lane;
+        uint32_t touch_n = 0xffffffffu, target = 0, eslot = 0;
+        bool new_rec = false, new_in = false, scatter = false;
+        uint64_t key = 0;
+        float value = 0.0f;
         if (item < prev_count) {
-            uint32_t n = d.ring_active[static_cast<uint64_t>(prev_slot) * cap + item];
+            const uint32_t n = d.ring_active[static_cast<uint64_t>(prev_slot) * cap + item];
             d.activation[n] = 0.0f;
-            touch(c, n);
-        } else if (item < cls_off[4]) {
-            int k = 0;
-            while (item >= cls_off[k + 1]) ++k;
-            uint32_t local = item - cls_off[k];
-            uint32_t r = local / S, j = local % S;
-            uint64_t rbase = static_cast<uint64_t>(cls_slot[k]) * cap + r;
-            uint32_t src = d.ring_active[rbase];
-            uint64_t slot = static_cast<uint64_t>(src) * S + j;
-            if (a.m.rec_delay[slot] != (8u >> k)) continue;
-            delivered += 1;
-            float act = d.ring_act[rbase];
-            float value = d.ring_value[rbase * S + j];
-            uint32_t target = a.m.rec_target[slot];
-            uint8_t br = a.m.rec_branch[slot];
-            if (trace) {
-                advance_trace(d.rec_trace, NS, d.rec_last, static_cast<uint32_t>(slot), tick, cfg);
-                d.rec_trace[slot] += act;
-                if (!d.rec_mark[slot]) {
-                    d.rec_mark[slot] = 1;
-                    uint32_t pos = atomicAdd(&c.ctl->rec_count[c.parity], 1u);
-                    d.rec_list[static_cast<uint64_t>(c.parity) * NS + pos] = static_cast<uint32_t>(slot);
+            touch_n = n;
+        } else if (item < off_in) {
+            const uint32_t k = (item >= off4 ? 1u : 0u) + (item >= off2 ? 1u : 0u) + (item >= off1 ? 1u : 0u);
+            const uint32_t lo = k == 0 ? off8 : k == 1 ? off4 : k == 2 ? off2 : off1;
+            const uint32_t rsk = k == 0 ? rs8 : k == 1 ? rs4 : k == 2 ? rs2 : rs1;
+            const uint32_t local = item - lo;
+            const uint32_t r = local / S, j = local % S;
+            const uint64_t rbase = static_cast<uint64_t>(rsk) * cap + r;
+            const uint32_t src = d.ring_active[rbase];
+            const uint64_t slot = static_cast<uint64_t>(src) * S + j;
+            if (a.m.rec_delay[slot] == (8u >> k)) {
+                delivered += 1;
+                const float act = d.ring_act[rbase];
+                value = d.ring_value[rbase * S + j];
+                target = a.m.rec_target[slot];
+                const uint8_t br = a.m.rec_branch[slot];
+                if (trace) {
+                    advance_trace(d.rec_trace, NS, d.rec_last, static_cast<uint32_t>(slot), tick, cfg);
+                    d.rec_trace[slot] += act;
+                    if (!d.rec_mark[slot]) {
+                        d.rec_mark[slot] = 1;
+                        new_rec = true;
+                        eslot = static_cast<uint32_t>(slot);
+                    }
+                }
+                if (target < cfg.neuron_count && br <= BR_GATE) {
+                    touch_n = target;
+                    scatter = true;
+                    key = (static_cast<uint64_t>(k) << 61) | (static_cast<uint64_t>(r) << 32) |
+                          (static_cast<uint64_t>(j) << 2) | br;
                 }
             }
-            if (target < cfg.neuron_count && br <= BR_GATE) {
-                touch(c, target);
-                uint32_t pos = atomicAdd(&d.bucket_count[target], 1u);
-                uint64_t key = (static_cast<uint64_t>(k) << 61) | (static_cast<uint64_t>(r) << 32) |
-                               (static_cast<uint64_t>(j) << 2) | br;
-                uint64_t at = a.m.bucket_offset[target] + pos;
-                d.bucket[2 * at] = key;
-                d.bucket[2 * at + 1] = __float_as_uint(value);
-            }
-        } else {
-            uint32_t i = item - cls_off[4];
-            uint64_t slot = static_cast<uint64_t>(sp.symbol) * F + i;
-            uint32_t target = a.m.in_target[slot];
-            uint8_t br = a.m.in_branch[slot];
-            float value = d.p.in_weight[slot];
+        } else if (item < total) {
+            const uint32_t i = item - off_in;
+            const uint64_t slot = static_cast<uint64_t>(sp.symbol) * F + i;
+            target = a.m.in_target[slot];
+            const uint8_t br = a.m.in_branch[slot];
+            value = d.p.in_weight[slot];
             if (trace) {
                 advance_trace(d.in_trace, NI, d.in_last, static_cast<uint32_t>(slot), tick, cfg);
                 d.in_trace[slot] += 1.0f;
                 if (!d.in_mark[slot]) {
                     d.in_mark[slot] = 1;
-                    uint32_t pos = atomicAdd(&c.ctl->in_count[c.parity], 1u);
-                    d.in_list[static_cast<uint64_t>(c.parity) * NI + pos] = static_cast<uint32_t>(slot);
+                    new_in = true;
+                    eslot = static_cast<uint32_t>(slot);
                 }
             }
             if (target < cfg.neuron_count && br <= BR_GATE) {
-                touch(c, target);
-                uint32_t pos = atomicAdd(&d.bucket_count[target], 1u);
-                uint64_t key = (4ULL << 61) | (static_cast<uint64_t>(i) << 2) | br;
-                uint64_t at = a.m.bucket_offset[target] + pos;
-                d.bucket[2 * at] = key;
-                d.bucket[2 * at + 1] = __float_as_uint(value);
+                touch_n = target;
+                scatter = true;
+                key = (4ULL << 61) | (static_cast<uint64_t>(i) << 2) | br;
             }
         }
+        uint32_t pos = wave_append(&ctl->rec_count[c.parity], new_rec);
+        if (new_rec) d.rec_list[static_cast<uint64_t>(c.parity) * NS + pos] = eslot;
+        pos = wave_append(&ctl->in_count[c.parity], new_in);
+        if (new_in) d.in_list[static_cast<uint64_t>(c.parity) * NI + pos] = eslot;
+        bool first = false;
+        if (touch_n != 0xffffffffu) first = atomicExch(&d.touched_epoch[touch_n], tick + 1) != tick + 1;
+        pos = wave_append(&ctl->tick_touched[tick & 1], first);
+        if (first) d.touched_list[pos] = touch_n;
+        if (scatter) {
+            const uint32_t p = atomicAdd(&d.bucket_count[target], 1u);
+            const uint64_t at = a.m.bucket_offset[target] + p;
+            d.bucket[2 * at] = key;
+            d.bucket[2 * at + 1] = __float_as_uint(value);
+        }
     }
-    add_count(&c.ctl->tick_events[tick & 1], delivered);
+    add_count(&ctl->tick_events[tick & 1], delivered);
 }
 
 // ---------------------------------------------------------------------------
-// Phase 2: bring each touched neuron to the current tick (runtime.rs:576-603)
-// and fold its delivered values in CPU order; resolve the context
-// (runtime.rs:641-677, model.rs:173-221) on one thread.
+// Phase 2: context resolution (runtime.rs:641-677, model.rs:173-221), one
+// thread per order on the last workgroup; per-block fold, drive and top-k on
+// one wave per block (runtime.rs:576-603, 701-708, 940-1011, 787-803).
 // ---------------------------------------------------------------------------
-__device__ void context_resolve(const StepCtx& c, const StepParams& sp) {
+__device__ void context_resolve(const StepCtx& c, const StepParams& sp, StepShared& sh) {
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = *c.d;
     LaneControl* ctl = c.ctl;
     const uint32_t max_order = cfg.context_max_order, E = cfg.context_embedding_dim;
-    uint32_t len = ctl->history_len;
-    if (len == max_order) {
-        for (uint32_t i = 1; i < len; ++i) ctl->history[i - 1] = ctl->history[i];
-        len -= 1;
-    }
-    ctl->history[len++] = sp.symbol;
-    ctl->history_len = len;
     const bool enabled = (sp.flags & kStepContext) != 0;
     const bool allocate = (sp.flags & kStepAllocate) != 0;
-    ctl->ctx_applied = enabled ? 1u : 0u;
-    uint32_t count = 0, probes = 0;
-    if (enabled) {
-        const float confidence_target = static_cast<float>(cfg.context_confidence_observations);
-        const uint32_t spo = cfg.context_slots_per_order;
-        float scale_sum = 0.0f;
-        for (uint32_t order = 1; order <= len; ++order) {
-            uint64_t key = context_key(ctl->history, len, order);
-            uint64_t base = static_cast<uint64_t>(order - 1) * spo;
-            uint64_t start = key % spo;
-            int64_t found = -1, empty = -1;
-            uint64_t weakest = base + start;
-            uint32_t weakest_obs = 0xffffffffu;
-            for (uint32_t off = 0; off < cfg.context_probe_limit; ++off) {
-                uint64_t slot = base + (start + off) % spo;
-                probes += 1;
-                uint64_t existing = d.p.ctx_keys[slot];
-                if (existing == key) {
-                    found = static_cast<int64_t>(slot);
-                    break;
-                }
-                if (existing == 0 && empty < 0) empty = static_cast<int64_t>(slot);
-                uint32_t obs = d.p.ctx_obs[slot];
-                if (obs < weakest_obs) {
-                    weakest_obs = obs;
-                    weakest = slot;
-                }
-            }
-            if (found < 0) {
-                if (!allocate) continue;
-                uint64_t slot = empty >= 0 ? static_cast<uint64_t>(empty) : weakest;
-                if (d.p.ctx_keys[slot] != key) {
-                    d.p.ctx_keys[slot] = key;
-                    d.p.ctx_obs[slot] = 0;
-                    for (uint32_t e = 0; e < E; ++e) d.p.ctx_emb[slot * E + e] = 0.0f;
-                }
-                found = static_cast<int64_t>(slot);
-            }
-            float obs = static_cast<float>(d.p.ctx_obs[found]);
-            float confidence = obs / (obs + confidence_target);
-            float scale = confidence * static_cast<float>(order);
-            ctl->ctx_slots[count] = static_cast<uint32_t>(found);
-            ctl->ctx_scales[count] = scale;
-            count += 1;
-            scale_sum += scale;
+    if (threadIdx.x == 0) {
+        uint32_t len = ctl->history_len;
+        for (uint32_t i = 0; i < len; ++i) sh.hist[i] = ctl->history[i];
+        if (len == max_order) {
+            for (uint32_t i = 1; i < len; ++i) sh.hist[i - 1] = sh.hist[i];
+            len -= 1;
         }
-        if (scale_sum > 0.0f)
-            for (uint32_t i = 0; i < count; ++i) ctl->ctx_scales[i] = ctl->ctx_scales[i] / scale_sum;
+        sh.hist[len++] = sp.symbol;
+        sh.hist_len = len;
+        for (uint32_t i = 0; i < len; ++i) ctl->history[i] = sh.hist[i];
+        ctl->history_len = len;
     }
-    ctl->ctx_count = count;
-    ctl->ctx_probes = probes;
+    __syncthreads();
+    const uint32_t len = sh.hist_len;
+    if (threadIdx.x < len && enabled) {
+        const uint32_t order = threadIdx.x + 1;
+        const uint64_t key = context_key(sh.hist, len, order);
+        const uint64_t spo = cfg.context_slots_per_order;
+        const uint64_t base = static_cast<uint64_t>(order - 1) * spo, start = key % spo;
+        int64_t found = -1, empty = -1;
+        uint64_t weakest = base + start;
+        uint32_t weakest_obs = 0xffffffffu, probes = 0;
+        for (uint32_t off = 0; off < cfg.context_probe_limit; ++off) {
+            const uint64_t slot = base + (start + off) % spo;
+            probes += 1;
+            const uint64_t existing = d.p.ctx_keys[slot];
+            if (existing == key) {
+                found = static_cast<int64_t>(slot);
+                break;
+            }
+            if (existing == 0 && empty < 0) empty = static_cast<int64_t>(slot);
+            const uint32_t obs = d.p.ctx_obs[slot];
+            if (obs < weakest_obs) {
+                weakest_obs = obs;
+                weakest = slot;
+            }
+        }
+        if (found < 0 && allocate) {
+            const uint64_t slot = empty >= 0 ? static_cast<uint64_t>(empty) : weakest;
+            d.p.ctx_keys[slot] = key;
+            d.p.ctx_obs[slot] = 0;
+            for (uint32_t e = 0; e < E; ++e) d.p.ctx_emb[slot * E + e] = 0.0f;
+            found = static_cast<int64_t>(slot);
+        }
+        float scale = 0.0f;
+        if (found >= 0) {
+            const float obs = static_cast<float>(d.p.ctx_obs[found]);
+            const float confidence = obs / (obs + static_cast<float>(cfg.context_confidence_observations));
+            scale = confidence * static_cast<float>(order);
+        }
+        sh.ctx_slot[threadIdx.x] = found;
+        sh.ctx_scale[threadIdx.x] = scale;
+        sh.ctx_probes[threadIdx.x] = probes;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t count = 0, probes = 0;
+        float scale_sum = 0.0f;
+        if (enabled) {
+            for (uint32_t t = 0; t < len; ++t) {
+                probes += sh.ctx_probes[t];
+                if (sh.ctx_slot[t] < 0) continue;
+                ctl->ctx_slots[count] = static_cast<uint32_t>(sh.ctx_slot[t]);
+                ctl->ctx_scales[count] = sh.ctx_scale[t];
+                scale_sum += sh.ctx_scale[t];
+                count += 1;
+            }
+            if (scale_sum > 0.0f)
+                for (uint32_t i = 0; i < count; ++i) ctl->ctx_scales[i] = ctl->ctx_scales[i] / scale_sum;
+        }
+        ctl->ctx_applied = enabled ? 1u : 0u;
+        ctl->ctx_count = count;
+        ctl->ctx_probes = probes;
+    }
 }
 
-__device__ void phase_fold(const StepCtx& c, const StepParams& sp) {
+// Fold the delivered values of neuron n in CPU delivery order after bringing
+// it to the current tick.
+__device__ __forceinline__ void fold_neuron(const StepCtx& c, uint32_t n) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = *c.d;
     const LeoConfig& cfg = a.cfg;
-    const uint32_t N = cfg.neuron_count;
-    const uint32_t tick = c.tick;
-    if (c.part == 0 && threadIdx.x == 0) context_resolve(c, sp);
-    const uint32_t touched = c.ctl->tick_touched[tick & 1];
-    for (uint32_t i = c.gtid; i < touched; i += c.gstride) {
-        uint32_t n = d.touched_list[i];
-        float b0 = d.branches[4 * n], b1 = d.branches[4 * n + 1], b2 = d.branches[4 * n + 2], b3 = d.branches[4 * n + 3];
-        uint32_t e = tick - d.last_tick[n];
-        if (e > 0) {
-            float bd = decay_for_elapsed(cfg.branch_decay, e);
-            b0 *= bd;
-            b1 *= bd;
-            b2 *= bd;
-            b3 *= bd;
-            d.membrane[n] *= decay_for_elapsed(cfg.membrane_decay, e);
-            d.fatigue[n] *= decay_for_elapsed(cfg.fatigue_decay, e);
-            d.adapt[n] *= decay_for_elapsed(cfg.adaptation_fast_decay, e);
-            d.adapt[N + n] *= decay_for_elapsed(cfg.adaptation_medium_decay, e);
-            d.adapt[2 * N + n] *= decay_for_elapsed(cfg.adaptation_slow_decay, e);
-            d.last_tick[n] = tick;
-        }
-        uint32_t cnt = d.bucket_count[n];
-        if (cnt > 0) {
-            uint64_t* ent = d.bucket + 2 * a.m.bucket_offset[n];
-            // insertion sort by order key (entries are (key, value) pairs)
-            for (uint32_t x = 1; x < cnt; ++x) {
-                uint64_t k = ent[2 * x], v = ent[2 * x + 1];
-                uint32_t y = x;
-                while (y > 0 && ent[2 * (y - 1)] > k) {
-                    ent[2 * y] = ent[2 * (y - 1)];
-                    ent[2 * y + 1] = ent[2 * (y - 1) + 1];
-                    --y;
-                }
-                ent[2 * y] = k;
-                ent[2 * y + 1] = v;
-            }
-            for (uint32_t x = 0; x < cnt; ++x) {
-                float v = __uint_as_float(static_cast<uint32_t>(ent[2 * x + 1]));
-                switch (static_cast<uint32_t>(ent[2 * x]) & 3u) {
-                    case 0: b0 += v; break;
-                    case 1: b1 += v; break;
-                    case 2: b2 += v; break;
-                    default: b3 += v; break;
-                }
-            }
-            d.bucket_count[n] = 0;
-        }
-        d.branches[4 * n] = b0;
-        d.branches[4 * n + 1] = b1;
-        d.branches[4 * n + 2] = b2;
-        d.branches[4 * n + 3] = b3;
+    const uint32_t N = cfg.neuron_count, tick = c.tick;
+    float b0 = d.branches[4 * n], b1 = d.branches[4 * n + 1], b2 = d.branches[4 * n + 2], b3 = d.branches[4 * n + 3];
+    const uint32_t e = tick - d.last_tick[n];
+    if (e > 0) {
+        const float bd = decay_for_elapsed(cfg.branch_decay, e);
+        b0 *= bd;
+        b1 *= bd;
+        b2 *= bd;
+        b3 *= bd;
+        d.membrane[n] *= decay_for_elapsed(cfg.membrane_decay, e);
+        d.fatigue[n] *= decay_for_elapsed(cfg.fatigue_decay, e);
+        d.adapt[n] *= decay_for_elapsed(cfg.adaptation_fast_decay, e);
+        d.adapt[N + n] *= decay_for_elapsed(cfg.adaptation_medium_decay, e);
+        d.adapt[2 * N + n] *= decay_for_elapsed(cfg.adaptation_slow_decay, e);
+        d.last_tick[n] = tick;
     }
+    const uint32_t cnt = d.bucket_count[n];
+    if (cnt > 0) {
+        uint64_t* ent = d.bucket + 2 * a.m.bucket_offset[n];
+        for (uint32_t x = 1; x < cnt; ++x) {  // insertion sort by delivery-order key
+            const uint64_t k = ent[2 * x], v = ent[2 * x + 1];
+            uint32_t y = x;
+            while (y > 0 && ent[2 * (y - 1)] > k) {
+                ent[2 * y] = ent[2 * (y - 1)];
+                ent[2 * y + 1] = ent[2 * (y - 1) + 1];
+                --y;
+            }
+            ent[2 * y] = k;
+            ent[2 * y + 1] = v;
+        }
+        for (uint32_t x = 0; x < cnt; ++x) {
+            const float v = __uint_as_float(static_cast<uint32_t>(ent[2 * x + 1]));
+            switch (static_cast<uint32_t>(ent[2 * x]) & 3u) {
+                case 0: b0 += v; break;
+                case 1: b1 += v; break;
+                case 2: b2 += v; break;
+                default: b3 += v; break;
+            }
+        }
+        d.bucket_count[n] = 0;
+    }
+    d.branches[4 * n] = b0;
+    d.branches[4 * n + 1] = b1;
+    d.branches[4 * n + 2] = b2;
+    d.branches[4 * n + 3] = b3;
 }
 
-// ---------------------------------------------------------------------------
-// Phase 3: drive, membrane and per-block top-k (runtime.rs:940-1011); with a
-// non-binding global cap also activation, selection marks and surrogates
-// (runtime.rs:1060-1067, 787-803).
-// ---------------------------------------------------------------------------
-__device__ void surrogate_for(const StepCtx& c, uint32_t n, float block_cutoff, float pop_cutoff) {
+__device__ void surrogate_for(const StepCtx& c, uint32_t n, float block_cutoff, float pop_cutoff, bool selected) {
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = *c.d;
     if (d.refractory_until[n] > c.tick) {
         d.surrogate[n] = 0.0f;
         return;
     }
-    float margin = d.membrane[n] - d.p.threshold[n];
-    float cutoff = maxnum(block_cutoff, pop_cutoff);
-    bool selected = d.selected_epoch[n] == c.tick + 1;
+    const float margin = d.membrane[n] - d.p.threshold[n];
+    const float cutoff = maxnum(block_cutoff, pop_cutoff);
     d.surrogate[n] = analog_rank_surrogate(margin, cutoff, selected, cfg.surrogate_width, cfg.surrogate_gain);
 }
 
-__device__ void phase_select(const StepCtx& c, uint64_t* s_keys, uint32_t* s_u32) {
+// One wave: fold, drive and top-k of block b (runtime.rs:940-1011). The
+// block's touched neurons are gathered first (all flag loads in flight at
+// once) and processed densely; candidates (activation > 0) are compacted into
+// the wave's LDS list, and each candidate's rank is the number of smaller
+// (activation desc, tie asc) keys, i.e. its position in the reference's
+// sorted order (keys are unique).
+constexpr uint32_t kMaxChunksPerBlock = kMaxBlockNeurons / kWaveSize;
+
+__device__ uint32_t select_block(const StepCtx& c, uint32_t b, float pi, uint64_t* cand, uint32_t* tl) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = *c.d;
     const LeoConfig& cfg = a.cfg;
     const uint32_t N = cfg.neuron_count, nb = cfg.neurons_per_block, limit = cfg.max_active_per_block;
-    const uint32_t tick = c.tick;
-    const uint32_t rot = tick % N;
-    const float pi = c.ctl->population_inhibition;
-    const uint32_t M = next_pow2(nb);
-    for (uint32_t b = c.part; b < cfg.block_count; b += c.P) {
-        if (threadIdx.x == 0) s_u32[0] = 0;
-        __syncthreads();
-        uint32_t local_candidates = 0;
-        for (uint32_t idx = threadIdx.x; idx < M; idx += kThreads) {
-            uint64_t key = ~0ULL;
-            if (idx < nb) {
-                uint32_t n = b * nb + idx;
-                if (d.touched_epoch[n] == tick + 1 && !(d.refractory_until[n] > tick)) {
-                    float gate = clampf(d.branches[4 * n + BR_GATE], 0.0f, 1.0f);
-                    float inhibitory = d.branches[4 * n + BR_INH];
-                    float net = d.branches[4 * n + BR_EXC] + d.branches[4 * n + BR_TEMP] * gate + inhibitory;
-                    float adaptation = d.adapt[n] + d.adapt[N + n] + d.adapt[2 * N + n];
-                    float drive = a.m.excitability[n] * net - d.fatigue[n] - adaptation - pi;
-                    float m = d.membrane[n] + drive;
-                    d.membrane[n] = m;
-                    float act = clampf(m - d.p.threshold[n], 0.0f, 1.0f);
-                    if (act > 0.0f) {
-                        key = selection_key(act, (n + N - rot) % N);
-                        local_candidates += 1;
-                    }
+    const uint32_t tick = c.tick, rot = tick % N;
+    const uint32_t lane = __lane_id();
+    const unsigned long long below = (1ULL << lane) - 1ULL;
+    const uint32_t chunks = (nb + kWaveSize - 1) / kWaveSize;
+    const uint32_t first = b * nb;
+    uint32_t tmask = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kMaxChunksPerBlock; ++k) {
+        const uint32_t idx = k * kWaveSize + lane;
+        if (k < chunks && idx < nb && d.touched_epoch[first + idx] == tick + 1) tmask |= 1u << k;
+    }
+    uint32_t touched = 0;
+    for (uint32_t k = 0; k < chunks; ++k) {
+        const bool t = (tmask >> k) & 1u;
+        const unsigned long long mask = __ballot(t);
+        if (t) tl[touched + __popcll(mask & below)] = first + k * kWaveSize + lane;
+        touched += static_cast<uint32_t>(__popcll(mask));
+    }
+    wave_sync();
+    uint32_t count = 0;
+    for (uint32_t base = 0; base < touched; base += kWaveSize) {
+        const uint32_t i = base + lane;
+        bool candidate = false;
+        uint64_t key = 0;
+        if (i < touched) {
+            const uint32_t n = tl[i];
+            fold_neuron(c, n);
+            if (!(d.refractory_until[n] > tick)) {
+                const float gate = clampf(d.branches[4 * n + BR_GATE], 0.0f, 1.0f);
+                const float inhibitory = d.branches[4 * n + BR_INH];
+                const float net = d.branches[4 * n + BR_EXC] + d.branches[4 * n + BR_TEMP] * gate + inhibitory;
+                const float adaptation = d.adapt[n] + d.adapt[N + n] + d.adapt[2 * N + n];
+                const float drive = a.m.excitability[n] * net - d.fatigue[n] - adaptation - pi;
+                const float m = d.membrane[n] + drive;
+                d.membrane[n] = m;
+                const float act = clampf(m - d.p.threshold[n], 0.0f, 1.0f);
+                if (act > 0.0f) {
+                    candidate = true;
+                    key = selection_key(act, (n + N - rot) % N);
                 }
             }
-            s_keys[idx] = key;
         }
-        if (local_candidates) atomicAdd(&s_u32[0], local_candidates);
-        __syncthreads();
-        const uint32_t count = s_u32[0];
-        if (count > 0) bitonic_sort_lds(s_keys, M);
-        const uint32_t winners = count < limit ? count : limit;
-        const float cutoff = count > limit ? key_activation(s_keys[limit]) : 0.0f;
-        for (uint32_t i = threadIdx.x; i < winners; i += kThreads) {
-            uint64_t key = s_keys[i];
-            uint32_t n = (static_cast<uint32_t>(key) + rot) % N;
-            d.block_winners[static_cast<uint64_t>(b) * limit + i] = n;
-            if (a.redundant_global) {
-                d.activation[n] = key_activation(key);
-                d.selected_epoch[n] = tick + 1;
-            }
-        }
-        if (threadIdx.x == 0) {
-            d.block_count[b] = winners;
-            d.block_cutoff[b] = cutoff;
-            if (count) atomicAdd(&c.ctl->tick_supra[tick & 1], count);
-        }
-        __syncthreads();
-        if (a.redundant_global) {
-            for (uint32_t idx = threadIdx.x; idx < nb; idx += kThreads) {
-                uint32_t n = b * nb + idx;
-                if (d.touched_epoch[n] == tick + 1) surrogate_for(c, n, cutoff, 0.0f);
-            }
-        }
-        __syncthreads();
+        const unsigned long long mask = __ballot(candidate);
+        if (candidate) cand[count + __popcll(mask & below)] = key;
+        count += static_cast<uint32_t>(__popcll(mask));
     }
+    wave_sync();
+    // ranks: winners go to their sorted position, rank `limit` gives the cutoff
+    unsigned long long cut_key = ~0ULL;
+    for (uint32_t base = 0; base < count; base += kWaveSize) {
+        const uint32_t i = base + lane;
+        const uint64_t mine = i < count ? cand[i] : ~0ULL;
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < count; ++j) rank += cand[j] < mine ? 1u : 0u;
+        if (i < count && rank < limit) d.block_winners[static_cast<uint64_t>(b) * limit + rank] = (static_cast<uint32_t>(mine) + rot) % N;
+        const unsigned long long cut = wave_min_u64(i < count && rank == limit ? mine : ~0ULL);
+        cut_key = cut < cut_key ? cut : cut_key;
+    }
+    const uint32_t winners = count < limit ? count : limit;
+    const float cutoff = cut_key != ~0ULL ? key_activation(cut_key) : 0.0f;
+    if (lane == 0) {
+        d.block_count[b] = winners;
+        d.block_cutoff[b] = cutoff;
+        if (count) atomicAdd(&c.ctl->tick_supra[tick & 1], count);
+    }
+    if (a.redundant_global) {
+        // the global cap cannot bind: activation and selection marks of the
+        // winners and surrogates of the touched (runtime.rs:1060-1067, 787-803);
+        // a candidate wins iff its key is below the rank-`limit` key
+        for (uint32_t i = lane; i < touched; i += kWaveSize) {
+            const uint32_t n = tl[i];
+            bool won = false;
+            if (!(d.refractory_until[n] > tick)) {
+                const float act = clampf(d.membrane[n] - d.p.threshold[n], 0.0f, 1.0f);
+                won = act > 0.0f && selection_key(act, (n + N - rot) % N) < cut_key;
+                if (won) {
+                    d.activation[n] = act;
+                    d.selected_epoch[n] = tick + 1;
+                }
+            }
+            surrogate_for(c, n, cutoff, 0.0f, won);
+        }
+    }
+    wave_sync();
+    return winners;
+}
+
+__device__ void phase_fold_select(const StepCtx& c, const StepParams& sp, StepShared& sh) {
+    const LeoConfig& cfg = c.a->cfg;
+    if (c.part == c.P - 1) context_resolve(c, sp, sh);
+    const uint32_t wave = threadIdx.x / kWaveSize, lane = __lane_id();
+    const uint32_t nwaves = c.P * kWavesPerGroup;
+    const uint32_t wv = c.part * kWavesPerGroup + wave;
+    const uint32_t per = (cfg.block_count + nwaves - 1) / nwaves;
+    const uint32_t b0 = wv * per, b1 = min(cfg.block_count, b0 + per);
+    const float pi = c.ctl->population_inhibition;
+    uint32_t total = 0;
+    const uint32_t nb = cfg.neurons_per_block;
+    uint64_t* cand = reinterpret_cast<uint64_t*>(step_lds) + static_cast<size_t>(wave) * nb;
+    uint32_t* tl = reinterpret_cast<uint32_t*>(step_lds + static_cast<size_t>(kWavesPerGroup) * nb * 8) + wave * nb;
+    for (uint32_t b = b0; b < b1; ++b) total += select_block(c, b, pi, cand, tl);
+    if (lane == 0) c.d->wave_total[wv] = total;
 }
 
 // ---------------------------------------------------------------------------
-// Phase 4a (workgroup 0): concatenate block winners into the active list of
-// this tick's ring slot; with a binding global cap, sort and truncate
-// (runtime.rs:1013-1057); update population inhibition (runtime.rs:1076-1082).
+// Phase 3: the active list of this tick (block winners concatenated in block
+// order, runtime.rs:1010-1013), population inhibition (runtime.rs:1076-1082)
+// and the forward eligibilities (runtime.rs:805-918).
 // ---------------------------------------------------------------------------
-__device__ void build_active(const StepCtx& c, uint64_t* s_keys, uint32_t* s_u32) {
+__device__ void write_active(const StepCtx& c) {
+    const LeoConfig& cfg = c.a->cfg;
+    const LaneDesc& d = *c.d;
+    const uint32_t cap = cfg.max_active_global, limit = cfg.max_active_per_block;
+    const uint32_t wave = threadIdx.x / kWaveSize, lane = __lane_id();
+    const uint32_t nwaves = c.P * kWavesPerGroup;
+    const uint32_t wv = c.part * kWavesPerGroup + wave;
+    const uint32_t per = (cfg.block_count + nwaves - 1) / nwaves;
+    const uint32_t rs = c.tick % kRing;
+    // offset of this wave's block range: winners of every earlier range
+    uint32_t before = 0, all = 0;
+    for (uint32_t base = 0; base < nwaves; base += kWaveSize) {
+        const uint32_t w = base + lane;
+        const uint32_t v = w < nwaves ? d.wave_total[w] : 0;
+        before += wave_sum_u32(w < wv ? v : 0);
+        all += wave_sum_u32(v);
+    }
+    const uint32_t b0 = wv * per, b1 = min(cfg.block_count, b0 + per);
+    uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
+    float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
+    uint32_t offset = before;
+    for (uint32_t b = b0; b < b1; ++b) {
+        const uint32_t v = d.block_count[b];
+        for (uint32_t i = lane; i < v; i += kWaveSize) {
+            const uint32_t n = d.block_winners[static_cast<uint64_t>(b) * limit + i];
+            act_list[offset + i] = n;
+            act_val[offset + i] = d.activation[n];
+        }
+        offset += v;
+    }
+    if (c.part == 0 && threadIdx.x == 0) {
+        LaneControl* ctl = c.ctl;
+        ctl->active_count = all;
+        ctl->block_selected = all;
+        ctl->clipped = 0;
+        ctl->pop_cutoff = 0.0f;
+        ctl->ring_tick[rs] = c.tick;
+        ctl->ring_count[rs] = all;
+        const float activity = static_cast<float>(all) / static_cast<float>(cfg.neuron_count);
+        ctl->population_inhibition = clampf(
+            ctl->population_inhibition + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
+            cfg.population_inhibition_max);
+    }
+}
+
+// Binding global cap (workgroup 0): sort every block winner by
+// (activation desc, tie asc), keep max_active_global (runtime.rs:1029-1057).
+__device__ void global_select(const StepCtx& c, StepShared& sh) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = *c.d;
     const LeoConfig& cfg = a.cfg;
     const uint32_t N = cfg.neuron_count, limit = cfg.max_active_per_block, cap = cfg.max_active_global;
-    const uint32_t tick = c.tick;
+    const uint32_t tick = c.tick, rot = tick % N;
     const uint32_t rs = tick % kRing;
-    uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
-    float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
-    // exclusive scan of block winner counts, in block order
+    uint64_t* keys = reinterpret_cast<uint64_t*>(step_lds);
     uint32_t running = 0;
-    const bool redundant = a.redundant_global != 0;
     for (uint32_t base = 0; base < cfg.block_count; base += kThreads) {
-        uint32_t b = base + threadIdx.x;
-        uint32_t v = b < cfg.block_count ? d.block_count[b] : 0;
-        s_u32[threadIdx.x] = v;
+        const uint32_t b = base + threadIdx.x;
+        const uint32_t v = b < cfg.block_count ? d.block_count[b] : 0;
+        sh.scan[threadIdx.x] = v;
         __syncthreads();
         for (uint32_t off = 1; off < kThreads; off <<= 1) {
-            uint32_t add = threadIdx.x >= off ? s_u32[threadIdx.x - off] : 0;
+            const uint32_t add = threadIdx.x >= off ? sh.scan[threadIdx.x - off] : 0;
             __syncthreads();
-            s_u32[threadIdx.x] += add;
+            sh.scan[threadIdx.x] += add;
             __syncthreads();
         }
-        uint32_t incl = s_u32[threadIdx.x];
-        uint32_t start = running + incl - v;
-        if (redundant) {
-            for (uint32_t i = 0; i < v; ++i) {
-                uint32_t n = d.block_winners[static_cast<uint64_t>(b) * limit + i];
-                act_list[start + i] = n;
-                act_val[start + i] = d.activation[n];
-            }
-        } else {
-            for (uint32_t i = 0; i < v; ++i) {
-                uint32_t n = d.block_winners[static_cast<uint64_t>(b) * limit + i];
-                if (start + i < kMaxBlockNeurons) {
-                    float act = clampf(d.membrane[n] - d.p.threshold[n], 0.0f, 1.0f);
-                    s_keys[start + i] = selection_key(act, (n + N - tick % N) % N);
-                }
+        const uint32_t start = running + sh.scan[threadIdx.x] - v;
+        for (uint32_t i = 0; i < v; ++i) {
+            const uint32_t n = d.block_winners[static_cast<uint64_t>(b) * limit + i];
+            if (start + i < kMaxBlockNeurons) {
+                const float act = clampf(d.membrane[n] - d.p.threshold[n], 0.0f, 1.0f);
+                keys[start + i] = selection_key(act, (n + N - rot) % N);
             }
         }
-        uint32_t chunk_total = s_u32[kThreads - 1];
+        const uint32_t chunk_total = sh.scan[kThreads - 1];
         __syncthreads();
         running += chunk_total;
     }
-    uint32_t active = running, clipped = 0;
+    uint32_t active = 0, clipped = 0;
     float pop_cutoff = 0.0f;
-    if (!redundant) {
-        if (running > kMaxBlockNeurons) {
-            if (threadIdx.x == 0) set_error(c.ctl, kErrCapacity);
-            active = 0;
-        } else {
-            uint32_t M = next_pow2(running < 2 ? 2 : running);
-            for (uint32_t i = running + threadIdx.x; i < M; i += kThreads) s_keys[i] = ~0ULL;
-            __syncthreads();
-            bitonic_sort_lds(s_keys, M);
-            active = running < cap ? running : cap;
-            clipped = running - active;
-            if (running > cap) pop_cutoff = clampf(key_activation(s_keys[cap]), 0.0f, cfg.population_inhibition_max);
-            for (uint32_t i = threadIdx.x; i < active; i += kThreads) {
-                uint64_t key = s_keys[i];
-                uint32_t n = (static_cast<uint32_t>(key) + tick % N) % N;
-                float act = key_activation(key);
-                act_list[i] = n;
-                act_val[i] = act;
-                d.activation[n] = act;
-                d.selected_epoch[n] = tick + 1;
-            }
+    if (running > kMaxBlockNeurons) {
+        if (threadIdx.x == 0) set_error(c.ctl, kErrCapacity);
+    } else {
+        const uint32_t M = next_pow2(running < 2 ? 2 : running);
+        for (uint32_t i = running + threadIdx.x; i < M; i += kThreads) keys[i] = ~0ULL;
+        __syncthreads();
+        bitonic_sort_lds(keys, M);
+        active = running < cap ? running : cap;
+        clipped = running - active;
+        if (running > cap) pop_cutoff = clampf(key_activation(keys[cap]), 0.0f, cfg.population_inhibition_max);
+        uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
+        float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
+        for (uint32_t i = threadIdx.x; i < active; i += kThreads) {
+            const uint64_t key = keys[i];
+            const uint32_t n = (static_cast<uint32_t>(key) + rot) % N;
+            const float act = key_activation(key);
+            act_list[i] = n;
+            act_val[i] = act;
+            d.activation[n] = act;
+            d.selected_epoch[n] = tick + 1;
         }
     }
+    __syncthreads();
     if (threadIdx.x == 0) {
         LaneControl* ctl = c.ctl;
         ctl->active_count = active;
@@ -625,17 +786,13 @@ __device__ void build_active(const StepCtx& c, uint64_t* s_keys, uint32_t* s_u32
         ctl->pop_cutoff = pop_cutoff;
         ctl->ring_tick[rs] = tick;
         ctl->ring_count[rs] = active;
-        float activity = static_cast<float>(active) / static_cast<float>(N);
-        float err = activity - cfg.target_activity;
-        ctl->population_inhibition =
-            clampf(ctl->population_inhibition + cfg.population_inhibition_rate * err, 0.0f, cfg.population_inhibition_max);
+        const float activity = static_cast<float>(active) / static_cast<float>(N);
+        ctl->population_inhibition = clampf(
+            ctl->population_inhibition + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
+            cfg.population_inhibition_max);
     }
 }
 
-// ---------------------------------------------------------------------------
-// Phase 4 (rest of the lane): forward eligibilities (runtime.rs:805-918).
-// Kept slots are compacted into the other list; dropped slots are unmarked.
-// ---------------------------------------------------------------------------
 __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uint64_t plane, uint32_t* last,
                                             uint32_t slot, uint32_t dst, uint8_t br) {
     const LeoConfig& cfg = c.a->cfg;
@@ -643,8 +800,8 @@ __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uin
     const uint32_t tick = c.tick;
     float bs = planes[slot], ms = planes[plane + slot], fs = planes[2 * plane + slot];
     float as0 = planes[3 * plane + slot], as1 = planes[4 * plane + slot], as2 = planes[5 * plane + slot];
-    float e = planes[6 * plane + slot];
-    uint32_t el = tick - last[slot];
+    const float e = planes[6 * plane + slot];
+    const uint32_t el = tick - last[slot];
     if (el > 0) {
         bs *= decay_for_elapsed(cfg.branch_decay, el);
         ms *= decay_for_elapsed(cfg.membrane_decay, el);
@@ -659,9 +816,10 @@ __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uin
     if (!touched || d.refractory_until[dst] > tick) {
         elig = e * cfg.eligibility_decay;
     } else {
-        float jac = branch_jacobian(br, c.a->m.excitability[dst], d.branches[4 * dst + BR_TEMP], d.branches[4 * dst + BR_GATE]);
-        float sur = d.surrogate[dst];
-        float asum = as0 + as1 + as2;
+        const float jac = branch_jacobian(br, c.a->m.excitability[dst], d.branches[4 * dst + BR_TEMP],
+                                          d.branches[4 * dst + BR_GATE]);
+        const float sur = d.surrogate[dst];
+        const float asum = as0 + as1 + as2;
         ms = ms + jac * bs - fs - asum;
         elig = sur * ms;
     }
@@ -685,6 +843,26 @@ __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uin
     return mag > cfg.eligibility_epsilon;
 }
 
+// Update every slot of one eligible list; kept slots are compacted into the
+// other list, dropped slots are unmarked.
+__device__ void eligibility_list(const StepCtx& c, float* planes, uint64_t plane, uint32_t* last, uint8_t* marks,
+                                 const uint32_t* cur, uint32_t cur_n, uint32_t* next, uint32_t* next_count,
+                                 const uint32_t* targets, const uint8_t* branches) {
+    const uint32_t lane = __lane_id();
+    for (uint32_t base = c.gtid - lane; base < cur_n; base += c.gstride) {
+        const uint32_t i = base + lane;
+        bool keep = false;
+        uint32_t slot = 0;
+        if (i < cur_n) {
+            slot = cur[i];
+            keep = update_slot(c, planes, plane, last, slot, targets[slot], branches[slot]);
+            if (!keep) marks[slot] = 0;
+        }
+        const uint32_t pos = wave_append(next_count, keep);
+        if (keep) next[pos] = slot;
+    }
+}
+
 __device__ void phase_eligibility(const StepCtx& c) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = *c.d;
@@ -692,42 +870,23 @@ __device__ void phase_eligibility(const StepCtx& c) {
     const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * cfg.synapses_per_neuron;
     const uint64_t NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
     const uint32_t p = c.parity, q = c.parity ^ 1;
-    const uint32_t rec_n = c.ctl->rec_count[p];
+    const uint32_t rec_n = c.ctl->rec_count[p], in_n = c.ctl->in_count[p];
     if (c.part == 0 && threadIdx.x == 0) {
         c.ctl->tick_scan_rec[c.tick & 1] = rec_n;
-        c.ctl->tick_scan_in[c.tick & 1] = c.ctl->in_count[p];
+        c.ctl->tick_scan_in[c.tick & 1] = in_n;
     }
-    const uint32_t* rec_cur = d.rec_list + p * NS;
-    uint32_t* rec_next = d.rec_list + q * NS;
-    for (uint32_t i = c.gtid; i < rec_n; i += c.gstride) {
-        uint32_t slot = rec_cur[i];
-        if (update_slot(c, d.rec_trace, NS, d.rec_last, slot, a.m.rec_target[slot], a.m.rec_branch[slot])) {
-            uint32_t pos = atomicAdd(&c.ctl->rec_count[q], 1u);
-            rec_next[pos] = slot;
-        } else {
-            d.rec_mark[slot] = 0;
-        }
-    }
-    const uint32_t in_n = c.ctl->in_count[p];
-    const uint32_t* in_cur = d.in_list + p * NI;
-    uint32_t* in_next = d.in_list + q * NI;
-    for (uint32_t i = c.gtid; i < in_n; i += c.gstride) {
-        uint32_t slot = in_cur[i];
-        if (update_slot(c, d.in_trace, NI, d.in_last, slot, a.m.in_target[slot], a.m.in_branch[slot])) {
-            uint32_t pos = atomicAdd(&c.ctl->in_count[q], 1u);
-            in_next[pos] = slot;
-        } else {
-            d.in_mark[slot] = 0;
-        }
-    }
+    eligibility_list(c, d.rec_trace, NS, d.rec_last, d.rec_mark, d.rec_list + p * NS, rec_n, d.rec_list + q * NS,
+                     &c.ctl->rec_count[q], a.m.rec_target, a.m.rec_branch);
+    eligibility_list(c, d.in_trace, NI, d.in_last, d.in_mark, d.in_list + p * NI, in_n, d.in_list + q * NI,
+                     &c.ctl->in_count[q], a.m.in_target, a.m.in_branch);
 }
 
 // ---------------------------------------------------------------------------
-// Phase 5: post-activation dynamics (runtime.rs:920-938), emission snapshot
-// (runtime.rs:1084-1106), and on one workgroup the readout, softmax and
+// Phase 4: post-activation dynamics (runtime.rs:920-938), emission snapshot
+// (runtime.rs:1084-1106), and on the last workgroup the readout, softmax and
 // errors (runtime.rs:1108-1197, 1205-1206).
 // ---------------------------------------------------------------------------
-__device__ void readout(const StepCtx& c, const StepParams& sp, float* s_f, float* s_f2, uint32_t* s_u32, uint32_t step_index) {
+__device__ void readout(const StepCtx& c, const StepParams& sp, StepShared& sh, uint32_t step_index) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = *c.d;
     const LeoConfig& cfg = a.cfg;
@@ -738,74 +897,120 @@ __device__ void readout(const StepCtx& c, const StepParams& sp, float* s_f, floa
     const uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
     const float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
     const uint32_t ctx_count = ctl->ctx_count;
-    // context latent (runtime.rs:1120-1136)
-    float* s_lat = s_f2;
+    const uint32_t wave = threadIdx.x / kWaveSize, lane = __lane_id();
+    float* lat = sh.aux;
+    // context latent (runtime.rs:1120-1136): serial over active slots per dimension
     for (uint32_t e = threadIdx.x; e < E; e += kThreads) {
-        float lat = 0.0f;
+        float v = 0.0f;
         for (uint32_t i = 0; i < ctx_count; ++i) {
-            float scale = ctl->ctx_scales[i];
+            const float scale = ctl->ctx_scales[i];
             if (scale <= 0.0f) continue;
-            lat += d.p.ctx_emb[static_cast<uint64_t>(ctl->ctx_slots[i]) * E + e] * scale;
+            v += d.p.ctx_emb[static_cast<uint64_t>(ctl->ctx_slots[i]) * E + e] * scale;
         }
-        s_lat[e] = lat;
-        d.ctx_latent[e] = lat;
+        lat[e] = v;
+        d.ctx_latent[e] = v;
     }
     __syncthreads();
-    for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) {
-        float l = d.p.bias[o];
-        for (uint32_t r = 0; r < A; ++r) l += d.p.out_w[static_cast<uint64_t>(act_list[r]) * kOutStride + o] * act_val[r];
-        if (ctx_count > 0) {
-            float contribution = 0.0f;
-            for (uint32_t e = 0; e < E; ++e) contribution += d.p.ctx_out[o * E + e] * s_lat[e];
-            l += contribution;
+    // logits[o] = bias[o] + sum over active in order of W[n][o]*a_n (+ context once):
+    // thread t owns outputs t and t+256; the row loads of four active neurons are
+    // issued ahead of their serial adds
+    const uint32_t o1 = threadIdx.x, o2 = threadIdx.x + kThreads;
+    const bool has2 = o2 < kOutputs;
+    float l1 = d.p.bias[o1], l2 = has2 ? d.p.bias[o2] : 0.0f;
+    uint32_t r = 0;
+    for (; r + 4 <= A; r += 4) {
+        const uint64_t n0 = act_list[r], n1 = act_list[r + 1], n2 = act_list[r + 2], n3 = act_list[r + 3];
+        const float a0 = act_val[r], a1 = act_val[r + 1], a2 = act_val[r + 2], a3 = act_val[r + 3];
+        const float w10 = d.p.out_w[n0 * kOutStride + o1], w11 = d.p.out_w[n1 * kOutStride + o1];
+        const float w12 = d.p.out_w[n2 * kOutStride + o1], w13 = d.p.out_w[n3 * kOutStride + o1];
+        float w20 = 0.0f, w21 = 0.0f, w22 = 0.0f, w23 = 0.0f;
+        if (has2) {
+            w20 = d.p.out_w[n0 * kOutStride + o2];
+            w21 = d.p.out_w[n1 * kOutStride + o2];
+            w22 = d.p.out_w[n2 * kOutStride + o2];
+            w23 = d.p.out_w[n3 * kOutStride + o2];
         }
-        s_f[o] = l;
-        d.logits[o] = l;
+        l1 += w10 * a0;
+        l1 += w11 * a1;
+        l1 += w12 * a2;
+        l1 += w13 * a3;
+        l2 += w20 * a0;
+        l2 += w21 * a1;
+        l2 += w22 * a2;
+        l2 += w23 * a3;
     }
-    __syncthreads();
-    // maximum (order-independent), exp, serial sum (runtime.rs:1169-1188)
-    if (threadIdx.x == 0) {
-        float mx = -INFINITY;
-        for (uint32_t o = 0; o < kOutputs; ++o) mx = maxnum(mx, s_f[o]);
-        s_f2[kThreads] = mx;
+    for (; r < A; ++r) {
+        const uint64_t n = act_list[r];
+        const float av = act_val[r];
+        l1 += d.p.out_w[n * kOutStride + o1] * av;
+        if (has2) l2 += d.p.out_w[n * kOutStride + o2] * av;
     }
+    if (ctx_count > 0) {
+        float c1 = 0.0f, c2 = 0.0f;
+        for (uint32_t e = 0; e < E; ++e) {
+            c1 += d.p.ctx_out[o1 * E + e] * lat[e];
+            if (has2) c2 += d.p.ctx_out[o2 * E + e] * lat[e];
+        }
+        l1 += c1;
+        l2 += c2;
+    }
+    sh.err[o1] = l1;
+    d.logits[o1] = l1;
+    if (has2) {
+        sh.err[o2] = l2;
+        d.logits[o2] = l2;
+    }
+    // maximum: order-independent, reduced across the workgroup
+    float mx = has2 ? maxnum(l1, l2) : l1;
+    for (int off = 32; off > 0; off >>= 1) mx = maxnum(mx, __shfl_xor(mx, off));
+    if (lane == 0) sh.redf[wave] = mx;
     __syncthreads();
-    const float mx = s_f2[kThreads];
-    __syncthreads();
-    for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) s_f2[o] = glibc_expf_nonpositive(s_f[o] - mx);
+    mx = sh.redf[0];
+    for (uint32_t w = 1; w < kWavesPerGroup; ++w) mx = maxnum(mx, sh.redf[w]);
+    // exp in parallel (glibc expf), then the serial sum of runtime.rs:1175-1180
+    sh.aux[o1] = glibc_expf_nonpositive(l1 - mx);
+    if (has2) sh.aux[o2] = glibc_expf_nonpositive(l2 - mx);
     __syncthreads();
     if (threadIdx.x == 0) {
         float sum = 0.0f;
-        for (uint32_t o = 0; o < kOutputs; ++o) sum += s_f2[o];
-        s_f[kOutStride] = sum;
+        for (uint32_t o = 0; o < kOutputs; ++o) sum += sh.aux[o];
+        sh.redf[0] = sum;
     }
     __syncthreads();
-    const float sum = s_f[kOutStride];
+    const float sum = sh.redf[0];
     const bool uniform = !finitef(sum) || sum <= 0.0f;
-    for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) {
-        float p = uniform ? 1.0f / static_cast<float>(kOutputs) : s_f2[o] / sum;
-        s_f[o] = p;
-        d.probs[o] = p;
-        float err = p;
-        if (static_cast<int32_t>(o) == sp.target_index) err = p - 1.0f;
-        d.errors[o] = err;
+    const float p1 = uniform ? 1.0f / static_cast<float>(kOutputs) : sh.aux[o1] / sum;
+    const float p2 = has2 ? (uniform ? 1.0f / static_cast<float>(kOutputs) : sh.aux[o2] / sum) : 0.0f;
+    d.probs[o1] = p1;
+    d.errors[o1] = static_cast<int32_t>(o1) == sp.target_index ? p1 - 1.0f : p1;
+    if (has2) {
+        d.probs[o2] = p2;
+        d.errors[o2] = static_cast<int32_t>(o2) == sp.target_index ? p2 - 1.0f : p2;
     }
+    // argmax: largest probability, first index among equals (runtime.rs:1190-1197);
+    // probabilities are non-negative, so their bit patterns order them
+    unsigned long long best = (static_cast<unsigned long long>(__float_as_uint(p1)) << 32) | (0xffffffffu - o1);
+    if (has2) {
+        const unsigned long long k2 = (static_cast<unsigned long long>(__float_as_uint(p2)) << 32) | (0xffffffffu - o2);
+        best = k2 > best ? k2 : best;
+    }
+    best = wave_max_u64(best);
+    __syncthreads();
+    if (lane == 0) sh.red[wave] = best;
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t best = 0;
-        for (uint32_t o = 1; o < kOutputs; ++o) {
-            // total order on non-negative probabilities == bit order
-            if (__float_as_uint(s_f[o]) > __float_as_uint(s_f[best])) best = o;
-        }
+        for (uint32_t w = 1; w < kWavesPerGroup; ++w) best = sh.red[w] > best ? sh.red[w] : best;
+        best = sh.red[0] > best ? sh.red[0] : best;
         StepRecord& rec = d.records[step_index];
-        rec.p_target = sp.target_index >= 0 ? s_f[sp.target_index] : 0.0f;
-        rec.predicted = best;
+        rec.predicted = 0xffffffffu - static_cast<uint32_t>(best);
     }
+    if (sp.target_index >= 0 && (threadIdx.x == static_cast<uint32_t>(sp.target_index) ||
+                                 (has2 && o2 == static_cast<uint32_t>(sp.target_index))))
+        d.records[step_index].p_target = threadIdx.x == static_cast<uint32_t>(sp.target_index) ? p1 : p2;
     __syncthreads();
 }
 
-__device__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step_index, float* s_f, float* s_f2,
-                           uint32_t* s_u32) {
+__device__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step_index, StepShared& sh) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = *c.d;
     const LeoConfig& cfg = a.cfg;
@@ -820,9 +1025,9 @@ __device__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step
     uint32_t inhibitory = 0;
     for (uint32_t item = c.gtid; item < total; item += c.gstride) {
         if (item < A) {
-            uint32_t n = act_list[item];
+            const uint32_t n = act_list[item];
+            const float act = d.activation[n];
             inhibitory += a.m.neuron_type[n] != 0 ? 1u : 0u;
-            float act = d.activation[n];
             d.fatigue[n] += cfg.fatigue_gain * act;
             d.adapt[n] += cfg.adaptation_fast_gain * act;
             d.adapt[N + n] += cfg.adaptation_medium_gain * act;
@@ -830,46 +1035,73 @@ __device__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step
             d.membrane[n] -= d.p.threshold[n] * cfg.membrane_reset_fraction;
             d.refractory_until[n] = refractory;
         } else {
-            uint32_t local = item - A;
-            uint32_t r = local / S, j = local % S;
-            uint64_t rb = static_cast<uint64_t>(rs) * cap + r;
+            const uint32_t local = item - A;
+            const uint32_t r = local / S, j = local % S;
+            const uint64_t rb = static_cast<uint64_t>(rs) * cap + r;
             d.ring_value[rb * S + j] = act_val[r] * d.p.rec_weight[static_cast<uint64_t>(act_list[r]) * S + j];
         }
     }
     add_count(&c.ctl->tick_ainh[c.tick & 1], inhibitory);
     const uint32_t readout_wg = c.P - 1;
-    if ((sp.flags & kStepOutput) && c.part == readout_wg) readout(c, sp, s_f, s_f2, s_u32, step_index);
-    if (c.part == readout_wg && threadIdx.x == 0) {
-        StepRecord& rec = d.records[step_index];
-        if (!(sp.flags & kStepOutput)) {
+    if (c.part == readout_wg) {
+        if (threadIdx.x == 0) {
+            StepRecord& rec = d.records[step_index];
+            LaneControl* ctl = c.ctl;
             rec.p_target = 0.0f;
             rec.predicted = 0;
+            rec.population_inhibition = ctl->population_inhibition;
+            rec.active = A;
+            rec.suprathreshold = ctl->tick_supra[c.tick & 1];
+            rec.block_selected = ctl->block_selected;
+            rec.clipped = ctl->clipped;
+            rec.context_cells = ctl->ctx_count;
+            rec.context_probes = ctl->ctx_probes;
+            rec.context_applied = ctl->ctx_applied;
+            rec.eligible_rec = ctl->rec_count[c.parity];
+            rec.eligible_in = ctl->in_count[c.parity];
+            rec.error_code = 0;
         }
-        LaneControl* ctl = c.ctl;
-        rec.population_inhibition = ctl->population_inhibition;
-        rec.active = A;
-        rec.suprathreshold = ctl->tick_supra[c.tick & 1];
-        rec.block_selected = ctl->block_selected;
-        rec.clipped = ctl->clipped;
-        rec.context_cells = ctl->ctx_count;
-        rec.context_probes = ctl->ctx_probes;
-        rec.context_applied = ctl->ctx_applied;
-        rec.eligible_rec = ctl->rec_count[c.parity];
-        rec.eligible_in = ctl->in_count[c.parity];
-        rec.error_code = 0;
+        if (sp.flags & kStepOutput) {
+            __syncthreads();
+            readout(c, sp, sh, step_index);
+        }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Phase 6: learning destinations and signals (runtime.rs:1214-1263).
+// Phase 5: learning destinations and signals (runtime.rs:1214-1263). Each wave
+// claims destinations, compacts them, and computes their serial 257-term dot
+// products from row tiles staged through LDS (coalesced row loads).
 // ---------------------------------------------------------------------------
-__device__ void phase_signals(const StepCtx& c, float* s_err) {
+// Serial 257-term dot of one output row with the errors, in output order
+// (runtime.rs:1245-1250); eight 16-byte row loads are in flight at a time.
+__device__ __forceinline__ float signal_dot(const float* __restrict__ row, const float* err) {
+    const float4* row4 = reinterpret_cast<const float4*>(row);
+    float acc = 0.0f;
+    for (uint32_t q = 0; q < kEndIndex / 4; q += 8) {
+        float4 v[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) v[u] = row4[q + u];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) {
+            const float* e = err + 4 * (q + u);
+            acc += v[u].x * e[0];
+            acc += v[u].y * e[1];
+            acc += v[u].z * e[2];
+            acc += v[u].w * e[3];
+        }
+    }
+    acc += row[kEndIndex] * err[kEndIndex];
+    return acc;
+}
+
+__device__ void phase_signals(const StepCtx& c, StepShared& sh) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = *c.d;
     const LeoConfig& cfg = a.cfg;
     const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * cfg.synapses_per_neuron;
     const uint64_t NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
-    for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) s_err[o] = d.errors[o];
+    for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = d.errors[o];
     __syncthreads();
     const uint32_t rec_n = c.ctl->rec_count[c.parity], in_n = c.ctl->in_count[c.parity];
     const uint32_t A = c.ctl->active_count;
@@ -878,75 +1110,97 @@ __device__ void phase_signals(const StepCtx& c, float* s_err) {
     const uint32_t* rec_cur = d.rec_list + c.parity * NS;
     const uint32_t* in_cur = d.in_list + c.parity * NI;
     const uint32_t total = rec_n + in_n + A;
-    uint32_t claimed = 0;
-    for (uint32_t item = c.gtid; item < total; item += c.gstride) {
-        uint32_t dst;
-        if (item < rec_n) dst = a.m.rec_target[rec_cur[item]];
-        else if (item < rec_n + in_n) dst = a.m.in_target[in_cur[item - rec_n]];
-        else dst = act_list[item - rec_n - in_n];
-        if (atomicExch(&d.dest_epoch[dst], c.dest_epoch) == c.dest_epoch) continue;
-        claimed += 1;
-        const float* row = d.p.out_w + static_cast<uint64_t>(dst) * kOutStride;
-        float signal = 0.0f;
-        for (uint32_t o = 0; o < kOutputs; ++o) signal += row[o] * s_err[o];
-        d.learning_signal[dst] = signal;
+    const uint32_t wave = threadIdx.x / kWaveSize, lane = __lane_id();
+    const unsigned long long below = (1ULL << lane) - 1ULL;
+    uint32_t* queue = sh.queue[wave];
+    uint32_t queued = 0, claimed = 0;
+    // claimed destinations are queued per wave and computed 64 at a time, one row per lane
+    for (uint32_t base = c.gtid - lane; base < total; base += c.gstride) {
+        const uint32_t item = base + lane;
+        bool won = false;
+        uint32_t dst = 0;
+        if (item < total) {
+            if (item < rec_n) dst = a.m.rec_target[rec_cur[item]];
+            else if (item < rec_n + in_n) dst = a.m.in_target[in_cur[item - rec_n]];
+            else dst = act_list[item - rec_n - in_n];
+            won = atomicExch(&d.dest_epoch[dst], c.dest_epoch) != c.dest_epoch;
+        }
+        const unsigned long long mask = __ballot(won);
+        if (won) queue[queued + __popcll(mask & below)] = dst;
+        queued += static_cast<uint32_t>(__popcll(mask));
+        claimed += won ? 1u : 0u;
+        if (queued >= kWaveSize) {
+            wave_sync();
+            const uint32_t mine = queue[lane];
+            const uint32_t rest = lane + kWaveSize < queued ? queue[lane + kWaveSize] : 0u;
+            wave_sync();
+            if (lane + kWaveSize < queued) queue[lane] = rest;
+            queued -= kWaveSize;
+            d.learning_signal[mine] = signal_dot(d.p.out_w + static_cast<uint64_t>(mine) * kOutStride, sh.err);
+        }
+    }
+    wave_sync();
+    if (lane < queued) {
+        const uint32_t mine = queue[lane];
+        d.learning_signal[mine] = signal_dot(d.p.out_w + static_cast<uint64_t>(mine) * kOutStride, sh.err);
     }
     add_count(&c.ctl->tick_dest[c.tick & 1], claimed);
 }
 
 // ---------------------------------------------------------------------------
-// Phase 7: output/bias/context updates (runtime.rs:1265-1303, 1318-1384),
+// Phase 6: output/bias/context updates (runtime.rs:1265-1303, 1318-1384),
 // recurrent and input synapses (runtime.rs:1451-1523), inhibitory
 // homeostasis (runtime.rs:1525-1565) and threshold homeostasis
 // (runtime.rs:1567-1593).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float inhibitory_step(const LeoConfig& cfg, float w, float src_act, float tgt_act, float strength) {
-    float err = tgt_act - cfg.target_activity;
-    float delta = bounded(-cfg.inhibitory_learning_rate * strength * src_act * err, cfg.max_update);
+    const float err = tgt_act - cfg.target_activity;
+    const float delta = bounded(-cfg.inhibitory_learning_rate * strength * src_act * err, cfg.max_update);
     return clampf(w + delta, cfg.weight_min, 0.0f);
 }
 
-__device__ void context_update(const StepCtx& c, const StepParams& sp, float* s_err, float* s_grad) {
+__device__ void context_update(const StepCtx& c, const StepParams& sp, StepShared& sh) {
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = *c.d;
     LaneControl* ctl = c.ctl;
     const uint32_t E = cfg.context_embedding_dim, count = ctl->ctx_count;
     const float lr = cfg.context_learning_rate, mu = cfg.max_update, wmin = cfg.weight_min, wmax = cfg.weight_max;
     const float strength = sp.supervised_strength;
+    float* grad = sh.aux;
     for (uint32_t e = threadIdx.x; e < E; e += kThreads) {
         float g = 0.0f;
-        for (uint32_t o = 0; o < kOutputs; ++o) g += d.p.ctx_out[o * E + e] * s_err[o];
-        s_grad[e] = g;
+        for (uint32_t o = 0; o < kOutputs; ++o) g += d.p.ctx_out[o * E + e] * sh.err[o];
+        grad[e] = g;
     }
     __syncthreads();
     if (threadIdx.x == 0) ctl->ctx_out_dirty = 1;
     for (uint32_t i = threadIdx.x; i < kOutputs * E; i += kThreads) {
-        uint32_t o = i / E, e = i % E;
-        float gradient = s_err[o] * d.ctx_latent[e];
-        float delta = bounded(-lr * strength * gradient, mu);
-        float updated = clampf(d.p.ctx_out[i] + delta, wmin, wmax);
+        const uint32_t o = i / E, e = i % E;
+        const float gradient = sh.err[o] * d.ctx_latent[e];
+        const float delta = bounded(-lr * strength * gradient, mu);
+        const float updated = clampf(d.p.ctx_out[i] + delta, wmin, wmax);
         if (!finitef(updated)) set_error(ctl, kErrContextProjection);
         d.p.ctx_out[i] = updated;
     }
     for (uint32_t i = threadIdx.x; i < count * E; i += kThreads) {
-        uint32_t k = i / E, e = i % E;
-        uint64_t slot = ctl->ctx_slots[k];
-        float gradient = ctl->ctx_scales[k] * s_grad[e];
-        float delta = bounded(-lr * strength * gradient, mu);
-        float updated = clampf(d.p.ctx_emb[slot * E + e] + delta, wmin, wmax);
+        const uint32_t k = i / E, e = i % E;
+        const uint64_t slot = ctl->ctx_slots[k];
+        const float gradient = ctl->ctx_scales[k] * grad[e];
+        const float delta = bounded(-lr * strength * gradient, mu);
+        const float updated = clampf(d.p.ctx_emb[slot * E + e] + delta, wmin, wmax);
         if (!finitef(updated)) set_error(ctl, kErrContextEmbedding);
         d.p.ctx_emb[slot * E + e] = updated;
     }
     for (uint32_t k = threadIdx.x; k < count; k += kThreads) {
-        uint32_t slot = ctl->ctx_slots[k];
+        const uint32_t slot = ctl->ctx_slots[k];
         mark_bit(d.ch_ctx, slot);
-        uint32_t obs = d.p.ctx_obs[slot];
+        const uint32_t obs = d.p.ctx_obs[slot];
         d.p.ctx_obs[slot] = obs == 0xffffffffu ? obs : obs + 1;
     }
     __syncthreads();
 }
 
-__device__ void phase_learn(const StepCtx& c, const StepParams& sp, float* s_err, float* s_grad) {
+__device__ void phase_learn(const StepCtx& c, const StepParams& sp, StepShared& sh) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = *c.d;
     const LeoConfig& cfg = a.cfg;
@@ -963,31 +1217,31 @@ __device__ void phase_learn(const StepCtx& c, const StepParams& sp, float* s_err
     const float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
     const float mu = cfg.max_update, wmin = cfg.weight_min, wmax = cfg.weight_max;
     if (learn) {
-        for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) s_err[o] = d.errors[o];
+        for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = d.errors[o];
         __syncthreads();
         const float ss = sp.supervised_strength;
         const float olr = cfg.output_learning_rate;
         // output rows of active neurons
         const uint32_t out_items = A * kOutputs;
         for (uint32_t item = c.gtid; item < out_items; item += c.gstride) {
-            uint32_t r = item / kOutputs, o = item % kOutputs;
-            uint32_t n = act_list[r];
-            float act = act_val[r];
+            const uint32_t r = item / kOutputs, o = item % kOutputs;
+            const uint32_t n = act_list[r];
+            const float act = act_val[r];
             if (o == 0) mark_bit(d.ch_out, n);
-            float raw = -olr * ss * s_err[o] * act;
+            const float raw = -olr * ss * sh.err[o] * act;
             float* w = d.p.out_w + static_cast<uint64_t>(n) * kOutStride + o;
             *w = clampf(*w + bounded(raw, mu), wmin, wmax);
         }
         // bias and context projection on the readout workgroup
         if (c.part == c.P - 1) {
             for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) {
-                float raw = -olr * ss * s_err[o];
-                float b = d.p.bias[o] + bounded(raw, mu);
+                const float raw = -olr * ss * sh.err[o];
+                const float b = d.p.bias[o] + bounded(raw, mu);
                 if (!finitef(b)) set_error(ctl, kErrBias);
                 d.p.bias[o] = b;
             }
             if (threadIdx.x == 0) ctl->bias_dirty = 1;
-            if (ctl->ctx_applied && ctl->ctx_count > 0) context_update(c, sp, s_err, s_grad);
+            if (ctl->ctx_applied && ctl->ctx_count > 0) context_update(c, sp, sh);
         }
         if (plastic) {
             const float cs = ss * sp.plasticity_scale;
@@ -995,21 +1249,21 @@ __device__ void phase_learn(const StepCtx& c, const StepParams& sp, float* s_err
             const uint32_t rec_n = ctl->rec_count[c.parity];
             const uint32_t* rec_cur = d.rec_list + c.parity * NS;
             for (uint32_t i = c.gtid; i < rec_n; i += c.gstride) {
-                uint32_t slot = rec_cur[i];
-                uint32_t dst = a.m.rec_target[slot];
-                uint32_t src = slot / S;
-                float e = d.rec_trace[6 * NS + slot];
-                float gradient = d.learning_signal[dst] * e;
-                float delta = bounded(-lr * cs * gradient, mu);
-                float old_w = d.p.rec_weight[slot];
+                const uint32_t slot = rec_cur[i];
+                const uint32_t dst = a.m.rec_target[slot];
+                const uint32_t src = slot / S;
+                const float e = d.rec_trace[6 * NS + slot];
+                const float gradient = d.learning_signal[dst] * e;
+                const float delta = bounded(-lr * cs * gradient, mu);
+                const float old_w = d.p.rec_weight[slot];
                 float nw = clampf(old_w + delta, wmin, wmax);
                 const bool excitatory = a.m.neuron_type[src] == 0;
                 nw = excitatory ? maxnum(nw, 0.0f) : fminf(nw, 0.0f);
                 if (!finitef(nw)) set_error(ctl, kErrRecurrent);
                 bool changed = nw != old_w;
                 if (!excitatory && d.selected_epoch[src] == tick + 1) {
-                    float tgt_act = d.activation[dst] > 0.0f ? 1.0f : 0.0f;
-                    float nw2 = inhibitory_step(cfg, nw, d.activation[src], tgt_act, sp.strength);
+                    const float tgt_act = d.activation[dst] > 0.0f ? 1.0f : 0.0f;
+                    const float nw2 = inhibitory_step(cfg, nw, d.activation[src], tgt_act, sp.strength);
                     if (!finitef(nw2)) set_error(ctl, kErrInhibitory);
                     changed = changed || nw2 != nw;
                     nw = nw2;
@@ -1020,13 +1274,13 @@ __device__ void phase_learn(const StepCtx& c, const StepParams& sp, float* s_err
             const uint32_t in_n = ctl->in_count[c.parity];
             const uint32_t* in_cur = d.in_list + c.parity * NI;
             for (uint32_t i = c.gtid; i < in_n; i += c.gstride) {
-                uint32_t slot = in_cur[i];
-                uint32_t dst = a.m.in_target[slot];
-                float e = d.in_trace[6 * NI + slot];
-                float gradient = d.learning_signal[dst] * e;
-                float delta = bounded(-lr * cs * gradient, mu);
-                float old_w = d.p.in_weight[slot];
-                float nw = clampf(old_w + delta, 0.0f, wmax);
+                const uint32_t slot = in_cur[i];
+                const uint32_t dst = a.m.in_target[slot];
+                const float e = d.in_trace[6 * NI + slot];
+                const float gradient = d.learning_signal[dst] * e;
+                const float delta = bounded(-lr * cs * gradient, mu);
+                const float old_w = d.p.in_weight[slot];
+                const float nw = clampf(old_w + delta, 0.0f, wmax);
                 if (!finitef(nw)) set_error(ctl, kErrInput);
                 if (nw != old_w) mark_bit(d.ch_in, slot);
                 d.p.in_weight[slot] = nw;
@@ -1036,15 +1290,15 @@ __device__ void phase_learn(const StepCtx& c, const StepParams& sp, float* s_err
         // already handled with their eligible slot above
         const uint32_t inh_items = A * S;
         for (uint32_t item = c.gtid; item < inh_items; item += c.gstride) {
-            uint32_t r = item / S, j = item % S;
-            uint32_t src = act_list[r];
+            const uint32_t r = item / S, j = item % S;
+            const uint32_t src = act_list[r];
             if (a.m.neuron_type[src] == 0) continue;
-            uint64_t slot = static_cast<uint64_t>(src) * S + j;
+            const uint64_t slot = static_cast<uint64_t>(src) * S + j;
             if (plastic && d.rec_mark[slot]) continue;
-            uint32_t dst = a.m.rec_target[slot];
-            float tgt_act = d.activation[dst] > 0.0f ? 1.0f : 0.0f;
-            float old_w = d.p.rec_weight[slot];
-            float nw = inhibitory_step(cfg, old_w, d.activation[src], tgt_act, sp.strength);
+            const uint32_t dst = a.m.rec_target[slot];
+            const float tgt_act = d.activation[dst] > 0.0f ? 1.0f : 0.0f;
+            const float old_w = d.p.rec_weight[slot];
+            const float nw = inhibitory_step(cfg, old_w, d.activation[src], tgt_act, sp.strength);
             if (!finitef(nw)) set_error(ctl, kErrInhibitory);
             if (nw != old_w) mark_bit(d.ch_rec, static_cast<uint32_t>(slot));
             d.p.rec_weight[slot] = nw;
@@ -1055,12 +1309,12 @@ __device__ void phase_learn(const StepCtx& c, const StepParams& sp, float* s_err
         const float pop_err = static_cast<float>(A) / N - cfg.target_activity;
         const uint32_t touched = ctl->tick_touched[tick & 1];
         for (uint32_t i = c.gtid; i < touched; i += c.gstride) {
-            uint32_t n = d.touched_list[i];
-            float local = d.activation[n] > 0.0f ? 1.0f : 0.0f;
-            float local_err = local - cfg.target_activity;
-            float delta = cfg.threshold_homeostasis_rate * (local_err + pop_err);
-            float old_t = d.p.threshold[n];
-            float nt = clampf(old_t + delta, 0.05f, 2.0f);
+            const uint32_t n = d.touched_list[i];
+            const float local = d.activation[n] > 0.0f ? 1.0f : 0.0f;
+            const float local_err = local - cfg.target_activity;
+            const float delta = cfg.threshold_homeostasis_rate * (local_err + pop_err);
+            const float old_t = d.p.threshold[n];
+            const float nt = clampf(old_t + delta, 0.05f, 2.0f);
             if (nt != old_t) mark_bit(d.ch_threshold, n);
             d.p.threshold[n] = nt;
         }
@@ -1092,17 +1346,18 @@ __device__ __forceinline__ bool phase_barrier(const StepCtx& c, uint32_t& target
     unsigned long long arrived = 0;
     const bool timer = kProfile && c.part == 0 && threadIdx.x == 0;
     if (timer) clock.arrive(phase, arrived);
-    bool ok = lane_barrier(c.ctl, c.P, target, spin_limit);
+    const bool ok = lane_barrier(c.ctl, c.P, target, spin_limit);
     if (timer) clock.release(phase, arrived);
     return ok;
 }
 
+// Step loop. Phases (barriers): deliver | fold+select (+context) | active list +
+// eligibility | post + readout | signals | learning. Frozen steps stop after
+// the post phase; a binding global cap inserts the global sort and the
+// surrogate pass before the eligibility update.
 template <bool kProfile>
 __device__ void lane_steps(const KernelArgs& args) {
-    __shared__ uint64_t s_keys[kMaxBlockNeurons];
-    __shared__ float s_f[kOutStride + 4];
-    __shared__ float s_f2[kOutStride + kThreads + 4];
-    __shared__ uint32_t s_u32[kThreads];
+    __shared__ StepShared sh;
     const uint32_t L = args.lane_count, P = args.wgs_per_lane;
     const uint32_t lane = blockIdx.x % L;
     StepCtx c;
@@ -1128,42 +1383,38 @@ __device__ void lane_steps(const KernelArgs& args) {
         const bool trace = (sp.flags & kStepLearnTrace) != 0;
         phase_deliver(c, sp, s);
         if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 0))) break;
-        phase_fold(c, sp);
+        phase_fold_select(c, sp, sh);
         if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 1))) break;
-        phase_select(c, s_keys, s_u32);
-        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 2))) break;
         if (redundant) {
-            if (c.part == 0) build_active(c, s_keys, s_u32);
+            write_active(c);
             if (trace) phase_eligibility(c);
         } else {
-            if (c.part == 0) build_active(c, s_keys, s_u32);
+            if (c.part == 0) global_select(c, sh);
             if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 7))) break;
             const uint32_t touched = c.ctl->tick_touched[c.tick & 1];
             const uint32_t nb = args.cfg.neurons_per_block;
             for (uint32_t i = c.gtid; i < touched; i += c.gstride) {
-                uint32_t n = c.d->touched_list[i];
-                surrogate_for(c, n, c.d->block_cutoff[n / nb], c.ctl->pop_cutoff);
+                const uint32_t n = c.d->touched_list[i];
+                surrogate_for(c, n, c.d->block_cutoff[n / nb], c.ctl->pop_cutoff, c.d->selected_epoch[n] == c.tick + 1);
             }
             if (trace) {
                 if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 7))) break;
                 phase_eligibility(c);
             }
         }
-        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 3))) break;
+        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 2))) break;
         if (trace) c.parity ^= 1;
-        phase_post(c, sp, s, s_f, s_f2, s_u32);
+        phase_post(c, sp, s, sh);
+        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 3))) break;
         const bool learn = (sp.flags & kStepLearn) != 0;
+        if (learn && sp.plasticity_scale > 0.0f) {
+            c.dest_epoch += 1;
+            phase_signals(c, sh);
+            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 4))) break;
+        }
         if (learn || !(sp.flags & kStepFrozen)) {
-            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 4))) break;
-            if (learn && sp.plasticity_scale > 0.0f) {
-                c.dest_epoch += 1;
-                phase_signals(c, s_f);
-                if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 5))) break;
-            }
-            phase_learn(c, sp, s_f, s_f2);
-            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 6))) break;
-        } else {
-            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 4))) break;
+            phase_learn(c, sp, sh);
+            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 5))) break;
         }
         c.tick += 1;
     }

@@ -520,7 +520,8 @@ void run_lanes(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     if (h->phase_profile)
         for (auto& r : runs) LEO_HIP_CHECK(hipMemsetAsync(r.lane->desc.phase_profile, 0, 2 * kPhases * 8, h->stream));
     LEO_HIP_CHECK(hipEventRecord(h->ev_start, h->stream));
-    LEO_HIP_CHECK(hipLaunchCooperativeKernel(kernel, dim3(count * P), dim3(kThreads), params, 0, h->stream));
+    LEO_HIP_CHECK(hipLaunchCooperativeKernel(kernel, dim3(count * P), dim3(kThreads), params,
+                                             step_lds_bytes(h->cfg.device.neurons_per_block), h->stream));
     LEO_HIP_CHECK(hipEventRecord(h->ev_stop, h->stream));
     std::vector<LaneControl> ctl(count);
     for (uint32_t i = 0; i < count; ++i) {
@@ -1294,7 +1295,8 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         h->cus = prop.multiProcessorCount;
         LEO_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&h->coop_blocks_per_cu,
                                                                    reinterpret_cast<const void*>(&leo::leo_lane_steps),
-                                                                   leo::kThreads, 0));
+                                                                   leo::kThreads,
+                                                                   leo::step_lds_bytes(config->device.neurons_per_block)));
         if (h->coop_blocks_per_cu <= 0) throw Error(LEO_ERR_DEVICE, "step kernel cannot be resident");
         if (const char* env = std::getenv("LEO_HIP_WGS_PER_LANE")) h->wgs_override = static_cast<uint32_t>(std::atoi(env));
         if (const char* env = std::getenv("LEO_HIP_PHASE_PROFILE")) h->phase_profile = std::atoi(env) != 0;
