@@ -59,6 +59,35 @@ def cpu_baseline(workload, model, data, offsets, replay: bool):
     }
 
 
+def copy_calibration(mib: int = 256, repeats: int = 4) -> int:
+    """Plain device copy of a known size, for scaling the FETCH_SIZE/WRITE_SIZE
+    counters of a profiled run into HBM bytes (torch's elementwise copy kernel)."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.arange(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(repeats):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_dispatch": n * 4, "dispatches": repeats}), flush=True)
+    return 0
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per step-kernel launch from the committed PMC summary of this
+    workload (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the copy-kernel
+    calibration), or None when no summary exists."""
+    path = ROOT / "profiles" / f"leo_lane_steps_workload{workload}_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -67,7 +96,11 @@ def main() -> int:
     ap.add_argument("--workload", default="B")
     ap.add_argument("--no-replay", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain device copy of known size (PMC counter calibration)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box in this setup has one MI355X, so --gpus {args.gpus} "
               "is not run (the lane-sharded multi-GPU design is described in DESIGN.md)", file=sys.stderr)
@@ -138,7 +171,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": measured_traffic(w.name),
             "kernel": "leo_lane_steps",
             "launches": ks["launches"],
             "kernel_ms_total": ks["kernel_ms"],
@@ -157,4 +190,6 @@ def main() -> int:
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    status = main()
+    if status:
+        sys.exit(status)

@@ -160,9 +160,10 @@ typedef struct LeoKernelStats {
     uint64_t active_inhibitory;
     uint64_t merge_launches;
     double merge_ms;
-    /* With LEO_HIP_PHASE_PROFILE=1 at creation: per step phase (deliver, fold,
-     * select, eligibility/active list, post/readout, signals, learn, extra), the
-     * microseconds workgroup 0 spent working and waiting at the phase barrier. */
+    /* With LEO_HIP_PHASE_PROFILE=1 at creation: per step phase (deliver,
+     * fold+select, active list+eligibility, post/readout, signals, learn, unused,
+     * binding-cap global selection), the microseconds workgroup 0 of the first
+     * lane spent working and waiting at the phase barrier. */
     double phase_work_us[8];
     double phase_wait_us[8];
 } LeoKernelStats;
@@ -249,6 +250,13 @@ int32_t leo_hip_training_step_batch(LeoHipRuntime* runtime, const uint32_t* symb
 /* RuntimeBackend::advance_frozen_batch (backend.rs:428-431). */
 int32_t leo_hip_advance_frozen_batch(LeoHipRuntime* runtime, const uint32_t* symbols,
                                      uint32_t count);
+/* RuntimeBackend::replay_streaming_batch (backend.rs:439-453): one mixed
+ * timeline without resets; targets[i] >= 0 positions are supervised with
+ * `permission`, targets[i] < 0 positions advance frozen state. Metrics are
+ * written to out[] for supervised positions only (*supervised of them). */
+int32_t leo_hip_replay_streaming_batch(LeoHipRuntime* runtime, const uint32_t* symbols,
+                                       const int32_t* targets, uint32_t count, int32_t permission,
+                                       LeoStepMetrics* out, uint32_t* supervised);
 /* RuntimeBackend::training_story_batch (backend.rs:457-463): one device lane
  * per story, each forked from the canonical revision at tick 0, followed by
  * the batch-end lane-ordered mean (parallel.rs:694-798). The canonical model

@@ -597,14 +597,16 @@ LeoStepMetrics to_metrics(const StepParams& sp, const StepRecord& rec, float los
 
 // Execute steps on the canonical runtime; stats and revision update the
 // canonical mirrors exactly as Runtime::step does.
+// `outputs[i]` asks for the readout of step i even when it does not learn.
 std::vector<LeoStepMetrics> canonical_steps(LeoHipRuntime* h, const std::vector<HostStep>& steps,
-                                            const std::vector<int32_t>& permissions, bool output) {
+                                            const std::vector<int32_t>& permissions, const std::vector<bool>& outputs) {
     Lane& lane = *h->canonical;
     LaneRun run{&lane, {}, {}};
     run.steps.reserve(steps.size());
     uint32_t tick = lane.tick;
     for (size_t i = 0; i < steps.size(); ++i)
-        run.steps.push_back(make_step(h->cfg, lane, steps[i].symbol, steps[i].target, permissions[i], tick++, output));
+        run.steps.push_back(
+            make_step(h->cfg, lane, steps[i].symbol, steps[i].target, permissions[i], tick++, outputs[i]));
     std::vector<LaneRun> runs;
     runs.push_back(std::move(run));
     run_lanes(h, runs);
@@ -621,6 +623,11 @@ std::vector<LeoStepMetrics> canonical_steps(LeoHipRuntime* h, const std::vector<
         out.push_back(m);
     }
     return out;
+}
+
+std::vector<LeoStepMetrics> canonical_steps(LeoHipRuntime* h, const std::vector<HostStep>& steps,
+                                            const std::vector<int32_t>& permissions, bool output) {
+    return canonical_steps(h, steps, permissions, std::vector<bool>(steps.size(), output));
 }
 
 void canonical_reset(LeoHipRuntime* h) {
@@ -1388,6 +1395,32 @@ int32_t leo_hip_advance_frozen_batch(LeoHipRuntime* h, const uint32_t* symbols, 
         std::vector<leo::HostStep> steps(count);
         for (uint32_t i = 0; i < count; ++i) steps[i] = {symbols[i], -1};
         leo::canonical_steps(h, steps, std::vector<int32_t>(count, LEO_FROZEN), false);
+    });
+}
+
+int32_t leo_hip_replay_streaming_batch(LeoHipRuntime* h, const uint32_t* symbols, const int32_t* targets,
+                                       uint32_t count, int32_t permission, LeoStepMetrics* out, uint32_t* supervised) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (supervised) *supervised = 0;
+        if (count == 0) return;
+        if (!symbols || !targets) throw Error(LEO_ERR_INVALID_ARGUMENT, "null step arrays");
+        std::vector<leo::HostStep> steps(count);
+        std::vector<int32_t> perms(count);
+        std::vector<bool> outputs(count);
+        for (uint32_t i = 0; i < count; ++i) {
+            steps[i] = {symbols[i], targets[i]};
+            perms[i] = targets[i] >= 0 ? permission : LEO_FROZEN;
+            outputs[i] = targets[i] >= 0;
+        }
+        auto m = leo::canonical_steps(h, steps, perms, outputs);
+        uint32_t k = 0;
+        for (uint32_t i = 0; i < count; ++i)
+            if (targets[i] >= 0) {
+                if (out) out[k] = m[i];
+                ++k;
+            }
+        if (supervised) *supervised = k;
     });
 }
 

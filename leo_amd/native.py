@@ -145,6 +145,7 @@ SIGNATURES = {
     "leo_hip_step": (_I32, [_P, _U32, _I32, _I32, _P]),
     "leo_hip_training_step_batch": (_I32, [_P, _P, _P, _U32, _I32, _P]),
     "leo_hip_advance_frozen_batch": (_I32, [_P, _P, _U32]),
+    "leo_hip_replay_streaming_batch": (_I32, [_P, _P, _P, _U32, _I32, _P, _P]),
     "leo_hip_training_story_batch": (_I32, [_P, _P, _P, _U32, _I32, _P, _P]),
     "leo_hip_train_batch": (_I32, [_P, _P, _P, _U32, _I32, _U32, _P, _P]),
     "leo_hip_download_model": (_I32, [_P, _P]),

@@ -168,6 +168,20 @@ class HipRuntime:
         if symbols.size:
             self._call("leo_hip_advance_frozen_batch", symbols.ctypes.data, symbols.size)
 
+    def replay_streaming_batch(self, steps: Sequence[Tuple[int, Optional[int]]], permission: int
+                               ) -> List[StepMetrics]:
+        """backend.rs:439-453: a mixed timeline; metrics for supervised positions only."""
+        n = len(steps)
+        if n == 0:
+            return []
+        symbols = np.array([s for s, _ in steps], dtype=np.uint32)
+        targets = np.array([-1 if t is None else t for _, t in steps], dtype=np.int32)
+        out = (native.LeoStepMetrics * n)()
+        supervised = ctypes.c_uint32()
+        self._call("leo_hip_replay_streaming_batch", symbols.ctypes.data, targets.ctypes.data, n, permission, out,
+                   ctypes.byref(supervised))
+        return [StepMetrics.from_c(out[i]) for i in range(supervised.value)]
+
     def training_story_batch(self, stories: Sequence[bytes], permission: int) -> Tuple[BatchReport, List[np.ndarray]]:
         """backend.rs:457-463: device lanes + the batch-end mean; returns per-story losses."""
         data, offsets = pack_stories(stories)

@@ -14,6 +14,18 @@
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
  * this library, and only as the checker or the CPU baseline. The product
  * (leo_amd/) never links or calls it.
+ *
+ * Pins (tests/test_oracle_reference.py, tests/test_known_answers.py): the
+ * reference's own unit tests of runtime.rs, runtime_smoke.rs, learning.rs,
+ * parallel.rs and main.rs restated against this library; brute force for
+ * block selection order and replay range selection; published SplitMix64 and
+ * FNV-1a vectors for the dropout hash and the context key.
+ *
+ * Parity unpinned (no reference-held vector covers them; the reference is Rust
+ * and cannot run here): multi-step Runtime::step trajectories on random
+ * models, context-slot eviction under collisions in the keyed context merge,
+ * and end-to-end train_story_batch + replay state. exp/ln are glibc expf/logf,
+ * the functions Rust's f32::exp/ln call on x86_64 Linux.
  */
 #ifndef LEO_ORACLE_H
 #define LEO_ORACLE_H

@@ -1,0 +1,87 @@
+"""Committed fixture (tests/golden/make_golden.py): two logical batches of
+workload A with 30% replay. The CPU test checks the oracle and the seeded model
+generator still reproduce it; the GPU test checks the HIP path against it bit
+for bit (per-step losses, replay schedule, every learned tensor)."""
+from __future__ import annotations
+
+import hashlib
+import json
+import pathlib
+
+import numpy as np
+import pytest
+
+from leo_amd import native
+from leo_amd.workload import WORKLOADS, workload_model
+
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
+TENSORS = ("threshold", "rec_weight", "in_weight", "out_weight", "bias", "ctx_keys", "ctx_emb", "ctx_obs", "ctx_out")
+
+
+def _fixture():
+    arrays = np.load(GOLDEN / "workloadA_batches.npz")
+    record = json.loads((GOLDEN / "workloadA_batches.json").read_text())
+    data = arrays["story_bytes"].tobytes()
+    stories, cursor = [], 0
+    for n in arrays["story_lengths"]:
+        stories.append(data[cursor:cursor + int(n)])
+        cursor += int(n)
+    return arrays, record, stories
+
+
+def _digest(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def _check_model(model, expected, label):
+    for name in TENSORS:
+        assert _digest(getattr(model, name)) == expected["digests"][name], f"{label}: {name}"
+    assert int(model.parameter_revision) == expected["parameter_revision"], label
+    for k, v in expected["statistics"].items():
+        assert model.statistics[k] == v, f"{label}: statistics {k}"
+
+
+def _run(runtime, train, record, stories):
+    losses = []
+    for (lo, hi), want in zip(record["batches"], record["reports"]):
+        rep, per_story = train(runtime, stories[lo:hi])
+        losses.extend(per_story)
+        assert int(rep.replay_segments) == want["replay_segments"]
+        assert int(rep.replay_steps) == want["replay_steps"]
+        assert int(rep.replay_prefix_steps) == want["replay_prefix_steps"]
+        assert int(rep.merge_fixed_parameter_updates) == want["merge_fixed_parameter_updates"]
+        assert int(rep.merge_context_keys) == want["merge_context_keys"]
+        assert float(rep.mean_loss) == want["mean_loss"]
+    return np.concatenate(losses).astype(np.float32)
+
+
+def test_seeded_model_generator_matches_fixture():
+    _, record, _ = _fixture()
+    _check_model(workload_model(WORKLOADS["A"]), record["initial"], "initial model")
+
+
+def test_oracle_reproduces_fixture(oracle):
+    arrays, record, stories = _fixture()
+    rt = oracle.OracleRuntime(workload_model(WORKLOADS["A"]))
+    losses = _run(rt, lambda r, s: r.train_story_batch(s, oracle.TRAINING, replay=True), record, stories)
+    assert np.array_equal(losses, arrays["losses"])
+    final = rt.model()
+    assert np.array_equal(final.threshold, arrays["threshold"]) and np.array_equal(final.bias, arrays["bias"])
+    _check_model(final, record["final"], "oracle")
+
+
+@pytest.mark.gpu
+def test_hip_path_matches_fixture(require_gpu):
+    from leo_amd.runtime import HipRuntime
+
+    arrays, record, stories = _fixture()
+    rt = HipRuntime(workload_model(WORKLOADS["A"]), device=0, max_lanes=2)
+    try:
+        print("golden: workload A, 2 batches, replay on", flush=True)
+        losses = _run(rt, lambda r, s: r.train_batch(s, native.TRAINING, replay=True), record, stories)
+        assert np.array_equal(losses, arrays["losses"])
+        final = rt.model()
+        assert np.array_equal(final.threshold, arrays["threshold"]) and np.array_equal(final.bias, arrays["bias"])
+        _check_model(final, record["final"], "hip")
+    finally:
+        rt.close()
