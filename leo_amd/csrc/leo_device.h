@@ -23,11 +23,11 @@ constexpr uint32_t kWaveSize = 64;
 constexpr uint32_t kWavesPerGroup = kThreads / kWaveSize;
 constexpr uint32_t kMaxWaves = 1024;     // selecting waves per lane (workgroups per lane <= 256)
 
-// Dynamic LDS of the step kernel: per wave a u64 candidate list and a u32
-// touched list of one block each; the binding-cap global sort (up to
-// kMaxBlockNeurons keys) reuses the front.
+// Dynamic LDS of the step kernel: per wave a u64 candidate list, a u32
+// touched list and an f32 margin list of one block each; the binding-cap
+// global sort (up to kMaxBlockNeurons keys) reuses the front.
 inline size_t step_lds_bytes(uint32_t neurons_per_block) {
-    const size_t lists = static_cast<size_t>(kWavesPerGroup) * neurons_per_block * (8 + 4);
+    const size_t lists = static_cast<size_t>(kWavesPerGroup) * neurons_per_block * (8 + 4 + 4);
     const size_t sort = static_cast<size_t>(kMaxBlockNeurons) * 8;
     return ((lists > sort ? lists : sort) + 15) / 16 * 16;
 }
@@ -110,6 +110,7 @@ struct LaneControl {
     uint32_t error_code;
     uint32_t barrier;                // lane-group barrier arrival counter
     uint32_t abort;
+    uint32_t xcc_mask;               // XCDs the lane's workgroups run on (bit per XCD)
     uint32_t ring_tick[kRing];       // tick whose active set ring slot holds (UINT32_MAX = empty)
     uint32_t ring_count[kRing];      // active count of that tick
     uint32_t tick_touched[2];        // touched count, indexed by tick parity
@@ -217,6 +218,8 @@ struct KernelArgs {
     uint32_t wgs_per_lane;
     uint32_t redundant_global;       // block_count*max_active_per_block <= max_active_global
     uint32_t spin_limit;
+    uint32_t lane_stride;            // workgroup b serves lane b % lane_stride (>= lane_count)
+    uint32_t local_sync;             // allow XCD-local lane barriers
 };
 
 // Batch-end mean of one fixed-parameter tensor (see leo_merge_fixed).

@@ -140,26 +140,56 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Lane-group barrier. Every thread releases its writes at agent scope, thread
-// 0 arrives on the lane's counter and waits for all P workgroups, and an
-// agent-scope acquire afterwards makes the other workgroups' writes visible.
-// The wait is bounded: on timeout the lane is aborted and every workgroup
-// leaves the step loop, so the grid always drains.
-__device__ bool lane_barrier(LaneControl* ctl, uint32_t P, uint32_t& target, uint32_t spin_limit) {
+// Loads of lane state written by other workgroups of the lane. A relaxed
+// agent-scope atomic load is a device-scope load (global_load ... sc1): it
+// misses the CU's L1 and reads the L2, so it never returns a line another CU
+// has since rewritten. Read-only topology uses plain loads.
+template <class T>
+__device__ __forceinline__ T ld(const T* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// XCD (accelerator complex die) this wave runs on.
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
+    return v;
+}
+
+// Lane-group barrier. Thread 0 of each of the P workgroups arrives on the
+// lane's counter and waits for the others; the wait is bounded, and on
+// timeout the lane is aborted so every workgroup leaves the step loop and the
+// grid drains.
+//
+// Visibility. With `local` (all workgroups of the lane verified to run on one
+// XCD, hence share one L2, and every cross-workgroup read done with ld()),
+// waiting until this thread's stores have completed to L2 is the whole release
+// and nothing needs invalidating. Otherwise agent-scope release/acquire fences
+// write back and invalidate the L2 so other XCDs see the data.
+__device__ bool lane_barrier(LaneControl* ctl, uint32_t P, uint32_t& target, uint32_t spin_limit, bool local) {
     __shared__ uint32_t s_abort;
     if (P == 1) {
         __syncthreads();
         return true;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (local) {
+        __builtin_amdgcn_s_waitcnt(0);
+    } else {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
         target += P;
-        __hip_atomic_fetch_add(&ctl->barrier, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        if (local) {
+            __hip_atomic_fetch_add(&ctl->barrier, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            __hip_atomic_fetch_add(&ctl->barrier, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        }
         uint32_t spins = 0;
         uint32_t aborted = 0;
-        while (__hip_atomic_load(&ctl->barrier, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            if (__hip_atomic_load(&ctl->abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+        while ((local ? ld(&ctl->barrier)
+                      : __hip_atomic_load(&ctl->barrier, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT)) < target) {
+            if (ld(&ctl->abort) != 0) {
                 aborted = 1;
                 break;
             }
@@ -174,7 +204,7 @@ __device__ bool lane_barrier(LaneControl* ctl, uint32_t P, uint32_t& target, uin
         s_abort = aborted;
     }
     __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (!local) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     return s_abort == 0;
 }
 
@@ -243,6 +273,7 @@ struct StepCtx {
     uint32_t gstride;
     uint32_t parity;   // current eligible list
     uint32_t dest_epoch;
+    bool local;        // workgroups of the lane share one L2 (see lane_barrier)
 };
 
 // ---------------------------------------------------------------------------
@@ -251,17 +282,21 @@ struct StepCtx {
 // (runtime.rs:710-766) is slot-local; branch adds go to per-target buckets
 // keyed by CPU delivery order and are folded in phase 2.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void advance_trace(float* planes, uint64_t plane, uint32_t* last, uint32_t slot,
-                                              uint32_t tick, const LeoConfig& cfg) {
-    uint32_t e = tick - last[slot];
-    if (e == 0) return;
-    planes[slot] *= decay_for_elapsed(cfg.branch_decay, e);
-    planes[plane + slot] *= decay_for_elapsed(cfg.membrane_decay, e);
-    planes[2 * plane + slot] *= decay_for_elapsed(cfg.fatigue_decay, e);
-    planes[3 * plane + slot] *= decay_for_elapsed(cfg.adaptation_fast_decay, e);
-    planes[4 * plane + slot] *= decay_for_elapsed(cfg.adaptation_medium_decay, e);
-    planes[5 * plane + slot] *= decay_for_elapsed(cfg.adaptation_slow_decay, e);
+// Brings one trace slot to `tick` (runtime.rs:710-766) and returns its
+// decayed branch-sensitivity plane value (the caller adds the activation).
+__device__ __forceinline__ float advance_trace(float* planes, uint64_t plane, uint32_t* last, uint32_t slot,
+                                               uint32_t tick, const LeoConfig& cfg) {
+    float bs = ld(&planes[slot]);
+    const uint32_t e = tick - ld(&last[slot]);
+    if (e == 0) return bs;
+    bs *= decay_for_elapsed(cfg.branch_decay, e);
+    planes[plane + slot] = ld(&planes[plane + slot]) * decay_for_elapsed(cfg.membrane_decay, e);
+    planes[2 * plane + slot] = ld(&planes[2 * plane + slot]) * decay_for_elapsed(cfg.fatigue_decay, e);
+    planes[3 * plane + slot] = ld(&planes[3 * plane + slot]) * decay_for_elapsed(cfg.adaptation_fast_decay, e);
+    planes[4 * plane + slot] = ld(&planes[4 * plane + slot]) * decay_for_elapsed(cfg.adaptation_medium_decay, e);
+    planes[5 * plane + slot] = ld(&planes[5 * plane + slot]) * decay_for_elapsed(cfg.adaptation_slow_decay, e);
     last[slot] = tick;
+    return bs;
 }
 
 // Late fields of a step record: work counters complete only after the step's
@@ -269,12 +304,12 @@ __device__ __forceinline__ void advance_trace(float* planes, uint64_t plane, uin
 __device__ void finalize_record(const LaneDesc& d, LaneControl* ctl, uint32_t step_index, uint32_t tick) {
     StepRecord& rec = d.records[step_index];
     const uint32_t k = tick & 1;
-    rec.events = ctl->tick_events[k];
-    rec.touched = ctl->tick_touched[k];
-    rec.scanned_rec = ctl->tick_scan_rec[k];
-    rec.scanned_in = ctl->tick_scan_in[k];
-    rec.destinations = ctl->tick_dest[k];
-    rec.active_inhibitory = ctl->tick_ainh[k];
+    rec.events = ld(&ctl->tick_events[k]);
+    rec.touched = ld(&ctl->tick_touched[k]);
+    rec.scanned_rec = ld(&ctl->tick_scan_rec[k]);
+    rec.scanned_in = ld(&ctl->tick_scan_in[k]);
+    rec.destinations = ld(&ctl->tick_dest[k]);
+    rec.active_inhibitory = ld(&ctl->tick_ainh[k]);
 }
 
 __device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t step_index) {
@@ -302,13 +337,13 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t s
     }
     // previous active set (runtime.rs:544-555)
     const uint32_t prev_slot = (tick + kRing - 1) % kRing;
-    const uint32_t prev_count = (tick > 0 && ctl->ring_tick[prev_slot] == tick - 1) ? ctl->ring_count[prev_slot] : 0;
+    const uint32_t prev_count = (tick > 0 && ld(&ctl->ring_tick[prev_slot]) == tick - 1) ? ld(&ctl->ring_count[prev_slot]) : 0;
     // delivery classes: delay 8, 4, 2, 1 in that order (chronological by emission tick)
     // (scalars, not arrays: a dynamically indexed private array lives in scratch)
     auto class_items = [&](uint32_t delay, uint32_t& rs) {
         rs = (tick + kRing - delay) % kRing;
-        const bool valid = tick >= delay && ctl->ring_tick[rs] == tick - delay;
-        return (valid ? ctl->ring_count[rs] : 0) * S;
+        const bool valid = tick >= delay && ld(&ctl->ring_tick[rs]) == tick - delay;
+        return (valid ? ld(&ctl->ring_count[rs]) : 0) * S;
     };
     uint32_t rs8, rs4, rs2, rs1;
     const uint32_t off8 = prev_count;
@@ -326,7 +361,7 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t s
         uint64_t key = 0;
         float value = 0.0f;
         if (item < prev_count) {
-            const uint32_t n = d.ring_active[static_cast<uint64_t>(prev_slot) * cap + item];
+            const uint32_t n = ld(&d.ring_active[static_cast<uint64_t>(prev_slot) * cap + item]);
             d.activation[n] = 0.0f;
             touch_n = n;
         } else if (item < off_in) {
@@ -336,18 +371,18 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t s
             const uint32_t local = item - lo;
             const uint32_t r = local / S, j = local % S;
             const uint64_t rbase = static_cast<uint64_t>(rsk) * cap + r;
-            const uint32_t src = d.ring_active[rbase];
+            const uint32_t src = ld(&d.ring_active[rbase]);
             const uint64_t slot = static_cast<uint64_t>(src) * S + j;
             if (a.m.rec_delay[slot] == (8u >> k)) {
                 delivered += 1;
-                const float act = d.ring_act[rbase];
-                value = d.ring_value[rbase * S + j];
+                const float act = ld(&d.ring_act[rbase]);
+                value = ld(&d.ring_value[rbase * S + j]);
                 target = a.m.rec_target[slot];
                 const uint8_t br = a.m.rec_branch[slot];
                 if (trace) {
-                    advance_trace(d.rec_trace, NS, d.rec_last, static_cast<uint32_t>(slot), tick, cfg);
-                    d.rec_trace[slot] += act;
-                    if (!d.rec_mark[slot]) {
+                    const float bs = advance_trace(d.rec_trace, NS, d.rec_last, static_cast<uint32_t>(slot), tick, cfg);
+                    d.rec_trace[slot] = bs + act;
+                    if (!ld(&d.rec_mark[slot])) {
                         d.rec_mark[slot] = 1;
                         new_rec = true;
                         eslot = static_cast<uint32_t>(slot);
@@ -365,11 +400,11 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t s
             const uint64_t slot = static_cast<uint64_t>(sp.symbol) * F + i;
             target = a.m.in_target[slot];
             const uint8_t br = a.m.in_branch[slot];
-            value = d.p.in_weight[slot];
+            value = ld(&d.p.in_weight[slot]);
             if (trace) {
-                advance_trace(d.in_trace, NI, d.in_last, static_cast<uint32_t>(slot), tick, cfg);
-                d.in_trace[slot] += 1.0f;
-                if (!d.in_mark[slot]) {
+                const float bs = advance_trace(d.in_trace, NI, d.in_last, static_cast<uint32_t>(slot), tick, cfg);
+                d.in_trace[slot] = bs + 1.0f;
+                if (!ld(&d.in_mark[slot])) {
                     d.in_mark[slot] = 1;
                     new_in = true;
                     eslot = static_cast<uint32_t>(slot);
@@ -412,8 +447,8 @@ __device__ void context_resolve(const StepCtx& c, const StepParams& sp, StepShar
     const bool enabled = (sp.flags & kStepContext) != 0;
     const bool allocate = (sp.flags & kStepAllocate) != 0;
     if (threadIdx.x == 0) {
-        uint32_t len = ctl->history_len;
-        for (uint32_t i = 0; i < len; ++i) sh.hist[i] = ctl->history[i];
+        uint32_t len = ld(&ctl->history_len);
+        for (uint32_t i = 0; i < len; ++i) sh.hist[i] = ld(&ctl->history[i]);
         if (len == max_order) {
             for (uint32_t i = 1; i < len; ++i) sh.hist[i - 1] = sh.hist[i];
             len -= 1;
@@ -432,17 +467,18 @@ __device__ void context_resolve(const StepCtx& c, const StepParams& sp, StepShar
         const uint64_t base = static_cast<uint64_t>(order - 1) * spo, start = key % spo;
         int64_t found = -1, empty = -1;
         uint64_t weakest = base + start;
-        uint32_t weakest_obs = 0xffffffffu, probes = 0;
+        uint32_t weakest_obs = 0xffffffffu, probes = 0, found_obs = 0;
         for (uint32_t off = 0; off < cfg.context_probe_limit; ++off) {
             const uint64_t slot = base + (start + off) % spo;
             probes += 1;
-            const uint64_t existing = d.p.ctx_keys[slot];
+            const uint64_t existing = ld(&d.p.ctx_keys[slot]);
+            const uint32_t obs = ld(&d.p.ctx_obs[slot]);
             if (existing == key) {
                 found = static_cast<int64_t>(slot);
+                found_obs = obs;
                 break;
             }
             if (existing == 0 && empty < 0) empty = static_cast<int64_t>(slot);
-            const uint32_t obs = d.p.ctx_obs[slot];
             if (obs < weakest_obs) {
                 weakest_obs = obs;
                 weakest = slot;
@@ -454,10 +490,11 @@ __device__ void context_resolve(const StepCtx& c, const StepParams& sp, StepShar
             d.p.ctx_obs[slot] = 0;
             for (uint32_t e = 0; e < E; ++e) d.p.ctx_emb[slot * E + e] = 0.0f;
             found = static_cast<int64_t>(slot);
+            found_obs = 0;
         }
         float scale = 0.0f;
         if (found >= 0) {
-            const float obs = static_cast<float>(d.p.ctx_obs[found]);
+            const float obs = static_cast<float>(found_obs);
             const float confidence = obs / (obs + static_cast<float>(cfg.context_confidence_observations));
             scale = confidence * static_cast<float>(order);
         }
@@ -469,17 +506,18 @@ __device__ void context_resolve(const StepCtx& c, const StepParams& sp, StepShar
     if (threadIdx.x == 0) {
         uint32_t count = 0, probes = 0;
         float scale_sum = 0.0f;
+        float scales[kMaxOrder];
         if (enabled) {
             for (uint32_t t = 0; t < len; ++t) {
                 probes += sh.ctx_probes[t];
                 if (sh.ctx_slot[t] < 0) continue;
                 ctl->ctx_slots[count] = static_cast<uint32_t>(sh.ctx_slot[t]);
-                ctl->ctx_scales[count] = sh.ctx_scale[t];
+                scales[count] = sh.ctx_scale[t];
                 scale_sum += sh.ctx_scale[t];
                 count += 1;
             }
-            if (scale_sum > 0.0f)
-                for (uint32_t i = 0; i < count; ++i) ctl->ctx_scales[i] = ctl->ctx_scales[i] / scale_sum;
+            for (uint32_t i = 0; i < count; ++i)
+                ctl->ctx_scales[i] = scale_sum > 0.0f ? scales[i] / scale_sum : scales[i];
         }
         ctl->ctx_applied = enabled ? 1u : 0u;
         ctl->ctx_count = count;
@@ -487,50 +525,104 @@ __device__ void context_resolve(const StepCtx& c, const StepParams& sp, StepShar
     }
 }
 
-// Fold the delivered values of neuron n in CPU delivery order after bringing
-// it to the current tick.
-__device__ __forceinline__ void fold_neuron(const StepCtx& c, uint32_t n) {
+// Sorts n <= 8 (key, value) pairs ascending by key with a fixed network
+// (entries n..7 hold ~0 keys and stay last).
+__device__ __forceinline__ void sort8(uint64_t (&k)[8], uint32_t (&v)[8]) {
+    auto cx = [&](int i, int j) {
+        if (k[j] < k[i]) {
+            const uint64_t tk = k[i];
+            k[i] = k[j];
+            k[j] = tk;
+            const uint32_t tv = v[i];
+            v[i] = v[j];
+            v[j] = tv;
+        }
+    };
+    cx(0, 2); cx(1, 3); cx(4, 6); cx(5, 7);
+    cx(0, 4); cx(1, 5); cx(2, 6); cx(3, 7);
+    cx(0, 1); cx(2, 3); cx(4, 5); cx(6, 7);
+    cx(2, 4); cx(3, 5);
+    cx(1, 4); cx(3, 6);
+    cx(1, 2); cx(3, 4); cx(5, 6);
+}
+
+// Brings touched neuron n to the current tick (runtime.rs:576-603), folds its
+// delivered values in CPU delivery order (runtime.rs:605-639, 701-708), and,
+// unless refractory, applies the drive (runtime.rs:940-975). Returns the
+// margin membrane - threshold; *refractory tells whether the neuron skipped.
+__device__ float fold_drive(const StepCtx& c, uint32_t n, float pi, bool* refractory) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = *c.d;
     const LeoConfig& cfg = a.cfg;
     const uint32_t N = cfg.neuron_count, tick = c.tick;
-    float b0 = d.branches[4 * n], b1 = d.branches[4 * n + 1], b2 = d.branches[4 * n + 2], b3 = d.branches[4 * n + 3];
-    const uint32_t e = tick - d.last_tick[n];
+    float b0 = ld(&d.branches[4 * n]), b1 = ld(&d.branches[4 * n + 1]);
+    float b2 = ld(&d.branches[4 * n + 2]), b3 = ld(&d.branches[4 * n + 3]);
+    float mem = ld(&d.membrane[n]), fat = ld(&d.fatigue[n]);
+    float ad0 = ld(&d.adapt[n]), ad1 = ld(&d.adapt[N + n]), ad2 = ld(&d.adapt[2 * N + n]);
+    const uint32_t last = ld(&d.last_tick[n]);
+    const uint32_t cnt = ld(&d.bucket_count[n]);
+    const bool refr = ld(&d.refractory_until[n]) > tick;
+    const float threshold = ld(&d.p.threshold[n]);
+    const uint32_t e = tick - last;
     if (e > 0) {
         const float bd = decay_for_elapsed(cfg.branch_decay, e);
         b0 *= bd;
         b1 *= bd;
         b2 *= bd;
         b3 *= bd;
-        d.membrane[n] *= decay_for_elapsed(cfg.membrane_decay, e);
-        d.fatigue[n] *= decay_for_elapsed(cfg.fatigue_decay, e);
-        d.adapt[n] *= decay_for_elapsed(cfg.adaptation_fast_decay, e);
-        d.adapt[N + n] *= decay_for_elapsed(cfg.adaptation_medium_decay, e);
-        d.adapt[2 * N + n] *= decay_for_elapsed(cfg.adaptation_slow_decay, e);
+        mem *= decay_for_elapsed(cfg.membrane_decay, e);
+        fat *= decay_for_elapsed(cfg.fatigue_decay, e);
+        ad0 *= decay_for_elapsed(cfg.adaptation_fast_decay, e);
+        ad1 *= decay_for_elapsed(cfg.adaptation_medium_decay, e);
+        ad2 *= decay_for_elapsed(cfg.adaptation_slow_decay, e);
+        d.fatigue[n] = fat;
+        d.adapt[n] = ad0;
+        d.adapt[N + n] = ad1;
+        d.adapt[2 * N + n] = ad2;
         d.last_tick[n] = tick;
     }
-    const uint32_t cnt = d.bucket_count[n];
     if (cnt > 0) {
         uint64_t* ent = d.bucket + 2 * a.m.bucket_offset[n];
-        for (uint32_t x = 1; x < cnt; ++x) {  // insertion sort by delivery-order key
-            const uint64_t k = ent[2 * x], v = ent[2 * x + 1];
-            uint32_t y = x;
-            while (y > 0 && ent[2 * (y - 1)] > k) {
-                ent[2 * y] = ent[2 * (y - 1)];
-                ent[2 * y + 1] = ent[2 * (y - 1) + 1];
-                --y;
-            }
-            ent[2 * y] = k;
-            ent[2 * y + 1] = v;
-        }
-        for (uint32_t x = 0; x < cnt; ++x) {
-            const float v = __uint_as_float(static_cast<uint32_t>(ent[2 * x + 1]));
-            switch (static_cast<uint32_t>(ent[2 * x]) & 3u) {
+        auto add = [&](uint64_t key, uint32_t bits) {
+            const float v = __uint_as_float(bits);
+            switch (static_cast<uint32_t>(key) & 3u) {
                 case 0: b0 += v; break;
                 case 1: b1 += v; break;
                 case 2: b2 += v; break;
                 default: b3 += v; break;
             }
+        };
+        if (cnt <= 8) {
+            uint64_t k[8];
+            uint32_t v[8];
+#pragma unroll
+            for (uint32_t x = 0; x < 8; ++x) {
+                k[x] = x < cnt ? ld(&ent[2 * x]) : ~0ULL;
+                v[x] = x < cnt ? static_cast<uint32_t>(ld(&ent[2 * x + 1])) : 0u;
+            }
+            sort8(k, v);
+#pragma unroll
+            for (uint32_t x = 0; x < 8; ++x)
+                if (x < cnt) add(k[x], v[x]);
+        } else {
+            // in-place insertion sort; every store completes before the
+            // following device-scope loads of the same entries
+            for (uint32_t x = 1; x < cnt; ++x) {
+                const uint64_t kx = ld(&ent[2 * x]), vx = ld(&ent[2 * x + 1]);
+                uint32_t y = x;
+                while (y > 0) {
+                    const uint64_t ky = ld(&ent[2 * (y - 1)]);
+                    if (ky <= kx) break;
+                    ent[2 * y] = ky;
+                    ent[2 * y + 1] = ld(&ent[2 * (y - 1) + 1]);
+                    __builtin_amdgcn_s_waitcnt(0);
+                    --y;
+                }
+                ent[2 * y] = kx;
+                ent[2 * y + 1] = vx;
+                __builtin_amdgcn_s_waitcnt(0);
+            }
+            for (uint32_t x = 0; x < cnt; ++x) add(ld(&ent[2 * x]), static_cast<uint32_t>(ld(&ent[2 * x + 1])));
         }
         d.bucket_count[n] = 0;
     }
@@ -538,18 +630,23 @@ __device__ __forceinline__ void fold_neuron(const StepCtx& c, uint32_t n) {
     d.branches[4 * n + 1] = b1;
     d.branches[4 * n + 2] = b2;
     d.branches[4 * n + 3] = b3;
+    *refractory = refr;
+    if (!refr) {
+        const float gate = clampf(b3, 0.0f, 1.0f);
+        const float net = b0 + b2 * gate + b1;
+        const float adaptation = ad0 + ad1 + ad2;
+        const float drive = a.m.excitability[n] * net - fat - adaptation - pi;
+        mem = mem + drive;
+    }
+    if (e > 0 || !refr) d.membrane[n] = mem;
+    return mem - threshold;
 }
 
-__device__ void surrogate_for(const StepCtx& c, uint32_t n, float block_cutoff, float pop_cutoff, bool selected) {
-    const LeoConfig& cfg = c.a->cfg;
-    const LaneDesc& d = *c.d;
-    if (d.refractory_until[n] > c.tick) {
-        d.surrogate[n] = 0.0f;
-        return;
-    }
-    const float margin = d.membrane[n] - d.p.threshold[n];
-    const float cutoff = maxnum(block_cutoff, pop_cutoff);
-    d.surrogate[n] = analog_rank_surrogate(margin, cutoff, selected, cfg.surrogate_width, cfg.surrogate_gain);
+// analog_rank_surrogate of a touched neuron (runtime.rs:787-803).
+__device__ __forceinline__ float surrogate_value(const LeoConfig& cfg, bool refractory, float margin, float cutoff,
+                                                 bool selected) {
+    if (refractory) return 0.0f;
+    return analog_rank_surrogate(margin, cutoff, selected, cfg.surrogate_width, cfg.surrogate_gain);
 }
 
 // One wave: fold, drive and top-k of block b (runtime.rs:940-1011). The
@@ -559,8 +656,9 @@ __device__ void surrogate_for(const StepCtx& c, uint32_t n, float block_cutoff, 
 // (activation desc, tie asc) keys, i.e. its position in the reference's
 // sorted order (keys are unique).
 constexpr uint32_t kMaxChunksPerBlock = kMaxBlockNeurons / kWaveSize;
+constexpr uint32_t kRefractoryBit = 0x80000000u;
 
-__device__ uint32_t select_block(const StepCtx& c, uint32_t b, float pi, uint64_t* cand, uint32_t* tl) {
+__device__ uint32_t select_block(const StepCtx& c, uint32_t b, float pi, uint64_t* cand, uint32_t* tl, float* tmar) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = *c.d;
     const LeoConfig& cfg = a.cfg;
@@ -574,7 +672,7 @@ __device__ uint32_t select_block(const StepCtx& c, uint32_t b, float pi, uint64_
 #pragma unroll
     for (uint32_t k = 0; k < kMaxChunksPerBlock; ++k) {
         const uint32_t idx = k * kWaveSize + lane;
-        if (k < chunks && idx < nb && d.touched_epoch[first + idx] == tick + 1) tmask |= 1u << k;
+        if (k < chunks && idx < nb && ld(&d.touched_epoch[first + idx]) == tick + 1) tmask |= 1u << k;
     }
     uint32_t touched = 0;
     for (uint32_t k = 0; k < chunks; ++k) {
@@ -591,20 +689,14 @@ __device__ uint32_t select_block(const StepCtx& c, uint32_t b, float pi, uint64_
         uint64_t key = 0;
         if (i < touched) {
             const uint32_t n = tl[i];
-            fold_neuron(c, n);
-            if (!(d.refractory_until[n] > tick)) {
-                const float gate = clampf(d.branches[4 * n + BR_GATE], 0.0f, 1.0f);
-                const float inhibitory = d.branches[4 * n + BR_INH];
-                const float net = d.branches[4 * n + BR_EXC] + d.branches[4 * n + BR_TEMP] * gate + inhibitory;
-                const float adaptation = d.adapt[n] + d.adapt[N + n] + d.adapt[2 * N + n];
-                const float drive = a.m.excitability[n] * net - d.fatigue[n] - adaptation - pi;
-                const float m = d.membrane[n] + drive;
-                d.membrane[n] = m;
-                const float act = clampf(m - d.p.threshold[n], 0.0f, 1.0f);
-                if (act > 0.0f) {
-                    candidate = true;
-                    key = selection_key(act, (n + N - rot) % N);
-                }
+            bool refractory = false;
+            const float margin = fold_drive(c, n, pi, &refractory);
+            tmar[i] = margin;
+            if (refractory) tl[i] = n | kRefractoryBit;
+            const float act = clampf(margin, 0.0f, 1.0f);
+            if (!refractory && act > 0.0f) {
+                candidate = true;
+                key = selection_key(act, (n + N - rot) % N);
             }
         }
         const unsigned long long mask = __ballot(candidate);
@@ -635,17 +727,20 @@ __device__ uint32_t select_block(const StepCtx& c, uint32_t b, float pi, uint64_
         // winners and surrogates of the touched (runtime.rs:1060-1067, 787-803);
         // a candidate wins iff its key is below the rank-`limit` key
         for (uint32_t i = lane; i < touched; i += kWaveSize) {
-            const uint32_t n = tl[i];
+            const uint32_t entry = tl[i];
+            const uint32_t n = entry & ~kRefractoryBit;
+            const bool refractory = (entry & kRefractoryBit) != 0;
+            const float margin = tmar[i];
             bool won = false;
-            if (!(d.refractory_until[n] > tick)) {
-                const float act = clampf(d.membrane[n] - d.p.threshold[n], 0.0f, 1.0f);
+            if (!refractory) {
+                const float act = clampf(margin, 0.0f, 1.0f);
                 won = act > 0.0f && selection_key(act, (n + N - rot) % N) < cut_key;
                 if (won) {
                     d.activation[n] = act;
                     d.selected_epoch[n] = tick + 1;
                 }
             }
-            surrogate_for(c, n, cutoff, 0.0f, won);
+            d.surrogate[n] = surrogate_value(cfg, refractory, margin, cutoff, won);
         }
     }
     wave_sync();
@@ -660,12 +755,13 @@ __device__ void phase_fold_select(const StepCtx& c, const StepParams& sp, StepSh
     const uint32_t wv = c.part * kWavesPerGroup + wave;
     const uint32_t per = (cfg.block_count + nwaves - 1) / nwaves;
     const uint32_t b0 = wv * per, b1 = min(cfg.block_count, b0 + per);
-    const float pi = c.ctl->population_inhibition;
+    const float pi = ld(&c.ctl->population_inhibition);
     uint32_t total = 0;
     const uint32_t nb = cfg.neurons_per_block;
     uint64_t* cand = reinterpret_cast<uint64_t*>(step_lds) + static_cast<size_t>(wave) * nb;
     uint32_t* tl = reinterpret_cast<uint32_t*>(step_lds + static_cast<size_t>(kWavesPerGroup) * nb * 8) + wave * nb;
-    for (uint32_t b = b0; b < b1; ++b) total += select_block(c, b, pi, cand, tl);
+    float* tmar = reinterpret_cast<float*>(step_lds + static_cast<size_t>(kWavesPerGroup) * nb * 12) + wave * nb;
+    for (uint32_t b = b0; b < b1; ++b) total += select_block(c, b, pi, cand, tl, tmar);
     if (lane == 0) c.d->wave_total[wv] = total;
 }
 
@@ -687,7 +783,7 @@ __device__ void write_active(const StepCtx& c) {
     uint32_t before = 0, all = 0;
     for (uint32_t base = 0; base < nwaves; base += kWaveSize) {
         const uint32_t w = base + lane;
-        const uint32_t v = w < nwaves ? d.wave_total[w] : 0;
+        const uint32_t v = w < nwaves ? ld(&d.wave_total[w]) : 0;
         before += wave_sum_u32(w < wv ? v : 0);
         all += wave_sum_u32(v);
     }
@@ -696,11 +792,11 @@ __device__ void write_active(const StepCtx& c) {
     float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
     uint32_t offset = before;
     for (uint32_t b = b0; b < b1; ++b) {
-        const uint32_t v = d.block_count[b];
+        const uint32_t v = ld(&d.block_count[b]);
         for (uint32_t i = lane; i < v; i += kWaveSize) {
-            const uint32_t n = d.block_winners[static_cast<uint64_t>(b) * limit + i];
+            const uint32_t n = ld(&d.block_winners[static_cast<uint64_t>(b) * limit + i]);
             act_list[offset + i] = n;
-            act_val[offset + i] = d.activation[n];
+            act_val[offset + i] = ld(&d.activation[n]);
         }
         offset += v;
     }
@@ -714,7 +810,7 @@ __device__ void write_active(const StepCtx& c) {
         ctl->ring_count[rs] = all;
         const float activity = static_cast<float>(all) / static_cast<float>(cfg.neuron_count);
         ctl->population_inhibition = clampf(
-            ctl->population_inhibition + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
+            ld(&ctl->population_inhibition) + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
             cfg.population_inhibition_max);
     }
 }
@@ -732,7 +828,7 @@ __device__ void global_select(const StepCtx& c, StepShared& sh) {
     uint32_t running = 0;
     for (uint32_t base = 0; base < cfg.block_count; base += kThreads) {
         const uint32_t b = base + threadIdx.x;
-        const uint32_t v = b < cfg.block_count ? d.block_count[b] : 0;
+        const uint32_t v = b < cfg.block_count ? ld(&d.block_count[b]) : 0;
         sh.scan[threadIdx.x] = v;
         __syncthreads();
         for (uint32_t off = 1; off < kThreads; off <<= 1) {
@@ -743,9 +839,9 @@ __device__ void global_select(const StepCtx& c, StepShared& sh) {
         }
         const uint32_t start = running + sh.scan[threadIdx.x] - v;
         for (uint32_t i = 0; i < v; ++i) {
-            const uint32_t n = d.block_winners[static_cast<uint64_t>(b) * limit + i];
+            const uint32_t n = ld(&d.block_winners[static_cast<uint64_t>(b) * limit + i]);
             if (start + i < kMaxBlockNeurons) {
-                const float act = clampf(d.membrane[n] - d.p.threshold[n], 0.0f, 1.0f);
+                const float act = clampf(ld(&d.membrane[n]) - ld(&d.p.threshold[n]), 0.0f, 1.0f);
                 keys[start + i] = selection_key(act, (n + N - rot) % N);
             }
         }
@@ -788,7 +884,7 @@ __device__ void global_select(const StepCtx& c, StepShared& sh) {
         ctl->ring_count[rs] = active;
         const float activity = static_cast<float>(active) / static_cast<float>(N);
         ctl->population_inhibition = clampf(
-            ctl->population_inhibition + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
+            ld(&ctl->population_inhibition) + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
             cfg.population_inhibition_max);
     }
 }
@@ -798,10 +894,10 @@ __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uin
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = *c.d;
     const uint32_t tick = c.tick;
-    float bs = planes[slot], ms = planes[plane + slot], fs = planes[2 * plane + slot];
-    float as0 = planes[3 * plane + slot], as1 = planes[4 * plane + slot], as2 = planes[5 * plane + slot];
-    const float e = planes[6 * plane + slot];
-    const uint32_t el = tick - last[slot];
+    float bs = ld(&planes[slot]), ms = ld(&planes[plane + slot]), fs = ld(&planes[2 * plane + slot]);
+    float as0 = ld(&planes[3 * plane + slot]), as1 = ld(&planes[4 * plane + slot]), as2 = ld(&planes[5 * plane + slot]);
+    const float e = ld(&planes[6 * plane + slot]);
+    const uint32_t el = tick - ld(&last[slot]);
     if (el > 0) {
         bs *= decay_for_elapsed(cfg.branch_decay, el);
         ms *= decay_for_elapsed(cfg.membrane_decay, el);
@@ -811,19 +907,19 @@ __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uin
         as2 *= decay_for_elapsed(cfg.adaptation_slow_decay, el);
         last[slot] = tick;
     }
-    const bool touched = d.touched_epoch[dst] == tick + 1;
+    const bool touched = ld(&d.touched_epoch[dst]) == tick + 1;
     float elig;
-    if (!touched || d.refractory_until[dst] > tick) {
+    if (!touched || ld(&d.refractory_until[dst]) > tick) {
         elig = e * cfg.eligibility_decay;
     } else {
-        const float jac = branch_jacobian(br, c.a->m.excitability[dst], d.branches[4 * dst + BR_TEMP],
-                                          d.branches[4 * dst + BR_GATE]);
-        const float sur = d.surrogate[dst];
+        const float jac = branch_jacobian(br, c.a->m.excitability[dst], ld(&d.branches[4 * dst + BR_TEMP]),
+                                          ld(&d.branches[4 * dst + BR_GATE]));
+        const float sur = ld(&d.surrogate[dst]);
         const float asum = as0 + as1 + as2;
         ms = ms + jac * bs - fs - asum;
         elig = sur * ms;
     }
-    if (touched && d.selected_epoch[dst] == tick + 1) {
+    if (touched && ld(&d.selected_epoch[dst]) == tick + 1) {
         fs += cfg.fatigue_gain * elig;
         as0 += cfg.adaptation_fast_gain * elig;
         as1 += cfg.adaptation_medium_gain * elig;
@@ -854,7 +950,7 @@ __device__ void eligibility_list(const StepCtx& c, float* planes, uint64_t plane
         bool keep = false;
         uint32_t slot = 0;
         if (i < cur_n) {
-            slot = cur[i];
+            slot = ld(&cur[i]);
             keep = update_slot(c, planes, plane, last, slot, targets[slot], branches[slot]);
             if (!keep) marks[slot] = 0;
         }
@@ -870,7 +966,7 @@ __device__ void phase_eligibility(const StepCtx& c) {
     const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * cfg.synapses_per_neuron;
     const uint64_t NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
     const uint32_t p = c.parity, q = c.parity ^ 1;
-    const uint32_t rec_n = c.ctl->rec_count[p], in_n = c.ctl->in_count[p];
+    const uint32_t rec_n = ld(&c.ctl->rec_count[p]), in_n = ld(&c.ctl->in_count[p]);
     if (c.part == 0 && threadIdx.x == 0) {
         c.ctl->tick_scan_rec[c.tick & 1] = rec_n;
         c.ctl->tick_scan_in[c.tick & 1] = in_n;
@@ -893,19 +989,19 @@ __device__ void readout(const StepCtx& c, const StepParams& sp, StepShared& sh, 
     LaneControl* ctl = c.ctl;
     const uint32_t cap = cfg.max_active_global, E = cfg.context_embedding_dim;
     const uint32_t rs = c.tick % kRing;
-    const uint32_t A = ctl->active_count;
+    const uint32_t A = ld(&ctl->active_count);
     const uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
     const float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
-    const uint32_t ctx_count = ctl->ctx_count;
+    const uint32_t ctx_count = ld(&ctl->ctx_count);
     const uint32_t wave = threadIdx.x / kWaveSize, lane = __lane_id();
     float* lat = sh.aux;
     // context latent (runtime.rs:1120-1136): serial over active slots per dimension
     for (uint32_t e = threadIdx.x; e < E; e += kThreads) {
         float v = 0.0f;
         for (uint32_t i = 0; i < ctx_count; ++i) {
-            const float scale = ctl->ctx_scales[i];
+            const float scale = ld(&ctl->ctx_scales[i]);
             if (scale <= 0.0f) continue;
-            v += d.p.ctx_emb[static_cast<uint64_t>(ctl->ctx_slots[i]) * E + e] * scale;
+            v += ld(&d.p.ctx_emb[static_cast<uint64_t>(ld(&ctl->ctx_slots[i])) * E + e]) * scale;
         }
         lat[e] = v;
         d.ctx_latent[e] = v;
@@ -916,19 +1012,20 @@ __device__ void readout(const StepCtx& c, const StepParams& sp, StepShared& sh, 
     // issued ahead of their serial adds
     const uint32_t o1 = threadIdx.x, o2 = threadIdx.x + kThreads;
     const bool has2 = o2 < kOutputs;
-    float l1 = d.p.bias[o1], l2 = has2 ? d.p.bias[o2] : 0.0f;
+    float l1 = ld(&d.p.bias[o1]), l2 = has2 ? ld(&d.p.bias[o2]) : 0.0f;
     uint32_t r = 0;
     for (; r + 4 <= A; r += 4) {
-        const uint64_t n0 = act_list[r], n1 = act_list[r + 1], n2 = act_list[r + 2], n3 = act_list[r + 3];
-        const float a0 = act_val[r], a1 = act_val[r + 1], a2 = act_val[r + 2], a3 = act_val[r + 3];
-        const float w10 = d.p.out_w[n0 * kOutStride + o1], w11 = d.p.out_w[n1 * kOutStride + o1];
-        const float w12 = d.p.out_w[n2 * kOutStride + o1], w13 = d.p.out_w[n3 * kOutStride + o1];
+        const uint64_t n0 = ld(&act_list[r]), n1 = ld(&act_list[r + 1]), n2 = ld(&act_list[r + 2]),
+                       n3 = ld(&act_list[r + 3]);
+        const float a0 = ld(&act_val[r]), a1 = ld(&act_val[r + 1]), a2 = ld(&act_val[r + 2]), a3 = ld(&act_val[r + 3]);
+        const float w10 = ld(&d.p.out_w[n0 * kOutStride + o1]), w11 = ld(&d.p.out_w[n1 * kOutStride + o1]);
+        const float w12 = ld(&d.p.out_w[n2 * kOutStride + o1]), w13 = ld(&d.p.out_w[n3 * kOutStride + o1]);
         float w20 = 0.0f, w21 = 0.0f, w22 = 0.0f, w23 = 0.0f;
         if (has2) {
-            w20 = d.p.out_w[n0 * kOutStride + o2];
-            w21 = d.p.out_w[n1 * kOutStride + o2];
-            w22 = d.p.out_w[n2 * kOutStride + o2];
-            w23 = d.p.out_w[n3 * kOutStride + o2];
+            w20 = ld(&d.p.out_w[n0 * kOutStride + o2]);
+            w21 = ld(&d.p.out_w[n1 * kOutStride + o2]);
+            w22 = ld(&d.p.out_w[n2 * kOutStride + o2]);
+            w23 = ld(&d.p.out_w[n3 * kOutStride + o2]);
         }
         l1 += w10 * a0;
         l1 += w11 * a1;
@@ -940,16 +1037,16 @@ __device__ void readout(const StepCtx& c, const StepParams& sp, StepShared& sh, 
         l2 += w23 * a3;
     }
     for (; r < A; ++r) {
-        const uint64_t n = act_list[r];
-        const float av = act_val[r];
-        l1 += d.p.out_w[n * kOutStride + o1] * av;
-        if (has2) l2 += d.p.out_w[n * kOutStride + o2] * av;
+        const uint64_t n = ld(&act_list[r]);
+        const float av = ld(&act_val[r]);
+        l1 += ld(&d.p.out_w[n * kOutStride + o1]) * av;
+        if (has2) l2 += ld(&d.p.out_w[n * kOutStride + o2]) * av;
     }
     if (ctx_count > 0) {
         float c1 = 0.0f, c2 = 0.0f;
         for (uint32_t e = 0; e < E; ++e) {
-            c1 += d.p.ctx_out[o1 * E + e] * lat[e];
-            if (has2) c2 += d.p.ctx_out[o2 * E + e] * lat[e];
+            c1 += ld(&d.p.ctx_out[o1 * E + e]) * lat[e];
+            if (has2) c2 += ld(&d.p.ctx_out[o2 * E + e]) * lat[e];
         }
         l1 += c1;
         l2 += c2;
@@ -1016,7 +1113,7 @@ __device__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step
     const LeoConfig& cfg = a.cfg;
     const uint32_t S = cfg.synapses_per_neuron, cap = cfg.max_active_global;
     const uint32_t rs = c.tick % kRing;
-    const uint32_t A = c.ctl->active_count;
+    const uint32_t A = ld(&c.ctl->active_count);
     const uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
     const float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
     const uint32_t total = A + A * S;
@@ -1025,20 +1122,20 @@ __device__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step
     uint32_t inhibitory = 0;
     for (uint32_t item = c.gtid; item < total; item += c.gstride) {
         if (item < A) {
-            const uint32_t n = act_list[item];
-            const float act = d.activation[n];
+            const uint32_t n = ld(&act_list[item]);
+            const float act = ld(&d.activation[n]);
             inhibitory += a.m.neuron_type[n] != 0 ? 1u : 0u;
-            d.fatigue[n] += cfg.fatigue_gain * act;
-            d.adapt[n] += cfg.adaptation_fast_gain * act;
-            d.adapt[N + n] += cfg.adaptation_medium_gain * act;
-            d.adapt[2 * N + n] += cfg.adaptation_slow_gain * act;
-            d.membrane[n] -= d.p.threshold[n] * cfg.membrane_reset_fraction;
+            d.fatigue[n] = ld(&d.fatigue[n]) + cfg.fatigue_gain * act;
+            d.adapt[n] = ld(&d.adapt[n]) + cfg.adaptation_fast_gain * act;
+            d.adapt[N + n] = ld(&d.adapt[N + n]) + cfg.adaptation_medium_gain * act;
+            d.adapt[2 * N + n] = ld(&d.adapt[2 * N + n]) + cfg.adaptation_slow_gain * act;
+            d.membrane[n] = ld(&d.membrane[n]) - ld(&d.p.threshold[n]) * cfg.membrane_reset_fraction;
             d.refractory_until[n] = refractory;
         } else {
             const uint32_t local = item - A;
             const uint32_t r = local / S, j = local % S;
             const uint64_t rb = static_cast<uint64_t>(rs) * cap + r;
-            d.ring_value[rb * S + j] = act_val[r] * d.p.rec_weight[static_cast<uint64_t>(act_list[r]) * S + j];
+            d.ring_value[rb * S + j] = ld(&act_val[r]) * ld(&d.p.rec_weight[static_cast<uint64_t>(ld(&act_list[r])) * S + j]);
         }
     }
     add_count(&c.ctl->tick_ainh[c.tick & 1], inhibitory);
@@ -1049,16 +1146,16 @@ __device__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step
             LaneControl* ctl = c.ctl;
             rec.p_target = 0.0f;
             rec.predicted = 0;
-            rec.population_inhibition = ctl->population_inhibition;
+            rec.population_inhibition = ld(&ctl->population_inhibition);
             rec.active = A;
-            rec.suprathreshold = ctl->tick_supra[c.tick & 1];
-            rec.block_selected = ctl->block_selected;
-            rec.clipped = ctl->clipped;
-            rec.context_cells = ctl->ctx_count;
-            rec.context_probes = ctl->ctx_probes;
-            rec.context_applied = ctl->ctx_applied;
-            rec.eligible_rec = ctl->rec_count[c.parity];
-            rec.eligible_in = ctl->in_count[c.parity];
+            rec.suprathreshold = ld(&ctl->tick_supra[c.tick & 1]);
+            rec.block_selected = ld(&ctl->block_selected);
+            rec.clipped = ld(&ctl->clipped);
+            rec.context_cells = ld(&ctl->ctx_count);
+            rec.context_probes = ld(&ctl->ctx_probes);
+            rec.context_applied = ld(&ctl->ctx_applied);
+            rec.eligible_rec = ld(&ctl->rec_count[c.parity]);
+            rec.eligible_in = ld(&ctl->in_count[c.parity]);
             rec.error_code = 0;
         }
         if (sp.flags & kStepOutput) {
@@ -1073,15 +1170,28 @@ __device__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step
 // claims destinations, compacts them, and computes their serial 257-term dot
 // products from row tiles staged through LDS (coalesced row loads).
 // ---------------------------------------------------------------------------
+// Device-scope 16-byte loads through a buffer resource (cache policy sc1: the
+// load misses the CU's L1 like ld()); the resource is wave-uniform and covers
+// `bytes` from `base` (loads beyond it return 0).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ f32x4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 16));
+}
+__device__ __forceinline__ float ld4(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, 0, 16));
+}
+
 // Serial 257-term dot of one output row with the errors, in output order
 // (runtime.rs:1245-1250); eight 16-byte row loads are in flight at a time.
-__device__ __forceinline__ float signal_dot(const float* __restrict__ row, const float* err) {
-    const float4* row4 = reinterpret_cast<const float4*>(row);
+__device__ __forceinline__ float signal_dot(__amdgpu_buffer_rsrc_t rows, uint32_t row_offset, const float* err) {
     float acc = 0.0f;
     for (uint32_t q = 0; q < kEndIndex / 4; q += 8) {
-        float4 v[8];
+        f32x4 v[8];
 #pragma unroll
-        for (uint32_t u = 0; u < 8; ++u) v[u] = row4[q + u];
+        for (uint32_t u = 0; u < 8; ++u) v[u] = ld16(rows, row_offset + 16 * (q + u));
 #pragma unroll
         for (uint32_t u = 0; u < 8; ++u) {
             const float* e = err + 4 * (q + u);
@@ -1091,7 +1201,7 @@ __device__ __forceinline__ float signal_dot(const float* __restrict__ row, const
             acc += v[u].w * e[3];
         }
     }
-    acc += row[kEndIndex] * err[kEndIndex];
+    acc += ld4(rows, row_offset + 4 * kEndIndex) * err[kEndIndex];
     return acc;
 }
 
@@ -1101,10 +1211,10 @@ __device__ void phase_signals(const StepCtx& c, StepShared& sh) {
     const LeoConfig& cfg = a.cfg;
     const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * cfg.synapses_per_neuron;
     const uint64_t NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
-    for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = d.errors[o];
+    for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = ld(&d.errors[o]);
     __syncthreads();
-    const uint32_t rec_n = c.ctl->rec_count[c.parity], in_n = c.ctl->in_count[c.parity];
-    const uint32_t A = c.ctl->active_count;
+    const uint32_t rec_n = ld(&c.ctl->rec_count[c.parity]), in_n = ld(&c.ctl->in_count[c.parity]);
+    const uint32_t A = ld(&c.ctl->active_count);
     const uint32_t rs = c.tick % kRing;
     const uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cfg.max_active_global;
     const uint32_t* rec_cur = d.rec_list + c.parity * NS;
@@ -1114,15 +1224,17 @@ __device__ void phase_signals(const StepCtx& c, StepShared& sh) {
     const unsigned long long below = (1ULL << lane) - 1ULL;
     uint32_t* queue = sh.queue[wave];
     uint32_t queued = 0, claimed = 0;
+    // the host limits N * kOutStride * 4 to below 2^31 bytes
+    const __amdgpu_buffer_rsrc_t rows = coherent_rsrc(d.p.out_w, cfg.neuron_count * kOutStride * 4);
     // claimed destinations are queued per wave and computed 64 at a time, one row per lane
     for (uint32_t base = c.gtid - lane; base < total; base += c.gstride) {
         const uint32_t item = base + lane;
         bool won = false;
         uint32_t dst = 0;
         if (item < total) {
-            if (item < rec_n) dst = a.m.rec_target[rec_cur[item]];
-            else if (item < rec_n + in_n) dst = a.m.in_target[in_cur[item - rec_n]];
-            else dst = act_list[item - rec_n - in_n];
+            if (item < rec_n) dst = a.m.rec_target[ld(&rec_cur[item])];
+            else if (item < rec_n + in_n) dst = a.m.in_target[ld(&in_cur[item - rec_n])];
+            else dst = ld(&act_list[item - rec_n - in_n]);
             won = atomicExch(&d.dest_epoch[dst], c.dest_epoch) != c.dest_epoch;
         }
         const unsigned long long mask = __ballot(won);
@@ -1136,13 +1248,13 @@ __device__ void phase_signals(const StepCtx& c, StepShared& sh) {
             wave_sync();
             if (lane + kWaveSize < queued) queue[lane] = rest;
             queued -= kWaveSize;
-            d.learning_signal[mine] = signal_dot(d.p.out_w + static_cast<uint64_t>(mine) * kOutStride, sh.err);
+            d.learning_signal[mine] = signal_dot(rows, mine * kOutStride * 4, sh.err);
         }
     }
     wave_sync();
     if (lane < queued) {
         const uint32_t mine = queue[lane];
-        d.learning_signal[mine] = signal_dot(d.p.out_w + static_cast<uint64_t>(mine) * kOutStride, sh.err);
+        d.learning_signal[mine] = signal_dot(rows, mine * kOutStride * 4, sh.err);
     }
     add_count(&c.ctl->tick_dest[c.tick & 1], claimed);
 }
@@ -1163,38 +1275,38 @@ __device__ void context_update(const StepCtx& c, const StepParams& sp, StepShare
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = *c.d;
     LaneControl* ctl = c.ctl;
-    const uint32_t E = cfg.context_embedding_dim, count = ctl->ctx_count;
+    const uint32_t E = cfg.context_embedding_dim, count = ld(&ctl->ctx_count);
     const float lr = cfg.context_learning_rate, mu = cfg.max_update, wmin = cfg.weight_min, wmax = cfg.weight_max;
     const float strength = sp.supervised_strength;
     float* grad = sh.aux;
     for (uint32_t e = threadIdx.x; e < E; e += kThreads) {
         float g = 0.0f;
-        for (uint32_t o = 0; o < kOutputs; ++o) g += d.p.ctx_out[o * E + e] * sh.err[o];
+        for (uint32_t o = 0; o < kOutputs; ++o) g += ld(&d.p.ctx_out[o * E + e]) * sh.err[o];
         grad[e] = g;
     }
     __syncthreads();
     if (threadIdx.x == 0) ctl->ctx_out_dirty = 1;
     for (uint32_t i = threadIdx.x; i < kOutputs * E; i += kThreads) {
         const uint32_t o = i / E, e = i % E;
-        const float gradient = sh.err[o] * d.ctx_latent[e];
+        const float gradient = sh.err[o] * ld(&d.ctx_latent[e]);
         const float delta = bounded(-lr * strength * gradient, mu);
-        const float updated = clampf(d.p.ctx_out[i] + delta, wmin, wmax);
+        const float updated = clampf(ld(&d.p.ctx_out[i]) + delta, wmin, wmax);
         if (!finitef(updated)) set_error(ctl, kErrContextProjection);
         d.p.ctx_out[i] = updated;
     }
     for (uint32_t i = threadIdx.x; i < count * E; i += kThreads) {
         const uint32_t k = i / E, e = i % E;
-        const uint64_t slot = ctl->ctx_slots[k];
-        const float gradient = ctl->ctx_scales[k] * grad[e];
+        const uint64_t slot = ld(&ctl->ctx_slots[k]);
+        const float gradient = ld(&ctl->ctx_scales[k]) * grad[e];
         const float delta = bounded(-lr * strength * gradient, mu);
-        const float updated = clampf(d.p.ctx_emb[slot * E + e] + delta, wmin, wmax);
+        const float updated = clampf(ld(&d.p.ctx_emb[slot * E + e]) + delta, wmin, wmax);
         if (!finitef(updated)) set_error(ctl, kErrContextEmbedding);
         d.p.ctx_emb[slot * E + e] = updated;
     }
     for (uint32_t k = threadIdx.x; k < count; k += kThreads) {
-        const uint32_t slot = ctl->ctx_slots[k];
+        const uint32_t slot = ld(&ctl->ctx_slots[k]);
         mark_bit(d.ch_ctx, slot);
-        const uint32_t obs = d.p.ctx_obs[slot];
+        const uint32_t obs = ld(&d.p.ctx_obs[slot]);
         d.p.ctx_obs[slot] = obs == 0xffffffffu ? obs : obs + 1;
     }
     __syncthreads();
@@ -1211,13 +1323,13 @@ __device__ void phase_learn(const StepCtx& c, const StepParams& sp, StepShared& 
     const uint32_t tick = c.tick;
     const bool learn = (sp.flags & kStepLearn) != 0;
     const bool plastic = learn && sp.plasticity_scale > 0.0f;
-    const uint32_t A = ctl->active_count;
+    const uint32_t A = ld(&ctl->active_count);
     const uint32_t rs = tick % kRing;
     const uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
     const float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
     const float mu = cfg.max_update, wmin = cfg.weight_min, wmax = cfg.weight_max;
     if (learn) {
-        for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = d.errors[o];
+        for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = ld(&d.errors[o]);
         __syncthreads();
         const float ss = sp.supervised_strength;
         const float olr = cfg.output_learning_rate;
@@ -1225,45 +1337,45 @@ __device__ void phase_learn(const StepCtx& c, const StepParams& sp, StepShared& 
         const uint32_t out_items = A * kOutputs;
         for (uint32_t item = c.gtid; item < out_items; item += c.gstride) {
             const uint32_t r = item / kOutputs, o = item % kOutputs;
-            const uint32_t n = act_list[r];
-            const float act = act_val[r];
+            const uint32_t n = ld(&act_list[r]);
+            const float act = ld(&act_val[r]);
             if (o == 0) mark_bit(d.ch_out, n);
             const float raw = -olr * ss * sh.err[o] * act;
             float* w = d.p.out_w + static_cast<uint64_t>(n) * kOutStride + o;
-            *w = clampf(*w + bounded(raw, mu), wmin, wmax);
+            *w = clampf(ld(w) + bounded(raw, mu), wmin, wmax);
         }
         // bias and context projection on the readout workgroup
         if (c.part == c.P - 1) {
             for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) {
                 const float raw = -olr * ss * sh.err[o];
-                const float b = d.p.bias[o] + bounded(raw, mu);
+                const float b = ld(&d.p.bias[o]) + bounded(raw, mu);
                 if (!finitef(b)) set_error(ctl, kErrBias);
                 d.p.bias[o] = b;
             }
             if (threadIdx.x == 0) ctl->bias_dirty = 1;
-            if (ctl->ctx_applied && ctl->ctx_count > 0) context_update(c, sp, sh);
+            if (ld(&ctl->ctx_applied) && ld(&ctl->ctx_count) > 0) context_update(c, sp, sh);
         }
         if (plastic) {
             const float cs = ss * sp.plasticity_scale;
             const float lr = cfg.recurrent_learning_rate;
-            const uint32_t rec_n = ctl->rec_count[c.parity];
+            const uint32_t rec_n = ld(&ctl->rec_count[c.parity]);
             const uint32_t* rec_cur = d.rec_list + c.parity * NS;
             for (uint32_t i = c.gtid; i < rec_n; i += c.gstride) {
-                const uint32_t slot = rec_cur[i];
+                const uint32_t slot = ld(&rec_cur[i]);
                 const uint32_t dst = a.m.rec_target[slot];
                 const uint32_t src = slot / S;
-                const float e = d.rec_trace[6 * NS + slot];
-                const float gradient = d.learning_signal[dst] * e;
+                const float e = ld(&d.rec_trace[6 * NS + slot]);
+                const float gradient = ld(&d.learning_signal[dst]) * e;
                 const float delta = bounded(-lr * cs * gradient, mu);
-                const float old_w = d.p.rec_weight[slot];
+                const float old_w = ld(&d.p.rec_weight[slot]);
                 float nw = clampf(old_w + delta, wmin, wmax);
                 const bool excitatory = a.m.neuron_type[src] == 0;
                 nw = excitatory ? maxnum(nw, 0.0f) : fminf(nw, 0.0f);
                 if (!finitef(nw)) set_error(ctl, kErrRecurrent);
                 bool changed = nw != old_w;
-                if (!excitatory && d.selected_epoch[src] == tick + 1) {
-                    const float tgt_act = d.activation[dst] > 0.0f ? 1.0f : 0.0f;
-                    const float nw2 = inhibitory_step(cfg, nw, d.activation[src], tgt_act, sp.strength);
+                if (!excitatory && ld(&d.selected_epoch[src]) == tick + 1) {
+                    const float tgt_act = ld(&d.activation[dst]) > 0.0f ? 1.0f : 0.0f;
+                    const float nw2 = inhibitory_step(cfg, nw, ld(&d.activation[src]), tgt_act, sp.strength);
                     if (!finitef(nw2)) set_error(ctl, kErrInhibitory);
                     changed = changed || nw2 != nw;
                     nw = nw2;
@@ -1271,15 +1383,15 @@ __device__ void phase_learn(const StepCtx& c, const StepParams& sp, StepShared& 
                 if (changed) mark_bit(d.ch_rec, slot);
                 d.p.rec_weight[slot] = nw;
             }
-            const uint32_t in_n = ctl->in_count[c.parity];
+            const uint32_t in_n = ld(&ctl->in_count[c.parity]);
             const uint32_t* in_cur = d.in_list + c.parity * NI;
             for (uint32_t i = c.gtid; i < in_n; i += c.gstride) {
-                const uint32_t slot = in_cur[i];
+                const uint32_t slot = ld(&in_cur[i]);
                 const uint32_t dst = a.m.in_target[slot];
-                const float e = d.in_trace[6 * NI + slot];
-                const float gradient = d.learning_signal[dst] * e;
+                const float e = ld(&d.in_trace[6 * NI + slot]);
+                const float gradient = ld(&d.learning_signal[dst]) * e;
                 const float delta = bounded(-lr * cs * gradient, mu);
-                const float old_w = d.p.in_weight[slot];
+                const float old_w = ld(&d.p.in_weight[slot]);
                 const float nw = clampf(old_w + delta, 0.0f, wmax);
                 if (!finitef(nw)) set_error(ctl, kErrInput);
                 if (nw != old_w) mark_bit(d.ch_in, slot);
@@ -1291,14 +1403,14 @@ __device__ void phase_learn(const StepCtx& c, const StepParams& sp, StepShared& 
         const uint32_t inh_items = A * S;
         for (uint32_t item = c.gtid; item < inh_items; item += c.gstride) {
             const uint32_t r = item / S, j = item % S;
-            const uint32_t src = act_list[r];
+            const uint32_t src = ld(&act_list[r]);
             if (a.m.neuron_type[src] == 0) continue;
             const uint64_t slot = static_cast<uint64_t>(src) * S + j;
-            if (plastic && d.rec_mark[slot]) continue;
+            if (plastic && ld(&d.rec_mark[slot])) continue;
             const uint32_t dst = a.m.rec_target[slot];
-            const float tgt_act = d.activation[dst] > 0.0f ? 1.0f : 0.0f;
-            const float old_w = d.p.rec_weight[slot];
-            const float nw = inhibitory_step(cfg, old_w, d.activation[src], tgt_act, sp.strength);
+            const float tgt_act = ld(&d.activation[dst]) > 0.0f ? 1.0f : 0.0f;
+            const float old_w = ld(&d.p.rec_weight[slot]);
+            const float nw = inhibitory_step(cfg, old_w, ld(&d.activation[src]), tgt_act, sp.strength);
             if (!finitef(nw)) set_error(ctl, kErrInhibitory);
             if (nw != old_w) mark_bit(d.ch_rec, static_cast<uint32_t>(slot));
             d.p.rec_weight[slot] = nw;
@@ -1307,13 +1419,13 @@ __device__ void phase_learn(const StepCtx& c, const StepParams& sp, StepShared& 
     if (!(sp.flags & kStepFrozen)) {
         const float N = static_cast<float>(cfg.neuron_count);
         const float pop_err = static_cast<float>(A) / N - cfg.target_activity;
-        const uint32_t touched = ctl->tick_touched[tick & 1];
+        const uint32_t touched = ld(&ctl->tick_touched[tick & 1]);
         for (uint32_t i = c.gtid; i < touched; i += c.gstride) {
-            const uint32_t n = d.touched_list[i];
-            const float local = d.activation[n] > 0.0f ? 1.0f : 0.0f;
+            const uint32_t n = ld(&d.touched_list[i]);
+            const float local = ld(&d.activation[n]) > 0.0f ? 1.0f : 0.0f;
             const float local_err = local - cfg.target_activity;
             const float delta = cfg.threshold_homeostasis_rate * (local_err + pop_err);
-            const float old_t = d.p.threshold[n];
+            const float old_t = ld(&d.p.threshold[n]);
             const float nt = clampf(old_t + delta, 0.05f, 2.0f);
             if (nt != old_t) mark_bit(d.ch_threshold, n);
             d.p.threshold[n] = nt;
@@ -1346,7 +1458,7 @@ __device__ __forceinline__ bool phase_barrier(const StepCtx& c, uint32_t& target
     unsigned long long arrived = 0;
     const bool timer = kProfile && c.part == 0 && threadIdx.x == 0;
     if (timer) clock.arrive(phase, arrived);
-    const bool ok = lane_barrier(c.ctl, c.P, target, spin_limit);
+    const bool ok = lane_barrier(c.ctl, c.P, target, spin_limit, c.local);
     if (timer) clock.release(phase, arrived);
     return ok;
 }
@@ -1355,26 +1467,39 @@ __device__ __forceinline__ bool phase_barrier(const StepCtx& c, uint32_t& target
 // eligibility | post + readout | signals | learning. Frozen steps stop after
 // the post phase; a binding global cap inserts the global sort and the
 // surrogate pass before the eligibility update.
+//
+// Workgroup b serves lane b % lane_stride (lane_stride is a multiple of the 8
+// XCDs, and workgroups are dealt to XCDs round-robin, so a lane's workgroups
+// normally share one XCD); workgroups of padding lanes exit at once. Before the
+// first step the lane checks where its workgroups actually run and uses the
+// cheap XCD-local barrier only if they all share one XCD.
 template <bool kProfile>
 __device__ void lane_steps(const KernelArgs& args) {
     __shared__ StepShared sh;
-    const uint32_t L = args.lane_count, P = args.wgs_per_lane;
-    const uint32_t lane = blockIdx.x % L;
+    const uint32_t stride = args.lane_stride, P = args.wgs_per_lane;
+    const uint32_t lane = blockIdx.x % stride;
+    if (lane >= args.lane_count) return;
     StepCtx c;
     c.a = &args;
     c.d = &args.lanes[lane];
     c.ctl = c.d->ctl;
-    c.part = blockIdx.x / L;
+    c.part = blockIdx.x / stride;
     c.P = P;
     c.gtid = c.part * kThreads + threadIdx.x;
     c.gstride = P * kThreads;
-    c.tick = c.ctl->tick;
-    c.parity = c.ctl->parity;
-    c.dest_epoch = c.ctl->dest_epoch;
+    c.tick = ld(&c.ctl->tick);
+    c.parity = ld(&c.ctl->parity);
+    c.dest_epoch = ld(&c.ctl->dest_epoch);
+    c.local = false;
     uint32_t target = 0;
     const uint32_t steps = c.d->step_count;
     const bool redundant = args.redundant_global != 0;
     const uint32_t spin = args.spin_limit;
+    if (P > 1 && args.local_sync) {
+        if (threadIdx.x == 0) atomicOr(&c.ctl->xcc_mask, 1u << xcc_id());
+        if (!lane_barrier(c.ctl, P, target, spin, false)) return;
+        c.local = __popc(ld(&c.ctl->xcc_mask)) == 1;
+    }
     PhaseClock clock;
     if (kProfile && c.part == 0 && threadIdx.x == 0) clock.start(c.d->phase_profile);
     bool ok = true;
@@ -1391,11 +1516,17 @@ __device__ void lane_steps(const KernelArgs& args) {
         } else {
             if (c.part == 0) global_select(c, sh);
             if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 7))) break;
-            const uint32_t touched = c.ctl->tick_touched[c.tick & 1];
+            const uint32_t touched = ld(&c.ctl->tick_touched[c.tick & 1]);
             const uint32_t nb = args.cfg.neurons_per_block;
+            const float pop_cutoff = ld(&c.ctl->pop_cutoff);
+            const LaneDesc& d = *c.d;
             for (uint32_t i = c.gtid; i < touched; i += c.gstride) {
-                const uint32_t n = c.d->touched_list[i];
-                surrogate_for(c, n, c.d->block_cutoff[n / nb], c.ctl->pop_cutoff, c.d->selected_epoch[n] == c.tick + 1);
+                const uint32_t n = ld(&d.touched_list[i]);
+                const bool refractory = ld(&d.refractory_until[n]) > c.tick;
+                const float margin = ld(&d.membrane[n]) - ld(&d.p.threshold[n]);
+                const float cutoff = maxnum(ld(&d.block_cutoff[n / nb]), pop_cutoff);
+                d.surrogate[n] = surrogate_value(args.cfg, refractory, margin, cutoff,
+                                                 ld(&d.selected_epoch[n]) == c.tick + 1);
             }
             if (trace) {
                 if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 7))) break;

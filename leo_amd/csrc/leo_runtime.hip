@@ -174,6 +174,8 @@ struct LeoHipRuntime {
     bool tracking = false;
     std::atomic<bool> busy{false};
     uint32_t wgs_override = 0;
+    uint32_t canonical_wgs_override = 0;
+    bool local_sync = true;
     LeoKernelStats telemetry{};
     bool phase_profile = false;
     double wall_clock_khz = 0.0;
@@ -348,6 +350,8 @@ KernelArgs kernel_args(LeoHipRuntime* h, LaneDesc* lanes, uint32_t count, uint32
     a.wgs_per_lane = P;
     a.redundant_global = (static_cast<uint64_t>(h->z.blocks) * h->z.limit <= h->z.cap) ? 1 : 0;
     a.spin_limit = 1u << 26;
+    a.lane_stride = count;
+    a.local_sync = h->local_sync ? 1 : 0;
     return a;
 }
 
@@ -377,12 +381,14 @@ void reset_lane_objects(LeoHipRuntime* h, const std::vector<Lane*>& lanes, bool 
     }
 }
 
-uint32_t choose_wgs_per_lane(LeoHipRuntime* h, uint32_t lanes) {
+uint32_t choose_wgs_per_lane(LeoHipRuntime* h, uint32_t lanes, bool canonical) {
     uint32_t coop = static_cast<uint32_t>(h->cus * h->coop_blocks_per_cu);
     uint32_t limit = std::max<uint32_t>(1, coop / std::max<uint32_t>(lanes, 1));
     limit = std::min<uint32_t>(limit, kMaxWaves / kWavesPerGroup);
     uint32_t want;
-    if (h->wgs_override) {
+    if (canonical && h->canonical_wgs_override) {
+        want = h->canonical_wgs_override;
+    } else if (h->wgs_override) {
         want = h->wgs_override;
     } else {
         // one selecting wave per block, and about one workgroup per 32K edges
@@ -506,21 +512,26 @@ void run_lanes(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
             lane.schedule.base + ((static_cast<size_t>(lane.schedule_capacity) * sizeof(StepParams) + 255) & ~size_t(255)));
         lane.desc.step_count = static_cast<uint32_t>(r.steps.size());
         upload(const_cast<StepParams*>(lane.desc.steps), r.steps.data(), r.steps.size() * sizeof(StepParams), h->stream);
-        LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->barrier, 0, 8, h->stream));  // barrier + abort
+        LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->barrier, 0, 12, h->stream));  // barrier, abort, xcc_mask
         LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->error_code, 0, 4, h->stream));
     }
     std::vector<Lane*> lanes;
     for (auto& r : runs) lanes.push_back(r.lane);
     stage_descs(h, lanes);
-    const uint32_t P = choose_wgs_per_lane(h, count);
+    // lanes are padded to a multiple of the 8 XCDs so that each lane's
+    // workgroups land on one XCD (see lane_steps)
+    const uint32_t padded = (count + 7) / 8 * 8;
+    const uint32_t P = choose_wgs_per_lane(h, padded, count == 1 && runs[0].lane == h->canonical.get());
+    const uint32_t stride = P > 1 ? padded : count;
     KernelArgs a = kernel_args(h, reinterpret_cast<LaneDesc*>(h->lane_descs.base), count, P);
+    a.lane_stride = stride;
     void* params[] = {&a};
     const void* kernel = h->phase_profile ? reinterpret_cast<const void*>(&leo_lane_steps_profiled)
                                           : reinterpret_cast<const void*>(&leo_lane_steps);
     if (h->phase_profile)
         for (auto& r : runs) LEO_HIP_CHECK(hipMemsetAsync(r.lane->desc.phase_profile, 0, 2 * kPhases * 8, h->stream));
     LEO_HIP_CHECK(hipEventRecord(h->ev_start, h->stream));
-    LEO_HIP_CHECK(hipLaunchCooperativeKernel(kernel, dim3(count * P), dim3(kThreads), params,
+    LEO_HIP_CHECK(hipLaunchCooperativeKernel(kernel, dim3(stride * P), dim3(kThreads), params,
                                              step_lds_bytes(h->cfg.device.neurons_per_block), h->stream));
     LEO_HIP_CHECK(hipEventRecord(h->ev_stop, h->stream));
     std::vector<LaneControl> ctl(count);
@@ -1279,6 +1290,8 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         leo::model_validate(*config, *model);
         if (config->device.neurons_per_block > leo::kMaxBlockNeurons)
             throw Error(LEO_ERR_UNSUPPORTED, "neurons_per_block above 1024 is not supported by the device selection");
+        if (static_cast<uint64_t>(config->device.neuron_count) * leo::kOutStride * 4 >= (1ULL << 31))
+            throw Error(LEO_ERR_UNSUPPORTED, "output projection above 2 GiB per lane is not supported");
         int devices = 0;
         if (hipGetDeviceCount(&devices) != hipSuccess || devices <= 0)
             throw Error(LEO_ERR_DEVICE, "GPU backend requested, but no HIP device is available");
@@ -1306,6 +1319,9 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
                                                                    leo::step_lds_bytes(config->device.neurons_per_block)));
         if (h->coop_blocks_per_cu <= 0) throw Error(LEO_ERR_DEVICE, "step kernel cannot be resident");
         if (const char* env = std::getenv("LEO_HIP_WGS_PER_LANE")) h->wgs_override = static_cast<uint32_t>(std::atoi(env));
+        if (const char* env = std::getenv("LEO_HIP_CANONICAL_WGS"))
+            h->canonical_wgs_override = static_cast<uint32_t>(std::atoi(env));
+        if (const char* env = std::getenv("LEO_HIP_AGENT_SYNC")) h->local_sync = std::atoi(env) == 0;
         if (const char* env = std::getenv("LEO_HIP_PHASE_PROFILE")) h->phase_profile = std::atoi(env) != 0;
         int clock_khz = 0;
         LEO_HIP_CHECK(hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, device));
