@@ -158,6 +158,7 @@ struct LaneDesc {
     uint64_t* bucket;        // 2 words per entry: delivery-order key, value bits
     // block selection
     uint32_t* block_winners; // blocks * max_active_per_block
+    float* block_winner_act; // blocks * max_active_per_block: activation of each winner
     uint32_t* block_count;   // blocks
     float* block_cutoff;     // blocks
     uint32_t* wave_total;    // kMaxWaves: block winners per selecting wave (block-range owner)

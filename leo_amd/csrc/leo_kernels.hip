@@ -146,7 +146,9 @@ __device__ __forceinline__ void wave_sync() {
 // has since rewritten. Read-only topology uses plain loads.
 template <class T>
 __device__ __forceinline__ T ld(const T* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // lane state is device memory: the global address space avoids flat loads
+    const auto g = (const __attribute__((address_space(1))) T*)(p);
+    return __hip_atomic_load(g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // XCD (accelerator complex die) this wave runs on.
@@ -255,6 +257,9 @@ struct alignas(16) StepShared {
     float ctx_scale[kMaxOrder];
     uint32_t ctx_probes[kMaxOrder];
     uint32_t hist_len;
+    // this workgroup's copy of the emission ring bookkeeping (LaneControl ring_*)
+    uint32_t ring_tick[kRing];
+    uint32_t ring_count[kRing];
 };
 
 // Dynamic LDS (step_lds_bytes): per wave a candidate-key list and a touched
@@ -264,7 +269,7 @@ extern __shared__ __align__(16) unsigned char step_lds[];
 
 struct StepCtx {
     const KernelArgs* a;
-    const LaneDesc* d;
+    LaneDesc d;
     LaneControl* ctl;
     uint32_t tick;
     uint32_t part;     // workgroup index within the lane group
@@ -312,9 +317,15 @@ __device__ void finalize_record(const LaneDesc& d, LaneControl* ctl, uint32_t st
     rec.active_inhibitory = ld(&ctl->tick_ainh[k]);
 }
 
-__device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t step_index) {
+// Entry p of target n's delivery bucket: the first two at fixed places
+// (2n, 2n+1), the rest in the target's overflow range.
+__device__ __forceinline__ uint64_t bucket_entry(const SharedModel& m, uint32_t n, uint32_t p) {
+    return p < 2 ? 2ull * n + p : m.bucket_offset[n] + (p - 2);
+}
+
+__device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t step_index, const StepShared& sh) {
     const KernelArgs& a = *c.a;
-    const LaneDesc& d = *c.d;
+    const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
     LaneControl* ctl = c.ctl;
     const uint32_t S = cfg.synapses_per_neuron, F = cfg.input_fanout, cap = cfg.max_active_global;
@@ -337,13 +348,13 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t s
     }
     // previous active set (runtime.rs:544-555)
     const uint32_t prev_slot = (tick + kRing - 1) % kRing;
-    const uint32_t prev_count = (tick > 0 && ld(&ctl->ring_tick[prev_slot]) == tick - 1) ? ld(&ctl->ring_count[prev_slot]) : 0;
+    const uint32_t prev_count = (tick > 0 && sh.ring_tick[prev_slot] == tick - 1) ? sh.ring_count[prev_slot] : 0;
     // delivery classes: delay 8, 4, 2, 1 in that order (chronological by emission tick)
     // (scalars, not arrays: a dynamically indexed private array lives in scratch)
     auto class_items = [&](uint32_t delay, uint32_t& rs) {
         rs = (tick + kRing - delay) % kRing;
-        const bool valid = tick >= delay && ld(&ctl->ring_tick[rs]) == tick - delay;
-        return (valid ? ld(&ctl->ring_count[rs]) : 0) * S;
+        const bool valid = tick >= delay && sh.ring_tick[rs] == tick - delay;
+        return (valid ? sh.ring_count[rs] : 0) * S;
     };
     uint32_t rs8, rs4, rs2, rs1;
     const uint32_t off8 = prev_count;
@@ -354,7 +365,12 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t s
     const uint32_t total = off_in + F;
     const uint32_t lane = __lane_id();
     uint32_t delivered = 0;
-    for (uint32_t base = c.gtid - lane; base < total; base += c.gstride) {
+    // with several workgroups the last one resolves the context meanwhile and
+    // takes no deliveries
+    const uint32_t workers = c.P > 1 ? c.P - 1 : 1;
+    const bool delivers = c.P == 1 || c.part < c.P - 1;
+    const uint32_t stride = workers * kThreads;
+    for (uint32_t base = c.gtid - lane; delivers && base < total; base += stride) {
         const uint32_t item = base + lane;
         uint32_t touch_n = 0xffffffffu, target = 0, eslot = 0;
         bool new_rec = false, new_in = false, scatter = false;
@@ -420,13 +436,12 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t s
         if (new_rec) d.rec_list[static_cast<uint64_t>(c.parity) * NS + pos] = eslot;
         pos = wave_append(&ctl->in_count[c.parity], new_in);
         if (new_in) d.in_list[static_cast<uint64_t>(c.parity) * NI + pos] = eslot;
-        bool first = false;
-        if (touch_n != 0xffffffffu) first = atomicExch(&d.touched_epoch[touch_n], tick + 1) != tick + 1;
-        pos = wave_append(&ctl->tick_touched[tick & 1], first);
-        if (first) d.touched_list[pos] = touch_n;
+        // touched mark (every writer stores the same epoch; the touched list is
+        // built per block in phase 2)
+        if (touch_n != 0xffffffffu) d.touched_epoch[touch_n] = tick + 1;
         if (scatter) {
             const uint32_t p = atomicAdd(&d.bucket_count[target], 1u);
-            const uint64_t at = a.m.bucket_offset[target] + p;
+            const uint64_t at = bucket_entry(a.m, target, p);
             d.bucket[2 * at] = key;
             d.bucket[2 * at + 1] = __float_as_uint(value);
         }
@@ -435,20 +450,24 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t s
 }
 
 // ---------------------------------------------------------------------------
-// Phase 2: context resolution (runtime.rs:641-677, model.rs:173-221), one
-// thread per order on the last workgroup; per-block fold, drive and top-k on
-// one wave per block (runtime.rs:576-603, 701-708, 940-1011, 787-803).
+// Context resolution (runtime.rs:641-677, model.rs:173-221), one thread per
+// order on the last workgroup during phase 1; phase 2 is the per-block fold,
+// drive and top-k on one wave per block (runtime.rs:576-603, 701-708,
+// 940-1011, 787-803).
 // ---------------------------------------------------------------------------
 __device__ void context_resolve(const StepCtx& c, const StepParams& sp, StepShared& sh) {
     const LeoConfig& cfg = c.a->cfg;
-    const LaneDesc& d = *c.d;
+    const LaneDesc& d = c.d;
     LaneControl* ctl = c.ctl;
     const uint32_t max_order = cfg.context_max_order, E = cfg.context_embedding_dim;
     const bool enabled = (sp.flags & kStepContext) != 0;
     const bool allocate = (sp.flags & kStepAllocate) != 0;
+    // the history entries and its length are loaded in one round
+    if (threadIdx.x < kMaxOrder) sh.hist[threadIdx.x] = ld(&ctl->history[threadIdx.x]);
+    if (threadIdx.x == kMaxOrder) sh.hist_len = ld(&ctl->history_len);
+    __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t len = ld(&ctl->history_len);
-        for (uint32_t i = 0; i < len; ++i) sh.hist[i] = ld(&ctl->history[i]);
+        uint32_t len = sh.hist_len;
         if (len == max_order) {
             for (uint32_t i = 1; i < len; ++i) sh.hist[i - 1] = sh.hist[i];
             len -= 1;
@@ -468,20 +487,44 @@ __device__ void context_resolve(const StepCtx& c, const StepParams& sp, StepShar
         int64_t found = -1, empty = -1;
         uint64_t weakest = base + start;
         uint32_t weakest_obs = 0xffffffffu, probes = 0, found_obs = 0;
-        for (uint32_t off = 0; off < cfg.context_probe_limit; ++off) {
+        // the probe window is loaded at once when it is short
+        constexpr uint32_t kWindow = 8;
+        const uint32_t limit = cfg.context_probe_limit;
+        uint64_t keys[kWindow];
+        uint32_t obs_w[kWindow];
+#pragma unroll
+        for (uint32_t off = 0; off < kWindow; ++off) {
             const uint64_t slot = base + (start + off) % spo;
+            keys[off] = off < limit ? ld(&d.p.ctx_keys[slot]) : 0;
+            obs_w[off] = off < limit ? ld(&d.p.ctx_obs[slot]) : 0;
+        }
+        bool done = false;
+        for (uint32_t off = 0; !done && off < limit; ++off) {
+            const uint64_t slot = base + (start + off) % spo;
+            uint64_t existing = 0;
+            uint32_t obs = 0;
+            if (off < kWindow) {
+#pragma unroll
+                for (uint32_t w = 0; w < kWindow; ++w)  // select from registers without indexing
+                    if (w == off) {
+                        existing = keys[w];
+                        obs = obs_w[w];
+                    }
+            } else {
+                existing = ld(&d.p.ctx_keys[slot]);
+                obs = ld(&d.p.ctx_obs[slot]);
+            }
             probes += 1;
-            const uint64_t existing = ld(&d.p.ctx_keys[slot]);
-            const uint32_t obs = ld(&d.p.ctx_obs[slot]);
             if (existing == key) {
                 found = static_cast<int64_t>(slot);
                 found_obs = obs;
-                break;
-            }
-            if (existing == 0 && empty < 0) empty = static_cast<int64_t>(slot);
-            if (obs < weakest_obs) {
-                weakest_obs = obs;
-                weakest = slot;
+                done = true;
+            } else {
+                if (existing == 0 && empty < 0) empty = static_cast<int64_t>(slot);
+                if (obs < weakest_obs) {
+                    weakest_obs = obs;
+                    weakest = slot;
+                }
             }
         }
         if (found < 0 && allocate) {
@@ -552,7 +595,7 @@ __device__ __forceinline__ void sort8(uint64_t (&k)[8], uint32_t (&v)[8]) {
 // margin membrane - threshold; *refractory tells whether the neuron skipped.
 __device__ float fold_drive(const StepCtx& c, uint32_t n, float pi, bool* refractory) {
     const KernelArgs& a = *c.a;
-    const LaneDesc& d = *c.d;
+    const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
     const uint32_t N = cfg.neuron_count, tick = c.tick;
     float b0 = ld(&d.branches[4 * n]), b1 = ld(&d.branches[4 * n + 1]);
@@ -561,6 +604,9 @@ __device__ float fold_drive(const StepCtx& c, uint32_t n, float pi, bool* refrac
     float ad0 = ld(&d.adapt[n]), ad1 = ld(&d.adapt[N + n]), ad2 = ld(&d.adapt[2 * N + n]);
     const uint32_t last = ld(&d.last_tick[n]);
     const uint32_t cnt = ld(&d.bucket_count[n]);
+    // the two fixed bucket entries are read with the state
+    const uint64_t* fixed = d.bucket + 4ull * n;
+    const uint64_t k0 = ld(&fixed[0]), v0 = ld(&fixed[1]), k1 = ld(&fixed[2]), v1 = ld(&fixed[3]);
     const bool refr = ld(&d.refractory_until[n]) > tick;
     const float threshold = ld(&d.p.threshold[n]);
     const uint32_t e = tick - last;
@@ -582,47 +628,62 @@ __device__ float fold_drive(const StepCtx& c, uint32_t n, float pi, bool* refrac
         d.last_tick[n] = tick;
     }
     if (cnt > 0) {
-        uint64_t* ent = d.bucket + 2 * a.m.bucket_offset[n];
+        // selects, not an indexed array (which would live in scratch)
         auto add = [&](uint64_t key, uint32_t bits) {
             const float v = __uint_as_float(bits);
-            switch (static_cast<uint32_t>(key) & 3u) {
-                case 0: b0 += v; break;
-                case 1: b1 += v; break;
-                case 2: b2 += v; break;
-                default: b3 += v; break;
-            }
+            const uint32_t br = static_cast<uint32_t>(key) & 3u;
+            b0 = br == 0 ? b0 + v : b0;
+            b1 = br == 1 ? b1 + v : b1;
+            b2 = br == 2 ? b2 + v : b2;
+            b3 = br == 3 ? b3 + v : b3;
         };
-        if (cnt <= 8) {
+        if (cnt == 1) {
+            add(k0, static_cast<uint32_t>(v0));
+        } else if (cnt == 2) {
+            if (k1 < k0) {
+                add(k1, static_cast<uint32_t>(v1));
+                add(k0, static_cast<uint32_t>(v0));
+            } else {
+                add(k0, static_cast<uint32_t>(v0));
+                add(k1, static_cast<uint32_t>(v1));
+            }
+        } else if (cnt <= 8) {
             uint64_t k[8];
             uint32_t v[8];
+            k[0] = k0;
+            v[0] = static_cast<uint32_t>(v0);
+            k[1] = k1;
+            v[1] = static_cast<uint32_t>(v1);
+            const uint64_t* over = d.bucket + 2 * a.m.bucket_offset[n];
 #pragma unroll
-            for (uint32_t x = 0; x < 8; ++x) {
-                k[x] = x < cnt ? ld(&ent[2 * x]) : ~0ULL;
-                v[x] = x < cnt ? static_cast<uint32_t>(ld(&ent[2 * x + 1])) : 0u;
+            for (uint32_t x = 2; x < 8; ++x) {
+                k[x] = x < cnt ? ld(&over[2 * (x - 2)]) : ~0ULL;
+                v[x] = x < cnt ? static_cast<uint32_t>(ld(&over[2 * (x - 2) + 1])) : 0u;
             }
             sort8(k, v);
 #pragma unroll
             for (uint32_t x = 0; x < 8; ++x)
                 if (x < cnt) add(k[x], v[x]);
         } else {
-            // in-place insertion sort; every store completes before the
-            // following device-scope loads of the same entries
-            for (uint32_t x = 1; x < cnt; ++x) {
-                const uint64_t kx = ld(&ent[2 * x]), vx = ld(&ent[2 * x + 1]);
-                uint32_t y = x;
-                while (y > 0) {
-                    const uint64_t ky = ld(&ent[2 * (y - 1)]);
-                    if (ky <= kx) break;
-                    ent[2 * y] = ky;
-                    ent[2 * y + 1] = ld(&ent[2 * (y - 1) + 1]);
-                    __builtin_amdgcn_s_waitcnt(0);
-                    --y;
+            // many deliveries: fold in key order by repeated minimum search
+            // (keys are unique; nothing is written back)
+            uint64_t last = 0;
+            bool started = false;
+            for (uint32_t t = 0; t < cnt; ++t) {
+                uint64_t best = ~0ULL;
+                uint32_t best_v = 0;
+                for (uint32_t x = 0; x < cnt; ++x) {
+                    const uint64_t at = bucket_entry(a.m, n, x);
+                    const uint64_t kx = ld(&d.bucket[2 * at]);
+                    if ((!started || kx > last) && kx < best) {
+                        best = kx;
+                        best_v = static_cast<uint32_t>(ld(&d.bucket[2 * at + 1]));
+                    }
                 }
-                ent[2 * y] = kx;
-                ent[2 * y + 1] = vx;
-                __builtin_amdgcn_s_waitcnt(0);
+                add(best, best_v);
+                last = best;
+                started = true;
             }
-            for (uint32_t x = 0; x < cnt; ++x) add(ld(&ent[2 * x]), static_cast<uint32_t>(ld(&ent[2 * x + 1])));
         }
         d.bucket_count[n] = 0;
     }
@@ -660,7 +721,7 @@ constexpr uint32_t kRefractoryBit = 0x80000000u;
 
 __device__ uint32_t select_block(const StepCtx& c, uint32_t b, float pi, uint64_t* cand, uint32_t* tl, float* tmar) {
     const KernelArgs& a = *c.a;
-    const LaneDesc& d = *c.d;
+    const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
     const uint32_t N = cfg.neuron_count, nb = cfg.neurons_per_block, limit = cfg.max_active_per_block;
     const uint32_t tick = c.tick, rot = tick % N;
@@ -681,6 +742,9 @@ __device__ uint32_t select_block(const StepCtx& c, uint32_t b, float pi, uint64_
         if (t) tl[touched + __popcll(mask & below)] = first + k * kWaveSize + lane;
         touched += static_cast<uint32_t>(__popcll(mask));
     }
+    // reserve this block's range of the lane's touched list (used after the fold)
+    uint32_t list_at = 0;
+    if (lane == 0 && touched) list_at = atomicAdd(&c.ctl->tick_touched[tick & 1], touched);
     wave_sync();
     uint32_t count = 0;
     for (uint32_t base = 0; base < touched; base += kWaveSize) {
@@ -711,7 +775,10 @@ __device__ uint32_t select_block(const StepCtx& c, uint32_t b, float pi, uint64_
         const uint64_t mine = i < count ? cand[i] : ~0ULL;
         uint32_t rank = 0;
         for (uint32_t j = 0; j < count; ++j) rank += cand[j] < mine ? 1u : 0u;
-        if (i < count && rank < limit) d.block_winners[static_cast<uint64_t>(b) * limit + rank] = (static_cast<uint32_t>(mine) + rot) % N;
+        if (i < count && rank < limit) {
+            d.block_winners[static_cast<uint64_t>(b) * limit + rank] = (static_cast<uint32_t>(mine) + rot) % N;
+            d.block_winner_act[static_cast<uint64_t>(b) * limit + rank] = key_activation(mine);
+        }
         const unsigned long long cut = wave_min_u64(i < count && rank == limit ? mine : ~0ULL);
         cut_key = cut < cut_key ? cut : cut_key;
     }
@@ -743,13 +810,14 @@ __device__ uint32_t select_block(const StepCtx& c, uint32_t b, float pi, uint64_
             d.surrogate[n] = surrogate_value(cfg, refractory, margin, cutoff, won);
         }
     }
+    list_at = __shfl(list_at, 0);
+    for (uint32_t i = lane; i < touched; i += kWaveSize) d.touched_list[list_at + i] = tl[i] & ~kRefractoryBit;
     wave_sync();
     return winners;
 }
 
-__device__ void phase_fold_select(const StepCtx& c, const StepParams& sp, StepShared& sh) {
+__device__ void phase_fold_select(const StepCtx& c) {
     const LeoConfig& cfg = c.a->cfg;
-    if (c.part == c.P - 1) context_resolve(c, sp, sh);
     const uint32_t wave = threadIdx.x / kWaveSize, lane = __lane_id();
     const uint32_t nwaves = c.P * kWavesPerGroup;
     const uint32_t wv = c.part * kWavesPerGroup + wave;
@@ -762,7 +830,7 @@ __device__ void phase_fold_select(const StepCtx& c, const StepParams& sp, StepSh
     uint32_t* tl = reinterpret_cast<uint32_t*>(step_lds + static_cast<size_t>(kWavesPerGroup) * nb * 8) + wave * nb;
     float* tmar = reinterpret_cast<float*>(step_lds + static_cast<size_t>(kWavesPerGroup) * nb * 12) + wave * nb;
     for (uint32_t b = b0; b < b1; ++b) total += select_block(c, b, pi, cand, tl, tmar);
-    if (lane == 0) c.d->wave_total[wv] = total;
+    if (lane == 0) c.d.wave_total[wv] = total;
 }
 
 // ---------------------------------------------------------------------------
@@ -772,13 +840,25 @@ __device__ void phase_fold_select(const StepCtx& c, const StepParams& sp, StepSh
 // ---------------------------------------------------------------------------
 __device__ void write_active(const StepCtx& c) {
     const LeoConfig& cfg = c.a->cfg;
-    const LaneDesc& d = *c.d;
+    const LaneDesc& d = c.d;
     const uint32_t cap = cfg.max_active_global, limit = cfg.max_active_per_block;
     const uint32_t wave = threadIdx.x / kWaveSize, lane = __lane_id();
     const uint32_t nwaves = c.P * kWavesPerGroup;
     const uint32_t wv = c.part * kWavesPerGroup + wave;
     const uint32_t per = (cfg.block_count + nwaves - 1) / nwaves;
     const uint32_t rs = c.tick % kRing;
+    const uint32_t b0 = wv * per, b1 = min(cfg.block_count, b0 + per);
+    uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
+    float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
+    // the winners of this wave's first block are loaded together with the
+    // per-wave totals (one round of loads in the common one-block case)
+    const uint32_t first_count = b0 < b1 ? ld(&d.block_count[b0]) : 0;
+    uint32_t first_n = 0;
+    float first_act = 0.0f;
+    if (b0 < b1 && lane < limit) {
+        first_n = ld(&d.block_winners[static_cast<uint64_t>(b0) * limit + lane]);
+        first_act = ld(&d.block_winner_act[static_cast<uint64_t>(b0) * limit + lane]);
+    }
     // offset of this wave's block range: winners of every earlier range
     uint32_t before = 0, all = 0;
     for (uint32_t base = 0; base < nwaves; base += kWaveSize) {
@@ -787,16 +867,14 @@ __device__ void write_active(const StepCtx& c) {
         before += wave_sum_u32(w < wv ? v : 0);
         all += wave_sum_u32(v);
     }
-    const uint32_t b0 = wv * per, b1 = min(cfg.block_count, b0 + per);
-    uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
-    float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
     uint32_t offset = before;
     for (uint32_t b = b0; b < b1; ++b) {
-        const uint32_t v = ld(&d.block_count[b]);
+        const uint32_t v = b == b0 ? first_count : ld(&d.block_count[b]);
         for (uint32_t i = lane; i < v; i += kWaveSize) {
-            const uint32_t n = ld(&d.block_winners[static_cast<uint64_t>(b) * limit + i]);
+            const bool pre = b == b0 && i == lane;
+            const uint32_t n = pre ? first_n : ld(&d.block_winners[static_cast<uint64_t>(b) * limit + i]);
             act_list[offset + i] = n;
-            act_val[offset + i] = ld(&d.activation[n]);
+            act_val[offset + i] = pre ? first_act : ld(&d.block_winner_act[static_cast<uint64_t>(b) * limit + i]);
         }
         offset += v;
     }
@@ -819,7 +897,7 @@ __device__ void write_active(const StepCtx& c) {
 // (activation desc, tie asc), keep max_active_global (runtime.rs:1029-1057).
 __device__ void global_select(const StepCtx& c, StepShared& sh) {
     const KernelArgs& a = *c.a;
-    const LaneDesc& d = *c.d;
+    const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
     const uint32_t N = cfg.neuron_count, limit = cfg.max_active_per_block, cap = cfg.max_active_global;
     const uint32_t tick = c.tick, rot = tick % N;
@@ -892,7 +970,7 @@ __device__ void global_select(const StepCtx& c, StepShared& sh) {
 __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uint64_t plane, uint32_t* last,
                                             uint32_t slot, uint32_t dst, uint8_t br) {
     const LeoConfig& cfg = c.a->cfg;
-    const LaneDesc& d = *c.d;
+    const LaneDesc& d = c.d;
     const uint32_t tick = c.tick;
     float bs = ld(&planes[slot]), ms = ld(&planes[plane + slot]), fs = ld(&planes[2 * plane + slot]);
     float as0 = ld(&planes[3 * plane + slot]), as1 = ld(&planes[4 * plane + slot]), as2 = ld(&planes[5 * plane + slot]);
@@ -961,7 +1039,7 @@ __device__ void eligibility_list(const StepCtx& c, float* planes, uint64_t plane
 
 __device__ void phase_eligibility(const StepCtx& c) {
     const KernelArgs& a = *c.a;
-    const LaneDesc& d = *c.d;
+    const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
     const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * cfg.synapses_per_neuron;
     const uint64_t NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
@@ -984,7 +1062,7 @@ __device__ void phase_eligibility(const StepCtx& c) {
 // ---------------------------------------------------------------------------
 __device__ void readout(const StepCtx& c, const StepParams& sp, StepShared& sh, uint32_t step_index) {
     const KernelArgs& a = *c.a;
-    const LaneDesc& d = *c.d;
+    const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
     LaneControl* ctl = c.ctl;
     const uint32_t cap = cfg.max_active_global, E = cfg.context_embedding_dim;
@@ -1109,7 +1187,7 @@ __device__ void readout(const StepCtx& c, const StepParams& sp, StepShared& sh, 
 
 __device__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step_index, StepShared& sh) {
     const KernelArgs& a = *c.a;
-    const LaneDesc& d = *c.d;
+    const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
     const uint32_t S = cfg.synapses_per_neuron, cap = cfg.max_active_global;
     const uint32_t rs = c.tick % kRing;
@@ -1139,6 +1217,10 @@ __device__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step
         }
     }
     add_count(&c.ctl->tick_ainh[c.tick & 1], inhibitory);
+    if (threadIdx.x == 0) {  // the next deliveries read this tick's ring entry from LDS
+        sh.ring_tick[rs] = c.tick;
+        sh.ring_count[rs] = A;
+    }
     const uint32_t readout_wg = c.P - 1;
     if (c.part == readout_wg) {
         if (threadIdx.x == 0) {
@@ -1207,7 +1289,7 @@ __device__ __forceinline__ float signal_dot(__amdgpu_buffer_rsrc_t rows, uint32_
 
 __device__ void phase_signals(const StepCtx& c, StepShared& sh) {
     const KernelArgs& a = *c.a;
-    const LaneDesc& d = *c.d;
+    const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
     const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * cfg.synapses_per_neuron;
     const uint64_t NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
@@ -1273,7 +1355,7 @@ __device__ __forceinline__ float inhibitory_step(const LeoConfig& cfg, float w, 
 
 __device__ void context_update(const StepCtx& c, const StepParams& sp, StepShared& sh) {
     const LeoConfig& cfg = c.a->cfg;
-    const LaneDesc& d = *c.d;
+    const LaneDesc& d = c.d;
     LaneControl* ctl = c.ctl;
     const uint32_t E = cfg.context_embedding_dim, count = ld(&ctl->ctx_count);
     const float lr = cfg.context_learning_rate, mu = cfg.max_update, wmin = cfg.weight_min, wmax = cfg.weight_max;
@@ -1312,9 +1394,9 @@ __device__ void context_update(const StepCtx& c, const StepParams& sp, StepShare
     __syncthreads();
 }
 
-__device__ void phase_learn(const StepCtx& c, const StepParams& sp, StepShared& sh) {
+__device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& sp, StepShared& sh) {
     const KernelArgs& a = *c.a;
-    const LaneDesc& d = *c.d;
+    const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
     LaneControl* ctl = c.ctl;
     const uint32_t S = cfg.synapses_per_neuron, cap = cfg.max_active_global;
@@ -1473,6 +1555,18 @@ __device__ __forceinline__ bool phase_barrier(const StepCtx& c, uint32_t& target
 // normally share one XCD); workgroups of padding lanes exit at once. Before the
 // first step the lane checks where its workgroups actually run and uses the
 // cheap XCD-local barrier only if they all share one XCD.
+// Copies a workgroup-uniform descriptor word by word into scalar registers.
+__device__ __forceinline__ LaneDesc load_uniform(const LaneDesc* p) {
+    static_assert(sizeof(LaneDesc) % 4 == 0, "descriptor is made of 32-bit words");
+    uint32_t w[sizeof(LaneDesc) / 4];
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+    for (uint32_t i = 0; i < sizeof(LaneDesc) / 4; ++i) w[i] = __builtin_amdgcn_readfirstlane(src[i]);
+    LaneDesc out;
+    __builtin_memcpy(&out, w, sizeof(LaneDesc));
+    return out;
+}
+
 template <bool kProfile>
 __device__ void lane_steps(const KernelArgs& args) {
     __shared__ StepShared sh;
@@ -1481,8 +1575,8 @@ __device__ void lane_steps(const KernelArgs& args) {
     if (lane >= args.lane_count) return;
     StepCtx c;
     c.a = &args;
-    c.d = &args.lanes[lane];
-    c.ctl = c.d->ctl;
+    c.d = load_uniform(&args.lanes[lane]);  // a private copy: its pointers stay in scalar registers
+    c.ctl = c.d.ctl;
     c.part = blockIdx.x / stride;
     c.P = P;
     c.gtid = c.part * kThreads + threadIdx.x;
@@ -1492,7 +1586,7 @@ __device__ void lane_steps(const KernelArgs& args) {
     c.dest_epoch = ld(&c.ctl->dest_epoch);
     c.local = false;
     uint32_t target = 0;
-    const uint32_t steps = c.d->step_count;
+    const uint32_t steps = c.d.step_count;
     const bool redundant = args.redundant_global != 0;
     const uint32_t spin = args.spin_limit;
     if (P > 1 && args.local_sync) {
@@ -1500,15 +1594,22 @@ __device__ void lane_steps(const KernelArgs& args) {
         if (!lane_barrier(c.ctl, P, target, spin, false)) return;
         c.local = __popc(ld(&c.ctl->xcc_mask)) == 1;
     }
+    if (threadIdx.x < kRing) {
+        sh.ring_tick[threadIdx.x] = ld(&c.ctl->ring_tick[threadIdx.x]);
+        sh.ring_count[threadIdx.x] = ld(&c.ctl->ring_count[threadIdx.x]);
+    }
+    __syncthreads();
     PhaseClock clock;
-    if (kProfile && c.part == 0 && threadIdx.x == 0) clock.start(c.d->phase_profile);
+    if (kProfile && c.part == 0 && threadIdx.x == 0) clock.start(c.d.phase_profile);
     bool ok = true;
     for (uint32_t s = 0; s < steps && ok; ++s) {
-        const StepParams sp = c.d->steps[s];
+        const StepParams sp = c.d.steps[s];
         const bool trace = (sp.flags & kStepLearnTrace) != 0;
-        phase_deliver(c, sp, s);
+        // the context (runtime.rs:641-677) is first read by the readout
+        if (c.part == c.P - 1) context_resolve(c, sp, sh);
+        phase_deliver(c, sp, s, sh);
         if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 0))) break;
-        phase_fold_select(c, sp, sh);
+        phase_fold_select(c);
         if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 1))) break;
         if (redundant) {
             write_active(c);
@@ -1519,7 +1620,7 @@ __device__ void lane_steps(const KernelArgs& args) {
             const uint32_t touched = ld(&c.ctl->tick_touched[c.tick & 1]);
             const uint32_t nb = args.cfg.neurons_per_block;
             const float pop_cutoff = ld(&c.ctl->pop_cutoff);
-            const LaneDesc& d = *c.d;
+            const LaneDesc& d = c.d;
             for (uint32_t i = c.gtid; i < touched; i += c.gstride) {
                 const uint32_t n = ld(&d.touched_list[i]);
                 const bool refractory = ld(&d.refractory_until[n]) > c.tick;
@@ -1550,15 +1651,21 @@ __device__ void lane_steps(const KernelArgs& args) {
         c.tick += 1;
     }
     if (ok && c.part == 0 && threadIdx.x == 0) {
-        if (steps > 0) finalize_record(*c.d, c.ctl, steps - 1, c.tick - 1);
+        if (steps > 0) finalize_record(c.d, c.ctl, steps - 1, c.tick - 1);
         c.ctl->tick = c.tick;
         c.ctl->parity = c.parity;
         c.ctl->dest_epoch = c.dest_epoch;
     }
 }
 
-__global__ void __launch_bounds__(kThreads) leo_lane_steps(KernelArgs args) { lane_steps<false>(args); }
-__global__ void __launch_bounds__(kThreads) leo_lane_steps_profiled(KernelArgs args) { lane_steps<true>(args); }
+// The arguments live in device memory (read with scalar loads): a by-value
+// argument whose address is taken is copied to scratch.
+__global__ void __launch_bounds__(kThreads) leo_lane_steps(const KernelArgs* __restrict__ args) {
+    lane_steps<false>(*args);
+}
+__global__ void __launch_bounds__(kThreads) leo_lane_steps_profiled(const KernelArgs* __restrict__ args) {
+    lane_steps<true>(*args);
+}
 
 // ---------------------------------------------------------------------------
 // reset_transient_state (runtime.rs:365-425) for every lane in args.

@@ -30,8 +30,8 @@
 
 namespace leo {
 
-__global__ void leo_lane_steps(KernelArgs args);
-__global__ void leo_lane_steps_profiled(KernelArgs args);
+__global__ void leo_lane_steps(const KernelArgs* args);
+__global__ void leo_lane_steps_profiled(const KernelArgs* args);
 __global__ void leo_reset_lanes(KernelArgs args, uint32_t set_tick, uint32_t new_tick);
 
 __global__ void leo_merge_fixed(MergeArgs m);
@@ -163,6 +163,7 @@ struct LeoHipRuntime {
     std::vector<std::unique_ptr<leo::Lane>> lanes;
     uint32_t max_lanes = 0;
     leo::Arena lane_descs;     // LaneDesc[max(1,max_lanes)]
+    leo::Arena kernel_args_buf;  // KernelArgs of the step kernel
     leo::Arena merge_scratch;  // lane pointer table + counters
     // host copies of the read-only topology (device copies are immutable)
     std::vector<float> excitability;
@@ -274,6 +275,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     size_t o_se = l.add<uint32_t>(z.n), o_su = l.add<float>(z.n), o_de = l.add<uint32_t>(z.n);
     size_t o_ls = l.add<float>(z.n), o_bc = l.add<uint32_t>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
     size_t o_bw = l.add<uint32_t>(z.blocks * z.limit), o_bn = l.add<uint32_t>(z.blocks), o_bcut = l.add<float>(z.blocks);
+    size_t o_bwa = l.add<float>(z.blocks * z.limit);
     size_t o_wt = l.add<uint32_t>(kMaxWaves);
     size_t o_ra = l.add<uint32_t>(kRing * z.cap), o_rv = l.add<float>(kRing * z.cap), o_rval = l.add<float>(kRing * z.cap * z.s);
     size_t o_rt = l.add<float>(7 * z.ns), o_rl = l.add<uint32_t>(z.ns), o_rm = l.add<uint8_t>(z.ns), o_rlist = l.add<uint32_t>(2 * z.ns);
@@ -303,6 +305,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     d.bucket_count = reinterpret_cast<uint32_t*>(b + o_bc);
     d.bucket = reinterpret_cast<uint64_t*>(b + o_bk);
     d.block_winners = reinterpret_cast<uint32_t*>(b + o_bw);
+    d.block_winner_act = reinterpret_cast<float*>(b + o_bwa);
     d.block_count = reinterpret_cast<uint32_t*>(b + o_bn);
     d.block_cutoff = reinterpret_cast<float*>(b + o_bcut);
     d.wave_total = reinterpret_cast<uint32_t*>(b + o_wt);
@@ -525,7 +528,10 @@ void run_lanes(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     const uint32_t stride = P > 1 ? padded : count;
     KernelArgs a = kernel_args(h, reinterpret_cast<LaneDesc*>(h->lane_descs.base), count, P);
     a.lane_stride = stride;
-    void* params[] = {&a};
+    if (!h->kernel_args_buf.base) h->kernel_args_buf.allocate(sizeof(KernelArgs));
+    upload(h->kernel_args_buf.base, &a, sizeof(KernelArgs), h->stream);
+    const KernelArgs* device_args = reinterpret_cast<const KernelArgs*>(h->kernel_args_buf.base);
+    void* params[] = {&device_args};
     const void* kernel = h->phase_profile ? reinterpret_cast<const void*>(&leo_lane_steps_profiled)
                                           : reinterpret_cast<const void*>(&leo_lane_steps);
     if (h->phase_profile)
@@ -707,8 +713,14 @@ void upload_topology(LeoHipRuntime* h, const LeoModelView& m) {
         }
         for (uint64_t i = 0; i < z.f; ++i) row_count[m.in_target[sym * z.f + i]] = 0;
     }
+    // entries 0 and 1 of target n live at 2n and 2n+1; the rest at
+    // offsets[n] + (p - 2), after the 2N fixed entries
     std::vector<uint64_t> offsets(z.n + 1, 0);
-    for (uint64_t n = 0; n < z.n; ++n) offsets[n + 1] = offsets[n] + cap[n] + row_max[n];
+    offsets[0] = 2 * z.n;
+    for (uint64_t n = 0; n < z.n; ++n) {
+        const uint64_t need = cap[n] + row_max[n];
+        offsets[n + 1] = offsets[n] + (need > 2 ? need - 2 : 0);
+    }
     h->z.bucket_total = offsets[z.n];
     Layout l;
     size_t o_ex = l.add<float>(z.n), o_ty = l.add<uint8_t>(z.n), o_rt = l.add<uint32_t>(z.ns);
