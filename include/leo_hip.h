@@ -166,6 +166,9 @@ typedef struct LeoKernelStats {
      * lane spent working and waiting at the phase barrier. */
     double phase_work_us[8];
     double phase_wait_us[8];
+    /* Story lanes resident on the device at once; larger batches run in
+     * groups of this many lanes (sized from free device memory at creation). */
+    uint64_t resident_lanes;
 } LeoKernelStats;
 
 /* Selectors for leo_hip_parameter_changes (ParameterChanges, runtime.rs:37-46). */

@@ -239,7 +239,17 @@ struct MergeArgs {
     float weight_min, weight_max;
     unsigned long long* updates;
     uint32_t* error;
+    // Lane groups (batches larger than the resident lanes): kMergeAccumulate
+    // continues the lane-ordered f64 sum of each element in acc (and the
+    // any-lane-changed flag in any), starting from zero when `first`;
+    // kMergeFinalize applies acc / total_lanes to the canonical tensor.
+    uint32_t mode;
+    uint32_t first;
+    uint32_t total_lanes;
+    double* acc;
+    uint8_t* any;
 };
+enum : uint32_t { kMergeDirect = 0, kMergeAccumulate = 1, kMergeFinalize = 2 };
 
 }  // namespace leo
 

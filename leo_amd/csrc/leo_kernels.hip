@@ -1746,14 +1746,41 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
 // ---------------------------------------------------------------------------
 
 
+__device__ __forceinline__ float merge_project(const MergeArgs& m, uint64_t i, float v) {
+    switch (m.kind) {
+        case kMergeThreshold: return clampf(v, 0.05f, 2.0f);
+        case kMergeRecurrent:
+            v = clampf(v, m.weight_min, m.weight_max);
+            return m.neuron_type[i / m.synapses_per_neuron] == 0 ? maxnum(v, 0.0f) : fminf(v, 0.0f);
+        case kMergeInput: return clampf(v, 0.0f, m.weight_max);
+        case kMergeOutput:
+        case kMergeContextOut: return clampf(v, m.weight_min, m.weight_max);
+        default: return v;
+    }
+}
+
 __global__ void __launch_bounds__(kThreads) leo_merge_fixed(MergeArgs m) {
     unsigned long long local = 0;
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < m.count;
          i += static_cast<uint64_t>(gridDim.x) * kThreads) {
         uint64_t at = m.row ? (i / m.row) * m.stride + (i % m.row) : i;
         const float base = m.canonical[at];
+        if (m.mode == kMergeFinalize) {
+            if (!m.any[i]) continue;
+            float v = base + static_cast<float>(m.acc[i] / static_cast<double>(m.total_lanes));
+            if (!finitef(v)) atomicCAS(m.error, 0u, 2u);
+            v = merge_project(m, i, v);
+            if (!finitef(v)) atomicCAS(m.error, 0u, 3u);
+            m.canonical[at] = v;
+            local += 1;
+            continue;
+        }
         double sum = 0.0;
         bool any = false;
+        if (m.mode == kMergeAccumulate && !m.first) {
+            sum = m.acc[i];
+            any = m.any[i] != 0;
+        }
         for (uint32_t l = 0; l < m.lane_count; ++l) {
             float delta = m.lanes[l][at] - base;
             if (delta != 0.0f) {
@@ -1762,20 +1789,15 @@ __global__ void __launch_bounds__(kThreads) leo_merge_fixed(MergeArgs m) {
                 sum += static_cast<double>(delta);
             }
         }
+        if (m.mode == kMergeAccumulate) {
+            m.acc[i] = sum;
+            m.any[i] = any ? 1 : 0;
+            continue;
+        }
         if (!any) continue;
         float v = base + static_cast<float>(sum / static_cast<double>(m.lane_count));
         if (!finitef(v)) atomicCAS(m.error, 0u, 2u);
-        switch (m.kind) {
-            case kMergeThreshold: v = clampf(v, 0.05f, 2.0f); break;
-            case kMergeRecurrent:
-                v = clampf(v, m.weight_min, m.weight_max);
-                v = m.neuron_type[i / m.synapses_per_neuron] == 0 ? maxnum(v, 0.0f) : fminf(v, 0.0f);
-                break;
-            case kMergeInput: v = clampf(v, 0.0f, m.weight_max); break;
-            case kMergeOutput:
-            case kMergeContextOut: v = clampf(v, m.weight_min, m.weight_max); break;
-            default: break;
-        }
+        v = merge_project(m, i, v);
         if (!finitef(v)) atomicCAS(m.error, 0u, 3u);
         m.canonical[at] = v;
         local += 1;

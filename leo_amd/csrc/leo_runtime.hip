@@ -164,6 +164,8 @@ struct LeoHipRuntime {
     uint32_t max_lanes = 0;
     leo::Arena lane_descs;     // LaneDesc[max(1,max_lanes)]
     leo::Arena kernel_args_buf;  // KernelArgs of the step kernel
+    leo::Arena merge_acc;        // f64 sums + changed flags of the lane-group merge
+    uint32_t resident_lanes = 0; // story lanes that fit on the device at once
     leo::Arena merge_scratch;  // lane pointer table + counters
     // host copies of the read-only topology (device copies are immutable)
     std::vector<float> excitability;
@@ -855,21 +857,38 @@ std::vector<uint64_t> bits_to_indices(const std::vector<uint32_t>& bits, uint64_
     return out;
 }
 
+// Context tables and changed-slot bits of story lanes, queued for download on
+// the runtime stream (valid after the next synchronisation).
+void download_lane_contexts(LeoHipRuntime* h, const std::vector<Lane*>& lanes, std::vector<HostContext>& lane_ctx,
+                            std::vector<std::vector<uint32_t>>& lane_bits) {
+    for (Lane* l : lanes) {
+        lane_ctx.push_back(download_context(h, l->desc.p));
+        lane_bits.push_back(download_bits(h, l->desc.ch_ctx, h->z.slots));
+    }
+}
+
+size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<HostContext>& lane_ctx,
+                                const std::vector<std::vector<uint32_t>>& lane_bits);
+
 size_t merge_context(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
+    std::vector<HostContext> lane_ctx;
+    std::vector<std::vector<uint32_t>> lane_bits;
+    download_lane_contexts(h, lanes, lane_ctx, lane_bits);
+    return merge_context_downloaded(h, lane_ctx, lane_bits);
+}
+
+// Keyed context merge (parallel.rs:1169-1345) over every lane's downloaded tables.
+size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<HostContext>& lane_ctx,
+                                const std::vector<std::vector<uint32_t>>& lane_bits) {
     const Sizes& z = h->z;
     const size_t E = z.e;
     const uint64_t spo = h->cfg.device.context_slots_per_order;
     HostContext master = download_context(h, h->canon);
-    std::vector<HostContext> lane_ctx;
-    std::vector<std::vector<uint32_t>> lane_bits;
-    for (Lane* l : lanes) {
-        lane_ctx.push_back(download_context(h, l->desc.p));
-        lane_bits.push_back(download_bits(h, l->desc.ch_ctx, z.slots));
-    }
     sync(h->stream);
+    const size_t lanes = lane_ctx.size();
     // per-lane deltas against the pre-merge canonical (context_deltas_for_slots)
-    std::vector<std::vector<ContextDelta>> deltas(lanes.size());
-    for (size_t li = 0; li < lanes.size(); ++li) {
+    std::vector<std::vector<ContextDelta>> deltas(lanes);
+    for (size_t li = 0; li < lanes; ++li) {
         const HostContext& t = lane_ctx[li];
         for (uint64_t slot : bits_to_indices(lane_bits[li], z.slots)) {
             uint64_t key = t.keys[slot];
@@ -898,11 +917,11 @@ size_t merge_context(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
         uint64_t obs;
     };
     std::vector<Merged> merged;
-    std::vector<size_t> pos(lanes.size(), 0);
+    std::vector<size_t> pos(lanes, 0);
     while (true) {
         bool found = false;
         std::pair<size_t, uint64_t> next{0, 0};
-        for (size_t li = 0; li < lanes.size(); ++li)
+        for (size_t li = 0; li < lanes; ++li)
             if (pos[li] < deltas[li].size()) {
                 auto k = std::make_pair(deltas[li][pos[li]].order, deltas[li][pos[li]].key);
                 if (!found || k < next) {
@@ -912,7 +931,7 @@ size_t merge_context(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
             }
         if (!found) break;
         Merged m{next.first, next.second, std::vector<double>(E, 0.0), 0};
-        for (size_t li = 0; li < lanes.size(); ++li) {
+        for (size_t li = 0; li < lanes; ++li) {
             if (pos[li] < deltas[li].size() && deltas[li][pos[li]].order == next.first && deltas[li][pos[li]].key == next.second) {
                 const ContextDelta& d = deltas[li][pos[li]];
                 for (size_t e = 0; e < E; ++e) {
@@ -929,7 +948,7 @@ size_t merge_context(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
         if (a.obs != b.obs) return a.obs > b.obs;
         return std::make_pair(a.order, a.key) < std::make_pair(b.order, b.key);
     });
-    const double divisor = static_cast<double>(lanes.size());
+    const double divisor = static_cast<double>(lanes);
     for (const Merged& m : merged) {
         int64_t slot = resolve_context_slot(master, h->cfg, m.order, m.key, true, E);
         for (size_t e = 0; e < E; ++e)
@@ -959,8 +978,18 @@ size_t merge_context(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
     return merged.size();
 }
 
-// Device mean of every fixed-parameter tensor (parallel.rs:746-782).
-uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
+// f64 sums + changed flags for every fixed-parameter element (lane groups).
+size_t merge_accumulator_bytes(const Sizes& z) {
+    const uint64_t elements = z.n + z.ns + z.ni + z.n * kOutputs + kOutputs + kOutputs * z.e;
+    return static_cast<size_t>(elements) * 9;
+}
+
+// Device mean of every fixed-parameter tensor (parallel.rs:746-782). kMergeDirect
+// merges `lanes` into the canonical tensors; with lane groups, kMergeAccumulate
+// adds one group's lanes (in lane order) to the f64 accumulators and
+// kMergeFinalize applies them over `total_lanes`.
+uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes, uint32_t mode = kMergeDirect,
+                     bool first = true, uint32_t total_lanes = 0) {
     const Sizes& z = h->z;
     const uint32_t L = static_cast<uint32_t>(lanes.size());
     // scratch: 6 pointer tables of L entries + 1 counter + error word
@@ -998,8 +1027,20 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
         {h->canon.bias, 4, kOutputs, 0, 0},
         {h->canon.ctx_out, 5, kOutputs * z.e, 0, 0},
     };
+    uint64_t elements = 0;
+    for (int j = 0; j < 6; ++j) elements += jobs[j].count;
+    if (mode != kMergeDirect && h->merge_acc.bytes < elements * 9) h->merge_acc.allocate(elements * 9);
+    uint64_t acc_at = 0;
     for (int j = 0; j < 6; ++j) {
         MergeArgs m{};
+        m.mode = mode;
+        m.first = first ? 1u : 0u;
+        m.total_lanes = total_lanes;
+        if (mode != kMergeDirect) {
+            m.acc = reinterpret_cast<double*>(h->merge_acc.base) + acc_at;
+            m.any = reinterpret_cast<uint8_t*>(h->merge_acc.base + elements * 8) + acc_at;
+        }
+        acc_at += jobs[j].count;
         m.canonical = jobs[j].canonical;
         m.lanes = reinterpret_cast<const float* const*>(base + static_cast<size_t>(j) * L * sizeof(float*));
         m.lane_count = L;
@@ -1045,83 +1086,110 @@ Lane& story_lane(LeoHipRuntime* h, uint32_t index) {
 void story_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets, uint32_t count, int32_t permission,
                  float* losses_out, LeoBatchReport& rep) {
     if (count == 0) throw Error(LEO_ERR_INVALID_ARGUMENT, "training batch cannot be empty");
-    if (count > h->max_lanes)
-        throw Error(LEO_ERR_UNSUPPORTED, "story batch exceeds the runtime's max_lanes (" + std::to_string(h->max_lanes) + ")");
-    auto t0 = std::chrono::steady_clock::now();
-    std::vector<Lane*> lanes;
-    for (uint32_t i = 0; i < count; ++i) {
+    for (uint32_t i = 0; i < count; ++i)
         if (offsets[i + 1] <= offsets[i]) throw Error(LEO_ERR_UNSUPPORTED, "empty stories are not supported in a device batch");
-        Lane& l = story_lane(h, i);
-        copy_params(l.desc.p, h->canon, h->z, h->stream);  // fork(base.clone())
-        clear_changes(l, h->z, h->stream);                  // enable_parameter_tracking
-        lanes.push_back(&l);
-    }
-    reset_lane_objects(h, lanes, true, 0);  // Runtime::new (tick 0) + begin_document
-    std::vector<LaneRun> runs;
-    for (uint32_t i = 0; i < count; ++i) {
-        LaneRun r{lanes[i], {}, {}};
-        auto steps = document_steps(bytes + offsets[i], static_cast<size_t>(offsets[i + 1] - offsets[i]));
-        uint32_t tick = 0;
-        for (auto& st : steps) r.steps.push_back(make_step(h->cfg, *lanes[i], st.symbol, st.target, permission, tick++, true));
-        runs.push_back(std::move(r));
-    }
-    run_lanes(h, runs);
-    auto t1 = std::chrono::steady_clock::now();
-    // per-lane statistics deltas (parallel.rs:1115-1137) and revision increments
+    // stories run in groups of the lanes that fit on the device; the groups'
+    // lanes join the batch-end mean in story order
+    const uint32_t resident = std::max<uint32_t>(1, std::min(h->resident_lanes, h->max_lanes));
+    const uint32_t groups = (count + resident - 1) / resident;
     const uint32_t S = h->cfg.device.synapses_per_neuron;
     LeoStatistics merged = h->stats;
     uint64_t revision_increment = 0;
     double weighted = 0.0;
     uint64_t targets = 0;
     size_t cursor = 0;
-    for (uint32_t i = 0; i < count; ++i) {
-        LeoStatistics st = h->stats;  // the forked worker starts from the canonical statistics
-        double loss_sum = 0.0;
-        uint64_t steps_with_loss = 0;
-        bool activity = false;
-        for (size_t k = 0; k < runs[i].steps.size(); ++k) {
-            const StepParams& sp = runs[i].steps[k];
-            const StepRecord& rec = runs[i].records[k];
-            float loss = step_loss(sp, rec);
-            account_step(st, sp, rec, loss, S);
-            if (!(sp.flags & kStepFrozen)) activity = true;
-            if (sp.flags & kStepLearn) revision_increment += 1;
-            float recorded = sp.target_index >= 0 ? loss : 0.0f;  // record_training_step
-            loss_sum += static_cast<double>(recorded);
-            steps_with_loss += 1;
-            if (losses_out) losses_out[cursor++] = recorded;
-            rep.activity_steps += 1;
-            rep.active_neurons_sum += rec.active;
-            rep.emitted_events += static_cast<uint64_t>(rec.active) * S;
+    double run_seconds = 0.0, merge_seconds = 0.0;
+    std::vector<HostContext> group_ctx;
+    std::vector<std::vector<uint32_t>> group_bits;
+    std::vector<Lane*> lanes;
+    for (uint32_t g = 0; g < groups; ++g) {
+        auto t0 = std::chrono::steady_clock::now();
+        const uint32_t lo = g * resident, hi = std::min(count, lo + resident);
+        lanes.clear();
+        for (uint32_t i = lo; i < hi; ++i) {
+            Lane& l = story_lane(h, i - lo);
+            copy_params(l.desc.p, h->canon, h->z, h->stream);  // fork(base.clone())
+            clear_changes(l, h->z, h->stream);                  // enable_parameter_tracking
+            lanes.push_back(&l);
         }
-        if (activity) st.processed_stories += 1;  // finish_document
-        double mean = loss_sum / static_cast<double>(std::max<uint64_t>(steps_with_loss, 1));
-        weighted += mean * static_cast<double>(steps_with_loss);
-        targets += steps_with_loss;
-        merged.processed_bytes += st.processed_bytes - h->stats.processed_bytes;
-        merged.processed_stories += st.processed_stories - h->stats.processed_stories;
-        merged.training_loss_sum += st.training_loss_sum - h->stats.training_loss_sum;
-        merged.training_targets += st.training_targets - h->stats.training_targets;
-        merged.active_neurons_sum += st.active_neurons_sum - h->stats.active_neurons_sum;
-        merged.active_neurons_peak = std::max(merged.active_neurons_peak, st.active_neurons_peak);
-        merged.synaptic_events += st.synaptic_events - h->stats.synaptic_events;
-        merged.persistent_ticks += st.persistent_ticks - h->stats.persistent_ticks;
+        reset_lane_objects(h, lanes, true, 0);  // Runtime::new (tick 0) + begin_document
+        std::vector<LaneRun> runs;
+        for (uint32_t i = lo; i < hi; ++i) {
+            LaneRun r{lanes[i - lo], {}, {}};
+            auto steps = document_steps(bytes + offsets[i], static_cast<size_t>(offsets[i + 1] - offsets[i]));
+            uint32_t tick = 0;
+            for (auto& st : steps)
+                r.steps.push_back(make_step(h->cfg, *lanes[i - lo], st.symbol, st.target, permission, tick++, true));
+            runs.push_back(std::move(r));
+        }
+        run_lanes(h, runs);
+        auto t1 = std::chrono::steady_clock::now();
+        run_seconds += std::chrono::duration<double>(t1 - t0).count();
+        // per-lane statistics deltas (parallel.rs:1115-1137) and revision increments
+        for (uint32_t i = lo; i < hi; ++i) {
+            const LaneRun& run = runs[i - lo];
+            LeoStatistics st = h->stats;  // the forked worker starts from the canonical statistics
+            double loss_sum = 0.0;
+            uint64_t steps_with_loss = 0;
+            bool activity = false;
+            for (size_t k = 0; k < run.steps.size(); ++k) {
+                const StepParams& sp = run.steps[k];
+                const StepRecord& rec = run.records[k];
+                float loss = step_loss(sp, rec);
+                account_step(st, sp, rec, loss, S);
+                if (!(sp.flags & kStepFrozen)) activity = true;
+                if (sp.flags & kStepLearn) revision_increment += 1;
+                float recorded = sp.target_index >= 0 ? loss : 0.0f;  // record_training_step
+                loss_sum += static_cast<double>(recorded);
+                steps_with_loss += 1;
+                if (losses_out) losses_out[cursor++] = recorded;
+                rep.activity_steps += 1;
+                rep.active_neurons_sum += rec.active;
+                rep.emitted_events += static_cast<uint64_t>(rec.active) * S;
+            }
+            if (activity) st.processed_stories += 1;  // finish_document
+            double mean = loss_sum / static_cast<double>(std::max<uint64_t>(steps_with_loss, 1));
+            weighted += mean * static_cast<double>(steps_with_loss);
+            targets += steps_with_loss;
+            merged.processed_bytes += st.processed_bytes - h->stats.processed_bytes;
+            merged.processed_stories += st.processed_stories - h->stats.processed_stories;
+            merged.training_loss_sum += st.training_loss_sum - h->stats.training_loss_sum;
+            merged.training_targets += st.training_targets - h->stats.training_targets;
+            merged.active_neurons_sum += st.active_neurons_sum - h->stats.active_neurons_sum;
+            merged.active_neurons_peak = std::max(merged.active_neurons_peak, st.active_neurons_peak);
+            merged.synaptic_events += st.synaptic_events - h->stats.synaptic_events;
+            merged.persistent_ticks += st.persistent_ticks - h->stats.persistent_ticks;
+        }
+        if (groups > 1) {
+            merge_fixed(h, lanes, kMergeAccumulate, g == 0, count);
+            download_lane_contexts(h, lanes, group_ctx, group_bits);
+            sync(h->stream);
+            merge_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
+        }
     }
     // batch-end mean (parallel.rs:715-798): fixed tensors on the device, keyed context on the host
-    uint64_t fixed = merge_fixed(h, lanes);
-    uint64_t ctx = merge_context(h, lanes);
+    auto t2 = std::chrono::steady_clock::now();
+    uint64_t fixed, ctx;
+    if (groups == 1) {
+        fixed = merge_fixed(h, lanes);
+        ctx = merge_context(h, lanes);
+    } else {
+        fixed = merge_fixed(h, {}, kMergeFinalize, false, count);
+        ctx = merge_context_downloaded(h, group_ctx, group_bits);
+    }
     h->stats = merged;
     h->revision += revision_increment;
     canonical_reset(h);  // runtime.reset_transient_state() after the merge
-    auto t2 = std::chrono::steady_clock::now();
+    auto t3 = std::chrono::steady_clock::now();
+    merge_seconds += std::chrono::duration<double>(t3 - t2).count();
     rep.mean_loss = weighted / static_cast<double>(std::max<uint64_t>(targets, 1));
     rep.targets = targets;
     rep.stories = count;
     rep.merge_workers = count;
     rep.merge_fixed_parameter_updates = fixed;
     rep.merge_context_keys = ctx;
-    rep.story_seconds += std::chrono::duration<double>(t1 - t0).count();
-    rep.merge_seconds += std::chrono::duration<double>(t2 - t1).count();
+    rep.story_seconds += run_seconds;
+    rep.merge_seconds += merge_seconds;
 }
 
 // training.rs:1782-1830
@@ -1348,6 +1416,17 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         std::vector<leo::Lane*> lanes{h->canonical.get()};
         leo::reset_lane_objects(h.get(), lanes, true, 0);  // Runtime::new: tick 0, empty state
         leo::sync(h->stream);
+        // story lanes resident at once: the first lane is allocated now to
+        // measure it; larger batches run in groups of this many lanes
+        leo::Lane& first = leo::story_lane(h.get(), 0);
+        const size_t per_lane = first.state.bytes + first.params.bytes;
+        size_t free_bytes = 0, total_bytes = 0;
+        LEO_HIP_CHECK(hipMemGetInfo(&free_bytes, &total_bytes));
+        const size_t reserve = leo::merge_accumulator_bytes(h->z) + (size_t(1) << 30);
+        const size_t fit = free_bytes > reserve ? (free_bytes - reserve) / std::max<size_t>(per_lane, 1) : 0;
+        h->resident_lanes = static_cast<uint32_t>(std::min<size_t>(h->max_lanes, 1 + fit));
+        if (const char* env = std::getenv("LEO_HIP_RESIDENT_LANES"))
+            h->resident_lanes = std::max<uint32_t>(1, std::min<uint32_t>(h->resident_lanes, std::atoi(env)));
         *out = h.release();
     });
 }
@@ -1678,7 +1757,10 @@ uint64_t leo_hip_current_tick(const LeoHipRuntime* h) { return h ? h->canonical-
 int32_t leo_hip_kernel_stats(LeoHipRuntime* h, LeoKernelStats* out, int32_t reset) {
     return guarded([&] {
         leo::BusyGuard g(h);
-        if (out) *out = h->telemetry;
+        if (out) {
+            *out = h->telemetry;
+            out->resident_lanes = h->resident_lanes;
+        }
         if (reset) h->telemetry = LeoKernelStats{};
     });
 }

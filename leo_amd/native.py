@@ -123,6 +123,7 @@ class LeoKernelStats(ctypes.Structure):
         ("kept_rec", ctypes.c_uint64), ("kept_in", ctypes.c_uint64), ("destinations", ctypes.c_uint64),
         ("active_inhibitory", ctypes.c_uint64), ("merge_launches", ctypes.c_uint64), ("merge_ms", ctypes.c_double),
         ("phase_work_us", ctypes.c_double * 8), ("phase_wait_us", ctypes.c_double * 8),
+        ("resident_lanes", ctypes.c_uint64),
     ]
 
 

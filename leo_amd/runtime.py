@@ -265,6 +265,11 @@ class HipRuntime:
         return out
 
     @property
+    def resident_lanes(self) -> int:
+        """Story lanes held on the device at once (larger batches run in groups)."""
+        return int(self.kernel_stats()["resident_lanes"])
+
+    @property
     def current_tick(self) -> int:
         return int(self._lib.leo_hip_current_tick(self._handle))
 

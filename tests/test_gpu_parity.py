@@ -140,3 +140,26 @@ def test_train_batch_with_replay_parity(require_gpu, oracle, make):
         assert grep.replay_prefix_steps == crep.replay_prefix_steps
     assert_models_equal(gpu.model(), cpu.model(), make)
     gpu.close()
+
+
+@pytest.mark.parametrize("make", ["test_toml", "small_redundant"])
+def test_story_batch_in_lane_groups_parity(require_gpu, oracle, make, monkeypatch):
+    # 5 stories with 2 resident lanes: groups 2+2+1 accumulate the lane-ordered
+    # f64 mean and the keyed context merge across groups
+    monkeypatch.setenv("LEO_HIP_RESIDENT_LANES", "2")
+    cfg = toml_test_config() if make == "test_toml" else small_redundant_config()
+    model = Model.initialize(cfg)
+    stories = [story(500 + k, 40 + 13 * k) for k in range(5)]
+    cpu = oracle.OracleRuntime(model)
+    gpu = _runtime(model)
+    assert gpu.resident_lanes == 2
+    for replay in (False, True):
+        crep, closs = cpu.train_story_batch(stories, oracle.TRAINING, replay=replay)
+        grep, gloss = gpu.train_batch(stories, native.TRAINING, replay=replay)
+        for a, b in zip(gloss, closs):
+            assert np.array_equal(a, b)
+        assert grep.merge_fixed_parameter_updates == crep.merge_fixed_parameter_updates
+        assert grep.merge_context_keys == crep.merge_context_keys
+        assert grep.mean_loss == crep.mean_loss
+    assert_models_equal(gpu.model(), cpu.model(), make)
+    gpu.close()
