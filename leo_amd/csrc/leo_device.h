@@ -23,11 +23,31 @@ constexpr uint32_t kWaveSize = 64;
 constexpr uint32_t kWavesPerGroup = kThreads / kWaveSize;
 constexpr uint32_t kMaxWaves = 1024;     // selecting waves per lane (workgroups per lane <= 256)
 
-// Dynamic LDS of the step kernel: per wave a u64 candidate list, a u32
-// touched list and an f32 margin list of one block each; the binding-cap
-// global sort (up to kMaxBlockNeurons keys) reuses the front.
+// Touched-neuron bitmap: each block owns ceil(neurons_per_block/32) words,
+// so no word is shared by two blocks (and no two selecting waves).
+inline __host__ __device__ uint32_t block_words(uint32_t neurons_per_block) { return (neurons_per_block + 31) / 32; }
+
+// Phase-2 window of a selecting wave: touched neurons folded and ranked at
+// once (at least one whole block, so a block never spans two windows).
+constexpr uint32_t kGroupBlocks = 64;    // blocks per bitmap load round
+constexpr uint32_t kWordsPerLane = 8;    // bitmap words per lane per load round
+inline __host__ __device__ uint32_t window_capacity(uint32_t neurons_per_block) {
+    return neurons_per_block > 256 ? neurons_per_block : 256;
+}
+// Per-wave bytes of the window: u64 keys and u32 entries (capacity each),
+// block cutoff keys (G), block starts (G+1), block candidate counts and
+// staged winner offsets (G each), and
+// the group's bitmap words with their list positions (64*kWordsPerLane each).
+inline __host__ __device__ size_t window_bytes(uint32_t neurons_per_block) {
+    const size_t c = window_capacity(neurons_per_block);
+    const size_t words = 64 * kWordsPerLane;
+    return (c * 12 + kGroupBlocks * 8 + (kGroupBlocks + 1) * 4 + kGroupBlocks * 8 + words * 8 + 15) / 16 * 16;
+}
+
+// Dynamic LDS of the step kernel: one phase-2 window per wave; the
+// binding-cap global sort (up to kMaxBlockNeurons keys) reuses the front.
 inline size_t step_lds_bytes(uint32_t neurons_per_block) {
-    const size_t lists = static_cast<size_t>(kWavesPerGroup) * neurons_per_block * (8 + 4 + 4);
+    const size_t lists = static_cast<size_t>(kWavesPerGroup) * window_bytes(neurons_per_block);
     const size_t sort = static_cast<size_t>(kMaxBlockNeurons) * 8;
     return ((lists > sort ? lists : sort) + 15) / 16 * 16;
 }
@@ -151,17 +171,18 @@ struct LaneDesc {
     uint32_t* touched_epoch; // == tick+1 when touched this tick
     uint32_t* touched_list;  // N
     uint32_t* selected_epoch;
-    float* surrogate;
     uint32_t* dest_epoch;
     float* learning_signal;
     uint32_t* bucket_count;  // N
     uint64_t* bucket;        // 2 words per entry: delivery-order key, value bits
     // block selection
-    uint32_t* block_winners; // blocks * max_active_per_block
-    float* block_winner_act; // blocks * max_active_per_block: activation of each winner
-    uint32_t* block_count;   // blocks
+    uint32_t* range_winners; // blocks * max_active_per_block: winners of each selecting wave's block
+                             // range in block order, compacted from the row of its first block
+    float* range_winner_act; // same layout: activation of each winner
     float* block_cutoff;     // blocks
-    uint32_t* wave_total;    // kMaxWaves: block winners per selecting wave (block-range owner)
+    uint32_t* block_epoch;   // blocks: tick+1 when the block's selection above is current
+    uint32_t* touched_bits;  // blocks * block_words: neurons touched this tick, cleared by phase 2
+    uint32_t* wave_total;    // kMaxWaves: block winners of each selecting wave's block range
     // ring: per slot, up to max_active_global active neurons, activation, and S snapshot values each
     uint32_t* ring_active;   // kRing * cap
     float* ring_act;         // kRing * cap

@@ -110,13 +110,29 @@ __device__ __forceinline__ uint32_t wave_append(uint32_t* counter, bool pred) {
     const uint32_t leader = static_cast<uint32_t>(__ffsll(static_cast<long long>(mask)) - 1);
     uint32_t base = 0;
     if (lane == leader) base = atomicAdd(counter, static_cast<uint32_t>(__popcll(mask)));
-    base = __shfl(base, static_cast<int>(leader));
+    base = __builtin_amdgcn_readlane(base, static_cast<int>(leader));
     return base + static_cast<uint32_t>(__popcll(mask & ((1ULL << lane) - 1ULL)));
 }
 
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+// Inclusive prefix sum over the wave by DPP row shifts (within 16-lane rows)
+// and row broadcasts (lane 15 into rows 1 and 3, lane 31 into rows 2 and 3):
+// VALU data movement without an LDS round trip. Every lane must be active.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), kCtrl, kRowMask, 0xf, true));
+}
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+    v += dpp_u32<0x111, 0xf>(v);  // row_shr:1
+    v += dpp_u32<0x112, 0xf>(v);  // row_shr:2
+    v += dpp_u32<0x114, 0xf>(v);  // row_shr:4
+    v += dpp_u32<0x118, 0xf>(v);  // row_shr:8
+    v += dpp_u32<0x142, 0xa>(v);  // row_bcast:15
+    v += dpp_u32<0x143, 0xc>(v);  // row_bcast:31
     return v;
+}
+// Sum over the wave (every lane must be active), uniform.
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+    return __builtin_amdgcn_readlane(wave_incl_scan_u32(v), kWaveSize - 1);
 }
 __device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long v) {
     for (int off = 32; off > 0; off >>= 1) {
@@ -132,6 +148,12 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
     }
     return v;
 }
+// Index of the calling wave in its workgroup, known to the compiler as uniform
+// (values derived from it live in scalar registers).
+__device__ __forceinline__ uint32_t wave_index() {
+    return __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
+}
+
 // Orders LDS traffic between lanes of one wave (the wave executes in lockstep;
 // this keeps the compiler from moving LDS accesses across the point).
 __device__ __forceinline__ void wave_sync() {
@@ -168,7 +190,7 @@ __device__ __forceinline__ uint32_t xcc_id() {
 // waiting until this thread's stores have completed to L2 is the whole release
 // and nothing needs invalidating. Otherwise agent-scope release/acquire fences
 // write back and invalidate the L2 so other XCDs see the data.
-__device__ bool lane_barrier(LaneControl* ctl, uint32_t P, uint32_t& target, uint32_t spin_limit, bool local) {
+__device__ __forceinline__ bool lane_barrier(LaneControl* ctl, uint32_t P, uint32_t& target, uint32_t spin_limit, bool local) {
     __shared__ uint32_t s_abort;
     if (P == 1) {
         __syncthreads();
@@ -262,9 +284,8 @@ struct alignas(16) StepShared {
     uint32_t ring_count[kRing];
 };
 
-// Dynamic LDS (step_lds_bytes): per wave a candidate-key list and a touched
-// list of neurons_per_block entries each; the binding-cap global sort reuses
-// the front.
+// Dynamic LDS (step_lds_bytes): one phase-2 window per wave (Window below);
+// the binding-cap global sort reuses the front.
 extern __shared__ __align__(16) unsigned char step_lds[];
 
 struct StepCtx {
@@ -306,7 +327,7 @@ __device__ __forceinline__ float advance_trace(float* planes, uint64_t plane, ui
 
 // Late fields of a step record: work counters complete only after the step's
 // last barrier, so the record is finished by the next step (or kernel end).
-__device__ void finalize_record(const LaneDesc& d, LaneControl* ctl, uint32_t step_index, uint32_t tick) {
+__device__ __forceinline__ void finalize_record(const LaneDesc& d, LaneControl* ctl, uint32_t step_index, uint32_t tick) {
     StepRecord& rec = d.records[step_index];
     const uint32_t k = tick & 1;
     rec.events = ld(&ctl->tick_events[k]);
@@ -323,7 +344,7 @@ __device__ __forceinline__ uint64_t bucket_entry(const SharedModel& m, uint32_t 
     return p < 2 ? 2ull * n + p : m.bucket_offset[n] + (p - 2);
 }
 
-__device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t step_index, const StepShared& sh) {
+__device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t step_index, const StepShared& sh) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -436,14 +457,19 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t s
         if (new_rec) d.rec_list[static_cast<uint64_t>(c.parity) * NS + pos] = eslot;
         pos = wave_append(&ctl->in_count[c.parity], new_in);
         if (new_in) d.in_list[static_cast<uint64_t>(c.parity) * NI + pos] = eslot;
-        // touched mark (every writer stores the same epoch; the touched list is
-        // built per block in phase 2)
-        if (touch_n != 0xffffffffu) d.touched_epoch[touch_n] = tick + 1;
         if (scatter) {
             const uint32_t p = atomicAdd(&d.bucket_count[target], 1u);
             const uint64_t at = bucket_entry(a.m, target, p);
             d.bucket[2 * at] = key;
             d.bucket[2 * at + 1] = __float_as_uint(value);
+        }
+        // touched marks: the epoch for phase 3, and the block's bitmap bit for
+        // phase 2 (setting a bit is idempotent, so every touch sets it)
+        if (touch_n != 0xffffffffu) {
+            const uint32_t nb = cfg.neurons_per_block;
+            const uint32_t blk = touch_n / nb, off = touch_n - blk * nb;
+            d.touched_epoch[touch_n] = tick + 1;
+            atomicOr(&d.touched_bits[blk * block_words(nb) + off / 32], 1u << (off & 31));
         }
     }
     add_count(&ctl->tick_events[tick & 1], delivered);
@@ -455,7 +481,7 @@ __device__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t s
 // drive and top-k on one wave per block (runtime.rs:576-603, 701-708,
 // 940-1011, 787-803).
 // ---------------------------------------------------------------------------
-__device__ void context_resolve(const StepCtx& c, const StepParams& sp, StepShared& sh) {
+__device__ __forceinline__ void context_resolve(const StepCtx& c, const StepParams& sp, StepShared& sh) {
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = c.d;
     LaneControl* ctl = c.ctl;
@@ -593,7 +619,7 @@ __device__ __forceinline__ void sort8(uint64_t (&k)[8], uint32_t (&v)[8]) {
 // delivered values in CPU delivery order (runtime.rs:605-639, 701-708), and,
 // unless refractory, applies the drive (runtime.rs:940-975). Returns the
 // margin membrane - threshold; *refractory tells whether the neuron skipped.
-__device__ float fold_drive(const StepCtx& c, uint32_t n, float pi, bool* refractory) {
+__device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float pi, bool* refractory) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -710,127 +736,188 @@ __device__ __forceinline__ float surrogate_value(const LeoConfig& cfg, bool refr
     return analog_rank_surrogate(margin, cutoff, selected, cfg.surrogate_width, cfg.surrogate_gain);
 }
 
-// One wave: fold, drive and top-k of block b (runtime.rs:940-1011). The
-// block's touched neurons are gathered first (all flag loads in flight at
-// once) and processed densely; candidates (activation > 0) are compacted into
-// the wave's LDS list, and each candidate's rank is the number of smaller
-// (activation desc, tie asc) keys, i.e. its position in the reference's
-// sorted order (keys are unique).
-constexpr uint32_t kMaxChunksPerBlock = kMaxBlockNeurons / kWaveSize;
-constexpr uint32_t kRefractoryBit = 0x80000000u;
+// Phase-2 window of one wave in dynamic LDS (window_bytes per wave): the
+// touched neurons of a group of blocks in neuron order, their selection keys,
+// and per group block its first list position, candidate count and the key of
+// rank `limit`; plus the group's bitmap words and their list positions.
+struct Window {
+    uint64_t* key;     // capacity: selection key, ~0 for a non-candidate
+    uint64_t* cut;     // kGroupBlocks
+    uint32_t* entry;   // capacity: (group block << 16) | offset in the block
+    uint32_t* start;   // kGroupBlocks + 1
+    uint32_t* cands;   // kGroupBlocks
+    uint32_t* woff;    // kGroupBlocks: first staged winner position of each group block
+    uint32_t* bits;    // kWaveSize * kWordsPerLane: bitmap words of the group
+    uint32_t* pos;     // kWaveSize * kWordsPerLane: list position of each word's first bit
+};
 
-__device__ uint32_t select_block(const StepCtx& c, uint32_t b, float pi, uint64_t* cand, uint32_t* tl, float* tmar) {
+static_assert(kGroupBlocks == kWaveSize, "one lane per group block");
+static_assert(kMaxBlockNeurons <= 0x10000u, "window entries hold a 16-bit offset in the block");
+
+__device__ __forceinline__ Window wave_window(uint32_t wave, uint32_t nb) {
+    unsigned char* base = step_lds + static_cast<size_t>(wave) * window_bytes(nb);
+    const uint32_t cap = window_capacity(nb);
+    Window w;
+    w.key = reinterpret_cast<uint64_t*>(base);
+    w.cut = w.key + cap;
+    w.entry = reinterpret_cast<uint32_t*>(w.cut + kGroupBlocks);
+    w.start = w.entry + cap;
+    w.cands = w.start + kGroupBlocks + 1;
+    w.woff = w.cands + kGroupBlocks;
+    w.bits = w.woff + kGroupBlocks;
+    w.pos = w.bits + kWaveSize * kWordsPerLane;
+    return w;
+}
+
+// Phase 2: each wave owns a range of blocks and takes it in groups of up to
+// kGroupBlocks blocks. Per group it loads (and clears) the group's touched
+// bitmap in one round of coalesced loads, lists the touched neurons in neuron
+// order, folds and drives them one lane each, and ranks every candidate within
+// its block: a candidate's rank is the number of smaller (activation desc, tie
+// asc) keys of its block, i.e. its position in the reference's sorted order
+// (runtime.rs:987-1011; keys are unique); rank `limit` gives the block cutoff.
+// The winners of the wave's range are staged in block order (runtime.rs:
+// 1010-1013), compacted from the range's first block row, so that phase 3
+// reads them in one round. A group with more touched neurons than the window
+// holds is taken in windows of whole blocks.
+__device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
     const uint32_t N = cfg.neuron_count, nb = cfg.neurons_per_block, limit = cfg.max_active_per_block;
     const uint32_t tick = c.tick, rot = tick % N;
-    const uint32_t lane = __lane_id();
-    const unsigned long long below = (1ULL << lane) - 1ULL;
-    const uint32_t chunks = (nb + kWaveSize - 1) / kWaveSize;
-    const uint32_t first = b * nb;
-    uint32_t tmask = 0;
-#pragma unroll
-    for (uint32_t k = 0; k < kMaxChunksPerBlock; ++k) {
-        const uint32_t idx = k * kWaveSize + lane;
-        if (k < chunks && idx < nb && ld(&d.touched_epoch[first + idx]) == tick + 1) tmask |= 1u << k;
-    }
-    uint32_t touched = 0;
-    for (uint32_t k = 0; k < chunks; ++k) {
-        const bool t = (tmask >> k) & 1u;
-        const unsigned long long mask = __ballot(t);
-        if (t) tl[touched + __popcll(mask & below)] = first + k * kWaveSize + lane;
-        touched += static_cast<uint32_t>(__popcll(mask));
-    }
-    // reserve this block's range of the lane's touched list (used after the fold)
-    uint32_t list_at = 0;
-    if (lane == 0 && touched) list_at = atomicAdd(&c.ctl->tick_touched[tick & 1], touched);
-    wave_sync();
-    uint32_t count = 0;
-    for (uint32_t base = 0; base < touched; base += kWaveSize) {
-        const uint32_t i = base + lane;
-        bool candidate = false;
-        uint64_t key = 0;
-        if (i < touched) {
-            const uint32_t n = tl[i];
-            bool refractory = false;
-            const float margin = fold_drive(c, n, pi, &refractory);
-            tmar[i] = margin;
-            if (refractory) tl[i] = n | kRefractoryBit;
-            const float act = clampf(margin, 0.0f, 1.0f);
-            if (!refractory && act > 0.0f) {
-                candidate = true;
-                key = selection_key(act, (n + N - rot) % N);
-            }
-        }
-        const unsigned long long mask = __ballot(candidate);
-        if (candidate) cand[count + __popcll(mask & below)] = key;
-        count += static_cast<uint32_t>(__popcll(mask));
-    }
-    wave_sync();
-    // ranks: winners go to their sorted position, rank `limit` gives the cutoff
-    unsigned long long cut_key = ~0ULL;
-    for (uint32_t base = 0; base < count; base += kWaveSize) {
-        const uint32_t i = base + lane;
-        const uint64_t mine = i < count ? cand[i] : ~0ULL;
-        uint32_t rank = 0;
-        for (uint32_t j = 0; j < count; ++j) rank += cand[j] < mine ? 1u : 0u;
-        if (i < count && rank < limit) {
-            d.block_winners[static_cast<uint64_t>(b) * limit + rank] = (static_cast<uint32_t>(mine) + rot) % N;
-            d.block_winner_act[static_cast<uint64_t>(b) * limit + rank] = key_activation(mine);
-        }
-        const unsigned long long cut = wave_min_u64(i < count && rank == limit ? mine : ~0ULL);
-        cut_key = cut < cut_key ? cut : cut_key;
-    }
-    const uint32_t winners = count < limit ? count : limit;
-    const float cutoff = cut_key != ~0ULL ? key_activation(cut_key) : 0.0f;
-    if (lane == 0) {
-        d.block_count[b] = winners;
-        d.block_cutoff[b] = cutoff;
-        if (count) atomicAdd(&c.ctl->tick_supra[tick & 1], count);
-    }
-    if (a.redundant_global) {
-        // the global cap cannot bind: activation and selection marks of the
-        // winners and surrogates of the touched (runtime.rs:1060-1067, 787-803);
-        // a candidate wins iff its key is below the rank-`limit` key
-        for (uint32_t i = lane; i < touched; i += kWaveSize) {
-            const uint32_t entry = tl[i];
-            const uint32_t n = entry & ~kRefractoryBit;
-            const bool refractory = (entry & kRefractoryBit) != 0;
-            const float margin = tmar[i];
-            bool won = false;
-            if (!refractory) {
-                const float act = clampf(margin, 0.0f, 1.0f);
-                won = act > 0.0f && selection_key(act, (n + N - rot) % N) < cut_key;
-                if (won) {
-                    d.activation[n] = act;
-                    d.selected_epoch[n] = tick + 1;
-                }
-            }
-            d.surrogate[n] = surrogate_value(cfg, refractory, margin, cutoff, won);
-        }
-    }
-    list_at = __shfl(list_at, 0);
-    for (uint32_t i = lane; i < touched; i += kWaveSize) d.touched_list[list_at + i] = tl[i] & ~kRefractoryBit;
-    wave_sync();
-    return winners;
-}
-
-__device__ void phase_fold_select(const StepCtx& c) {
-    const LeoConfig& cfg = c.a->cfg;
-    const uint32_t wave = threadIdx.x / kWaveSize, lane = __lane_id();
+    const uint32_t wave = wave_index(), lane = __lane_id();
     const uint32_t nwaves = c.P * kWavesPerGroup;
     const uint32_t wv = c.part * kWavesPerGroup + wave;
-    const uint32_t per = (cfg.block_count + nwaves - 1) / nwaves;
-    const uint32_t b0 = wv * per, b1 = min(cfg.block_count, b0 + per);
+    const uint32_t range = (cfg.block_count + nwaves - 1) / nwaves;
+    const uint32_t b0 = min(cfg.block_count, wv * range), b1 = min(cfg.block_count, b0 + range);
+    const uint32_t wpb = block_words(nb);
+    const uint32_t group = min(kGroupBlocks, kWaveSize * kWordsPerLane / wpb);
+    const uint32_t cap = window_capacity(nb);
     const float pi = ld(&c.ctl->population_inhibition);
-    uint32_t total = 0;
-    const uint32_t nb = cfg.neurons_per_block;
-    uint64_t* cand = reinterpret_cast<uint64_t*>(step_lds) + static_cast<size_t>(wave) * nb;
-    uint32_t* tl = reinterpret_cast<uint32_t*>(step_lds + static_cast<size_t>(kWavesPerGroup) * nb * 8) + wave * nb;
-    float* tmar = reinterpret_cast<float*>(step_lds + static_cast<size_t>(kWavesPerGroup) * nb * 12) + wave * nb;
-    for (uint32_t b = b0; b < b1; ++b) total += select_block(c, b, pi, cand, tl, tmar);
-    if (lane == 0) c.d.wave_total[wv] = total;
+    const Window w = wave_window(wave, nb);
+    w.cands[lane] = 0;
+    w.cut[lane] = ~0ULL;
+    const uint64_t row0 = static_cast<uint64_t>(b0) * limit;
+    uint32_t supra = 0, staged = 0;
+    for (uint32_t gb = b0; gb < b1; gb += group) {
+        const uint32_t gn = min(group, b1 - gb), gw = gn * wpb;
+        uint32_t* bits = d.touched_bits + static_cast<uint64_t>(gb) * wpb;
+        uint32_t word[kWordsPerLane];
+#pragma unroll
+        for (uint32_t k = 0; k < kWordsPerLane; ++k) {
+            const uint32_t at = k * kWaveSize + lane;
+            word[k] = at < gw ? ld(&bits[at]) : 0u;
+        }
+        // list positions in word order (row k holds words k*64 .. k*64+63)
+        uint32_t total = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < kWordsPerLane; ++k) {
+            const uint32_t at = k * kWaveSize + lane;
+            if (k * kWaveSize < gw) {
+                const uint32_t cnt = __popc(word[k]);
+                const uint32_t incl = wave_incl_scan_u32(cnt);
+                const uint32_t p = total + incl - cnt;
+                w.bits[at] = word[k];
+                w.pos[at] = p;
+                if (at < gw && at % wpb == 0) w.start[at / wpb] = p;
+                if (word[k]) bits[at] = 0u;
+                total += __builtin_amdgcn_readlane(incl, kWaveSize - 1);
+            }
+        }
+        if (lane == 0) w.start[gn] = total;
+        uint32_t list_at = 0;
+        if (lane == 0 && total) list_at = atomicAdd(&c.ctl->tick_touched[tick & 1], total);
+        wave_sync();
+        for (uint32_t lo = 0; lo < total;) {
+            uint32_t hi = total;
+            if (total - lo > cap) {
+                // the last block boundary within the window (a block holds at most nb <= cap)
+                uint32_t best = lo;
+                for (uint32_t g = lane; g <= gn; g += kWaveSize) {
+                    const uint32_t st = w.start[g];
+                    if (st <= lo + cap && st > best) best = st;
+                }
+                hi = static_cast<uint32_t>(wave_max_u64(best));
+            }
+            for (uint32_t k = 0; k < kWordsPerLane; ++k) {
+                const uint32_t at = k * kWaveSize + lane;
+                if (at >= gw) break;
+                uint32_t v = w.bits[at], p = w.pos[at];
+                if (p >= hi || p + __popc(v) <= lo) continue;
+                const uint32_t g = at / wpb, base = (at - g * wpb) * 32;
+                while (v) {
+                    const uint32_t bit = __ffs(v) - 1;
+                    v &= v - 1;
+                    if (p >= lo && p < hi) w.entry[p - lo] = (g << 16) | (base + bit);
+                    ++p;
+                }
+            }
+            wave_sync();
+            const uint32_t cnt = hi - lo;
+            const uint32_t listed = __builtin_amdgcn_readfirstlane(list_at) + lo;
+            for (uint32_t i = lane; i < cnt; i += kWaveSize) {
+                const uint32_t e = w.entry[i];
+                const uint32_t g = e >> 16;
+                const uint32_t n = (gb + g) * nb + (e & 0xffffu);
+                bool refractory = false;
+                const float act = clampf(fold_drive(c, n, pi, &refractory), 0.0f, 1.0f);
+                const bool candidate = !refractory && act > 0.0f;
+                w.key[i] = candidate ? selection_key(act, (n + N - rot) % N) : ~0ULL;
+                if (candidate) atomicAdd(&w.cands[g], 1u);
+                d.touched_list[listed + i] = n;
+            }
+            wave_sync();
+            {
+                // staged positions of this window's blocks (block order)
+                const bool in = lane < gn && w.start[lane] >= lo && w.start[lane] < hi;
+                const uint32_t win = in ? min(w.cands[lane], limit) : 0u;
+                const uint32_t incl = wave_incl_scan_u32(win);
+                if (in) w.woff[lane] = staged + incl - win;
+                staged += __builtin_amdgcn_readlane(incl, kWaveSize - 1);
+            }
+            wave_sync();
+            for (uint32_t i = lane; i < cnt; i += kWaveSize) {
+                const uint64_t mine = w.key[i];
+                if (mine == ~0ULL) continue;
+                const uint32_t g = w.entry[i] >> 16;
+                const uint32_t s0 = w.start[g] - lo, s1 = w.start[g + 1] - lo;
+                uint32_t rank = 0;
+                for (uint32_t j = s0; j < s1; ++j) rank += w.key[j] < mine ? 1u : 0u;
+                if (rank < limit) {
+                    const uint32_t n = (static_cast<uint32_t>(mine) + rot) % N;
+                    const float act = key_activation(mine);
+                    const uint64_t at = row0 + w.woff[g] + rank;
+                    d.range_winners[at] = n;
+                    d.range_winner_act[at] = act;
+                    if (a.redundant_global) {  // the global cap cannot bind (runtime.rs:1060-1067)
+                        d.activation[n] = act;
+                        d.selected_epoch[n] = tick + 1;
+                    }
+                } else if (rank == limit) {
+                    w.cut[g] = mine;
+                }
+            }
+            wave_sync();
+            lo = hi;
+        }
+        // block results; a block without touched neurons keeps a stale epoch
+        // (no winners, cutoff 0)
+        if (lane < gn && w.start[lane + 1] > w.start[lane]) {
+            const uint32_t b = gb + lane;
+            d.block_cutoff[b] = w.cut[lane] != ~0ULL ? key_activation(w.cut[lane]) : 0.0f;
+            d.block_epoch[b] = tick + 1;
+            supra += w.cands[lane];
+        }
+        w.cands[lane] = 0;
+        w.cut[lane] = ~0ULL;
+        wave_sync();
+    }
+    supra = wave_sum_u32(supra);
+    if (lane == 0) {
+        if (supra) atomicAdd(&c.ctl->tick_supra[tick & 1], supra);
+        d.wave_total[wv] = staged;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -838,28 +925,27 @@ __device__ void phase_fold_select(const StepCtx& c) {
 // order, runtime.rs:1010-1013), population inhibition (runtime.rs:1076-1082)
 // and the forward eligibilities (runtime.rs:805-918).
 // ---------------------------------------------------------------------------
-__device__ void write_active(const StepCtx& c) {
+__device__ __forceinline__ void write_active(const StepCtx& c) {
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = c.d;
     const uint32_t cap = cfg.max_active_global, limit = cfg.max_active_per_block;
-    const uint32_t wave = threadIdx.x / kWaveSize, lane = __lane_id();
+    const uint32_t wave = wave_index(), lane = __lane_id();
     const uint32_t nwaves = c.P * kWavesPerGroup;
     const uint32_t wv = c.part * kWavesPerGroup + wave;
-    const uint32_t per = (cfg.block_count + nwaves - 1) / nwaves;
+    const uint32_t range = (cfg.block_count + nwaves - 1) / nwaves;
     const uint32_t rs = c.tick % kRing;
-    const uint32_t b0 = wv * per, b1 = min(cfg.block_count, b0 + per);
-    uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
-    float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
-    // the winners of this wave's first block are loaded together with the
-    // per-wave totals (one round of loads in the common one-block case)
-    const uint32_t first_count = b0 < b1 ? ld(&d.block_count[b0]) : 0;
+    const uint32_t b0 = min(cfg.block_count, wv * range), b1 = min(cfg.block_count, b0 + range);
+    const uint64_t row0 = static_cast<uint64_t>(b0) * limit;
+    const uint32_t slots = (b1 - b0) * limit;
+    // one round of loads: the per-wave totals, and the first 64 staged winners
+    // of this wave's range
     uint32_t first_n = 0;
     float first_act = 0.0f;
-    if (b0 < b1 && lane < limit) {
-        first_n = ld(&d.block_winners[static_cast<uint64_t>(b0) * limit + lane]);
-        first_act = ld(&d.block_winner_act[static_cast<uint64_t>(b0) * limit + lane]);
+    if (lane < slots) {
+        first_n = ld(&d.range_winners[row0 + lane]);
+        first_act = ld(&d.range_winner_act[row0 + lane]);
     }
-    // offset of this wave's block range: winners of every earlier range
+    const uint32_t mine = ld(&d.wave_total[wv]);
     uint32_t before = 0, all = 0;
     for (uint32_t base = 0; base < nwaves; base += kWaveSize) {
         const uint32_t w = base + lane;
@@ -867,16 +953,12 @@ __device__ void write_active(const StepCtx& c) {
         before += wave_sum_u32(w < wv ? v : 0);
         all += wave_sum_u32(v);
     }
-    uint32_t offset = before;
-    for (uint32_t b = b0; b < b1; ++b) {
-        const uint32_t v = b == b0 ? first_count : ld(&d.block_count[b]);
-        for (uint32_t i = lane; i < v; i += kWaveSize) {
-            const bool pre = b == b0 && i == lane;
-            const uint32_t n = pre ? first_n : ld(&d.block_winners[static_cast<uint64_t>(b) * limit + i]);
-            act_list[offset + i] = n;
-            act_val[offset + i] = pre ? first_act : ld(&d.block_winner_act[static_cast<uint64_t>(b) * limit + i]);
-        }
-        offset += v;
+    uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap + before;
+    float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap + before;
+    for (uint32_t i = lane; i < mine; i += kWaveSize) {
+        const bool pre = i == lane;
+        act_list[i] = pre ? first_n : ld(&d.range_winners[row0 + i]);
+        act_val[i] = pre ? first_act : ld(&d.range_winner_act[row0 + i]);
     }
     if (c.part == 0 && threadIdx.x == 0) {
         LaneControl* ctl = c.ctl;
@@ -895,7 +977,7 @@ __device__ void write_active(const StepCtx& c) {
 
 // Binding global cap (workgroup 0): sort every block winner by
 // (activation desc, tie asc), keep max_active_global (runtime.rs:1029-1057).
-__device__ void global_select(const StepCtx& c, StepShared& sh) {
+__device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -903,10 +985,13 @@ __device__ void global_select(const StepCtx& c, StepShared& sh) {
     const uint32_t tick = c.tick, rot = tick % N;
     const uint32_t rs = tick % kRing;
     uint64_t* keys = reinterpret_cast<uint64_t*>(step_lds);
+    const uint32_t nwaves = c.P * kWavesPerGroup;
+    const uint32_t range = (cfg.block_count + nwaves - 1) / nwaves;
     uint32_t running = 0;
-    for (uint32_t base = 0; base < cfg.block_count; base += kThreads) {
-        const uint32_t b = base + threadIdx.x;
-        const uint32_t v = b < cfg.block_count ? ld(&d.block_count[b]) : 0;
+    for (uint32_t base = 0; base < nwaves; base += kThreads) {
+        const uint32_t wv = base + threadIdx.x;
+        const uint64_t row0 = static_cast<uint64_t>(min(cfg.block_count, wv * range)) * limit;
+        const uint32_t v = wv < nwaves ? ld(&d.wave_total[wv]) : 0;
         sh.scan[threadIdx.x] = v;
         __syncthreads();
         for (uint32_t off = 1; off < kThreads; off <<= 1) {
@@ -917,10 +1002,9 @@ __device__ void global_select(const StepCtx& c, StepShared& sh) {
         }
         const uint32_t start = running + sh.scan[threadIdx.x] - v;
         for (uint32_t i = 0; i < v; ++i) {
-            const uint32_t n = ld(&d.block_winners[static_cast<uint64_t>(b) * limit + i]);
             if (start + i < kMaxBlockNeurons) {
-                const float act = clampf(ld(&d.membrane[n]) - ld(&d.p.threshold[n]), 0.0f, 1.0f);
-                keys[start + i] = selection_key(act, (n + N - rot) % N);
+                const uint32_t n = ld(&d.range_winners[row0 + i]);
+                keys[start + i] = selection_key(ld(&d.range_winner_act[row0 + i]), (n + N - rot) % N);
             }
         }
         const uint32_t chunk_total = sh.scan[kThreads - 1];
@@ -968,7 +1052,7 @@ __device__ void global_select(const StepCtx& c, StepShared& sh) {
 }
 
 __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uint64_t plane, uint32_t* last,
-                                            uint32_t slot, uint32_t dst, uint8_t br) {
+                                            uint32_t slot, uint32_t dst, uint8_t br, float pop_cutoff) {
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = c.d;
     const uint32_t tick = c.tick;
@@ -985,19 +1069,32 @@ __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uin
         as2 *= decay_for_elapsed(cfg.adaptation_slow_decay, el);
         last[slot] = tick;
     }
-    const bool touched = ld(&d.touched_epoch[dst]) == tick + 1;
+    // every destination value in one round of loads (most are used only when
+    // the destination was touched and is not refractory)
+    const uint32_t blk = dst / cfg.neurons_per_block;
+    const uint32_t touched_epoch = ld(&d.touched_epoch[dst]), selected_epoch = ld(&d.selected_epoch[dst]);
+    const uint32_t refractory_until = ld(&d.refractory_until[dst]);
+    const float temporal = ld(&d.branches[4 * dst + BR_TEMP]), gate_acc = ld(&d.branches[4 * dst + BR_GATE]);
+    const uint32_t block_epoch = ld(&d.block_epoch[blk]);
+    const float block_cut = ld(&d.block_cutoff[blk]);
+    const float membrane = ld(&d.membrane[dst]), threshold = ld(&d.p.threshold[dst]);
+    const float excitability = c.a->m.excitability[dst];
+    const bool touched = touched_epoch == tick + 1;
+    const bool selected = selected_epoch == tick + 1;
     float elig;
-    if (!touched || ld(&d.refractory_until[dst]) > tick) {
+    if (!touched || refractory_until > tick) {
         elig = e * cfg.eligibility_decay;
     } else {
-        const float jac = branch_jacobian(br, c.a->m.excitability[dst], ld(&d.branches[4 * dst + BR_TEMP]),
-                                          ld(&d.branches[4 * dst + BR_GATE]));
-        const float sur = ld(&d.surrogate[dst]);
+        const float jac = branch_jacobian(br, excitability, temporal, gate_acc);
+        // the destination's selection surrogate (runtime.rs:787-803), a pure
+        // function of its state after selection, evaluated where it is used
+        const float block_cutoff = block_epoch == tick + 1 ? block_cut : 0.0f;
+        const float sur = surrogate_value(cfg, false, membrane - threshold, maxnum(block_cutoff, pop_cutoff), selected);
         const float asum = as0 + as1 + as2;
         ms = ms + jac * bs - fs - asum;
         elig = sur * ms;
     }
-    if (touched && ld(&d.selected_epoch[dst]) == tick + 1) {
+    if (touched && selected) {
         fs += cfg.fatigue_gain * elig;
         as0 += cfg.adaptation_fast_gain * elig;
         as1 += cfg.adaptation_medium_gain * elig;
@@ -1019,9 +1116,9 @@ __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uin
 
 // Update every slot of one eligible list; kept slots are compacted into the
 // other list, dropped slots are unmarked.
-__device__ void eligibility_list(const StepCtx& c, float* planes, uint64_t plane, uint32_t* last, uint8_t* marks,
+__device__ __forceinline__ void eligibility_list(const StepCtx& c, float* planes, uint64_t plane, uint32_t* last, uint8_t* marks,
                                  const uint32_t* cur, uint32_t cur_n, uint32_t* next, uint32_t* next_count,
-                                 const uint32_t* targets, const uint8_t* branches) {
+                                 const uint32_t* targets, const uint8_t* branches, float pop_cutoff) {
     const uint32_t lane = __lane_id();
     for (uint32_t base = c.gtid - lane; base < cur_n; base += c.gstride) {
         const uint32_t i = base + lane;
@@ -1029,7 +1126,7 @@ __device__ void eligibility_list(const StepCtx& c, float* planes, uint64_t plane
         uint32_t slot = 0;
         if (i < cur_n) {
             slot = ld(&cur[i]);
-            keep = update_slot(c, planes, plane, last, slot, targets[slot], branches[slot]);
+            keep = update_slot(c, planes, plane, last, slot, targets[slot], branches[slot], pop_cutoff);
             if (!keep) marks[slot] = 0;
         }
         const uint32_t pos = wave_append(next_count, keep);
@@ -1037,7 +1134,7 @@ __device__ void eligibility_list(const StepCtx& c, float* planes, uint64_t plane
     }
 }
 
-__device__ void phase_eligibility(const StepCtx& c) {
+__device__ __forceinline__ void phase_eligibility(const StepCtx& c) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -1049,10 +1146,11 @@ __device__ void phase_eligibility(const StepCtx& c) {
         c.ctl->tick_scan_rec[c.tick & 1] = rec_n;
         c.ctl->tick_scan_in[c.tick & 1] = in_n;
     }
+    const float pop_cutoff = a.redundant_global ? 0.0f : ld(&c.ctl->pop_cutoff);
     eligibility_list(c, d.rec_trace, NS, d.rec_last, d.rec_mark, d.rec_list + p * NS, rec_n, d.rec_list + q * NS,
-                     &c.ctl->rec_count[q], a.m.rec_target, a.m.rec_branch);
+                     &c.ctl->rec_count[q], a.m.rec_target, a.m.rec_branch, pop_cutoff);
     eligibility_list(c, d.in_trace, NI, d.in_last, d.in_mark, d.in_list + p * NI, in_n, d.in_list + q * NI,
-                     &c.ctl->in_count[q], a.m.in_target, a.m.in_branch);
+                     &c.ctl->in_count[q], a.m.in_target, a.m.in_branch, pop_cutoff);
 }
 
 // ---------------------------------------------------------------------------
@@ -1060,7 +1158,7 @@ __device__ void phase_eligibility(const StepCtx& c) {
 // (runtime.rs:1084-1106), and on the last workgroup the readout, softmax and
 // errors (runtime.rs:1108-1197, 1205-1206).
 // ---------------------------------------------------------------------------
-__device__ void readout(const StepCtx& c, const StepParams& sp, StepShared& sh, uint32_t step_index) {
+__device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, StepShared& sh, uint32_t step_index) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -1071,7 +1169,7 @@ __device__ void readout(const StepCtx& c, const StepParams& sp, StepShared& sh, 
     const uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
     const float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
     const uint32_t ctx_count = ld(&ctl->ctx_count);
-    const uint32_t wave = threadIdx.x / kWaveSize, lane = __lane_id();
+    const uint32_t wave = wave_index(), lane = __lane_id();
     float* lat = sh.aux;
     // context latent (runtime.rs:1120-1136): serial over active slots per dimension
     for (uint32_t e = threadIdx.x; e < E; e += kThreads) {
@@ -1185,7 +1283,7 @@ __device__ void readout(const StepCtx& c, const StepParams& sp, StepShared& sh, 
     __syncthreads();
 }
 
-__device__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step_index, StepShared& sh) {
+__device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step_index, StepShared& sh) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -1287,7 +1385,7 @@ __device__ __forceinline__ float signal_dot(__amdgpu_buffer_rsrc_t rows, uint32_
     return acc;
 }
 
-__device__ void phase_signals(const StepCtx& c, StepShared& sh) {
+__device__ __forceinline__ void phase_signals(const StepCtx& c, StepShared& sh) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -1302,7 +1400,7 @@ __device__ void phase_signals(const StepCtx& c, StepShared& sh) {
     const uint32_t* rec_cur = d.rec_list + c.parity * NS;
     const uint32_t* in_cur = d.in_list + c.parity * NI;
     const uint32_t total = rec_n + in_n + A;
-    const uint32_t wave = threadIdx.x / kWaveSize, lane = __lane_id();
+    const uint32_t wave = wave_index(), lane = __lane_id();
     const unsigned long long below = (1ULL << lane) - 1ULL;
     uint32_t* queue = sh.queue[wave];
     uint32_t queued = 0, claimed = 0;
@@ -1353,7 +1451,7 @@ __device__ __forceinline__ float inhibitory_step(const LeoConfig& cfg, float w, 
     return clampf(w + delta, cfg.weight_min, 0.0f);
 }
 
-__device__ void context_update(const StepCtx& c, const StepParams& sp, StepShared& sh) {
+__device__ __forceinline__ void context_update(const StepCtx& c, const StepParams& sp, StepShared& sh) {
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = c.d;
     LaneControl* ctl = c.ctl;
@@ -1545,10 +1643,10 @@ __device__ __forceinline__ bool phase_barrier(const StepCtx& c, uint32_t& target
     return ok;
 }
 
-// Step loop. Phases (barriers): deliver | fold+select (+context) | active list +
+// Step loop. Phases (barriers): deliver (+context) | fold+select | active list +
 // eligibility | post + readout | signals | learning. Frozen steps stop after
-// the post phase; a binding global cap inserts the global sort and the
-// surrogate pass before the eligibility update.
+// the post phase; a binding global cap inserts the global sort before the
+// eligibility update.
 //
 // Workgroup b serves lane b % lane_stride (lane_stride is a multiple of the 8
 // XCDs, and workgroups are dealt to XCDs round-robin, so a lane's workgroups
@@ -1568,7 +1666,7 @@ __device__ __forceinline__ LaneDesc load_uniform(const LaneDesc* p) {
 }
 
 template <bool kProfile>
-__device__ void lane_steps(const KernelArgs& args) {
+__device__ __forceinline__ void lane_steps(const KernelArgs& args) {
     __shared__ StepShared sh;
     const uint32_t stride = args.lane_stride, P = args.wgs_per_lane;
     const uint32_t lane = blockIdx.x % stride;
@@ -1616,19 +1714,6 @@ __device__ void lane_steps(const KernelArgs& args) {
             if (trace) phase_eligibility(c);
         } else {
             if (c.part == 0) global_select(c, sh);
-            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 7))) break;
-            const uint32_t touched = ld(&c.ctl->tick_touched[c.tick & 1]);
-            const uint32_t nb = args.cfg.neurons_per_block;
-            const float pop_cutoff = ld(&c.ctl->pop_cutoff);
-            const LaneDesc& d = c.d;
-            for (uint32_t i = c.gtid; i < touched; i += c.gstride) {
-                const uint32_t n = ld(&d.touched_list[i]);
-                const bool refractory = ld(&d.refractory_until[n]) > c.tick;
-                const float margin = ld(&d.membrane[n]) - ld(&d.p.threshold[n]);
-                const float cutoff = maxnum(ld(&d.block_cutoff[n / nb]), pop_cutoff);
-                d.surrogate[n] = surrogate_value(args.cfg, refractory, margin, cutoff,
-                                                 ld(&d.selected_epoch[n]) == c.tick + 1);
-            }
             if (trace) {
                 if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 7))) break;
                 phase_eligibility(c);
@@ -1695,7 +1780,6 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
         d.last_tick[i] = tick;
         d.touched_epoch[i] = 0;
         d.selected_epoch[i] = 0;
-        d.surrogate[i] = 0.0f;
         d.bucket_count[i] = 0;
     }
     for (uint64_t i = t0; i < 7 * NS; i += ts) d.rec_trace[i] = 0.0f;
@@ -1709,6 +1793,10 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
         d.in_mark[i] = 0;
     }
     for (uint64_t i = t0; i < cfg.context_embedding_dim; i += ts) d.ctx_latent[i] = 0.0f;
+    for (uint64_t i = t0; i < cfg.block_count; i += ts) d.block_epoch[i] = 0;
+    const uint64_t bit_words = static_cast<uint64_t>(cfg.block_count) * block_words(cfg.neurons_per_block);
+    for (uint64_t i = t0; i < bit_words; i += ts) d.touched_bits[i] = 0;
+    for (uint64_t i = t0; i < kMaxWaves; i += ts) d.wave_total[i] = 0;
     if (part == 0 && threadIdx.x == 0) {
         LaneControl* ctl = d.ctl;
         ctl->tick = tick;

@@ -84,7 +84,7 @@ struct Layout {
 };
 
 struct Sizes {
-    uint64_t n, s, f, ns, ni, slots, e, blocks, limit, cap, bucket_total;
+    uint64_t n, s, f, ns, ni, slots, e, blocks, block_words, limit, cap, bucket_total;
     uint64_t words(uint64_t count) const { return (count + 31) / 32; }
 };
 
@@ -166,6 +166,7 @@ struct LeoHipRuntime {
     leo::Arena kernel_args_buf;  // KernelArgs of the step kernel
     leo::Arena merge_acc;        // f64 sums + changed flags of the lane-group merge
     uint32_t resident_lanes = 0; // story lanes that fit on the device at once
+    uint32_t max_steps_override = 0;
     leo::Arena merge_scratch;  // lane pointer table + counters
     // host copies of the read-only topology (device copies are immutable)
     std::vector<float> excitability;
@@ -216,6 +217,7 @@ Sizes sizes_of(const LeoHostConfig& c) {
     z.slots = static_cast<uint64_t>(c.device.context_max_order) * c.device.context_slots_per_order;
     z.e = c.device.context_embedding_dim;
     z.blocks = c.device.block_count;
+    z.block_words = block_words(c.device.neurons_per_block);
     z.limit = c.device.max_active_per_block;
     z.cap = c.device.max_active_global;
     return z;
@@ -274,11 +276,12 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     size_t o_mem = l.add<float>(z.n), o_act = l.add<float>(z.n), o_fat = l.add<float>(z.n);
     size_t o_ref = l.add<uint32_t>(z.n), o_br = l.add<float>(4 * z.n), o_last = l.add<uint32_t>(z.n);
     size_t o_ad = l.add<float>(3 * z.n), o_te = l.add<uint32_t>(z.n), o_tl = l.add<uint32_t>(z.n);
-    size_t o_se = l.add<uint32_t>(z.n), o_su = l.add<float>(z.n), o_de = l.add<uint32_t>(z.n);
+    size_t o_se = l.add<uint32_t>(z.n), o_de = l.add<uint32_t>(z.n);
     size_t o_ls = l.add<float>(z.n), o_bc = l.add<uint32_t>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
-    size_t o_bw = l.add<uint32_t>(z.blocks * z.limit), o_bn = l.add<uint32_t>(z.blocks), o_bcut = l.add<float>(z.blocks);
+    size_t o_bw = l.add<uint32_t>(z.blocks * z.limit), o_bcut = l.add<float>(z.blocks);
     size_t o_bwa = l.add<float>(z.blocks * z.limit);
     size_t o_wt = l.add<uint32_t>(kMaxWaves);
+    size_t o_bep = l.add<uint32_t>(z.blocks), o_tb = l.add<uint32_t>(z.blocks * z.block_words);
     size_t o_ra = l.add<uint32_t>(kRing * z.cap), o_rv = l.add<float>(kRing * z.cap), o_rval = l.add<float>(kRing * z.cap * z.s);
     size_t o_rt = l.add<float>(7 * z.ns), o_rl = l.add<uint32_t>(z.ns), o_rm = l.add<uint8_t>(z.ns), o_rlist = l.add<uint32_t>(2 * z.ns);
     size_t o_it = l.add<float>(7 * z.ni), o_il = l.add<uint32_t>(z.ni), o_im = l.add<uint8_t>(z.ni), o_ilist = l.add<uint32_t>(2 * z.ni);
@@ -301,16 +304,16 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     d.touched_epoch = reinterpret_cast<uint32_t*>(b + o_te);
     d.touched_list = reinterpret_cast<uint32_t*>(b + o_tl);
     d.selected_epoch = reinterpret_cast<uint32_t*>(b + o_se);
-    d.surrogate = reinterpret_cast<float*>(b + o_su);
     d.dest_epoch = reinterpret_cast<uint32_t*>(b + o_de);
     d.learning_signal = reinterpret_cast<float*>(b + o_ls);
     d.bucket_count = reinterpret_cast<uint32_t*>(b + o_bc);
     d.bucket = reinterpret_cast<uint64_t*>(b + o_bk);
-    d.block_winners = reinterpret_cast<uint32_t*>(b + o_bw);
-    d.block_winner_act = reinterpret_cast<float*>(b + o_bwa);
-    d.block_count = reinterpret_cast<uint32_t*>(b + o_bn);
+    d.range_winners = reinterpret_cast<uint32_t*>(b + o_bw);
+    d.range_winner_act = reinterpret_cast<float*>(b + o_bwa);
     d.block_cutoff = reinterpret_cast<float*>(b + o_bcut);
     d.wave_total = reinterpret_cast<uint32_t*>(b + o_wt);
+    d.block_epoch = reinterpret_cast<uint32_t*>(b + o_bep);
+    d.touched_bits = reinterpret_cast<uint32_t*>(b + o_tb);
     d.ring_active = reinterpret_cast<uint32_t*>(b + o_ra);
     d.ring_act = reinterpret_cast<float*>(b + o_rv);
     d.ring_value = reinterpret_cast<float*>(b + o_rval);
@@ -497,7 +500,7 @@ void account_launch(LeoHipRuntime* h, const std::vector<LaneRun>& runs, float ms
 }
 
 // One cooperative launch over all given lanes (each with its own schedule).
-void run_lanes(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
+void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     const uint32_t count = static_cast<uint32_t>(runs.size());
     if (count == 0) return;
     uint64_t max_tick = 0;
@@ -572,6 +575,43 @@ void run_lanes(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
             throw Error(LEO_ERR_NUMERICAL, "device numerical guard tripped (code " + std::to_string(code) + ")");
         }
         if (ctl[i].tick != runs[i].lane->tick) throw Error(LEO_ERR_INTERNAL, "device lane tick diverged from the host mirror");
+    }
+}
+
+// Steps per launch: a launch stays around a second even when every synapse
+// slot of every lane is eligible (about 140 bytes per slot and step at
+// ~4 TB/s), so a long schedule never becomes one multi-minute dispatch.
+size_t max_steps_per_launch(const LeoHipRuntime* h, size_t lanes) {
+    if (h->max_steps_override) return h->max_steps_override;
+    const double bytes_per_step = static_cast<double>(h->z.ns) * 140.0 * static_cast<double>(std::max<size_t>(lanes, 1));
+    const double steps = 4e12 / std::max(bytes_per_step, 1.0);
+    return static_cast<size_t>(std::min(4096.0, std::max(8.0, steps)));
+}
+
+// Runs the lanes' schedules, in several launches when they are long.
+void run_lanes(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
+    size_t longest = 0;
+    for (const LaneRun& r : runs) longest = std::max(longest, r.steps.size());
+    const size_t chunk = max_steps_per_launch(h, runs.size());
+    if (longest <= chunk) {
+        run_lanes_once(h, runs);
+        return;
+    }
+    for (LaneRun& r : runs) r.records.resize(r.steps.size());
+    for (size_t at = 0; at < longest; at += chunk) {
+        std::vector<LaneRun> part;
+        std::vector<size_t> index;
+        for (size_t i = 0; i < runs.size(); ++i) {
+            const size_t n = runs[i].steps.size();
+            if (at >= n) continue;
+            const size_t end = std::min(n, at + chunk);
+            part.push_back(LaneRun{runs[i].lane, std::vector<StepParams>(runs[i].steps.begin() + at,
+                                                                         runs[i].steps.begin() + end), {}});
+            index.push_back(i);
+        }
+        run_lanes_once(h, part);
+        for (size_t k = 0; k < part.size(); ++k)
+            std::copy(part[k].records.begin(), part[k].records.end(), runs[index[k]].records.begin() + at);
     }
 }
 
@@ -1402,6 +1442,8 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         if (const char* env = std::getenv("LEO_HIP_CANONICAL_WGS"))
             h->canonical_wgs_override = static_cast<uint32_t>(std::atoi(env));
         if (const char* env = std::getenv("LEO_HIP_AGENT_SYNC")) h->local_sync = std::atoi(env) == 0;
+        if (const char* env = std::getenv("LEO_HIP_MAX_STEPS_PER_LAUNCH"))
+            h->max_steps_override = static_cast<uint32_t>(std::max(1, std::atoi(env)));
         if (const char* env = std::getenv("LEO_HIP_PHASE_PROFILE")) h->phase_profile = std::atoi(env) != 0;
         int clock_khz = 0;
         LEO_HIP_CHECK(hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, device));
@@ -1738,7 +1780,8 @@ int32_t leo_hip_read_state(LeoHipRuntime* h, int32_t which, float* out, uint64_t
                 case LEO_STATE_ADAPT0: src = d.adapt; n = z.n; break;
                 case LEO_STATE_ADAPT1: src = d.adapt + z.n; n = z.n; break;
                 case LEO_STATE_ADAPT2: src = d.adapt + 2 * z.n; n = z.n; break;
-                case LEO_STATE_SURROGATE: src = d.surrogate; n = z.n; break;
+                case LEO_STATE_SURROGATE:
+                    throw Error(LEO_ERR_UNSUPPORTED, "surrogates are evaluated where the eligibility update uses them, not stored");
                 case LEO_STATE_LOGITS: src = d.logits; n = leo::kOutputs; break;
                 case LEO_STATE_PROBABILITIES: src = d.probs; n = leo::kOutputs; break;
                 case LEO_STATE_ERRORS: src = d.errors; n = leo::kOutputs; break;

@@ -163,3 +163,23 @@ def test_story_batch_in_lane_groups_parity(require_gpu, oracle, make, monkeypatc
         assert grep.mean_loss == crep.mean_loss
     assert_models_equal(gpu.model(), cpu.model(), make)
     gpu.close()
+
+
+def test_chunked_launches_and_agent_barriers_parity(require_gpu, oracle, monkeypatch):
+    # schedules split into launches of 7 steps, and the agent-scope barrier
+    # fallback, give the same bits as one launch with XCD-local barriers
+    monkeypatch.setenv("LEO_HIP_MAX_STEPS_PER_LAUNCH", "7")
+    monkeypatch.setenv("LEO_HIP_AGENT_SYNC", "1")
+    cfg = small_redundant_config()
+    model = Model.initialize(cfg)
+    stories = [story(600 + k, 50 + 9 * k) for k in range(3)]
+    cpu = oracle.OracleRuntime(model)
+    gpu = _runtime(model)
+    crep, closs = cpu.train_story_batch(stories, oracle.TRAINING, replay=True)
+    grep, gloss = gpu.train_batch(stories, native.TRAINING, replay=True)
+    for a, b in zip(gloss, closs):
+        assert np.array_equal(a, b)
+    assert grep.replay_steps == crep.replay_steps
+    assert_models_equal(gpu.model(), cpu.model(), "chunked")
+    assert gpu.kernel_stats()["launches"] > 10
+    gpu.close()
