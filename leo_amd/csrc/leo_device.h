@@ -22,6 +22,7 @@ constexpr uint32_t kMaxBlockNeurons = 1024;
 constexpr uint32_t kWaveSize = 64;
 constexpr uint32_t kWavesPerGroup = kThreads / kWaveSize;
 constexpr uint32_t kMaxWaves = 1024;     // selecting waves per lane (workgroups per lane <= 256)
+constexpr uint32_t kXcds = 8;            // accelerator complex dies of an MI355X (workgroups dispatched round-robin)
 
 // Touched-neuron bitmap: each block owns ceil(neurons_per_block/32) words,
 // so no word is shared by two blocks (and no two selecting waves).
@@ -44,10 +45,23 @@ inline __host__ __device__ size_t window_bytes(uint32_t neurons_per_block) {
     return (c * 12 + kGroupBlocks * 8 + (kGroupBlocks + 1) * 4 + kGroupBlocks * 8 + words * 8 + 15) / 16 * 16;
 }
 
-// Dynamic LDS of the step kernel: one phase-2 window per wave; the
-// binding-cap global sort (up to kMaxBlockNeurons keys) reuses the front.
+// Learning-signal row staging of one wave: 64 output rows, one 128-byte line
+// (32 floats) of each at a time, rows padded to 33 floats (conflict-free
+// column reads).
+constexpr uint32_t kStageRowFloats = 33;
+constexpr size_t kStageBytes = 64 * kStageRowFloats * 4;
+
+// Per-wave share of the dynamic LDS: the phase-2 window, reused by the
+// learning-signal staging.
+inline __host__ __device__ size_t wave_lds_bytes(uint32_t neurons_per_block) {
+    const size_t w = window_bytes(neurons_per_block);
+    return ((w > kStageBytes ? w : kStageBytes) + 15) / 16 * 16;
+}
+
+// Dynamic LDS of the step kernel: one share per wave; the binding-cap global
+// sort (up to kMaxBlockNeurons keys) reuses the front.
 inline size_t step_lds_bytes(uint32_t neurons_per_block) {
-    const size_t lists = static_cast<size_t>(kWavesPerGroup) * window_bytes(neurons_per_block);
+    const size_t lists = static_cast<size_t>(kWavesPerGroup) * wave_lds_bytes(neurons_per_block);
     const size_t sort = static_cast<size_t>(kMaxBlockNeurons) * 8;
     return ((lists > sort ? lists : sort) + 15) / 16 * 16;
 }
@@ -187,6 +201,7 @@ struct LaneDesc {
     uint32_t* ring_active;   // kRing * cap
     float* ring_act;         // kRing * cap
     float* ring_value;       // kRing * cap * S
+    uint32_t* ring_edge;     // kRing * cap * S: packed synapse of each snapshot value (target, delay, branch)
     // recurrent traces (N*S): branch, membrane, fatigue, 3 adaptation sensitivities, eligibility
     float* rec_trace;        // 7 * NS (SoA planes)
     uint32_t* rec_last;      // NS
@@ -230,7 +245,21 @@ struct SharedModel {
     const uint32_t* in_target;
     const uint8_t* in_branch;
     const uint64_t* bucket_offset;   // N+1
+    const uint32_t* rec_edge;        // N*S: pack_edge(target, delay, branch) of each recurrent slot
 };
+
+// A recurrent synapse packed into one word: target (28 bits), log2 of the
+// delay (1, 2, 4 or 8) and the branch. The model validation guarantees the
+// ranges; neuron_count is limited to 2^28.
+constexpr uint32_t kEdgeTargetBits = 28;
+constexpr uint32_t kMaxPackedNeurons = 1u << kEdgeTargetBits;
+inline __host__ __device__ uint32_t pack_edge(uint32_t target, uint32_t delay, uint32_t branch) {
+    const uint32_t log2_delay = delay >= 8 ? 3u : delay >= 4 ? 2u : delay >= 2 ? 1u : 0u;
+    return target | (log2_delay << kEdgeTargetBits) | (branch << (kEdgeTargetBits + 2));
+}
+inline __host__ __device__ uint32_t edge_target(uint32_t e) { return e & (kMaxPackedNeurons - 1); }
+inline __host__ __device__ uint32_t edge_delay(uint32_t e) { return 1u << ((e >> kEdgeTargetBits) & 3u); }
+inline __host__ __device__ uint32_t edge_branch(uint32_t e) { return e >> (kEdgeTargetBits + 2); }
 
 struct KernelArgs {
     LeoConfig cfg;

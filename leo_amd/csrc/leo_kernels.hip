@@ -211,9 +211,13 @@ __device__ __forceinline__ bool lane_barrier(LaneControl* ctl, uint32_t P, uint3
         }
         uint32_t spins = 0;
         uint32_t aborted = 0;
-        while ((local ? ld(&ctl->barrier)
-                      : __hip_atomic_load(&ctl->barrier, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT)) < target) {
-            if (ld(&ctl->abort) != 0) {
+        for (;;) {
+            // the counter and the abort flag are polled in one round trip
+            const uint32_t abort_flag = ld(&ctl->abort);
+            const uint32_t arrived = local ? ld(&ctl->barrier)
+                                           : __hip_atomic_load(&ctl->barrier, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+            if (arrived >= target) break;
+            if (abort_flag != 0) {
                 aborted = 1;
                 break;
             }
@@ -393,9 +397,9 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
     const uint32_t stride = workers * kThreads;
     for (uint32_t base = c.gtid - lane; delivers && base < total; base += stride) {
         const uint32_t item = base + lane;
-        uint32_t touch_n = 0xffffffffu, target = 0, eslot = 0;
-        bool new_rec = false, new_in = false, scatter = false;
-        uint64_t key = 0;
+        uint32_t touch_n = 0xffffffffu, target = 0;
+        bool scatter = false, rec = false, inj = false;
+        uint64_t key = 0, rbase = 0, slot = 0;
         float value = 0.0f;
         if (item < prev_count) {
             const uint32_t n = ld(&d.ring_active[static_cast<uint64_t>(prev_slot) * cap + item]);
@@ -407,56 +411,33 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
             const uint32_t rsk = k == 0 ? rs8 : k == 1 ? rs4 : k == 2 ? rs2 : rs1;
             const uint32_t local = item - lo;
             const uint32_t r = local / S, j = local % S;
-            const uint64_t rbase = static_cast<uint64_t>(rsk) * cap + r;
-            const uint32_t src = ld(&d.ring_active[rbase]);
-            const uint64_t slot = static_cast<uint64_t>(src) * S + j;
-            if (a.m.rec_delay[slot] == (8u >> k)) {
+            rbase = static_cast<uint64_t>(rsk) * cap + r;
+            // the emission snapshot holds the synapse with its value: the
+            // scatter needs no load that depends on the source
+            const uint32_t edge = ld(&d.ring_edge[rbase * S + j]);
+            const float v = ld(&d.ring_value[rbase * S + j]);
+            if (edge_delay(edge) == (8u >> k)) {
                 delivered += 1;
-                const float act = ld(&d.ring_act[rbase]);
-                value = ld(&d.ring_value[rbase * S + j]);
-                target = a.m.rec_target[slot];
-                const uint8_t br = a.m.rec_branch[slot];
-                if (trace) {
-                    const float bs = advance_trace(d.rec_trace, NS, d.rec_last, static_cast<uint32_t>(slot), tick, cfg);
-                    d.rec_trace[slot] = bs + act;
-                    if (!ld(&d.rec_mark[slot])) {
-                        d.rec_mark[slot] = 1;
-                        new_rec = true;
-                        eslot = static_cast<uint32_t>(slot);
-                    }
-                }
-                if (target < cfg.neuron_count && br <= BR_GATE) {
-                    touch_n = target;
-                    scatter = true;
-                    key = (static_cast<uint64_t>(k) << 61) | (static_cast<uint64_t>(r) << 32) |
-                          (static_cast<uint64_t>(j) << 2) | br;
-                }
+                rec = true;
+                value = v;
+                target = edge_target(edge);
+                touch_n = target;
+                scatter = true;
+                slot = j;  // completed with the source below (traces only)
+                key = (static_cast<uint64_t>(k) << 61) | (static_cast<uint64_t>(r) << 32) |
+                      (static_cast<uint64_t>(j) << 2) | edge_branch(edge);
             }
         } else if (item < total) {
             const uint32_t i = item - off_in;
-            const uint64_t slot = static_cast<uint64_t>(sp.symbol) * F + i;
+            slot = static_cast<uint64_t>(sp.symbol) * F + i;
             target = a.m.in_target[slot];
             const uint8_t br = a.m.in_branch[slot];
             value = ld(&d.p.in_weight[slot]);
-            if (trace) {
-                const float bs = advance_trace(d.in_trace, NI, d.in_last, static_cast<uint32_t>(slot), tick, cfg);
-                d.in_trace[slot] = bs + 1.0f;
-                if (!ld(&d.in_mark[slot])) {
-                    d.in_mark[slot] = 1;
-                    new_in = true;
-                    eslot = static_cast<uint32_t>(slot);
-                }
-            }
-            if (target < cfg.neuron_count && br <= BR_GATE) {
-                touch_n = target;
-                scatter = true;
-                key = (4ULL << 61) | (static_cast<uint64_t>(i) << 2) | br;
-            }
+            inj = true;
+            touch_n = target;
+            scatter = true;
+            key = (4ULL << 61) | (static_cast<uint64_t>(i) << 2) | br;
         }
-        uint32_t pos = wave_append(&ctl->rec_count[c.parity], new_rec);
-        if (new_rec) d.rec_list[static_cast<uint64_t>(c.parity) * NS + pos] = eslot;
-        pos = wave_append(&ctl->in_count[c.parity], new_in);
-        if (new_in) d.in_list[static_cast<uint64_t>(c.parity) * NI + pos] = eslot;
         if (scatter) {
             const uint32_t p = atomicAdd(&d.bucket_count[target], 1u);
             const uint64_t at = bucket_entry(a.m, target, p);
@@ -471,6 +452,32 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
             d.touched_epoch[touch_n] = tick + 1;
             atomicOr(&d.touched_bits[blk * block_words(nb) + off / 32], 1u << (off & 31));
         }
+        // trace activation of the delivering slot (runtime.rs:710-766)
+        bool new_rec = false, new_in = false;
+        uint32_t eslot = 0;
+        if (trace && rec) {
+            const float act = ld(&d.ring_act[rbase]);
+            slot += static_cast<uint64_t>(ld(&d.ring_active[rbase])) * S;
+            const float bs = advance_trace(d.rec_trace, NS, d.rec_last, static_cast<uint32_t>(slot), tick, cfg);
+            d.rec_trace[slot] = bs + act;
+            if (!ld(&d.rec_mark[slot])) {
+                d.rec_mark[slot] = 1;
+                new_rec = true;
+                eslot = static_cast<uint32_t>(slot);
+            }
+        } else if (trace && inj) {
+            const float bs = advance_trace(d.in_trace, NI, d.in_last, static_cast<uint32_t>(slot), tick, cfg);
+            d.in_trace[slot] = bs + 1.0f;
+            if (!ld(&d.in_mark[slot])) {
+                d.in_mark[slot] = 1;
+                new_in = true;
+                eslot = static_cast<uint32_t>(slot);
+            }
+        }
+        uint32_t pos = wave_append(&ctl->rec_count[c.parity], new_rec);
+        if (new_rec) d.rec_list[static_cast<uint64_t>(c.parity) * NS + pos] = eslot;
+        pos = wave_append(&ctl->in_count[c.parity], new_in);
+        if (new_in) d.in_list[static_cast<uint64_t>(c.parity) * NI + pos] = eslot;
     }
     add_count(&ctl->tick_events[tick & 1], delivered);
 }
@@ -755,7 +762,7 @@ static_assert(kGroupBlocks == kWaveSize, "one lane per group block");
 static_assert(kMaxBlockNeurons <= 0x10000u, "window entries hold a 16-bit offset in the block");
 
 __device__ __forceinline__ Window wave_window(uint32_t wave, uint32_t nb) {
-    unsigned char* base = step_lds + static_cast<size_t>(wave) * window_bytes(nb);
+    unsigned char* base = step_lds + static_cast<size_t>(wave) * wave_lds_bytes(nb);
     const uint32_t cap = window_capacity(nb);
     Window w;
     w.key = reinterpret_cast<uint64_t*>(base);
@@ -925,7 +932,8 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
 // order, runtime.rs:1010-1013), population inhibition (runtime.rs:1076-1082)
 // and the forward eligibilities (runtime.rs:805-918).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void write_active(const StepCtx& c) {
+__device__ __forceinline__ void write_active(const StepCtx& c, const StepParams& sp, uint32_t step_index,
+                                             StepShared& sh, bool fuse_post) {
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = c.d;
     const uint32_t cap = cfg.max_active_global, limit = cfg.max_active_per_block;
@@ -960,6 +968,7 @@ __device__ __forceinline__ void write_active(const StepCtx& c) {
         act_list[i] = pre ? first_n : ld(&d.range_winners[row0 + i]);
         act_val[i] = pre ? first_act : ld(&d.range_winner_act[row0 + i]);
     }
+    const float activity = static_cast<float>(all) / static_cast<float>(cfg.neuron_count);
     if (c.part == 0 && threadIdx.x == 0) {
         LaneControl* ctl = c.ctl;
         ctl->active_count = all;
@@ -968,10 +977,65 @@ __device__ __forceinline__ void write_active(const StepCtx& c) {
         ctl->pop_cutoff = 0.0f;
         ctl->ring_tick[rs] = c.tick;
         ctl->ring_count[rs] = all;
-        const float activity = static_cast<float>(all) / static_cast<float>(cfg.neuron_count);
-        ctl->population_inhibition = clampf(
+        const float pi = clampf(
             ld(&ctl->population_inhibition) + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
             cfg.population_inhibition_max);
+        ctl->population_inhibition = pi;
+        if (fuse_post) {
+            // the step record the post phase would write (no readout this step)
+            StepRecord& rec = d.records[step_index];
+            rec.p_target = 0.0f;
+            rec.predicted = 0;
+            rec.population_inhibition = pi;
+            rec.active = all;
+            rec.suprathreshold = ld(&ctl->tick_supra[c.tick & 1]);
+            rec.block_selected = all;
+            rec.clipped = 0;
+            rec.context_cells = ld(&ctl->ctx_count);
+            rec.context_probes = ld(&ctl->ctx_probes);
+            rec.context_applied = ld(&ctl->ctx_applied);
+            rec.eligible_rec = ld(&ctl->rec_count[c.parity]);
+            rec.eligible_in = ld(&ctl->in_count[c.parity]);
+            rec.error_code = 0;
+        }
+    }
+    if (!fuse_post) return;
+    // Post-fire updates of this wave's winners and their emission snapshots
+    // (the post phase, runtime.rs:920-938, 1084-1106), folded in here when no
+    // eligibility update or readout of this step reads the state in between.
+    // The wave's first 64 winners are shared through its phase-2 LDS window.
+    const uint32_t S = cfg.synapses_per_neuron, N = cfg.neuron_count;
+    const Window w = wave_window(wave, cfg.neurons_per_block);
+    w.entry[lane] = first_n;
+    w.pos[lane] = __float_as_uint(first_act);
+    wave_sync();
+    const uint32_t refractory = c.tick + cfg.refractory_ticks + 1;
+    const uint32_t items = mine * (1 + S);
+    uint32_t inhibitory = 0;
+    for (uint32_t item = lane; item < items; item += kWaveSize) {
+        const uint32_t r = item < mine ? item : (item - mine) / S;
+        const uint32_t n = r < kWaveSize ? w.entry[r] : ld(&d.range_winners[row0 + r]);
+        const float act = r < kWaveSize ? __uint_as_float(w.pos[r]) : ld(&d.range_winner_act[row0 + r]);
+        if (item < mine) {
+            inhibitory += c.a->m.neuron_type[n] != 0 ? 1u : 0u;
+            d.fatigue[n] = ld(&d.fatigue[n]) + cfg.fatigue_gain * act;
+            d.adapt[n] = ld(&d.adapt[n]) + cfg.adaptation_fast_gain * act;
+            d.adapt[N + n] = ld(&d.adapt[N + n]) + cfg.adaptation_medium_gain * act;
+            d.adapt[2 * N + n] = ld(&d.adapt[2 * N + n]) + cfg.adaptation_slow_gain * act;
+            d.membrane[n] = ld(&d.membrane[n]) - ld(&d.p.threshold[n]) * cfg.membrane_reset_fraction;
+            d.refractory_until[n] = refractory;
+        } else {
+            const uint32_t j = (item - mine) - r * S;
+            const uint64_t slot = static_cast<uint64_t>(n) * S + j;
+            const uint64_t at = (static_cast<uint64_t>(rs) * cap + before + r) * S + j;
+            d.ring_value[at] = act * ld(&d.p.rec_weight[slot]);
+            d.ring_edge[at] = c.a->m.rec_edge[slot];
+        }
+    }
+    add_count(&c.ctl->tick_ainh[c.tick & 1], inhibitory);
+    if (threadIdx.x == 0) {  // the next deliveries read this tick's ring entry from LDS
+        sh.ring_tick[rs] = c.tick;
+        sh.ring_count[rs] = all;
     }
 }
 
@@ -1311,7 +1375,9 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
             const uint32_t local = item - A;
             const uint32_t r = local / S, j = local % S;
             const uint64_t rb = static_cast<uint64_t>(rs) * cap + r;
-            d.ring_value[rb * S + j] = ld(&act_val[r]) * ld(&d.p.rec_weight[static_cast<uint64_t>(ld(&act_list[r])) * S + j]);
+            const uint64_t slot = static_cast<uint64_t>(ld(&act_list[r])) * S + j;
+            d.ring_value[rb * S + j] = ld(&act_val[r]) * ld(&d.p.rec_weight[slot]);
+            d.ring_edge[rb * S + j] = a.m.rec_edge[slot];
         }
     }
     add_count(&c.ctl->tick_ainh[c.tick & 1], inhibitory);
@@ -1347,8 +1413,9 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
 
 // ---------------------------------------------------------------------------
 // Phase 5: learning destinations and signals (runtime.rs:1214-1263). Each wave
-// claims destinations, compacts them, and computes their serial 257-term dot
-// products from row tiles staged through LDS (coalesced row loads).
+// claims destinations, queues them, and computes their serial 257-term dot
+// products 64 at a time from output rows staged through LDS (coalesced row
+// loads).
 // ---------------------------------------------------------------------------
 // Device-scope 16-byte loads through a buffer resource (cache policy sc1: the
 // load misses the CU's L1 like ld()); the resource is wave-uniform and covers
@@ -1366,22 +1433,55 @@ __device__ __forceinline__ float ld4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off
 
 // Serial 257-term dot of one output row with the errors, in output order
 // (runtime.rs:1245-1250); eight 16-byte row loads are in flight at a time.
-__device__ __forceinline__ float signal_dot(__amdgpu_buffer_rsrc_t rows, uint32_t row_offset, const float* err) {
+// Learning signals of up to 64 destinations, one per lane (`dst` on lanes
+// below `count`; every lane of the wave calls): the output rows are streamed
+// through the wave's LDS stage one 128-byte line at a time, 8 whole lines per
+// load instruction, with the next line in flight while the current one is
+// summed; each lane then adds its row's 257 products in the reference's
+// order (runtime.rs:1214-1263).
+__device__ __forceinline__ float signal_rows(__amdgpu_buffer_rsrc_t rows, uint32_t dst, uint32_t count, const float* err,
+                                             float* stage) {
+    constexpr uint32_t kLines = kEndIndex / 32;  // 128-byte lines before the end-class weight
+    const uint32_t lane = __lane_id();
+    const uint32_t seg = lane & 7, sub = lane >> 3;
+    // this lane loads 16 bytes of rows sub, 8 + sub, ..., 56 + sub
+    uint32_t off[8];
+    bool live[8];
+#pragma unroll
+    for (uint32_t k = 0; k < 8; ++k) {
+        const uint32_t row = 8 * k + sub;
+        live[k] = row < count;
+        off[k] = static_cast<uint32_t>(__shfl(static_cast<int>(dst), static_cast<int>(row))) * (kOutStride * 4) + seg * 16;
+    }
+    const float tail = lane < count ? ld4(rows, dst * (kOutStride * 4) + 4 * kEndIndex) : 0.0f;
+    f32x4 v[8];
+#pragma unroll
+    for (uint32_t k = 0; k < 8; ++k) v[k] = live[k] ? ld16(rows, off[k]) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float acc = 0.0f;
-    for (uint32_t q = 0; q < kEndIndex / 4; q += 8) {
-        f32x4 v[8];
+    for (uint32_t line = 0; line < kLines; ++line) {
+        wave_sync();
 #pragma unroll
-        for (uint32_t u = 0; u < 8; ++u) v[u] = ld16(rows, row_offset + 16 * (q + u));
+        for (uint32_t k = 0; k < 8; ++k) {
+            float* st = stage + (8 * k + sub) * kStageRowFloats + seg * 4;
+            st[0] = v[k].x;
+            st[1] = v[k].y;
+            st[2] = v[k].z;
+            st[3] = v[k].w;
+        }
+        wave_sync();
+        if (line + 1 < kLines) {
 #pragma unroll
-        for (uint32_t u = 0; u < 8; ++u) {
-            const float* e = err + 4 * (q + u);
-            acc += v[u].x * e[0];
-            acc += v[u].y * e[1];
-            acc += v[u].z * e[2];
-            acc += v[u].w * e[3];
+            for (uint32_t k = 0; k < 8; ++k)
+                v[k] = live[k] ? ld16(rows, off[k] + (line + 1) * 128) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        if (lane < count) {
+            const float* r = stage + lane * kStageRowFloats;
+            const float* e = err + line * 32;
+#pragma unroll
+            for (uint32_t o = 0; o < 32; ++o) acc += r[o] * e[o];
         }
     }
-    acc += ld4(rows, row_offset + 4 * kEndIndex) * err[kEndIndex];
+    acc += tail * err[kEndIndex];
     return acc;
 }
 
@@ -1406,6 +1506,7 @@ __device__ __forceinline__ void phase_signals(const StepCtx& c, StepShared& sh) 
     uint32_t queued = 0, claimed = 0;
     // the host limits N * kOutStride * 4 to below 2^31 bytes
     const __amdgpu_buffer_rsrc_t rows = coherent_rsrc(d.p.out_w, cfg.neuron_count * kOutStride * 4);
+    float* stage = reinterpret_cast<float*>(step_lds + static_cast<size_t>(wave) * wave_lds_bytes(cfg.neurons_per_block));
     // claimed destinations are queued per wave and computed 64 at a time, one row per lane
     for (uint32_t base = c.gtid - lane; base < total; base += c.gstride) {
         const uint32_t item = base + lane;
@@ -1428,13 +1529,14 @@ __device__ __forceinline__ void phase_signals(const StepCtx& c, StepShared& sh) 
             wave_sync();
             if (lane + kWaveSize < queued) queue[lane] = rest;
             queued -= kWaveSize;
-            d.learning_signal[mine] = signal_dot(rows, mine * kOutStride * 4, sh.err);
+            d.learning_signal[mine] = signal_rows(rows, mine, kWaveSize, sh.err, stage);
         }
     }
     wave_sync();
-    if (lane < queued) {
-        const uint32_t mine = queue[lane];
-        d.learning_signal[mine] = signal_dot(rows, mine * kOutStride * 4, sh.err);
+    if (queued > 0) {
+        const uint32_t mine = lane < queued ? queue[lane] : 0u;
+        const float sig = signal_rows(rows, mine, queued, sh.err, stage);
+        if (lane < queued) d.learning_signal[mine] = sig;
     }
     add_count(&c.ctl->tick_dest[c.tick & 1], claimed);
 }
@@ -1709,8 +1811,11 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 0))) break;
         phase_fold_select(c);
         if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 1))) break;
+        // steps without eligibility updates or readout fold the post phase
+        // into the active-list write (one barrier fewer)
+        const bool fused = redundant && !trace && !(sp.flags & kStepOutput);
         if (redundant) {
-            write_active(c);
+            write_active(c, sp, s, sh, fused);
             if (trace) phase_eligibility(c);
         } else {
             if (c.part == 0) global_select(c, sh);
@@ -1720,9 +1825,11 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             }
         }
         if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 2))) break;
-        if (trace) c.parity ^= 1;
-        phase_post(c, sp, s, sh);
-        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 3))) break;
+        if (!fused) {
+            if (trace) c.parity ^= 1;
+            phase_post(c, sp, s, sh);
+            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 3))) break;
+        }
         const bool learn = (sp.flags & kStepLearn) != 0;
         if (learn && sp.plasticity_scale > 0.0f) {
             c.dest_epoch += 1;

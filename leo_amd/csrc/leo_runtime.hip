@@ -283,6 +283,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     size_t o_wt = l.add<uint32_t>(kMaxWaves);
     size_t o_bep = l.add<uint32_t>(z.blocks), o_tb = l.add<uint32_t>(z.blocks * z.block_words);
     size_t o_ra = l.add<uint32_t>(kRing * z.cap), o_rv = l.add<float>(kRing * z.cap), o_rval = l.add<float>(kRing * z.cap * z.s);
+    size_t o_redge = l.add<uint32_t>(kRing * z.cap * z.s);
     size_t o_rt = l.add<float>(7 * z.ns), o_rl = l.add<uint32_t>(z.ns), o_rm = l.add<uint8_t>(z.ns), o_rlist = l.add<uint32_t>(2 * z.ns);
     size_t o_it = l.add<float>(7 * z.ni), o_il = l.add<uint32_t>(z.ni), o_im = l.add<uint8_t>(z.ni), o_ilist = l.add<uint32_t>(2 * z.ni);
     size_t o_lg = l.add<float>(kOutStride), o_pr = l.add<float>(kOutStride), o_er = l.add<float>(kOutStride);
@@ -317,6 +318,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     d.ring_active = reinterpret_cast<uint32_t*>(b + o_ra);
     d.ring_act = reinterpret_cast<float*>(b + o_rv);
     d.ring_value = reinterpret_cast<float*>(b + o_rval);
+    d.ring_edge = reinterpret_cast<uint32_t*>(b + o_redge);
     d.rec_trace = reinterpret_cast<float*>(b + o_rt);
     d.rec_last = reinterpret_cast<uint32_t*>(b + o_rl);
     d.rec_mark = reinterpret_cast<uint8_t*>(b + o_rm);
@@ -404,6 +406,13 @@ uint32_t choose_wgs_per_lane(LeoHipRuntime* h, uint32_t lanes, bool canonical) {
         uint64_t by_edges = h->z.ns / 32768;
         want = static_cast<uint32_t>(std::max<uint64_t>(1, std::max(by_blocks, by_edges)));
         want = std::min<uint32_t>(want, 64);
+        if (canonical) {
+            // the canonical lane is latency-bound (replay): its workgroups
+            // share one XCD, one per CU (measured: a second workgroup per CU
+            // slows its steps)
+            const uint32_t per_xcd = std::max<uint32_t>(1, static_cast<uint32_t>(h->cus) / kXcds);
+            want = static_cast<uint32_t>(std::min<uint64_t>(per_xcd, std::max<uint64_t>(1, std::max(2 * by_blocks, by_edges))));
+        }
     }
     return std::max<uint32_t>(1, std::min(want, limit));
 }
@@ -526,9 +535,9 @@ void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     std::vector<Lane*> lanes;
     for (auto& r : runs) lanes.push_back(r.lane);
     stage_descs(h, lanes);
-    // lanes are padded to a multiple of the 8 XCDs so that each lane's
+    // lanes are padded to a multiple of the XCD count so that each lane's
     // workgroups land on one XCD (see lane_steps)
-    const uint32_t padded = (count + 7) / 8 * 8;
+    const uint32_t padded = (count + kXcds - 1) / kXcds * kXcds;
     const uint32_t P = choose_wgs_per_lane(h, padded, count == 1 && runs[0].lane == h->canonical.get());
     const uint32_t stride = P > 1 ? padded : count;
     KernelArgs a = kernel_args(h, reinterpret_cast<LaneDesc*>(h->lane_descs.base), count, P);
@@ -767,7 +776,7 @@ void upload_topology(LeoHipRuntime* h, const LeoModelView& m) {
     Layout l;
     size_t o_ex = l.add<float>(z.n), o_ty = l.add<uint8_t>(z.n), o_rt = l.add<uint32_t>(z.ns);
     size_t o_rb = l.add<uint8_t>(z.ns), o_rd = l.add<uint8_t>(z.ns), o_it = l.add<uint32_t>(z.ni);
-    size_t o_ib = l.add<uint8_t>(z.ni), o_off = l.add<uint64_t>(z.n + 1);
+    size_t o_ib = l.add<uint8_t>(z.ni), o_off = l.add<uint64_t>(z.n + 1), o_edge = l.add<uint32_t>(z.ns);
     h->shared.allocate(l.cursor);
     char* b = h->shared.base;
     h->sm.excitability = reinterpret_cast<const float*>(b + o_ex);
@@ -778,6 +787,9 @@ void upload_topology(LeoHipRuntime* h, const LeoModelView& m) {
     h->sm.in_target = reinterpret_cast<const uint32_t*>(b + o_it);
     h->sm.in_branch = reinterpret_cast<const uint8_t*>(b + o_ib);
     h->sm.bucket_offset = reinterpret_cast<const uint64_t*>(b + o_off);
+    h->sm.rec_edge = reinterpret_cast<const uint32_t*>(b + o_edge);
+    std::vector<uint32_t> edges(z.ns);
+    for (uint64_t i = 0; i < z.ns; ++i) edges[i] = pack_edge(m.rec_target[i], m.rec_delay[i], m.rec_branch[i]);
     hipStream_t s = h->stream;
     upload(b + o_ex, m.excitability, z.n * 4, s);
     upload(b + o_ty, m.neuron_type, z.n, s);
@@ -787,6 +799,7 @@ void upload_topology(LeoHipRuntime* h, const LeoModelView& m) {
     upload(b + o_it, m.in_target, z.ni * 4, s);
     upload(b + o_ib, m.in_branch, z.ni, s);
     upload(b + o_off, offsets.data(), offsets.size() * 8, s);
+    upload(b + o_edge, edges.data(), z.ns * 4, s);
     sync(s);
 }
 
@@ -1408,6 +1421,8 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
     return guarded([&] {
         if (!config || !model || !out) throw Error(LEO_ERR_INVALID_ARGUMENT, "null argument");
         leo::model_validate(*config, *model);
+        if (config->device.neuron_count > leo::kMaxPackedNeurons)
+            throw Error(LEO_ERR_UNSUPPORTED, "neuron_count above 2^28 is not supported by the packed synapse layout");
         if (config->device.neurons_per_block > leo::kMaxBlockNeurons)
             throw Error(LEO_ERR_UNSUPPORTED, "neurons_per_block above 1024 is not supported by the device selection");
         if (static_cast<uint64_t>(config->device.neuron_count) * leo::kOutStride * 4 >= (1ULL << 31))
