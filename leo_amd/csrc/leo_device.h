@@ -9,6 +9,16 @@
 
 #include "leo_hip_abi.h"
 
+// Device memory pointers in the structures below are global-address-space
+// pointers in the kernels' device code (global_* rather than flat memory
+// instructions, which would also count against the LDS wait counter); every
+// other view, the host runtime included, sees plain pointers of the same size.
+#if defined(__HIP_DEVICE_COMPILE__) && defined(LEO_KERNEL_TRANSLATION_UNIT)
+#define LEO_GLOBAL __attribute__((address_space(1)))
+#else
+#define LEO_GLOBAL
+#endif
+
 namespace leo {
 
 constexpr uint32_t kSymbols = 258;
@@ -159,93 +169,93 @@ struct LaneControl {
 // Learned parameters of a lane (private copy for story lanes, the canonical
 // image for the canonical runtime).
 struct LaneParams {
-    float* threshold;        // N
-    float* rec_weight;       // N*S (slot = src*S + j)
-    float* in_weight;        // 258*F
-    float* out_w;            // N * kOutStride, neuron-major
-    float* bias;             // kOutStride
-    uint64_t* ctx_keys;      // slots
-    float* ctx_emb;          // slots * E
-    uint32_t* ctx_obs;       // slots
-    float* ctx_out;          // 257 * E, output-major
+    float LEO_GLOBAL* threshold;        // N
+    float LEO_GLOBAL* rec_weight;       // N*S (slot = src*S + j)
+    float LEO_GLOBAL* in_weight;        // 258*F
+    float LEO_GLOBAL* out_w;            // N * kOutStride, neuron-major
+    float LEO_GLOBAL* bias;             // kOutStride
+    uint64_t LEO_GLOBAL* ctx_keys;      // slots
+    float LEO_GLOBAL* ctx_emb;          // slots * E
+    uint32_t LEO_GLOBAL* ctx_obs;       // slots
+    float LEO_GLOBAL* ctx_out;          // 257 * E, output-major
 };
 
 // Everything a kernel needs to run one lane.
 struct LaneDesc {
     LaneParams p;
-    LaneControl* ctl;
+    LaneControl LEO_GLOBAL* ctl;
     // neuron state (N)
-    float* membrane;
-    float* activation;
-    float* fatigue;
-    uint32_t* refractory_until;
-    float* branches;         // N*4
-    uint32_t* last_tick;
-    float* adapt;            // 3*N (fast, medium, slow)
-    uint32_t* touched_epoch; // == tick+1 when touched this tick
-    uint32_t* touched_list;  // N
-    uint32_t* selected_epoch;
-    uint32_t* dest_epoch;
-    float* learning_signal;
-    uint32_t* bucket_count;  // N
-    uint64_t* bucket;        // 2 words per entry: delivery-order key, value bits
+    float LEO_GLOBAL* membrane;
+    float LEO_GLOBAL* activation;
+    float LEO_GLOBAL* fatigue;
+    uint32_t LEO_GLOBAL* refractory_until;
+    float LEO_GLOBAL* branches;         // N*4
+    uint32_t LEO_GLOBAL* last_tick;
+    float LEO_GLOBAL* adapt;            // 3*N (fast, medium, slow)
+    uint32_t LEO_GLOBAL* touched_epoch; // == tick+1 when touched this tick
+    uint32_t LEO_GLOBAL* touched_list;  // N
+    uint32_t LEO_GLOBAL* selected_epoch;
+    uint32_t LEO_GLOBAL* dest_epoch;
+    float LEO_GLOBAL* learning_signal;
+    uint32_t LEO_GLOBAL* bucket_count;  // N
+    uint64_t LEO_GLOBAL* bucket;        // 2 words per entry: delivery-order key, value bits
     // block selection
-    uint32_t* range_winners; // blocks * max_active_per_block: winners of each selecting wave's block
+    uint32_t LEO_GLOBAL* range_winners; // blocks * max_active_per_block: winners of each selecting wave's block
                              // range in block order, compacted from the row of its first block
-    float* range_winner_act; // same layout: activation of each winner
-    float* block_cutoff;     // blocks
-    uint32_t* block_epoch;   // blocks: tick+1 when the block's selection above is current
-    uint32_t* touched_bits;  // blocks * block_words: neurons touched this tick, cleared by phase 2
-    uint32_t* wave_total;    // kMaxWaves: block winners of each selecting wave's block range
+    float LEO_GLOBAL* range_winner_act; // same layout: activation of each winner
+    float LEO_GLOBAL* block_cutoff;     // blocks
+    uint32_t LEO_GLOBAL* block_epoch;   // blocks: tick+1 when the block's selection above is current
+    uint32_t LEO_GLOBAL* touched_bits;  // blocks * block_words: neurons touched this tick, cleared by phase 2
+    uint32_t LEO_GLOBAL* wave_total;    // kMaxWaves: block winners of each selecting wave's block range
     // ring: per slot, up to max_active_global active neurons, activation, and S snapshot values each
-    uint32_t* ring_active;   // kRing * cap
-    float* ring_act;         // kRing * cap
-    float* ring_value;       // kRing * cap * S
-    uint32_t* ring_edge;     // kRing * cap * S: packed synapse of each snapshot value (target, delay, branch)
+    uint32_t LEO_GLOBAL* ring_active;   // kRing * cap
+    float LEO_GLOBAL* ring_act;         // kRing * cap
+    float LEO_GLOBAL* ring_value;       // kRing * cap * S
+    uint32_t LEO_GLOBAL* ring_edge;     // kRing * cap * S: packed synapse of each snapshot value (target, delay, branch)
     // recurrent traces (N*S): branch, membrane, fatigue, 3 adaptation sensitivities, eligibility
-    float* rec_trace;        // 7 * NS (SoA planes)
-    uint32_t* rec_last;      // NS
-    uint8_t* rec_mark;       // NS
-    uint32_t* rec_list;      // 2 * NS
+    float LEO_GLOBAL* rec_trace;        // 7 * NS (SoA planes)
+    uint32_t LEO_GLOBAL* rec_last;      // NS
+    uint8_t LEO_GLOBAL* rec_mark;       // NS
+    uint32_t LEO_GLOBAL* rec_list;      // 2 * NS
     // input traces (258*F)
-    float* in_trace;         // 7 * NI
-    uint32_t* in_last;
-    uint8_t* in_mark;
-    uint32_t* in_list;       // 2 * NI
+    float LEO_GLOBAL* in_trace;         // 7 * NI
+    uint32_t LEO_GLOBAL* in_last;
+    uint8_t LEO_GLOBAL* in_mark;
+    uint32_t LEO_GLOBAL* in_list;       // 2 * NI
     // readout
-    float* logits;           // kOutStride
-    float* probs;            // kOutStride
-    float* errors;           // kOutStride
-    float* ctx_latent;       // E
+    float LEO_GLOBAL* logits;           // kOutStride
+    float LEO_GLOBAL* probs;            // kOutStride
+    float LEO_GLOBAL* errors;           // kOutStride
+    float LEO_GLOBAL* ctx_latent;       // E
     // change tracking bitmaps (ParameterChanges)
-    uint32_t* ch_threshold;  // ceil(N/32)
-    uint32_t* ch_rec;        // ceil(NS/32)
-    uint32_t* ch_in;         // ceil(NI/32)
-    uint32_t* ch_out;        // ceil(N/32)
-    uint32_t* ch_ctx;        // ceil(slots/32)
+    uint32_t LEO_GLOBAL* ch_threshold;  // ceil(N/32)
+    uint32_t LEO_GLOBAL* ch_rec;        // ceil(NS/32)
+    uint32_t LEO_GLOBAL* ch_in;         // ceil(NI/32)
+    uint32_t LEO_GLOBAL* ch_out;        // ceil(N/32)
+    uint32_t LEO_GLOBAL* ch_ctx;        // ceil(slots/32)
     // schedule for the current launch
-    const StepParams* steps;
-    StepRecord* records;
+    const StepParams LEO_GLOBAL* steps;
+    StepRecord LEO_GLOBAL* records;
     uint32_t step_count;
     uint32_t pad;
     // phase profile (profiling kernel only): per phase, summed wall-clock ticks of
     // workgroup 0's own work [0..kPhases) and of its barrier wait [kPhases..2*kPhases)
-    unsigned long long* phase_profile;
+    unsigned long long LEO_GLOBAL* phase_profile;
 };
 
 constexpr uint32_t kPhases = 8;
 
 // Read-only model data shared by every lane.
 struct SharedModel {
-    const float* excitability;
-    const uint8_t* neuron_type;
-    const uint32_t* rec_target;
-    const uint8_t* rec_branch;
-    const uint8_t* rec_delay;
-    const uint32_t* in_target;
-    const uint8_t* in_branch;
-    const uint64_t* bucket_offset;   // N+1
-    const uint32_t* rec_edge;        // N*S: pack_edge(target, delay, branch) of each recurrent slot
+    const float LEO_GLOBAL* excitability;
+    const uint8_t LEO_GLOBAL* neuron_type;
+    const uint32_t LEO_GLOBAL* rec_target;
+    const uint8_t LEO_GLOBAL* rec_branch;
+    const uint8_t LEO_GLOBAL* rec_delay;
+    const uint32_t LEO_GLOBAL* in_target;
+    const uint8_t LEO_GLOBAL* in_branch;
+    const uint64_t LEO_GLOBAL* bucket_offset;   // N+1
+    const uint32_t LEO_GLOBAL* rec_edge;        // N*S: pack_edge(target, delay, branch) of each recurrent slot
 };
 
 // A recurrent synapse packed into one word: target (28 bits), log2 of the
@@ -277,7 +287,7 @@ struct KernelArgs {
 enum : uint32_t { kMergeThreshold = 0, kMergeRecurrent, kMergeInput, kMergeOutput, kMergeBias, kMergeContextOut };
 
 struct MergeArgs {
-    float* canonical;
+    float LEO_GLOBAL* canonical;
     const float* const* lanes;   // per-lane pointer to the same tensor
     uint32_t lane_count;
     uint32_t kind;
@@ -285,10 +295,10 @@ struct MergeArgs {
     uint32_t row;                // logical row length for padded layouts (output: 257)
     uint32_t stride;             // physical row stride (output: kOutStride)
     uint32_t synapses_per_neuron;
-    const uint8_t* neuron_type;
+    const uint8_t LEO_GLOBAL* neuron_type;
     float weight_min, weight_max;
-    unsigned long long* updates;
-    uint32_t* error;
+    unsigned long long LEO_GLOBAL* updates;
+    uint32_t LEO_GLOBAL* error;
     // Lane groups (batches larger than the resident lanes): kMergeAccumulate
     // continues the lane-ordered f64 sum of each element in acc (and the
     // any-lane-changed flag in any), starting from zero when `first`;
@@ -296,8 +306,8 @@ struct MergeArgs {
     uint32_t mode;
     uint32_t first;
     uint32_t total_lanes;
-    double* acc;
-    uint8_t* any;
+    double LEO_GLOBAL* acc;
+    uint8_t LEO_GLOBAL* any;
 };
 enum : uint32_t { kMergeDirect = 0, kMergeAccumulate = 1, kMergeFinalize = 2 };
 

@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 
 #include "glibc_expf.h"
+#define LEO_KERNEL_TRANSLATION_UNIT  // global-address-space descriptor pointers
 #include "leo_device.h"
 
 namespace leo {
@@ -37,22 +38,40 @@ __device__ __forceinline__ float maxnum(float a, float b) {  // Rust f32::max
 }
 __device__ __forceinline__ bool finitef(float v) { return (__float_as_uint(v) & 0x7f800000u) != 0x7f800000u; }
 
-// compiler-rt powisf2 (Rust f32::powi with a runtime exponent).
-__device__ __forceinline__ float powisf2(float a, int b) {
-    float r = 1.0f;
+// decay_for_elapsed (runtime.rs:78-85: 1 for 0 ticks, the base for 1, else
+// Rust's f32::powi, i.e. compiler-rt's powisf2 square-and-multiply) of the six
+// state decays (branch, membrane, fatigue, fast, medium and slow adaptation)
+// for one elapsed count, in one loop over the exponent's bits: each base sees
+// exactly powisf2's sequence of multiplications.
+struct StateDecays {
+    float branch, membrane, fatigue, fast, medium, slow;
+};
+__device__ __forceinline__ StateDecays state_decays(const LeoConfig& cfg, uint32_t elapsed) {
+    float a0 = cfg.branch_decay, a1 = cfg.membrane_decay, a2 = cfg.fatigue_decay;
+    float a3 = cfg.adaptation_fast_decay, a4 = cfg.adaptation_medium_decay, a5 = cfg.adaptation_slow_decay;
+    if (elapsed == 0) return {1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f};
+    if (elapsed == 1) return {a0, a1, a2, a3, a4, a5};
+    float r0 = 1.0f, r1 = 1.0f, r2 = 1.0f, r3 = 1.0f, r4 = 1.0f, r5 = 1.0f;
+    int b = static_cast<int>(elapsed > 0x7fffffffu ? 0x7fffffffu : elapsed);
     while (true) {
-        if (b & 1) r *= a;
+        if (b & 1) {
+            r0 *= a0;
+            r1 *= a1;
+            r2 *= a2;
+            r3 *= a3;
+            r4 *= a4;
+            r5 *= a5;
+        }
         b /= 2;
         if (b == 0) break;
-        a *= a;
+        a0 *= a0;
+        a1 *= a1;
+        a2 *= a2;
+        a3 *= a3;
+        a4 *= a4;
+        a5 *= a5;
     }
-    return r;
-}
-// runtime.rs:78-85
-__device__ __forceinline__ float decay_for_elapsed(float base, uint32_t elapsed) {
-    if (elapsed == 0) return 1.0f;
-    if (elapsed == 1) return base;
-    return powisf2(base, static_cast<int>(elapsed > 0x7fffffffu ? 0x7fffffffu : elapsed));
+    return {r0, r1, r2, r3, r4, r5};
 }
 // learning.rs:7-24
 __device__ __forceinline__ float analog_rank_surrogate(float margin, float cutoff, bool selected, float width,
@@ -295,7 +314,7 @@ extern __shared__ __align__(16) unsigned char step_lds[];
 struct StepCtx {
     const KernelArgs* a;
     LaneDesc d;
-    LaneControl* ctl;
+    LaneControl LEO_GLOBAL* ctl;
     uint32_t tick;
     uint32_t part;     // workgroup index within the lane group
     uint32_t P;
@@ -316,36 +335,59 @@ struct StepCtx {
 // decayed branch-sensitivity plane value (the caller adds the activation).
 __device__ __forceinline__ float advance_trace(float* planes, uint64_t plane, uint32_t* last, uint32_t slot,
                                                uint32_t tick, const LeoConfig& cfg) {
+    // every plane in one round of loads
     float bs = ld(&planes[slot]);
+    const float ms = ld(&planes[plane + slot]), fs = ld(&planes[2 * plane + slot]);
+    const float f0 = ld(&planes[3 * plane + slot]), f1 = ld(&planes[4 * plane + slot]), f2 = ld(&planes[5 * plane + slot]);
     const uint32_t e = tick - ld(&last[slot]);
     if (e == 0) return bs;
-    bs *= decay_for_elapsed(cfg.branch_decay, e);
-    planes[plane + slot] = ld(&planes[plane + slot]) * decay_for_elapsed(cfg.membrane_decay, e);
-    planes[2 * plane + slot] = ld(&planes[2 * plane + slot]) * decay_for_elapsed(cfg.fatigue_decay, e);
-    planes[3 * plane + slot] = ld(&planes[3 * plane + slot]) * decay_for_elapsed(cfg.adaptation_fast_decay, e);
-    planes[4 * plane + slot] = ld(&planes[4 * plane + slot]) * decay_for_elapsed(cfg.adaptation_medium_decay, e);
-    planes[5 * plane + slot] = ld(&planes[5 * plane + slot]) * decay_for_elapsed(cfg.adaptation_slow_decay, e);
+    const StateDecays k = state_decays(cfg, e);
+    bs *= k.branch;
+    planes[plane + slot] = ms * k.membrane;
+    planes[2 * plane + slot] = fs * k.fatigue;
+    planes[3 * plane + slot] = f0 * k.fast;
+    planes[4 * plane + slot] = f1 * k.medium;
+    planes[5 * plane + slot] = f2 * k.slow;
     last[slot] = tick;
     return bs;
 }
 
 // Late fields of a step record: work counters complete only after the step's
 // last barrier, so the record is finished by the next step (or kernel end).
-__device__ __forceinline__ void finalize_record(const LaneDesc& d, LaneControl* ctl, uint32_t step_index, uint32_t tick) {
-    StepRecord& rec = d.records[step_index];
+__device__ __forceinline__ void finalize_record(const LaneDesc& d, LaneControl LEO_GLOBAL* ctl, uint32_t step_index,
+                                                uint32_t tick) {
     const uint32_t k = tick & 1;
-    rec.events = ld(&ctl->tick_events[k]);
-    rec.touched = ld(&ctl->tick_touched[k]);
-    rec.scanned_rec = ld(&ctl->tick_scan_rec[k]);
-    rec.scanned_in = ld(&ctl->tick_scan_in[k]);
-    rec.destinations = ld(&ctl->tick_dest[k]);
-    rec.active_inhibitory = ld(&ctl->tick_ainh[k]);
+    // all loads first (one round trip), then the stores
+    const uint32_t events = ld(&ctl->tick_events[k]), touched = ld(&ctl->tick_touched[k]);
+    const uint32_t scanned_rec = ld(&ctl->tick_scan_rec[k]), scanned_in = ld(&ctl->tick_scan_in[k]);
+    const uint32_t destinations = ld(&ctl->tick_dest[k]), inhibitory = ld(&ctl->tick_ainh[k]);
+    StepRecord LEO_GLOBAL& rec = d.records[step_index];
+    rec.events = events;
+    rec.touched = touched;
+    rec.scanned_rec = scanned_rec;
+    rec.scanned_in = scanned_in;
+    rec.destinations = destinations;
+    rec.active_inhibitory = inhibitory;
+}
+// Once tick-1 is complete (phase 3 of `tick`, by one thread): its record is
+// finished and its per-tick counters, which tick+1 reuses, are cleared.
+__device__ __forceinline__ void roll_counters(const StepCtx& c, uint32_t step_index) {
+    LaneControl LEO_GLOBAL* ctl = c.ctl;
+    if (step_index > 0) finalize_record(c.d, ctl, step_index - 1, c.tick - 1);
+    const uint32_t n = (c.tick + 1) & 1;
+    ctl->tick_touched[n] = 0;
+    ctl->tick_supra[n] = 0;
+    ctl->tick_events[n] = 0;
+    ctl->tick_dest[n] = 0;
+    ctl->tick_ainh[n] = 0;
+    ctl->tick_scan_rec[n] = 0;
+    ctl->tick_scan_in[n] = 0;
 }
 
 // Entry p of target n's delivery bucket: the first two at fixed places
 // (2n, 2n+1), the rest in the target's overflow range.
-__device__ __forceinline__ uint64_t bucket_entry(const SharedModel& m, uint32_t n, uint32_t p) {
-    return p < 2 ? 2ull * n + p : m.bucket_offset[n] + (p - 2);
+__device__ __forceinline__ uint64_t bucket_entry(uint64_t overflow, uint32_t n, uint32_t p) {
+    return p < 2 ? 2ull * n + p : overflow + (p - 2);
 }
 
 __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t step_index, const StepShared& sh) {
@@ -358,16 +400,7 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
     const uint64_t NI = static_cast<uint64_t>(kSymbols) * F;
     const bool trace = (sp.flags & kStepLearnTrace) != 0;
     const uint32_t tick = c.tick;
-    if (c.part == 0 && threadIdx.x == 0) {
-        if (step_index > 0) finalize_record(d, ctl, step_index - 1, tick - 1);
-        const uint32_t n = (tick + 1) & 1;
-        ctl->tick_touched[n] = 0;
-        ctl->tick_supra[n] = 0;
-        ctl->tick_events[n] = 0;
-        ctl->tick_dest[n] = 0;
-        ctl->tick_ainh[n] = 0;
-        ctl->tick_scan_rec[n] = 0;
-        ctl->tick_scan_in[n] = 0;
+    if (c.part == 0 && threadIdx.x == 0) {  // this step's next eligible lists
         ctl->rec_count[c.parity ^ 1] = 0;
         ctl->in_count[c.parity ^ 1] = 0;
     }
@@ -439,8 +472,10 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
             key = (4ULL << 61) | (static_cast<uint64_t>(i) << 2) | br;
         }
         if (scatter) {
+            // the overflow offset is loaded with the counter increment (one round trip)
+            const uint64_t overflow = a.m.bucket_offset[target];
             const uint32_t p = atomicAdd(&d.bucket_count[target], 1u);
-            const uint64_t at = bucket_entry(a.m, target, p);
+            const uint64_t at = bucket_entry(overflow, target, p);
             d.bucket[2 * at] = key;
             d.bucket[2 * at + 1] = __float_as_uint(value);
         }
@@ -637,6 +672,7 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
     float ad0 = ld(&d.adapt[n]), ad1 = ld(&d.adapt[N + n]), ad2 = ld(&d.adapt[2 * N + n]);
     const uint32_t last = ld(&d.last_tick[n]);
     const uint32_t cnt = ld(&d.bucket_count[n]);
+    const uint64_t overflow = a.m.bucket_offset[n];  // loaded with the state (used when cnt > 2)
     // the two fixed bucket entries are read with the state
     const uint64_t* fixed = d.bucket + 4ull * n;
     const uint64_t k0 = ld(&fixed[0]), v0 = ld(&fixed[1]), k1 = ld(&fixed[2]), v1 = ld(&fixed[3]);
@@ -644,16 +680,16 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
     const float threshold = ld(&d.p.threshold[n]);
     const uint32_t e = tick - last;
     if (e > 0) {
-        const float bd = decay_for_elapsed(cfg.branch_decay, e);
-        b0 *= bd;
-        b1 *= bd;
-        b2 *= bd;
-        b3 *= bd;
-        mem *= decay_for_elapsed(cfg.membrane_decay, e);
-        fat *= decay_for_elapsed(cfg.fatigue_decay, e);
-        ad0 *= decay_for_elapsed(cfg.adaptation_fast_decay, e);
-        ad1 *= decay_for_elapsed(cfg.adaptation_medium_decay, e);
-        ad2 *= decay_for_elapsed(cfg.adaptation_slow_decay, e);
+        const StateDecays k = state_decays(cfg, e);
+        b0 *= k.branch;
+        b1 *= k.branch;
+        b2 *= k.branch;
+        b3 *= k.branch;
+        mem *= k.membrane;
+        fat *= k.fatigue;
+        ad0 *= k.fast;
+        ad1 *= k.medium;
+        ad2 *= k.slow;
         d.fatigue[n] = fat;
         d.adapt[n] = ad0;
         d.adapt[N + n] = ad1;
@@ -687,7 +723,7 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
             v[0] = static_cast<uint32_t>(v0);
             k[1] = k1;
             v[1] = static_cast<uint32_t>(v1);
-            const uint64_t* over = d.bucket + 2 * a.m.bucket_offset[n];
+            const uint64_t LEO_GLOBAL* over = d.bucket + 2 * overflow;
 #pragma unroll
             for (uint32_t x = 2; x < 8; ++x) {
                 k[x] = x < cnt ? ld(&over[2 * (x - 2)]) : ~0ULL;
@@ -706,7 +742,7 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
                 uint64_t best = ~0ULL;
                 uint32_t best_v = 0;
                 for (uint32_t x = 0; x < cnt; ++x) {
-                    const uint64_t at = bucket_entry(a.m, n, x);
+                    const uint64_t at = bucket_entry(overflow, n, x);
                     const uint64_t kx = ld(&d.bucket[2 * at]);
                     if ((!started || kx > last) && kx < best) {
                         best = kx;
@@ -970,32 +1006,43 @@ __device__ __forceinline__ void write_active(const StepCtx& c, const StepParams&
     }
     const float activity = static_cast<float>(all) / static_cast<float>(cfg.neuron_count);
     if (c.part == 0 && threadIdx.x == 0) {
-        LaneControl* ctl = c.ctl;
+        LaneControl LEO_GLOBAL* ctl = c.ctl;
+        // the loads of this block go out together, before any store
+        const float pi_old = ld(&ctl->population_inhibition);
+        uint32_t supra = 0, cells = 0, probes = 0, applied = 0, rec_n = 0, in_n = 0;
+        if (fuse_post) {
+            supra = ld(&ctl->tick_supra[c.tick & 1]);
+            cells = ld(&ctl->ctx_count);
+            probes = ld(&ctl->ctx_probes);
+            applied = ld(&ctl->ctx_applied);
+            rec_n = ld(&ctl->rec_count[c.parity]);
+            in_n = ld(&ctl->in_count[c.parity]);
+        }
+        roll_counters(c, step_index);
         ctl->active_count = all;
         ctl->block_selected = all;
         ctl->clipped = 0;
         ctl->pop_cutoff = 0.0f;
         ctl->ring_tick[rs] = c.tick;
         ctl->ring_count[rs] = all;
-        const float pi = clampf(
-            ld(&ctl->population_inhibition) + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
-            cfg.population_inhibition_max);
+        const float pi = clampf(pi_old + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
+                                cfg.population_inhibition_max);
         ctl->population_inhibition = pi;
         if (fuse_post) {
             // the step record the post phase would write (no readout this step)
-            StepRecord& rec = d.records[step_index];
+            StepRecord LEO_GLOBAL& rec = d.records[step_index];
             rec.p_target = 0.0f;
             rec.predicted = 0;
             rec.population_inhibition = pi;
             rec.active = all;
-            rec.suprathreshold = ld(&ctl->tick_supra[c.tick & 1]);
+            rec.suprathreshold = supra;
             rec.block_selected = all;
             rec.clipped = 0;
-            rec.context_cells = ld(&ctl->ctx_count);
-            rec.context_probes = ld(&ctl->ctx_probes);
-            rec.context_applied = ld(&ctl->ctx_applied);
-            rec.eligible_rec = ld(&ctl->rec_count[c.parity]);
-            rec.eligible_in = ld(&ctl->in_count[c.parity]);
+            rec.context_cells = cells;
+            rec.context_probes = probes;
+            rec.context_applied = applied;
+            rec.eligible_rec = rec_n;
+            rec.eligible_in = in_n;
             rec.error_code = 0;
         }
     }
@@ -1041,7 +1088,7 @@ __device__ __forceinline__ void write_active(const StepCtx& c, const StepParams&
 
 // Binding global cap (workgroup 0): sort every block winner by
 // (activation desc, tie asc), keep max_active_global (runtime.rs:1029-1057).
-__device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh) {
+__device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, uint32_t step_index) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -1101,6 +1148,7 @@ __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh) 
     }
     __syncthreads();
     if (threadIdx.x == 0) {
+        roll_counters(c, step_index);
         LaneControl* ctl = c.ctl;
         ctl->active_count = active;
         ctl->block_selected = running;
@@ -1125,12 +1173,13 @@ __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uin
     const float e = ld(&planes[6 * plane + slot]);
     const uint32_t el = tick - ld(&last[slot]);
     if (el > 0) {
-        bs *= decay_for_elapsed(cfg.branch_decay, el);
-        ms *= decay_for_elapsed(cfg.membrane_decay, el);
-        fs *= decay_for_elapsed(cfg.fatigue_decay, el);
-        as0 *= decay_for_elapsed(cfg.adaptation_fast_decay, el);
-        as1 *= decay_for_elapsed(cfg.adaptation_medium_decay, el);
-        as2 *= decay_for_elapsed(cfg.adaptation_slow_decay, el);
+        const StateDecays k = state_decays(cfg, el);
+        bs *= k.branch;
+        ms *= k.membrane;
+        fs *= k.fatigue;
+        as0 *= k.fast;
+        as1 *= k.medium;
+        as2 *= k.slow;
         last[slot] = tick;
     }
     // every destination value in one round of loads (most are used only when
@@ -1388,20 +1437,26 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
     const uint32_t readout_wg = c.P - 1;
     if (c.part == readout_wg) {
         if (threadIdx.x == 0) {
-            StepRecord& rec = d.records[step_index];
-            LaneControl* ctl = c.ctl;
+            LaneControl LEO_GLOBAL* ctl = c.ctl;
+            // the loads go out together, before any store
+            const float pi = ld(&ctl->population_inhibition);
+            const uint32_t supra = ld(&ctl->tick_supra[c.tick & 1]), selected = ld(&ctl->block_selected);
+            const uint32_t clipped = ld(&ctl->clipped), cells = ld(&ctl->ctx_count);
+            const uint32_t probes = ld(&ctl->ctx_probes), applied = ld(&ctl->ctx_applied);
+            const uint32_t rec_n = ld(&ctl->rec_count[c.parity]), in_n = ld(&ctl->in_count[c.parity]);
+            StepRecord LEO_GLOBAL& rec = d.records[step_index];
             rec.p_target = 0.0f;
             rec.predicted = 0;
-            rec.population_inhibition = ld(&ctl->population_inhibition);
+            rec.population_inhibition = pi;
             rec.active = A;
-            rec.suprathreshold = ld(&ctl->tick_supra[c.tick & 1]);
-            rec.block_selected = ld(&ctl->block_selected);
-            rec.clipped = ld(&ctl->clipped);
-            rec.context_cells = ld(&ctl->ctx_count);
-            rec.context_probes = ld(&ctl->ctx_probes);
-            rec.context_applied = ld(&ctl->ctx_applied);
-            rec.eligible_rec = ld(&ctl->rec_count[c.parity]);
-            rec.eligible_in = ld(&ctl->in_count[c.parity]);
+            rec.suprathreshold = supra;
+            rec.block_selected = selected;
+            rec.clipped = clipped;
+            rec.context_cells = cells;
+            rec.context_probes = probes;
+            rec.context_applied = applied;
+            rec.eligible_rec = rec_n;
+            rec.eligible_in = in_n;
             rec.error_code = 0;
         }
         if (sp.flags & kStepOutput) {
@@ -1802,8 +1857,26 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
     PhaseClock clock;
     if (kProfile && c.part == 0 && threadIdx.x == 0) clock.start(c.d.phase_profile);
     bool ok = true;
+    // the next step's parameters are fetched one step ahead with vector loads
+    // (a scalar load would be waited for at the next LDS access)
+    constexpr uint32_t kStepWords = sizeof(StepParams) / 4;
+    static_assert(sizeof(StepParams) % 4 == 0, "step parameters are 32-bit words");
+    uint32_t ahead[kStepWords];
+    auto fetch = [&](uint32_t index) {
+        const uint32_t LEO_GLOBAL* src = reinterpret_cast<const uint32_t LEO_GLOBAL*>(c.d.steps + index);
+#pragma unroll
+        for (uint32_t i = 0; i < kStepWords; ++i) ahead[i] = ld(&src[i]);
+    };
+    if (steps > 0) fetch(0);
     for (uint32_t s = 0; s < steps && ok; ++s) {
-        const StepParams sp = c.d.steps[s];
+        StepParams sp;
+        {
+            uint32_t w[kStepWords];
+#pragma unroll
+            for (uint32_t i = 0; i < kStepWords; ++i) w[i] = __builtin_amdgcn_readfirstlane(ahead[i]);
+            __builtin_memcpy(&sp, w, sizeof(StepParams));
+        }
+        if (s + 1 < steps) fetch(s + 1);
         const bool trace = (sp.flags & kStepLearnTrace) != 0;
         // the context (runtime.rs:641-677) is first read by the readout
         if (c.part == c.P - 1) context_resolve(c, sp, sh);
@@ -1818,7 +1891,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             write_active(c, sp, s, sh, fused);
             if (trace) phase_eligibility(c);
         } else {
-            if (c.part == 0) global_select(c, sh);
+            if (c.part == 0) global_select(c, sh, s);
             if (trace) {
                 if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 7))) break;
                 phase_eligibility(c);
