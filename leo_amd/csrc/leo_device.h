@@ -7,6 +7,7 @@
 
 #include <stdint.h>
 
+#include "fast_div.h"
 #include "leo_hip_abi.h"
 
 // Device memory pointers in the structures below are global-address-space
@@ -281,6 +282,9 @@ struct KernelArgs {
     uint32_t spin_limit;
     uint32_t lane_stride;            // workgroup b serves lane b % lane_stride (>= lane_count)
     uint32_t local_sync;             // allow XCD-local lane barriers
+    FastDiv div_synapses;            // synapses_per_neuron
+    FastDiv div_block;               // neurons_per_block
+    FastDiv div_block_words;         // block_words(neurons_per_block)
 };
 
 // Batch-end mean of one fixed-parameter tensor (see leo_merge_fixed).

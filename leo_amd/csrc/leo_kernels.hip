@@ -36,6 +36,11 @@ __device__ __forceinline__ float maxnum(float a, float b) {  // Rust f32::max
     if (b != b) return a;
     return a > b ? a : b;
 }
+// (a + b) mod n for a, b < n
+__device__ __forceinline__ uint32_t add_mod(uint32_t a, uint32_t b, uint32_t n) {
+    const uint32_t v = a + b;
+    return v >= n ? v - n : v;
+}
 __device__ __forceinline__ bool finitef(float v) { return (__float_as_uint(v) & 0x7f800000u) != 0x7f800000u; }
 
 // decay_for_elapsed (runtime.rs:78-85: 1 for 0 ticks, the base for 1, else
@@ -443,7 +448,7 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
             const uint32_t lo = k == 0 ? off8 : k == 1 ? off4 : k == 2 ? off2 : off1;
             const uint32_t rsk = k == 0 ? rs8 : k == 1 ? rs4 : k == 2 ? rs2 : rs1;
             const uint32_t local = item - lo;
-            const uint32_t r = local / S, j = local % S;
+            const uint32_t r = fast_div(local, a.div_synapses), j = local - r * S;
             rbase = static_cast<uint64_t>(rsk) * cap + r;
             // the emission snapshot holds the synapse with its value: the
             // scatter needs no load that depends on the source
@@ -483,7 +488,7 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
         // phase 2 (setting a bit is idempotent, so every touch sets it)
         if (touch_n != 0xffffffffu) {
             const uint32_t nb = cfg.neurons_per_block;
-            const uint32_t blk = touch_n / nb, off = touch_n - blk * nb;
+            const uint32_t blk = fast_div(touch_n, a.div_block), off = touch_n - blk * nb;
             d.touched_epoch[touch_n] = tick + 1;
             atomicOr(&d.touched_bits[blk * block_words(nb) + off / 32], 1u << (off & 31));
         }
@@ -863,11 +868,14 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
                 const uint32_t p = total + incl - cnt;
                 w.bits[at] = word[k];
                 w.pos[at] = p;
-                if (at < gw && at % wpb == 0) w.start[at / wpb] = p;
+
                 if (word[k]) bits[at] = 0u;
                 total += __builtin_amdgcn_readlane(incl, kWaveSize - 1);
             }
         }
+        // block starts: the list position of each block's first word
+        wave_sync();
+        if (lane < gn) w.start[lane] = w.pos[lane * wpb];
         if (lane == 0) w.start[gn] = total;
         uint32_t list_at = 0;
         if (lane == 0 && total) list_at = atomicAdd(&c.ctl->tick_touched[tick & 1], total);
@@ -888,7 +896,7 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
                 if (at >= gw) break;
                 uint32_t v = w.bits[at], p = w.pos[at];
                 if (p >= hi || p + __popc(v) <= lo) continue;
-                const uint32_t g = at / wpb, base = (at - g * wpb) * 32;
+                const uint32_t g = fast_div(at, a.div_block_words), base = (at - g * wpb) * 32;
                 while (v) {
                     const uint32_t bit = __ffs(v) - 1;
                     v &= v - 1;
@@ -906,7 +914,7 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
                 bool refractory = false;
                 const float act = clampf(fold_drive(c, n, pi, &refractory), 0.0f, 1.0f);
                 const bool candidate = !refractory && act > 0.0f;
-                w.key[i] = candidate ? selection_key(act, (n + N - rot) % N) : ~0ULL;
+                w.key[i] = candidate ? selection_key(act, add_mod(n, N - rot, N)) : ~0ULL;
                 if (candidate) atomicAdd(&w.cands[g], 1u);
                 d.touched_list[listed + i] = n;
             }
@@ -928,7 +936,7 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
                 uint32_t rank = 0;
                 for (uint32_t j = s0; j < s1; ++j) rank += w.key[j] < mine ? 1u : 0u;
                 if (rank < limit) {
-                    const uint32_t n = (static_cast<uint32_t>(mine) + rot) % N;
+                    const uint32_t n = add_mod(static_cast<uint32_t>(mine), rot, N);
                     const float act = key_activation(mine);
                     const uint64_t at = row0 + w.woff[g] + rank;
                     d.range_winners[at] = n;
@@ -1060,7 +1068,7 @@ __device__ __forceinline__ void write_active(const StepCtx& c, const StepParams&
     const uint32_t items = mine * (1 + S);
     uint32_t inhibitory = 0;
     for (uint32_t item = lane; item < items; item += kWaveSize) {
-        const uint32_t r = item < mine ? item : (item - mine) / S;
+        const uint32_t r = item < mine ? item : fast_div(item - mine, c.a->div_synapses);
         const uint32_t n = r < kWaveSize ? w.entry[r] : ld(&d.range_winners[row0 + r]);
         const float act = r < kWaveSize ? __uint_as_float(w.pos[r]) : ld(&d.range_winner_act[row0 + r]);
         if (item < mine) {
@@ -1115,7 +1123,7 @@ __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, 
         for (uint32_t i = 0; i < v; ++i) {
             if (start + i < kMaxBlockNeurons) {
                 const uint32_t n = ld(&d.range_winners[row0 + i]);
-                keys[start + i] = selection_key(ld(&d.range_winner_act[row0 + i]), (n + N - rot) % N);
+                keys[start + i] = selection_key(ld(&d.range_winner_act[row0 + i]), add_mod(n, N - rot, N));
             }
         }
         const uint32_t chunk_total = sh.scan[kThreads - 1];
@@ -1138,7 +1146,7 @@ __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, 
         float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
         for (uint32_t i = threadIdx.x; i < active; i += kThreads) {
             const uint64_t key = keys[i];
-            const uint32_t n = (static_cast<uint32_t>(key) + rot) % N;
+            const uint32_t n = add_mod(static_cast<uint32_t>(key), rot, N);
             const float act = key_activation(key);
             act_list[i] = n;
             act_val[i] = act;
@@ -1184,7 +1192,7 @@ __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uin
     }
     // every destination value in one round of loads (most are used only when
     // the destination was touched and is not refractory)
-    const uint32_t blk = dst / cfg.neurons_per_block;
+    const uint32_t blk = fast_div(dst, c.a->div_block);
     const uint32_t touched_epoch = ld(&d.touched_epoch[dst]), selected_epoch = ld(&d.selected_epoch[dst]);
     const uint32_t refractory_until = ld(&d.refractory_until[dst]);
     const float temporal = ld(&d.branches[4 * dst + BR_TEMP]), gate_acc = ld(&d.branches[4 * dst + BR_GATE]);
@@ -1422,7 +1430,7 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
             d.refractory_until[n] = refractory;
         } else {
             const uint32_t local = item - A;
-            const uint32_t r = local / S, j = local % S;
+            const uint32_t r = fast_div(local, a.div_synapses), j = local - r * S;
             const uint64_t rb = static_cast<uint64_t>(rs) * cap + r;
             const uint64_t slot = static_cast<uint64_t>(ld(&act_list[r])) * S + j;
             d.ring_value[rb * S + j] = ld(&act_val[r]) * ld(&d.p.rec_weight[slot]);
@@ -1700,7 +1708,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
             for (uint32_t i = c.gtid; i < rec_n; i += c.gstride) {
                 const uint32_t slot = ld(&rec_cur[i]);
                 const uint32_t dst = a.m.rec_target[slot];
-                const uint32_t src = slot / S;
+                const uint32_t src = fast_div(slot, a.div_synapses);
                 const float e = ld(&d.rec_trace[6 * NS + slot]);
                 const float gradient = ld(&d.learning_signal[dst]) * e;
                 const float delta = bounded(-lr * cs * gradient, mu);
@@ -1739,7 +1747,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
         // already handled with their eligible slot above
         const uint32_t inh_items = A * S;
         for (uint32_t item = c.gtid; item < inh_items; item += c.gstride) {
-            const uint32_t r = item / S, j = item % S;
+            const uint32_t r = fast_div(item, a.div_synapses), j = item - r * S;
             const uint32_t src = ld(&act_list[r]);
             if (a.m.neuron_type[src] == 0) continue;
             const uint64_t slot = static_cast<uint64_t>(src) * S + j;

@@ -362,6 +362,9 @@ KernelArgs kernel_args(LeoHipRuntime* h, LaneDesc* lanes, uint32_t count, uint32
     a.spin_limit = 1u << 26;
     a.lane_stride = count;
     a.local_sync = h->local_sync ? 1 : 0;
+    a.div_synapses = make_fast_div(h->cfg.device.synapses_per_neuron);
+    a.div_block = make_fast_div(h->cfg.device.neurons_per_block);
+    a.div_block_words = make_fast_div(block_words(h->cfg.device.neurons_per_block));
     return a;
 }
 
@@ -411,7 +414,7 @@ uint32_t choose_wgs_per_lane(LeoHipRuntime* h, uint32_t lanes, bool canonical) {
             // share one XCD, one per CU (measured: a second workgroup per CU
             // slows its steps)
             const uint32_t per_xcd = std::max<uint32_t>(1, static_cast<uint32_t>(h->cus) / kXcds);
-            want = static_cast<uint32_t>(std::min<uint64_t>(per_xcd, std::max<uint64_t>(1, std::max(2 * by_blocks, by_edges))));
+            want = std::min<uint32_t>(want, per_xcd);
         }
     }
     return std::max<uint32_t>(1, std::min(want, limit));
@@ -1421,6 +1424,8 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
     return guarded([&] {
         if (!config || !model || !out) throw Error(LEO_ERR_INVALID_ARGUMENT, "null argument");
         leo::model_validate(*config, *model);
+        if (static_cast<uint64_t>(config->device.neuron_count) * config->device.synapses_per_neuron >= (1ull << 31))
+            throw Error(LEO_ERR_UNSUPPORTED, "neuron_count * synapses_per_neuron at or above 2^31 is not supported");
         if (config->device.neuron_count > leo::kMaxPackedNeurons)
             throw Error(LEO_ERR_UNSUPPORTED, "neuron_count above 2^28 is not supported by the packed synapse layout");
         if (config->device.neurons_per_block > leo::kMaxBlockNeurons)

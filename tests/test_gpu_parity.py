@@ -183,3 +183,31 @@ def test_chunked_launches_and_agent_barriers_parity(require_gpu, oracle, monkeyp
     assert_models_equal(gpu.model(), cpu.model(), "chunked")
     assert gpu.kernel_stats()["launches"] > 10
     gpu.close()
+
+
+@pytest.mark.parametrize("wgs", ["1", "2"])
+def test_dense_touch_multi_window_parity(require_gpu, oracle, monkeypatch, wgs):
+    # one or two workgroups per lane make every selecting wave own several
+    # blocks, and an input fan-out of three quarters of the units touches well
+    # over a window's 256 entries per wave and step: the phase-2 fold and block
+    # ranking run in several windows of whole blocks
+    monkeypatch.setenv("LEO_HIP_WGS_PER_LANE", wgs)
+    cfg = small_redundant_config(neurons=4096, synapses=16, fanout=3072, per_block=8)
+    model = Model.initialize(cfg)
+    cpu = oracle.OracleRuntime(model)
+    gpu = _runtime(model)
+    cpu.begin_document()
+    gpu.begin_document()
+    text = story(31, 24)
+    for i, (sym, tgt) in enumerate(_document_steps(text)):
+        print(f"wgs {wgs} step {i} symbol {sym} target {tgt}", flush=True)
+        cm = cpu.step(sym, tgt, oracle.TRAINING)
+        gm = gpu.step(sym, tgt, native.TRAINING)
+        assert gm.active_neurons == cm.active_neurons, (i, gm.active_neurons, cm.active_neurons)
+        assert gm.loss == cm.loss, (i, gm.loss, cm.loss)
+        _compare_step_state(gpu, cpu, f"step {i}")
+    stats = gpu.kernel_stats()
+    # more touched neurons per wave than one window holds
+    assert stats["touched"] / max(stats["lane_steps"], 1) > int(wgs) * 4 * 256
+    assert_models_equal(gpu.model(), cpu.model(), "after document")
+    gpu.close()
