@@ -24,7 +24,10 @@ namespace leo {
 
 constexpr uint32_t kSymbols = 258;
 constexpr uint32_t kOutputs = 257;
-constexpr uint32_t kOutStride = 260;      // neuron-major output row, padded to 16 B
+// Neuron-major output row: 257 weights padded to 1,152 B, nine whole 128-byte
+// cache lines, so every row starts line-aligned and each learning-signal chunk
+// load reads exactly one line (a 1,040 B row would straddle lines).
+constexpr uint32_t kOutStride = 288;
 constexpr uint32_t kEndIndex = 256;
 constexpr uint32_t kRing = 9;             // delay ring: max delay 8 + 1 (runtime.rs:200-208)
 constexpr uint32_t kMaxOrder = 16;        // config.rs:452-456
