@@ -1171,15 +1171,57 @@ __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, 
     }
 }
 
-__device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uint64_t plane, uint32_t* last,
-                                            uint32_t slot, uint32_t dst, uint8_t br, float pop_cutoff) {
-    const LeoConfig& cfg = c.a->cfg;
+// One eligible slot's update (runtime.rs:805-918) in parts, so that a lane
+// can keep the loads of two slots in flight together: the slot's trace planes
+// and last tick with the destination's touched and selected epochs, then --
+// only for a destination touched this tick (a few percent of the eligible
+// slots of a large model) -- the rest of the destination's state, then the
+// update and its stores. Each destination field lives in its own array, so a
+// load that is not needed would still fetch a whole cache line.
+struct SlotInputs {
+    float bs, ms, fs, as0, as1, as2, e;
+    uint32_t last;
+    uint32_t touched_epoch, selected_epoch, refractory_until, block_epoch;
+    float temporal, gate_acc, block_cut, membrane, threshold, excitability;
+};
+
+__device__ __forceinline__ void load_slot(SlotInputs& in, const float LEO_GLOBAL* planes, uint64_t plane,
+                                          const uint32_t LEO_GLOBAL* last, uint32_t slot) {
+    in.bs = ld(&planes[slot]);
+    in.ms = ld(&planes[plane + slot]);
+    in.fs = ld(&planes[2 * plane + slot]);
+    in.as0 = ld(&planes[3 * plane + slot]);
+    in.as1 = ld(&planes[4 * plane + slot]);
+    in.as2 = ld(&planes[5 * plane + slot]);
+    in.e = ld(&planes[6 * plane + slot]);
+    in.last = ld(&last[slot]);
+}
+
+__device__ __forceinline__ void load_epochs(SlotInputs& in, const StepCtx& c, uint32_t dst) {
+    in.touched_epoch = ld(&c.d.touched_epoch[dst]);
+    in.selected_epoch = ld(&c.d.selected_epoch[dst]);
+}
+
+__device__ __forceinline__ void load_destination(SlotInputs& in, const StepCtx& c, uint32_t dst) {
     const LaneDesc& d = c.d;
+    const uint32_t blk = fast_div(dst, c.a->div_block);
+    in.refractory_until = ld(&d.refractory_until[dst]);
+    in.temporal = ld(&d.branches[4 * dst + BR_TEMP]);
+    in.gate_acc = ld(&d.branches[4 * dst + BR_GATE]);
+    in.block_epoch = ld(&d.block_epoch[blk]);
+    in.block_cut = ld(&d.block_cutoff[blk]);
+    in.membrane = ld(&d.membrane[dst]);
+    in.threshold = ld(&d.p.threshold[dst]);
+    in.excitability = c.a->m.excitability[dst];
+}
+
+__device__ __forceinline__ bool finish_slot(const StepCtx& c, const SlotInputs& in, float LEO_GLOBAL* planes,
+                                            uint64_t plane, uint32_t LEO_GLOBAL* last, uint32_t slot, uint8_t br,
+                                            float pop_cutoff) {
+    const LeoConfig& cfg = c.a->cfg;
     const uint32_t tick = c.tick;
-    float bs = ld(&planes[slot]), ms = ld(&planes[plane + slot]), fs = ld(&planes[2 * plane + slot]);
-    float as0 = ld(&planes[3 * plane + slot]), as1 = ld(&planes[4 * plane + slot]), as2 = ld(&planes[5 * plane + slot]);
-    const float e = ld(&planes[6 * plane + slot]);
-    const uint32_t el = tick - ld(&last[slot]);
+    float bs = in.bs, ms = in.ms, fs = in.fs, as0 = in.as0, as1 = in.as1, as2 = in.as2;
+    const uint32_t el = tick - in.last;
     if (el > 0) {
         const StateDecays k = state_decays(cfg, el);
         bs *= k.branch;
@@ -1190,27 +1232,18 @@ __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uin
         as2 *= k.slow;
         last[slot] = tick;
     }
-    // every destination value in one round of loads (most are used only when
-    // the destination was touched and is not refractory)
-    const uint32_t blk = fast_div(dst, c.a->div_block);
-    const uint32_t touched_epoch = ld(&d.touched_epoch[dst]), selected_epoch = ld(&d.selected_epoch[dst]);
-    const uint32_t refractory_until = ld(&d.refractory_until[dst]);
-    const float temporal = ld(&d.branches[4 * dst + BR_TEMP]), gate_acc = ld(&d.branches[4 * dst + BR_GATE]);
-    const uint32_t block_epoch = ld(&d.block_epoch[blk]);
-    const float block_cut = ld(&d.block_cutoff[blk]);
-    const float membrane = ld(&d.membrane[dst]), threshold = ld(&d.p.threshold[dst]);
-    const float excitability = c.a->m.excitability[dst];
-    const bool touched = touched_epoch == tick + 1;
-    const bool selected = selected_epoch == tick + 1;
+    const bool touched = in.touched_epoch == tick + 1;
+    const bool selected = in.selected_epoch == tick + 1;
     float elig;
-    if (!touched || refractory_until > tick) {
-        elig = e * cfg.eligibility_decay;
+    if (!touched || in.refractory_until > tick) {
+        elig = in.e * cfg.eligibility_decay;
     } else {
-        const float jac = branch_jacobian(br, excitability, temporal, gate_acc);
+        const float jac = branch_jacobian(br, in.excitability, in.temporal, in.gate_acc);
         // the destination's selection surrogate (runtime.rs:787-803), a pure
         // function of its state after selection, evaluated where it is used
-        const float block_cutoff = block_epoch == tick + 1 ? block_cut : 0.0f;
-        const float sur = surrogate_value(cfg, false, membrane - threshold, maxnum(block_cutoff, pop_cutoff), selected);
+        const float block_cutoff = in.block_epoch == tick + 1 ? in.block_cut : 0.0f;
+        const float sur =
+            surrogate_value(cfg, false, in.membrane - in.threshold, maxnum(block_cutoff, pop_cutoff), selected);
         const float asum = as0 + as1 + as2;
         ms = ms + jac * bs - fs - asum;
         elig = sur * ms;
@@ -1235,23 +1268,60 @@ __device__ __forceinline__ bool update_slot(const StepCtx& c, float* planes, uin
     return mag > cfg.eligibility_epsilon;
 }
 
-// Update every slot of one eligible list; kept slots are compacted into the
-// other list, dropped slots are unmarked.
-__device__ __forceinline__ void eligibility_list(const StepCtx& c, float* planes, uint64_t plane, uint32_t* last, uint8_t* marks,
-                                 const uint32_t* cur, uint32_t cur_n, uint32_t* next, uint32_t* next_count,
-                                 const uint32_t* targets, const uint8_t* branches, float pop_cutoff) {
+// Wave-aggregated append of two predicates per lane (every lane active): one
+// atomic for the wave; lane order within each predicate, the first's before
+// the second's.
+__device__ __forceinline__ void wave_append2(uint32_t LEO_GLOBAL* counter, bool p0, bool p1, uint32_t& pos0,
+                                             uint32_t& pos1) {
+    const unsigned long long m0 = __ballot(p0), m1 = __ballot(p1);
+    const uint32_t n0 = static_cast<uint32_t>(__popcll(m0));
+    const uint32_t total = n0 + static_cast<uint32_t>(__popcll(m1));
+    uint32_t base = 0;
+    if (total != 0 && __lane_id() == 0) base = atomicAdd(counter, total);
+    base = __builtin_amdgcn_readfirstlane(base);
+    const unsigned long long below = (1ULL << __lane_id()) - 1ULL;
+    pos0 = base + static_cast<uint32_t>(__popcll(m0 & below));
+    pos1 = base + n0 + static_cast<uint32_t>(__popcll(m1 & below));
+}
+
+// Eligible slots of one list, two per lane per iteration (their loads in
+// flight together); kept slots are compacted into the next list.
+__device__ __forceinline__ void eligibility_list(const StepCtx& c, float LEO_GLOBAL* planes, uint64_t plane,
+                                                 uint32_t LEO_GLOBAL* last, uint8_t LEO_GLOBAL* marks,
+                                                 const uint32_t LEO_GLOBAL* cur, uint32_t cur_n,
+                                                 uint32_t LEO_GLOBAL* next, uint32_t LEO_GLOBAL* next_count,
+                                                 const uint32_t* targets, const uint8_t* branches, float pop_cutoff) {
     const uint32_t lane = __lane_id();
-    for (uint32_t base = c.gtid - lane; base < cur_n; base += c.gstride) {
-        const uint32_t i = base + lane;
-        bool keep = false;
-        uint32_t slot = 0;
-        if (i < cur_n) {
-            slot = ld(&cur[i]);
-            keep = update_slot(c, planes, plane, last, slot, targets[slot], branches[slot], pop_cutoff);
-            if (!keep) marks[slot] = 0;
+    for (uint32_t base = c.gtid - lane; base < cur_n; base += 2 * c.gstride) {
+        const uint32_t i0 = base + lane, i1 = base + c.gstride + lane;
+        const bool v0 = i0 < cur_n, v1 = i1 < cur_n;
+        const uint32_t s0 = v0 ? ld(&cur[i0]) : 0u;
+        const uint32_t s1 = v1 ? ld(&cur[i1]) : 0u;
+        uint32_t t0 = 0, t1 = 0;
+        uint8_t r0 = 0, r1 = 0;
+        SlotInputs a0{}, a1{};
+        if (v0) {
+            t0 = targets[s0];
+            r0 = branches[s0];
+            load_slot(a0, planes, plane, last, s0);
         }
-        const uint32_t pos = wave_append(next_count, keep);
-        if (keep) next[pos] = slot;
+        if (v1) {
+            t1 = targets[s1];
+            r1 = branches[s1];
+            load_slot(a1, planes, plane, last, s1);
+        }
+        if (v0) load_epochs(a0, c, t0);
+        if (v1) load_epochs(a1, c, t1);
+        if (v0 && a0.touched_epoch == c.tick + 1) load_destination(a0, c, t0);
+        if (v1 && a1.touched_epoch == c.tick + 1) load_destination(a1, c, t1);
+        const bool k0 = v0 && finish_slot(c, a0, planes, plane, last, s0, r0, pop_cutoff);
+        const bool k1 = v1 && finish_slot(c, a1, planes, plane, last, s1, r1, pop_cutoff);
+        if (v0 && !k0) marks[s0] = 0;
+        if (v1 && !k1) marks[s1] = 0;
+        uint32_t p0, p1;
+        wave_append2(next_count, k0, k1, p0, p1);
+        if (k0) next[p0] = s0;
+        if (k1) next[p1] = s1;
     }
 }
 
