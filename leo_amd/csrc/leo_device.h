@@ -184,6 +184,11 @@ struct LaneParams {
     float LEO_GLOBAL* ctx_out;          // 257 * E, output-major
 };
 
+// Trace slot marks: a clean slot (0) has not been written since the last
+// reset and holds zeros; a listed slot is on the eligible list; a dropped
+// slot has left the list and keeps its (sub-epsilon) values.
+constexpr uint8_t kMarkClean = 0, kMarkListed = 1, kMarkDropped = 2;
+
 // Everything a kernel needs to run one lane.
 struct LaneDesc {
     LaneParams p;
@@ -219,12 +224,12 @@ struct LaneDesc {
     // recurrent traces (N*S): branch, membrane, fatigue, 3 adaptation sensitivities, eligibility
     float LEO_GLOBAL* rec_trace;        // 7 * NS (SoA planes)
     uint32_t LEO_GLOBAL* rec_last;      // NS
-    uint8_t LEO_GLOBAL* rec_mark;       // NS
+    uint8_t LEO_GLOBAL* rec_mark;       // NS: kMark*
     uint32_t LEO_GLOBAL* rec_list;      // 2 * NS
     // input traces (258*F)
     float LEO_GLOBAL* in_trace;         // 7 * NI
     uint32_t LEO_GLOBAL* in_last;
-    uint8_t LEO_GLOBAL* in_mark;
+    uint8_t LEO_GLOBAL* in_mark;        // NI: kMark*
     uint32_t LEO_GLOBAL* in_list;       // 2 * NI
     // readout
     float LEO_GLOBAL* logits;           // kOutStride

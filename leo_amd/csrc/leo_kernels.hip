@@ -500,16 +500,16 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
             slot += static_cast<uint64_t>(ld(&d.ring_active[rbase])) * S;
             const float bs = advance_trace(d.rec_trace, NS, d.rec_last, static_cast<uint32_t>(slot), tick, cfg);
             d.rec_trace[slot] = bs + act;
-            if (!ld(&d.rec_mark[slot])) {
-                d.rec_mark[slot] = 1;
+            if (ld(&d.rec_mark[slot]) != kMarkListed) {
+                d.rec_mark[slot] = kMarkListed;
                 new_rec = true;
                 eslot = static_cast<uint32_t>(slot);
             }
         } else if (trace && inj) {
             const float bs = advance_trace(d.in_trace, NI, d.in_last, static_cast<uint32_t>(slot), tick, cfg);
             d.in_trace[slot] = bs + 1.0f;
-            if (!ld(&d.in_mark[slot])) {
-                d.in_mark[slot] = 1;
+            if (ld(&d.in_mark[slot]) != kMarkListed) {
+                d.in_mark[slot] = kMarkListed;
                 new_in = true;
                 eslot = static_cast<uint32_t>(slot);
             }
@@ -1316,8 +1316,8 @@ __device__ __forceinline__ void eligibility_list(const StepCtx& c, float LEO_GLO
         if (v1 && a1.touched_epoch == c.tick + 1) load_destination(a1, c, t1);
         const bool k0 = v0 && finish_slot(c, a0, planes, plane, last, s0, r0, pop_cutoff);
         const bool k1 = v1 && finish_slot(c, a1, planes, plane, last, s1, r1, pop_cutoff);
-        if (v0 && !k0) marks[s0] = 0;
-        if (v1 && !k1) marks[s1] = 0;
+        if (v0 && !k0) marks[s0] = kMarkDropped;
+        if (v1 && !k1) marks[s1] = kMarkDropped;
         uint32_t p0, p1;
         wave_append2(next_count, k0, k1, p0, p1);
         if (k0) next[p0] = s0;
@@ -1821,7 +1821,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
             const uint32_t src = ld(&act_list[r]);
             if (a.m.neuron_type[src] == 0) continue;
             const uint64_t slot = static_cast<uint64_t>(src) * S + j;
-            if (plastic && ld(&d.rec_mark[slot])) continue;
+            if (plastic && ld(&d.rec_mark[slot]) == kMarkListed) continue;
             const uint32_t dst = a.m.rec_target[slot];
             const float tgt_act = ld(&d.activation[dst]) > 0.0f ? 1.0f : 0.0f;
             const float old_w = ld(&d.p.rec_weight[slot]);
@@ -2012,7 +2012,54 @@ __global__ void __launch_bounds__(kThreads) leo_lane_steps_profiled(const Kernel
 
 // ---------------------------------------------------------------------------
 // reset_transient_state (runtime.rs:365-425) for every lane in args.
+//
+// Recurrent trace slots are cleared from their marks: a slot whose mark is 0
+// has not been written since the last reset, so its seven values are still
+// zero (1 = listed as eligible, 2 = dropped from the list with its values
+// kept). Every group of 16 slots with a nonzero mark is zeroed whole with
+// vector stores; a clean slot keeps its last tick, which only scales zeros,
+// unless the tick is set (a new tick may lie below it, so every last tick is
+// rewritten).
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ void fill_u32(uint32_t LEO_GLOBAL* p, uint64_t n, uint32_t v, uint64_t t0, uint64_t ts) {
+    // p is 256-byte aligned (lane-state layout)
+    const uint64_t n4 = n / 4;
+    uint4 LEO_GLOBAL* q = reinterpret_cast<uint4 LEO_GLOBAL*>(p);
+    const uint4 w = make_uint4(v, v, v, v);
+    for (uint64_t i = t0; i < n4; i += ts) q[i] = w;
+    for (uint64_t i = 4 * n4 + t0; i < n; i += ts) p[i] = v;
+}
+
+__device__ __forceinline__ void fill_f32(float LEO_GLOBAL* p, uint64_t n, uint64_t t0, uint64_t ts) {
+    fill_u32(reinterpret_cast<uint32_t LEO_GLOBAL*>(p), n, 0u, t0, ts);
+}
+
+__device__ __forceinline__ void clear_trace_group(const LaneDesc& d, uint64_t NS, uint64_t g, uint32_t tick,
+                                                  bool set_tick) {
+    uint4 LEO_GLOBAL* marks = reinterpret_cast<uint4 LEO_GLOBAL*>(d.rec_mark);
+    const uint4 m = marks[g];  // a launch of its own: plain loads see the previous kernels' stores
+    const uint4 zero = make_uint4(0u, 0u, 0u, 0u), t = make_uint4(tick, tick, tick, tick);
+    uint4 LEO_GLOBAL* last = reinterpret_cast<uint4 LEO_GLOBAL*>(d.rec_last + 16 * g);
+    const bool dirty = (m.x | m.y | m.z | m.w) != 0u;
+    if (dirty) {
+#pragma unroll
+        for (uint64_t p = 0; p < 7; ++p) {
+            uint4 LEO_GLOBAL* plane = reinterpret_cast<uint4 LEO_GLOBAL*>(d.rec_trace + p * NS + 16 * g);
+            plane[0] = zero;
+            plane[1] = zero;
+            plane[2] = zero;
+            plane[3] = zero;
+        }
+        marks[g] = zero;
+    }
+    if (dirty || set_tick) {
+        last[0] = t;
+        last[1] = t;
+        last[2] = t;
+        last[3] = t;
+    }
+}
+
 __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uint32_t set_tick, uint32_t new_tick) {
     const LeoConfig& cfg = args.cfg;
     const uint32_t L = args.lane_count;
@@ -2023,37 +2070,31 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
     const uint64_t N = cfg.neuron_count, S = cfg.synapses_per_neuron;
     const uint64_t NS = N * S, NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
     const uint64_t t0 = static_cast<uint64_t>(part) * kThreads + threadIdx.x, ts = static_cast<uint64_t>(parts) * kThreads;
-    for (uint64_t i = t0; i < N; i += ts) {
-        d.membrane[i] = 0.0f;
-        d.activation[i] = 0.0f;
-        d.fatigue[i] = 0.0f;
-        d.refractory_until[i] = 0;
-        d.branches[4 * i] = 0.0f;
-        d.branches[4 * i + 1] = 0.0f;
-        d.branches[4 * i + 2] = 0.0f;
-        d.branches[4 * i + 3] = 0.0f;
-        d.adapt[i] = 0.0f;
-        d.adapt[N + i] = 0.0f;
-        d.adapt[2 * N + i] = 0.0f;
-        d.last_tick[i] = tick;
-        d.touched_epoch[i] = 0;
-        d.selected_epoch[i] = 0;
-        d.bucket_count[i] = 0;
+    fill_f32(d.membrane, N, t0, ts);
+    fill_f32(d.activation, N, t0, ts);
+    fill_f32(d.fatigue, N, t0, ts);
+    fill_u32(d.refractory_until, N, 0u, t0, ts);
+    fill_f32(d.branches, 4 * N, t0, ts);
+    fill_f32(d.adapt, 3 * N, t0, ts);
+    fill_u32(d.last_tick, N, tick, t0, ts);
+    fill_u32(d.touched_epoch, N, 0u, t0, ts);
+    fill_u32(d.selected_epoch, N, 0u, t0, ts);
+    fill_u32(d.bucket_count, N, 0u, t0, ts);
+    const uint64_t groups = NS / 16;
+    for (uint64_t g = t0; g < groups; g += ts) clear_trace_group(d, NS, g, tick, set_tick != 0);
+    for (uint64_t i = 16 * groups + t0; i < NS; i += ts) {
+        if (d.rec_mark[i] != 0 || set_tick) {
+            for (uint64_t p = 0; p < 7; ++p) d.rec_trace[p * NS + i] = 0.0f;
+            d.rec_last[i] = tick;
+            d.rec_mark[i] = 0;
+        }
     }
-    for (uint64_t i = t0; i < 7 * NS; i += ts) d.rec_trace[i] = 0.0f;
-    for (uint64_t i = t0; i < NS; i += ts) {
-        d.rec_last[i] = tick;
-        d.rec_mark[i] = 0;
-    }
-    for (uint64_t i = t0; i < 7 * NI; i += ts) d.in_trace[i] = 0.0f;
-    for (uint64_t i = t0; i < NI; i += ts) {
-        d.in_last[i] = tick;
-        d.in_mark[i] = 0;
-    }
+    fill_f32(d.in_trace, 7 * NI, t0, ts);
+    fill_u32(d.in_last, NI, tick, t0, ts);
+    for (uint64_t i = t0; i < NI; i += ts) d.in_mark[i] = 0;
     for (uint64_t i = t0; i < cfg.context_embedding_dim; i += ts) d.ctx_latent[i] = 0.0f;
-    for (uint64_t i = t0; i < cfg.block_count; i += ts) d.block_epoch[i] = 0;
-    const uint64_t bit_words = static_cast<uint64_t>(cfg.block_count) * block_words(cfg.neurons_per_block);
-    for (uint64_t i = t0; i < bit_words; i += ts) d.touched_bits[i] = 0;
+    fill_u32(d.block_epoch, cfg.block_count, 0u, t0, ts);
+    fill_u32(d.touched_bits, static_cast<uint64_t>(cfg.block_count) * block_words(cfg.neurons_per_block), 0u, t0, ts);
     for (uint64_t i = t0; i < kMaxWaves; i += ts) d.wave_total[i] = 0;
     if (part == 0 && threadIdx.x == 0) {
         LaneControl* ctl = d.ctl;

@@ -167,6 +167,7 @@ struct LeoHipRuntime {
     leo::Arena merge_acc;        // f64 sums + changed flags of the lane-group merge
     uint32_t resident_lanes = 0; // story lanes that fit on the device at once
     uint32_t max_steps_override = 0;
+    float last_launch_ms = 0.0f;  // duration of the latest lane-steps launch (HIP events)
     leo::Arena merge_scratch;  // lane pointer table + counters
     // host copies of the read-only topology (device copies are immutable)
     std::vector<float> excitability;
@@ -373,7 +374,9 @@ KernelArgs kernel_args(LeoHipRuntime* h, LaneDesc* lanes, uint32_t count, uint32
 void reset_lanes(LeoHipRuntime* h, uint32_t count, bool set_tick, uint32_t new_tick) {
     LaneDesc* descs = reinterpret_cast<LaneDesc*>(h->lane_descs.base);
     KernelArgs a = kernel_args(h, descs, count, 1);
-    uint32_t grid = count * 64;
+    // about four workgroups per CU in all, at least 64 per lane
+    const uint32_t parts = std::max<uint32_t>(64, static_cast<uint32_t>(4 * h->cus) / std::max<uint32_t>(count, 1));
+    uint32_t grid = count * parts;
     hipLaunchKernelGGL(leo_reset_lanes, dim3(grid), dim3(kThreads), 0, h->stream, a, set_tick ? 1u : 0u, new_tick);
     LEO_HIP_CHECK(hipGetLastError());
 }
@@ -566,6 +569,7 @@ void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     sync(h->stream);
     float ms = 0.0f;
     LEO_HIP_CHECK(hipEventElapsedTime(&ms, h->ev_start, h->ev_stop));
+    h->last_launch_ms = ms;
     account_launch(h, runs, ms);
     if (h->phase_profile) {
         // lane 0 of the launch is representative (lanes run the same phase sequence)
@@ -590,9 +594,10 @@ void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     }
 }
 
-// Steps per launch: a launch stays around a second even when every synapse
-// slot of every lane is eligible (about 140 bytes per slot and step at
-// ~4 TB/s), so a long schedule never becomes one multi-minute dispatch.
+// Steps of the first launch of a long schedule: a launch stays around a
+// second even when every synapse slot of every lane is eligible (about 140
+// bytes per slot and step at ~4 TB/s), so a long schedule never becomes one
+// multi-minute dispatch.
 size_t max_steps_per_launch(const LeoHipRuntime* h, size_t lanes) {
     if (h->max_steps_override) return h->max_steps_override;
     const double bytes_per_step = static_cast<double>(h->z.ns) * 140.0 * static_cast<double>(std::max<size_t>(lanes, 1));
@@ -600,23 +605,35 @@ size_t max_steps_per_launch(const LeoHipRuntime* h, size_t lanes) {
     return static_cast<size_t>(std::min(4096.0, std::max(8.0, steps)));
 }
 
+// Later launches of a long schedule are sized from the last one's measured
+// duration toward a quarter of a second (at most 4x growth per launch), so
+// the step cost actually seen, not the worst case, sets the launch count.
+size_t next_chunk(const LeoHipRuntime* h, size_t chunk) {
+    if (h->max_steps_override) return h->max_steps_override;
+    constexpr double kTargetMs = 250.0;
+    const double factor = std::min(4.0, kTargetMs / std::max<double>(h->last_launch_ms, 0.01));
+    const double next = static_cast<double>(chunk) * factor;
+    return static_cast<size_t>(std::min(4096.0, std::max(8.0, next)));
+}
+
 // Runs the lanes' schedules, in several launches when they are long.
 void run_lanes(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     size_t longest = 0;
     for (const LaneRun& r : runs) longest = std::max(longest, r.steps.size());
-    const size_t chunk = max_steps_per_launch(h, runs.size());
+    size_t chunk = max_steps_per_launch(h, runs.size());
     if (longest <= chunk) {
         run_lanes_once(h, runs);
         return;
     }
     for (LaneRun& r : runs) r.records.resize(r.steps.size());
-    for (size_t at = 0; at < longest; at += chunk) {
+    for (size_t at = 0; at < longest;) {
+        const size_t step = chunk;
         std::vector<LaneRun> part;
         std::vector<size_t> index;
         for (size_t i = 0; i < runs.size(); ++i) {
             const size_t n = runs[i].steps.size();
             if (at >= n) continue;
-            const size_t end = std::min(n, at + chunk);
+            const size_t end = std::min(n, at + step);
             part.push_back(LaneRun{runs[i].lane, std::vector<StepParams>(runs[i].steps.begin() + at,
                                                                          runs[i].steps.begin() + end), {}});
             index.push_back(i);
@@ -624,6 +641,8 @@ void run_lanes(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
         run_lanes_once(h, part);
         for (size_t k = 0; k < part.size(); ++k)
             std::copy(part[k].records.begin(), part[k].records.end(), runs[index[k]].records.begin() + at);
+        at += step;
+        chunk = next_chunk(h, step);
     }
 }
 

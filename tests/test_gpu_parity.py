@@ -3,6 +3,8 @@ same seeded inputs. Worklists, masks and model tensors are compared bit for
 bit; the HIP kernels reproduce the CPU executor's FP32 operation order."""
 from __future__ import annotations
 
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -66,6 +68,37 @@ def test_step_by_step_parity(require_gpu, oracle, make):
         assert gm.population_inhibition == cm.population_inhibition, i
         _compare_step_state(gpu, cpu, f"step {i}")
     assert_models_equal(gpu.model(), cpu.model(), "after document")
+    gpu.close()
+
+
+def test_reset_after_dropped_slots_parity(require_gpu, oracle):
+    # slots that left the eligible list keep sub-epsilon values; the reset
+    # between documents clears them from their marks, and the second
+    # document's traces match the oracle's dense reset step by step (a large
+    # epsilon makes slots leave the list within the first document)
+    cfg = small_redundant_config()
+    cfg = dataclasses.replace(cfg, learning=dataclasses.replace(cfg.learning, eligibility_epsilon=0.03))
+    model = Model.initialize(cfg)
+    cpu = oracle.OracleRuntime(model)
+    gpu = _runtime(model)
+    dropped = False
+    for doc, (seed, n) in enumerate(((41, 60), (42, 40))):
+        cpu.begin_document()
+        gpu.begin_document()
+        previous = 0
+        for i, (sym, tgt) in enumerate(_document_steps(story(seed, n))):
+            print(f"document {doc} step {i}", flush=True)
+            cm = cpu.step(sym, tgt, oracle.TRAINING)
+            gm = gpu.step(sym, tgt, native.TRAINING)
+            assert gm.loss == cm.loss, (doc, i)
+            dropped |= doc == 0 and gm.eligible_recurrent_synapses < previous
+            previous = gm.eligible_recurrent_synapses
+            if doc == 1:
+                _compare_step_state(gpu, cpu, f"document {doc} step {i}")
+        cpu.finish_document()
+        gpu.finish_document()
+    assert dropped, "the first document never dropped an eligible slot"
+    assert_models_equal(gpu.model(), cpu.model(), "after two documents")
     gpu.close()
 
 
