@@ -116,13 +116,19 @@ __device__ __forceinline__ void set_error(LaneControl* ctl, uint32_t code) { ato
 __device__ __forceinline__ void mark_bit(uint32_t* bits, uint32_t index) { atomicOr(&bits[index >> 5], 1u << (index & 31)); }
 
 // Workgroup-wide sum of a per-thread count, added to *global once.
-__device__ void add_count(uint32_t* global, uint32_t local) {
+// Workgroup total of a per-thread count, valid on thread 0.
+__device__ uint32_t wg_total(uint32_t local) {
     __shared__ uint32_t s_count;
     if (threadIdx.x == 0) s_count = 0;
     __syncthreads();
     if (local) atomicAdd(&s_count, local);
     __syncthreads();
-    if (threadIdx.x == 0 && s_count) atomicAdd(global, s_count);
+    return s_count;
+}
+
+__device__ void add_count(uint32_t* global, uint32_t local) {
+    const uint32_t total = wg_total(local);
+    if (threadIdx.x == 0 && total) atomicAdd(global, total);
 }
 
 // Wave-aggregated append: one atomic per wave instead of one per lane. Must be
@@ -395,7 +401,37 @@ __device__ __forceinline__ uint64_t bucket_entry(uint64_t overflow, uint32_t n, 
     return p < 2 ? 2ull * n + p : overflow + (p - 2);
 }
 
-__device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams& sp, uint32_t step_index, const StepShared& sh) {
+// One delivery into target's bucket (the fold of phase 2 orders the bucket
+// by key); true when it is the target's first delivery of the tick.
+__device__ __forceinline__ bool scatter_event(const StepCtx& c, uint32_t target, uint64_t key, float value) {
+    // the overflow offset is loaded with the counter increment (one round trip)
+    const uint64_t overflow = c.a->m.bucket_offset[target];
+    const uint32_t p = atomicAdd(&c.d.bucket_count[target], 1u);
+    const uint64_t at = bucket_entry(overflow, target, p);
+    c.d.bucket[2 * at] = key;
+    c.d.bucket[2 * at + 1] = __float_as_uint(value);
+    return p == 0;
+}
+
+// Touched marks of neuron n at `tick`: the epoch for phase 3, and the block's
+// bitmap bit for phase 2. A delivery marks its target only when it is the
+// target's first of the tick (bucket count 0); setting a bit is idempotent,
+// so a neuron also marked as previously active is marked twice harmlessly.
+__device__ __forceinline__ void touch_neuron(const StepCtx& c, uint32_t n, uint32_t tick) {
+    const uint32_t nb = c.a->cfg.neurons_per_block;
+    const uint32_t blk = fast_div(n, c.a->div_block), off = n - blk * nb;
+    c.d.touched_epoch[n] = tick + 1;
+    atomicOr(&c.d.touched_bits[blk * block_words(nb) + off / 32], 1u << (off & 31));
+}
+
+// `ahead`: the next tick's delivery, run in the current tick's last phase
+// (a frozen step after a fused one). The selecting waves have already
+// handled the current tick's winners (activation reset, touch, delay-1
+// events), so only delay classes 8, 4, 2 and the injection remain, and the
+// event count is returned (thread 0) to be added once the counters of that
+// tick have been rolled.
+__device__ __forceinline__ uint32_t phase_deliver(const StepCtx& c, const StepParams& sp, const StepShared& sh,
+                                                  bool ahead, uint32_t carried) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -404,14 +440,15 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
     const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * S;
     const uint64_t NI = static_cast<uint64_t>(kSymbols) * F;
     const bool trace = (sp.flags & kStepLearnTrace) != 0;
-    const uint32_t tick = c.tick;
+    const uint32_t tick = c.tick + (ahead ? 1u : 0u);
     if (c.part == 0 && threadIdx.x == 0) {  // this step's next eligible lists
         ctl->rec_count[c.parity ^ 1] = 0;
         ctl->in_count[c.parity ^ 1] = 0;
     }
     // previous active set (runtime.rs:544-555)
     const uint32_t prev_slot = (tick + kRing - 1) % kRing;
-    const uint32_t prev_count = (tick > 0 && sh.ring_tick[prev_slot] == tick - 1) ? sh.ring_count[prev_slot] : 0;
+    const uint32_t prev_count =
+        (!ahead && tick > 0 && sh.ring_tick[prev_slot] == tick - 1) ? sh.ring_count[prev_slot] : 0;
     // delivery classes: delay 8, 4, 2, 1 in that order (chronological by emission tick)
     // (scalars, not arrays: a dynamically indexed private array lives in scratch)
     auto class_items = [&](uint32_t delay, uint32_t& rs) {
@@ -419,15 +456,16 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
         const bool valid = tick >= delay && sh.ring_tick[rs] == tick - delay;
         return (valid ? sh.ring_count[rs] : 0) * S;
     };
-    uint32_t rs8, rs4, rs2, rs1;
+    uint32_t rs8, rs4, rs2, rs1 = 0;
     const uint32_t off8 = prev_count;
     const uint32_t off4 = off8 + class_items(8, rs8);
     const uint32_t off2 = off4 + class_items(4, rs4);
     const uint32_t off1 = off2 + class_items(2, rs2);
-    const uint32_t off_in = off1 + class_items(1, rs1);
+    const uint32_t items1 = ahead ? 0u : class_items(1, rs1);
+    const uint32_t off_in = off1 + items1;
     const uint32_t total = off_in + F;
     const uint32_t lane = __lane_id();
-    uint32_t delivered = 0;
+    uint32_t delivered = carried;
     // with several workgroups the last one resolves the context meanwhile and
     // takes no deliveries
     const uint32_t workers = c.P > 1 ? c.P - 1 : 1;
@@ -459,7 +497,6 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
                 rec = true;
                 value = v;
                 target = edge_target(edge);
-                touch_n = target;
                 scatter = true;
                 slot = j;  // completed with the source below (traces only)
                 key = (static_cast<uint64_t>(k) << 61) | (static_cast<uint64_t>(r) << 32) |
@@ -472,30 +509,18 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
             const uint8_t br = a.m.in_branch[slot];
             value = ld(&d.p.in_weight[slot]);
             inj = true;
-            touch_n = target;
             scatter = true;
             key = (4ULL << 61) | (static_cast<uint64_t>(i) << 2) | br;
         }
-        if (scatter) {
-            // the overflow offset is loaded with the counter increment (one round trip)
-            const uint64_t overflow = a.m.bucket_offset[target];
-            const uint32_t p = atomicAdd(&d.bucket_count[target], 1u);
-            const uint64_t at = bucket_entry(overflow, target, p);
-            d.bucket[2 * at] = key;
-            d.bucket[2 * at + 1] = __float_as_uint(value);
-        }
-        // touched marks: the epoch for phase 3, and the block's bitmap bit for
-        // phase 2 (setting a bit is idempotent, so every touch sets it)
-        if (touch_n != 0xffffffffu) {
-            const uint32_t nb = cfg.neurons_per_block;
-            const uint32_t blk = fast_div(touch_n, a.div_block), off = touch_n - blk * nb;
-            d.touched_epoch[touch_n] = tick + 1;
-            atomicOr(&d.touched_bits[blk * block_words(nb) + off / 32], 1u << (off & 31));
-        }
+        if (scatter && scatter_event(c, target, key, value)) touch_n = target;
+        if (touch_n != 0xffffffffu) touch_neuron(c, touch_n, tick);
+        // frozen steps skip the appends below: their wave-uniform counter
+        // read would wait for this item's stores before the next item's loads
+        if (!trace) continue;
         // trace activation of the delivering slot (runtime.rs:710-766)
         bool new_rec = false, new_in = false;
         uint32_t eslot = 0;
-        if (trace && rec) {
+        if (rec) {
             const float act = ld(&d.ring_act[rbase]);
             slot += static_cast<uint64_t>(ld(&d.ring_active[rbase])) * S;
             const float bs = advance_trace(d.rec_trace, NS, d.rec_last, static_cast<uint32_t>(slot), tick, cfg);
@@ -505,7 +530,7 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
                 new_rec = true;
                 eslot = static_cast<uint32_t>(slot);
             }
-        } else if (trace && inj) {
+        } else if (inj) {
             const float bs = advance_trace(d.in_trace, NI, d.in_last, static_cast<uint32_t>(slot), tick, cfg);
             d.in_trace[slot] = bs + 1.0f;
             if (ld(&d.in_mark[slot]) != kMarkListed) {
@@ -519,7 +544,9 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
         pos = wave_append(&ctl->in_count[c.parity], new_in);
         if (new_in) d.in_list[static_cast<uint64_t>(c.parity) * NI + pos] = eslot;
     }
+    if (ahead) return wg_total(delivered);
     add_count(&ctl->tick_events[tick & 1], delivered);
+    return 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -976,8 +1003,19 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
 // order, runtime.rs:1010-1013), population inhibition (runtime.rs:1076-1082)
 // and the forward eligibilities (runtime.rs:805-918).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void write_active(const StepCtx& c, const StepParams& sp, uint32_t step_index,
-                                             StepShared& sh, bool fuse_post) {
+// Context counters of a fused step's record, read in phase 2: the next step's
+// context resolution may run in the same phase as the record write.
+struct FusedRecord {
+    uint32_t cells, probes, applied;
+};
+
+// With `ahead` (a fused step followed by a frozen one) each wave also starts
+// the next tick for its own winners: activation reset and touch (the next
+// tick's previous active set, runtime.rs:544-555) and the delivery of their
+// delay-1 events, which the next tick would otherwise read back from the
+// ring. Returns this thread's count of those events.
+__device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepParams& sp, uint32_t step_index,
+                                                 StepShared& sh, bool fuse_post, const FusedRecord& fr, bool ahead) {
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = c.d;
     const uint32_t cap = cfg.max_active_global, limit = cfg.max_active_per_block;
@@ -1020,9 +1058,9 @@ __device__ __forceinline__ void write_active(const StepCtx& c, const StepParams&
         uint32_t supra = 0, cells = 0, probes = 0, applied = 0, rec_n = 0, in_n = 0;
         if (fuse_post) {
             supra = ld(&ctl->tick_supra[c.tick & 1]);
-            cells = ld(&ctl->ctx_count);
-            probes = ld(&ctl->ctx_probes);
-            applied = ld(&ctl->ctx_applied);
+            cells = fr.cells;
+            probes = fr.probes;
+            applied = fr.applied;
             rec_n = ld(&ctl->rec_count[c.parity]);
             in_n = ld(&ctl->in_count[c.parity]);
         }
@@ -1054,7 +1092,7 @@ __device__ __forceinline__ void write_active(const StepCtx& c, const StepParams&
             rec.error_code = 0;
         }
     }
-    if (!fuse_post) return;
+    if (!fuse_post) return 0;
     // Post-fire updates of this wave's winners and their emission snapshots
     // (the post phase, runtime.rs:920-938, 1084-1106), folded in here when no
     // eligibility update or readout of this step reads the state in between.
@@ -1065,26 +1103,41 @@ __device__ __forceinline__ void write_active(const StepCtx& c, const StepParams&
     w.pos[lane] = __float_as_uint(first_act);
     wave_sync();
     const uint32_t refractory = c.tick + cfg.refractory_ticks + 1;
-    const uint32_t items = mine * (1 + S);
-    uint32_t inhibitory = 0;
-    for (uint32_t item = lane; item < items; item += kWaveSize) {
-        const uint32_t r = item < mine ? item : fast_div(item - mine, c.a->div_synapses);
+    uint32_t inhibitory = 0, delivered = 0;
+    for (uint32_t r = lane; r < mine; r += kWaveSize) {
         const uint32_t n = r < kWaveSize ? w.entry[r] : ld(&d.range_winners[row0 + r]);
         const float act = r < kWaveSize ? __uint_as_float(w.pos[r]) : ld(&d.range_winner_act[row0 + r]);
-        if (item < mine) {
-            inhibitory += c.a->m.neuron_type[n] != 0 ? 1u : 0u;
-            d.fatigue[n] = ld(&d.fatigue[n]) + cfg.fatigue_gain * act;
-            d.adapt[n] = ld(&d.adapt[n]) + cfg.adaptation_fast_gain * act;
-            d.adapt[N + n] = ld(&d.adapt[N + n]) + cfg.adaptation_medium_gain * act;
-            d.adapt[2 * N + n] = ld(&d.adapt[2 * N + n]) + cfg.adaptation_slow_gain * act;
-            d.membrane[n] = ld(&d.membrane[n]) - ld(&d.p.threshold[n]) * cfg.membrane_reset_fraction;
-            d.refractory_until[n] = refractory;
-        } else {
-            const uint32_t j = (item - mine) - r * S;
-            const uint64_t slot = static_cast<uint64_t>(n) * S + j;
-            const uint64_t at = (static_cast<uint64_t>(rs) * cap + before + r) * S + j;
-            d.ring_value[at] = act * ld(&d.p.rec_weight[slot]);
-            d.ring_edge[at] = c.a->m.rec_edge[slot];
+        inhibitory += c.a->m.neuron_type[n] != 0 ? 1u : 0u;
+        d.fatigue[n] = ld(&d.fatigue[n]) + cfg.fatigue_gain * act;
+        d.adapt[n] = ld(&d.adapt[n]) + cfg.adaptation_fast_gain * act;
+        d.adapt[N + n] = ld(&d.adapt[N + n]) + cfg.adaptation_medium_gain * act;
+        d.adapt[2 * N + n] = ld(&d.adapt[2 * N + n]) + cfg.adaptation_slow_gain * act;
+        d.membrane[n] = ld(&d.membrane[n]) - ld(&d.p.threshold[n]) * cfg.membrane_reset_fraction;
+        d.refractory_until[n] = refractory;
+        if (ahead) {
+            d.activation[n] = 0.0f;
+            touch_neuron(c, n, c.tick + 1);
+        }
+    }
+    // emission snapshots
+    const uint32_t items = mine * S;
+    for (uint32_t item = lane; item < items; item += kWaveSize) {
+        const uint32_t r = fast_div(item, c.a->div_synapses), j = item - r * S;
+        const uint32_t n = r < kWaveSize ? w.entry[r] : ld(&d.range_winners[row0 + r]);
+        const float act = r < kWaveSize ? __uint_as_float(w.pos[r]) : ld(&d.range_winner_act[row0 + r]);
+        const uint64_t slot = static_cast<uint64_t>(n) * S + j;
+        const uint64_t at = (static_cast<uint64_t>(rs) * cap + before + r) * S + j;
+        const float value = act * ld(&d.p.rec_weight[slot]);
+        const uint32_t edge = c.a->m.rec_edge[slot];
+        d.ring_value[at] = value;
+        d.ring_edge[at] = edge;
+        if (ahead && edge_delay(edge) == 1) {
+            // delay class 1 of the next tick, keyed by active rank as its
+            // delivery from the ring would be
+            const uint64_t key = (3ull << 61) | (static_cast<uint64_t>(before + r) << 32) |
+                                 (static_cast<uint64_t>(j) << 2) | edge_branch(edge);
+            if (scatter_event(c, edge_target(edge), key, value)) touch_neuron(c, edge_target(edge), c.tick + 1);
+            delivered += 1;
         }
     }
     add_count(&c.ctl->tick_ainh[c.tick & 1], inhibitory);
@@ -1092,6 +1145,7 @@ __device__ __forceinline__ void write_active(const StepCtx& c, const StepParams&
         sh.ring_tick[rs] = c.tick;
         sh.ring_count[rs] = all;
     }
+    return delivered;
 }
 
 // Binding global cap (workgroup 0): sort every block winner by
@@ -1945,29 +1999,60 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
 #pragma unroll
         for (uint32_t i = 0; i < kStepWords; ++i) ahead[i] = ld(&src[i]);
     };
-    if (steps > 0) fetch(0);
-    for (uint32_t s = 0; s < steps && ok; ++s) {
-        StepParams sp;
-        {
-            uint32_t w[kStepWords];
+    auto params = [&]() {
+        StepParams p;
+        uint32_t w[kStepWords];
 #pragma unroll
-            for (uint32_t i = 0; i < kStepWords; ++i) w[i] = __builtin_amdgcn_readfirstlane(ahead[i]);
-            __builtin_memcpy(&sp, w, sizeof(StepParams));
-        }
+        for (uint32_t i = 0; i < kStepWords; ++i) w[i] = __builtin_amdgcn_readfirstlane(ahead[i]);
+        __builtin_memcpy(&p, w, sizeof(StepParams));
+        return p;
+    };
+    if (steps > 0) fetch(0);
+    // a step whose delivery ran in the previous step's last phase, and the
+    // event count of that delivery (thread 0 of each workgroup)
+    bool delivered_ahead = false;
+    uint32_t pending_events = 0;
+    for (uint32_t s = 0; s < steps && ok; ++s) {
+        const StepParams sp = params();
         if (s + 1 < steps) fetch(s + 1);
         const bool trace = (sp.flags & kStepLearnTrace) != 0;
-        // the context (runtime.rs:641-677) is first read by the readout
-        if (c.part == c.P - 1) context_resolve(c, sp, sh);
-        phase_deliver(c, sp, s, sh);
-        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 0))) break;
-        phase_fold_select(c);
-        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 1))) break;
+        const bool learn = (sp.flags & kStepLearn) != 0;
         // steps without eligibility updates or readout fold the post phase
         // into the active-list write (one barrier fewer)
         const bool fused = redundant && !trace && !(sp.flags & kStepOutput);
+        if (!delivered_ahead) {
+            // the context (runtime.rs:641-677) is first read by the readout
+            if (c.part == c.P - 1) context_resolve(c, sp, sh);
+            phase_deliver(c, sp, sh, false, 0);
+            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 0))) break;
+        } else if (threadIdx.x == 0 && pending_events != 0) {
+            // the previous step's write_active has rolled this tick's counters
+            atomicAdd(&c.ctl->tick_events[c.tick & 1], pending_events);
+        }
+        FusedRecord fr{0, 0, 0};
+        if (fused && c.part == 0 && threadIdx.x == 0) {
+            fr.cells = ld(&c.ctl->ctx_count);
+            fr.probes = ld(&c.ctl->ctx_probes);
+            fr.applied = ld(&c.ctl->ctx_applied);
+        }
+        phase_fold_select(c);
+        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 1))) break;
+        // a fused step followed by a frozen one starts the next tick in its
+        // last phase: the next delivery and context resolution run before
+        // this step's closing barrier (one barrier fewer again)
+        StepParams next{};
+        bool pipeline = false;
+        if (fused && !learn && s + 1 < steps) {
+            next = params();
+            pipeline = (next.flags & kStepLearnTrace) == 0;
+        }
         if (redundant) {
-            write_active(c, sp, s, sh, fused);
+            const uint32_t own = write_active(c, sp, s, sh, fused, fr, pipeline);
             if (trace) phase_eligibility(c);
+            if (pipeline) {
+                if (c.part == c.P - 1) context_resolve(c, next, sh);
+                pending_events = phase_deliver(c, next, sh, true, own);
+            }
         } else {
             if (c.part == 0) global_select(c, sh, s);
             if (trace) {
@@ -1981,7 +2066,6 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             phase_post(c, sp, s, sh);
             if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 3))) break;
         }
-        const bool learn = (sp.flags & kStepLearn) != 0;
         if (learn && sp.plasticity_scale > 0.0f) {
             c.dest_epoch += 1;
             phase_signals(c, sh);
@@ -1991,6 +2075,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             phase_learn(c, sp, sh);
             if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 5))) break;
         }
+        delivered_ahead = pipeline;
         c.tick += 1;
     }
     if (ok && c.part == 0 && threadIdx.x == 0) {
