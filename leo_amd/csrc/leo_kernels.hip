@@ -336,6 +336,12 @@ struct StepCtx {
     bool local;        // workgroups of the lane share one L2 (see lane_barrier)
 };
 
+// Waves that own selection blocks: with several workgroups per lane the last
+// one owns none (it resolves the context and takes deliveries instead).
+__device__ __forceinline__ uint32_t selecting_waves(const StepCtx& c) {
+    return (c.P > 1 ? c.P - 1 : 1) * kWavesPerGroup;
+}
+
 // ---------------------------------------------------------------------------
 // Phase 1: start_tick (runtime.rs:537-561), event delivery scatter
 // (runtime.rs:605-625) and injection (runtime.rs:627-639). Trace activation
@@ -365,27 +371,41 @@ __device__ __forceinline__ float advance_trace(float* planes, uint64_t plane, ui
 
 // Late fields of a step record: work counters complete only after the step's
 // last barrier, so the record is finished by the next step (or kernel end).
+struct LateCounters {
+    uint32_t events, touched, scanned_rec, scanned_in, destinations, inhibitory;
+};
+
+__device__ __forceinline__ LateCounters load_late_counters(LaneControl LEO_GLOBAL* ctl, uint32_t tick) {
+    const uint32_t k = tick & 1;
+    LateCounters v;
+    v.events = ld(&ctl->tick_events[k]);
+    v.touched = ld(&ctl->tick_touched[k]);
+    v.scanned_rec = ld(&ctl->tick_scan_rec[k]);
+    v.scanned_in = ld(&ctl->tick_scan_in[k]);
+    v.destinations = ld(&ctl->tick_dest[k]);
+    v.inhibitory = ld(&ctl->tick_ainh[k]);
+    return v;
+}
+
+__device__ __forceinline__ void store_late_record(const LaneDesc& d, uint32_t step_index, const LateCounters& v) {
+    StepRecord LEO_GLOBAL& rec = d.records[step_index];
+    rec.events = v.events;
+    rec.touched = v.touched;
+    rec.scanned_rec = v.scanned_rec;
+    rec.scanned_in = v.scanned_in;
+    rec.destinations = v.destinations;
+    rec.active_inhibitory = v.inhibitory;
+}
+
+// all loads first (one round trip), then the stores
 __device__ __forceinline__ void finalize_record(const LaneDesc& d, LaneControl LEO_GLOBAL* ctl, uint32_t step_index,
                                                 uint32_t tick) {
-    const uint32_t k = tick & 1;
-    // all loads first (one round trip), then the stores
-    const uint32_t events = ld(&ctl->tick_events[k]), touched = ld(&ctl->tick_touched[k]);
-    const uint32_t scanned_rec = ld(&ctl->tick_scan_rec[k]), scanned_in = ld(&ctl->tick_scan_in[k]);
-    const uint32_t destinations = ld(&ctl->tick_dest[k]), inhibitory = ld(&ctl->tick_ainh[k]);
-    StepRecord LEO_GLOBAL& rec = d.records[step_index];
-    rec.events = events;
-    rec.touched = touched;
-    rec.scanned_rec = scanned_rec;
-    rec.scanned_in = scanned_in;
-    rec.destinations = destinations;
-    rec.active_inhibitory = inhibitory;
+    store_late_record(d, step_index, load_late_counters(ctl, tick));
 }
-// Once tick-1 is complete (phase 3 of `tick`, by one thread): its record is
-// finished and its per-tick counters, which tick+1 reuses, are cleared.
-__device__ __forceinline__ void roll_counters(const StepCtx& c, uint32_t step_index) {
-    LaneControl LEO_GLOBAL* ctl = c.ctl;
-    if (step_index > 0) finalize_record(c.d, ctl, step_index - 1, c.tick - 1);
-    const uint32_t n = (c.tick + 1) & 1;
+
+// Clears the per-tick counters that tick+1 reuses.
+__device__ __forceinline__ void clear_counters(LaneControl LEO_GLOBAL* ctl, uint32_t tick) {
+    const uint32_t n = (tick + 1) & 1;
     ctl->tick_touched[n] = 0;
     ctl->tick_supra[n] = 0;
     ctl->tick_events[n] = 0;
@@ -393,6 +413,13 @@ __device__ __forceinline__ void roll_counters(const StepCtx& c, uint32_t step_in
     ctl->tick_ainh[n] = 0;
     ctl->tick_scan_rec[n] = 0;
     ctl->tick_scan_in[n] = 0;
+}
+// Once tick-1 is complete (phase 3 of `tick`, by one thread): its record is
+// finished and its per-tick counters, which tick+1 reuses, are cleared.
+__device__ __forceinline__ void roll_counters(const StepCtx& c, uint32_t step_index) {
+    LaneControl LEO_GLOBAL* ctl = c.ctl;
+    if (step_index > 0) finalize_record(c.d, ctl, step_index - 1, c.tick - 1);
+    clear_counters(ctl, c.tick);
 }
 
 // Entry p of target n's delivery bucket: the first two at fixed places
@@ -424,129 +451,180 @@ __device__ __forceinline__ void touch_neuron(const StepCtx& c, uint32_t n, uint3
     atomicOr(&c.d.touched_bits[blk * block_words(nb) + off / 32], 1u << (off & 31));
 }
 
+// The items of one tick's delivery: the previous active set, the ring
+// snapshots of delay classes 8, 4, 2, 1 (all S synapses of each source,
+// kept when the synapse's delay matches) and the symbol's F input edges.
 // `ahead`: the next tick's delivery, run in the current tick's last phase
-// (a frozen step after a fused one). The selecting waves have already
-// handled the current tick's winners (activation reset, touch, delay-1
-// events), so only delay classes 8, 4, 2 and the injection remain, and the
-// event count is returned (thread 0) to be added once the counters of that
-// tick have been rolled.
-__device__ __forceinline__ uint32_t phase_deliver(const StepCtx& c, const StepParams& sp, const StepShared& sh,
-                                                  bool ahead, uint32_t carried) {
-    const KernelArgs& a = *c.a;
-    const LaneDesc& d = c.d;
-    const LeoConfig& cfg = a.cfg;
-    LaneControl* ctl = c.ctl;
-    const uint32_t S = cfg.synapses_per_neuron, F = cfg.input_fanout, cap = cfg.max_active_global;
-    const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * S;
-    const uint64_t NI = static_cast<uint64_t>(kSymbols) * F;
-    const bool trace = (sp.flags & kStepLearnTrace) != 0;
-    const uint32_t tick = c.tick + (ahead ? 1u : 0u);
-    if (c.part == 0 && threadIdx.x == 0) {  // this step's next eligible lists
-        ctl->rec_count[c.parity ^ 1] = 0;
-        ctl->in_count[c.parity ^ 1] = 0;
-    }
+// (a frozen step after a fused one). The selecting waves handle the current
+// tick's winners there (activation reset, touch, delay-1 events), so only
+// delay classes 8, 4, 2 and the injection remain.
+struct DeliverPlan {
+    uint32_t tick, prev_slot, prev_count, off4, off2, off1, off_in, total;
+    uint32_t rs8, rs4, rs2, rs1;
+    uint32_t stride;  // items per round over the delivering workgroups
+    bool delivers;    // this workgroup takes deliveries
+};
+
+__device__ __forceinline__ DeliverPlan deliver_plan(const StepCtx& c, const StepShared& sh, bool ahead) {
+    const uint32_t S = c.a->cfg.synapses_per_neuron, F = c.a->cfg.input_fanout;
+    DeliverPlan p;
+    const uint32_t tick = p.tick = c.tick + (ahead ? 1u : 0u);
     // previous active set (runtime.rs:544-555)
-    const uint32_t prev_slot = (tick + kRing - 1) % kRing;
-    const uint32_t prev_count =
-        (!ahead && tick > 0 && sh.ring_tick[prev_slot] == tick - 1) ? sh.ring_count[prev_slot] : 0;
+    p.prev_slot = (tick + kRing - 1) % kRing;
+    p.prev_count = (!ahead && tick > 0 && sh.ring_tick[p.prev_slot] == tick - 1) ? sh.ring_count[p.prev_slot] : 0;
     // delivery classes: delay 8, 4, 2, 1 in that order (chronological by emission tick)
-    // (scalars, not arrays: a dynamically indexed private array lives in scratch)
     auto class_items = [&](uint32_t delay, uint32_t& rs) {
         rs = (tick + kRing - delay) % kRing;
         const bool valid = tick >= delay && sh.ring_tick[rs] == tick - delay;
         return (valid ? sh.ring_count[rs] : 0) * S;
     };
-    uint32_t rs8, rs4, rs2, rs1 = 0;
-    const uint32_t off8 = prev_count;
-    const uint32_t off4 = off8 + class_items(8, rs8);
-    const uint32_t off2 = off4 + class_items(4, rs4);
-    const uint32_t off1 = off2 + class_items(2, rs2);
-    const uint32_t items1 = ahead ? 0u : class_items(1, rs1);
-    const uint32_t off_in = off1 + items1;
-    const uint32_t total = off_in + F;
-    const uint32_t lane = __lane_id();
-    uint32_t delivered = carried;
+    p.rs1 = 0;
+    p.off4 = p.prev_count + class_items(8, p.rs8);
+    p.off2 = p.off4 + class_items(4, p.rs4);
+    p.off1 = p.off2 + class_items(2, p.rs2);
+    p.off_in = p.off1 + (ahead ? 0u : class_items(1, p.rs1));
+    p.total = p.off_in + F;
     // with several workgroups the last one resolves the context meanwhile and
-    // takes no deliveries
-    const uint32_t workers = c.P > 1 ? c.P - 1 : 1;
-    const bool delivers = c.P == 1 || c.part < c.P - 1;
-    const uint32_t stride = workers * kThreads;
-    for (uint32_t base = c.gtid - lane; delivers && base < total; base += stride) {
-        const uint32_t item = base + lane;
-        uint32_t touch_n = 0xffffffffu, target = 0;
-        bool scatter = false, rec = false, inj = false;
-        uint64_t key = 0, rbase = 0, slot = 0;
-        float value = 0.0f;
-        if (item < prev_count) {
-            const uint32_t n = ld(&d.ring_active[static_cast<uint64_t>(prev_slot) * cap + item]);
-            d.activation[n] = 0.0f;
-            touch_n = n;
-        } else if (item < off_in) {
-            const uint32_t k = (item >= off4 ? 1u : 0u) + (item >= off2 ? 1u : 0u) + (item >= off1 ? 1u : 0u);
-            const uint32_t lo = k == 0 ? off8 : k == 1 ? off4 : k == 2 ? off2 : off1;
-            const uint32_t rsk = k == 0 ? rs8 : k == 1 ? rs4 : k == 2 ? rs2 : rs1;
-            const uint32_t local = item - lo;
-            const uint32_t r = fast_div(local, a.div_synapses), j = local - r * S;
-            rbase = static_cast<uint64_t>(rsk) * cap + r;
-            // the emission snapshot holds the synapse with its value: the
-            // scatter needs no load that depends on the source
-            const uint32_t edge = ld(&d.ring_edge[rbase * S + j]);
-            const float v = ld(&d.ring_value[rbase * S + j]);
-            if (edge_delay(edge) == (8u >> k)) {
-                delivered += 1;
-                rec = true;
-                value = v;
-                target = edge_target(edge);
-                scatter = true;
-                slot = j;  // completed with the source below (traces only)
-                key = (static_cast<uint64_t>(k) << 61) | (static_cast<uint64_t>(r) << 32) |
-                      (static_cast<uint64_t>(j) << 2) | edge_branch(edge);
-            }
-        } else if (item < total) {
-            const uint32_t i = item - off_in;
-            slot = static_cast<uint64_t>(sp.symbol) * F + i;
-            target = a.m.in_target[slot];
-            const uint8_t br = a.m.in_branch[slot];
-            value = ld(&d.p.in_weight[slot]);
-            inj = true;
-            scatter = true;
-            key = (4ULL << 61) | (static_cast<uint64_t>(i) << 2) | br;
-        }
-        if (scatter && scatter_event(c, target, key, value)) touch_n = target;
-        if (touch_n != 0xffffffffu) touch_neuron(c, touch_n, tick);
-        // frozen steps skip the appends below: their wave-uniform counter
-        // read would wait for this item's stores before the next item's loads
-        if (!trace) continue;
-        // trace activation of the delivering slot (runtime.rs:710-766)
-        bool new_rec = false, new_in = false;
-        uint32_t eslot = 0;
-        if (rec) {
-            const float act = ld(&d.ring_act[rbase]);
-            slot += static_cast<uint64_t>(ld(&d.ring_active[rbase])) * S;
-            const float bs = advance_trace(d.rec_trace, NS, d.rec_last, static_cast<uint32_t>(slot), tick, cfg);
-            d.rec_trace[slot] = bs + act;
-            if (ld(&d.rec_mark[slot]) != kMarkListed) {
-                d.rec_mark[slot] = kMarkListed;
-                new_rec = true;
-                eslot = static_cast<uint32_t>(slot);
-            }
-        } else if (inj) {
-            const float bs = advance_trace(d.in_trace, NI, d.in_last, static_cast<uint32_t>(slot), tick, cfg);
-            d.in_trace[slot] = bs + 1.0f;
-            if (ld(&d.in_mark[slot]) != kMarkListed) {
-                d.in_mark[slot] = kMarkListed;
-                new_in = true;
-                eslot = static_cast<uint32_t>(slot);
-            }
-        }
-        uint32_t pos = wave_append(&ctl->rec_count[c.parity], new_rec);
-        if (new_rec) d.rec_list[static_cast<uint64_t>(c.parity) * NS + pos] = eslot;
-        pos = wave_append(&ctl->in_count[c.parity], new_in);
-        if (new_in) d.in_list[static_cast<uint64_t>(c.parity) * NI + pos] = eslot;
+    // takes no deliveries, except ahead (the context then waits for phase 2)
+    p.stride = (ahead || c.P == 1 ? c.P : c.P - 1) * kThreads;
+    p.delivers = ahead || c.P == 1 || c.part < c.P - 1;
+    return p;
+}
+
+// One delivery item of this thread, between its loads and its scatter.
+struct DeliverItem {
+    uint32_t touch_n, target;
+    uint64_t key, rbase, slot;
+    float value;
+    uint32_t edge;
+    uint32_t cls;      // delay class of a ring item (0..3 for delay 8, 4, 2, 1)
+    bool ring, inj;
+};
+
+// The item's loads (no dependent load: the emission snapshot holds the
+// synapse with its value).
+__device__ __forceinline__ DeliverItem deliver_fetch(const StepCtx& c, const StepParams& sp, const DeliverPlan& p,
+                                                     uint32_t item) {
+    const KernelArgs& a = *c.a;
+    const LaneDesc& d = c.d;
+    const uint32_t S = a.cfg.synapses_per_neuron, F = a.cfg.input_fanout, cap = a.cfg.max_active_global;
+    DeliverItem it;
+    it.touch_n = 0xffffffffu;
+    it.target = 0;
+    it.key = it.rbase = it.slot = 0;
+    it.value = 0.0f;
+    it.edge = 0;
+    it.cls = 0;
+    it.ring = it.inj = false;
+    if (item < p.prev_count) {
+        it.touch_n = ld(&d.ring_active[static_cast<uint64_t>(p.prev_slot) * cap + item]);
+    } else if (item < p.off_in) {
+        // the class's first item and ring slot as sums of masked steps: a
+        // select among the plan's fields becomes a load from private memory
+        const uint32_t c4 = item >= p.off4 ? 1u : 0u, c2 = item >= p.off2 ? 1u : 0u, c1 = item >= p.off1 ? 1u : 0u;
+        const uint32_t k = c4 + c2 + c1;
+        const uint32_t lo = p.prev_count + c4 * (p.off4 - p.prev_count) + c2 * (p.off2 - p.off4) + c1 * (p.off1 - p.off2);
+        const uint32_t rsk = p.rs8 + c4 * (p.rs4 - p.rs8) + c2 * (p.rs2 - p.rs4) + c1 * (p.rs1 - p.rs2);
+        const uint32_t local = item - lo;
+        const uint32_t r = fast_div(local, a.div_synapses), j = local - r * S;
+        it.rbase = static_cast<uint64_t>(rsk) * cap + r;
+        it.edge = ld(&d.ring_edge[it.rbase * S + j]);
+        it.value = ld(&d.ring_value[it.rbase * S + j]);
+        it.cls = k;
+        it.slot = j;  // completed with the source at the trace activation
+        it.key = (static_cast<uint64_t>(k) << 61) | (static_cast<uint64_t>(r) << 32) | (static_cast<uint64_t>(j) << 2);
+        it.ring = true;
+    } else if (item < p.total) {
+        const uint32_t i = item - p.off_in;
+        it.slot = static_cast<uint64_t>(sp.symbol) * F + i;
+        it.target = a.m.in_target[it.slot];
+        it.key = (4ULL << 61) | (static_cast<uint64_t>(i) << 2) | a.m.in_branch[it.slot];
+        it.value = ld(&d.p.in_weight[it.slot]);
+        it.inj = true;
     }
-    if (ahead) return wg_total(delivered);
-    add_count(&ctl->tick_events[tick & 1], delivered);
-    return 0;
+    return it;
+}
+
+// The item's scatter and touch, and for trace steps the trace activation of
+// the delivering slot (runtime.rs:710-766) with its eligible-list append.
+// Every lane of the wave calls (the appends are wave-aggregated).
+__device__ __forceinline__ void deliver_commit(const StepCtx& c, const StepParams& sp, const DeliverPlan& p,
+                                               DeliverItem& it, uint32_t& delivered) {
+    const KernelArgs& a = *c.a;
+    const LaneDesc& d = c.d;
+    const LeoConfig& cfg = a.cfg;
+    LaneControl* ctl = c.ctl;
+    const uint32_t S = cfg.synapses_per_neuron;
+    const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * S;
+    const uint64_t NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
+    bool scatter = it.inj;
+    if (it.ring) {
+        it.ring = edge_delay(it.edge) == (8u >> it.cls);
+        if (it.ring) {
+            delivered += 1;
+            it.target = edge_target(it.edge);
+            it.key |= edge_branch(it.edge);
+            scatter = true;
+        }
+    } else if (it.touch_n != 0xffffffffu) {
+        d.activation[it.touch_n] = 0.0f;
+    }
+    if (scatter && scatter_event(c, it.target, it.key, it.value)) it.touch_n = it.target;
+    if (it.touch_n != 0xffffffffu) touch_neuron(c, it.touch_n, p.tick);
+    // frozen steps skip the appends below: their wave-uniform counter read
+    // would wait for this item's stores before the next item's loads
+    if (!(sp.flags & kStepLearnTrace)) return;
+    bool new_rec = false, new_in = false;
+    uint32_t eslot = 0;
+    if (it.ring) {
+        const float act = ld(&d.ring_act[it.rbase]);
+        const uint64_t slot = it.slot + static_cast<uint64_t>(ld(&d.ring_active[it.rbase])) * S;
+        const float bs = advance_trace(d.rec_trace, NS, d.rec_last, static_cast<uint32_t>(slot), p.tick, cfg);
+        d.rec_trace[slot] = bs + act;
+        if (ld(&d.rec_mark[slot]) != kMarkListed) {
+            d.rec_mark[slot] = kMarkListed;
+            new_rec = true;
+            eslot = static_cast<uint32_t>(slot);
+        }
+    } else if (it.inj) {
+        const float bs = advance_trace(d.in_trace, NI, d.in_last, static_cast<uint32_t>(it.slot), p.tick, cfg);
+        d.in_trace[it.slot] = bs + 1.0f;
+        if (ld(&d.in_mark[it.slot]) != kMarkListed) {
+            d.in_mark[it.slot] = kMarkListed;
+            new_in = true;
+            eslot = static_cast<uint32_t>(it.slot);
+        }
+    }
+    uint32_t pos = wave_append(&ctl->rec_count[c.parity], new_rec);
+    if (new_rec) d.rec_list[static_cast<uint64_t>(c.parity) * NS + pos] = eslot;
+    pos = wave_append(&ctl->in_count[c.parity], new_in);
+    if (new_in) d.in_list[static_cast<uint64_t>(c.parity) * NI + pos] = eslot;
+}
+
+// Items from `first` on, one per thread per round.
+__device__ __forceinline__ void deliver_items(const StepCtx& c, const StepParams& sp, const DeliverPlan& p,
+                                              uint32_t first, uint32_t& delivered) {
+    const uint32_t lane = __lane_id();
+    for (uint32_t base = first - lane; p.delivers && base < p.total; base += p.stride) {
+        DeliverItem it = deliver_fetch(c, sp, p, base + lane);
+        deliver_commit(c, sp, p, it, delivered);
+    }
+}
+
+// Reset of this step's next eligible lists (trace steps append to them).
+__device__ __forceinline__ void reset_next_lists(const StepCtx& c) {
+    if (c.part == 0 && threadIdx.x == 0) {
+        c.ctl->rec_count[c.parity ^ 1] = 0;
+        c.ctl->in_count[c.parity ^ 1] = 0;
+    }
+}
+
+__device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams& sp, const StepShared& sh) {
+    reset_next_lists(c);
+    const DeliverPlan p = deliver_plan(c, sh, false);
+    uint32_t delivered = 0;
+    deliver_items(c, sp, p, c.gtid, delivered);
+    add_count(&c.ctl->tick_events[p.tick & 1], delivered);
 }
 
 // ---------------------------------------------------------------------------
@@ -583,7 +661,14 @@ __device__ __forceinline__ void context_resolve(const StepCtx& c, const StepPara
         const uint32_t order = threadIdx.x + 1;
         const uint64_t key = context_key(sh.hist, len, order);
         const uint64_t spo = cfg.context_slots_per_order;
-        const uint64_t base = static_cast<uint64_t>(order - 1) * spo, start = key % spo;
+        // slots per order is uniform; a power of two needs no 64-bit division
+        const uint64_t base = static_cast<uint64_t>(order - 1) * spo;
+        const uint64_t start = (spo & (spo - 1)) == 0 ? key & (spo - 1) : key % spo;
+        // probe_limit <= slots_per_order (config.rs:457): one wrap at most
+        auto probe_slot = [&](uint32_t off) {
+            const uint64_t at = start + off;
+            return base + (at >= spo ? at - spo : at);
+        };
         int64_t found = -1, empty = -1;
         uint64_t weakest = base + start;
         uint32_t weakest_obs = 0xffffffffu, probes = 0, found_obs = 0;
@@ -594,13 +679,13 @@ __device__ __forceinline__ void context_resolve(const StepCtx& c, const StepPara
         uint32_t obs_w[kWindow];
 #pragma unroll
         for (uint32_t off = 0; off < kWindow; ++off) {
-            const uint64_t slot = base + (start + off) % spo;
+            const uint64_t slot = probe_slot(off);
             keys[off] = off < limit ? ld(&d.p.ctx_keys[slot]) : 0;
             obs_w[off] = off < limit ? ld(&d.p.ctx_obs[slot]) : 0;
         }
         bool done = false;
         for (uint32_t off = 0; !done && off < limit; ++off) {
-            const uint64_t slot = base + (start + off) % spo;
+            const uint64_t slot = probe_slot(off);
             uint64_t existing = 0;
             uint32_t obs = 0;
             if (off < kWindow) {
@@ -862,7 +947,7 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
     const uint32_t N = cfg.neuron_count, nb = cfg.neurons_per_block, limit = cfg.max_active_per_block;
     const uint32_t tick = c.tick, rot = tick % N;
     const uint32_t wave = wave_index(), lane = __lane_id();
-    const uint32_t nwaves = c.P * kWavesPerGroup;
+    const uint32_t nwaves = selecting_waves(c);
     const uint32_t wv = c.part * kWavesPerGroup + wave;
     const uint32_t range = (cfg.block_count + nwaves - 1) / nwaves;
     const uint32_t b0 = min(cfg.block_count, wv * range), b1 = min(cfg.block_count, b0 + range);
@@ -1003,32 +1088,55 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
 // order, runtime.rs:1010-1013), population inhibition (runtime.rs:1076-1082)
 // and the forward eligibilities (runtime.rs:805-918).
 // ---------------------------------------------------------------------------
-// Context counters of a fused step's record, read in phase 2: the next step's
-// context resolution may run in the same phase as the record write.
-struct FusedRecord {
-    uint32_t cells, probes, applied;
-};
-
-// With `ahead` (a fused step followed by a frozen one) each wave also starts
-// the next tick for its own winners: activation reset and touch (the next
-// tick's previous active set, runtime.rs:544-555) and the delivery of their
-// delay-1 events, which the next tick would otherwise read back from the
-// ring. Returns this thread's count of those events.
+// With `ahead` (a fused step followed by a frozen one, `next`) the next
+// tick's delivery runs here too: each wave starts the next tick for its own
+// winners (activation reset and touch, runtime.rs:544-555, and the delivery
+// of their delay-1 events, which the next tick would otherwise read back
+// from the ring), and the delivering workgroups take the remaining items.
+// The memory operations are grouped into three rounds: the winners with the
+// first next-tick item; the winners' state and synapses with that item's
+// bucket increment; the delay-1 bucket increments. Returns this thread's
+// count of delivered events.
 __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepParams& sp, uint32_t step_index,
-                                                 StepShared& sh, bool fuse_post, const FusedRecord& fr, bool ahead) {
+                                                 StepShared& sh, bool fuse_post, bool ahead,
+                                                 const StepParams& next) {
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = c.d;
     const uint32_t cap = cfg.max_active_global, limit = cfg.max_active_per_block;
     const uint32_t wave = wave_index(), lane = __lane_id();
-    const uint32_t nwaves = c.P * kWavesPerGroup;
+    const uint32_t nwaves = selecting_waves(c);
     const uint32_t wv = c.part * kWavesPerGroup + wave;
     const uint32_t range = (cfg.block_count + nwaves - 1) / nwaves;
     const uint32_t rs = c.tick % kRing;
     const uint32_t b0 = min(cfg.block_count, wv * range), b1 = min(cfg.block_count, b0 + range);
     const uint64_t row0 = static_cast<uint64_t>(b0) * limit;
     const uint32_t slots = (b1 - b0) * limit;
-    // one round of loads: the per-wave totals, and the first 64 staged winners
-    // of this wave's range
+    // round 1: the per-wave totals, the first 64 staged winners of this
+    // wave's range, and this thread's first item of the next tick
+    // the recording thread's loads go out in the same round
+    const bool recorder = c.part == 0 && threadIdx.x == 0;
+    float pi_old = 0.0f;
+    uint32_t supra = 0, rec_n = 0, in_n = 0, cells = 0, probes = 0, applied = 0;
+    LateCounters late{};
+    if (recorder) {
+        pi_old = ld(&c.ctl->population_inhibition);
+        if (fuse_post) {
+            supra = ld(&c.ctl->tick_supra[c.tick & 1]);
+            rec_n = ld(&c.ctl->rec_count[c.parity]);
+            in_n = ld(&c.ctl->in_count[c.parity]);
+            // the context of this step is resolved (phase 1 or 2); the next
+            // step's resolution runs after these loads (phase 2 of the next
+            // step, or below on the same workgroup)
+            cells = ld(&c.ctl->ctx_count);
+            probes = ld(&c.ctl->ctx_probes);
+            applied = ld(&c.ctl->ctx_applied);
+        }
+        if (step_index > 0) late = load_late_counters(c.ctl, c.tick - 1);
+    }
+    const DeliverPlan np = deliver_plan(c, sh, true);
+    const bool deliver_next = ahead && np.delivers;
+    DeliverItem item0 = deliver_fetch(c, next, np, deliver_next ? c.gtid : np.total);
+    if (ahead) reset_next_lists(c);
     uint32_t first_n = 0;
     float first_act = 0.0f;
     if (lane < slots) {
@@ -1051,20 +1159,12 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
         act_val[i] = pre ? first_act : ld(&d.range_winner_act[row0 + i]);
     }
     const float activity = static_cast<float>(all) / static_cast<float>(cfg.neuron_count);
-    if (c.part == 0 && threadIdx.x == 0) {
+    if (recorder) {
+        // tick-1's record is finished and its counters, which tick+1 reuses,
+        // are cleared (tick-1 is complete)
         LaneControl LEO_GLOBAL* ctl = c.ctl;
-        // the loads of this block go out together, before any store
-        const float pi_old = ld(&ctl->population_inhibition);
-        uint32_t supra = 0, cells = 0, probes = 0, applied = 0, rec_n = 0, in_n = 0;
-        if (fuse_post) {
-            supra = ld(&ctl->tick_supra[c.tick & 1]);
-            cells = fr.cells;
-            probes = fr.probes;
-            applied = fr.applied;
-            rec_n = ld(&ctl->rec_count[c.parity]);
-            in_n = ld(&ctl->in_count[c.parity]);
-        }
-        roll_counters(c, step_index);
+        if (step_index > 0) store_late_record(d, step_index - 1, late);
+        clear_counters(ctl, c.tick);
         ctl->active_count = all;
         ctl->block_selected = all;
         ctl->clipped = 0;
@@ -1103,32 +1203,25 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     w.pos[lane] = __float_as_uint(first_act);
     wave_sync();
     const uint32_t refractory = c.tick + cfg.refractory_ticks + 1;
+    const uint32_t items = mine * S;
     uint32_t inhibitory = 0, delivered = 0;
-    for (uint32_t r = lane; r < mine; r += kWaveSize) {
-        const uint32_t n = r < kWaveSize ? w.entry[r] : ld(&d.range_winners[row0 + r]);
-        const float act = r < kWaveSize ? __uint_as_float(w.pos[r]) : ld(&d.range_winner_act[row0 + r]);
-        inhibitory += c.a->m.neuron_type[n] != 0 ? 1u : 0u;
-        d.fatigue[n] = ld(&d.fatigue[n]) + cfg.fatigue_gain * act;
-        d.adapt[n] = ld(&d.adapt[n]) + cfg.adaptation_fast_gain * act;
-        d.adapt[N + n] = ld(&d.adapt[N + n]) + cfg.adaptation_medium_gain * act;
-        d.adapt[2 * N + n] = ld(&d.adapt[2 * N + n]) + cfg.adaptation_slow_gain * act;
-        d.membrane[n] = ld(&d.membrane[n]) - ld(&d.p.threshold[n]) * cfg.membrane_reset_fraction;
+    auto post_fire = [&](uint32_t n, float act, float fat, float ad0, float ad1, float ad2, float mem, float thr,
+                         uint8_t type) {
+        inhibitory += type != 0 ? 1u : 0u;
+        d.fatigue[n] = fat + cfg.fatigue_gain * act;
+        d.adapt[n] = ad0 + cfg.adaptation_fast_gain * act;
+        d.adapt[N + n] = ad1 + cfg.adaptation_medium_gain * act;
+        d.adapt[2 * N + n] = ad2 + cfg.adaptation_slow_gain * act;
+        d.membrane[n] = mem - thr * cfg.membrane_reset_fraction;
         d.refractory_until[n] = refractory;
         if (ahead) {
             d.activation[n] = 0.0f;
             touch_neuron(c, n, c.tick + 1);
         }
-    }
-    // emission snapshots
-    const uint32_t items = mine * S;
-    for (uint32_t item = lane; item < items; item += kWaveSize) {
-        const uint32_t r = fast_div(item, c.a->div_synapses), j = item - r * S;
-        const uint32_t n = r < kWaveSize ? w.entry[r] : ld(&d.range_winners[row0 + r]);
-        const float act = r < kWaveSize ? __uint_as_float(w.pos[r]) : ld(&d.range_winner_act[row0 + r]);
-        const uint64_t slot = static_cast<uint64_t>(n) * S + j;
+    };
+    auto snapshot = [&](uint32_t r, uint32_t j, float act, float weight, uint32_t edge) {
         const uint64_t at = (static_cast<uint64_t>(rs) * cap + before + r) * S + j;
-        const float value = act * ld(&d.p.rec_weight[slot]);
-        const uint32_t edge = c.a->m.rec_edge[slot];
+        const float value = act * weight;
         d.ring_value[at] = value;
         d.ring_edge[at] = edge;
         if (ahead && edge_delay(edge) == 1) {
@@ -1139,7 +1232,51 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
             if (scatter_event(c, edge_target(edge), key, value)) touch_neuron(c, edge_target(edge), c.tick + 1);
             delivered += 1;
         }
+    };
+    // round 2: the first winner and synapse of each lane, and the bucket
+    // increment of this thread's first next-tick item
+    const bool pf = lane < mine, sn = lane < items;
+    float fat = 0.0f, ad0 = 0.0f, ad1 = 0.0f, ad2 = 0.0f, mem = 0.0f, thr = 0.0f;
+    uint8_t type = 0;
+    if (pf) {
+        fat = ld(&d.fatigue[first_n]);
+        ad0 = ld(&d.adapt[first_n]);
+        ad1 = ld(&d.adapt[N + first_n]);
+        ad2 = ld(&d.adapt[2 * N + first_n]);
+        mem = ld(&d.membrane[first_n]);
+        thr = ld(&d.p.threshold[first_n]);
+        type = c.a->m.neuron_type[first_n];
     }
+    uint32_t r0 = 0, j0 = 0, edge0 = 0;
+    float act0 = 0.0f, weight0 = 0.0f;
+    if (sn) {
+        r0 = fast_div(lane, c.a->div_synapses);
+        j0 = lane - r0 * S;
+        const uint32_t n = w.entry[r0];
+        act0 = __uint_as_float(w.pos[r0]);
+        const uint64_t slot = static_cast<uint64_t>(n) * S + j0;
+        weight0 = ld(&d.p.rec_weight[slot]);
+        edge0 = c.a->m.rec_edge[slot];
+    }
+    if (deliver_next) deliver_commit(c, next, np, item0, delivered);
+    // round 3: the delay-1 bucket increments
+    if (pf) post_fire(first_n, first_act, fat, ad0, ad1, ad2, mem, thr, type);
+    if (sn) snapshot(r0, j0, act0, weight0, edge0);
+    // further rounds: more than 64 winners or synapses in this wave, more
+    // next-tick items than delivering threads
+    for (uint32_t r = lane + kWaveSize; r < mine; r += kWaveSize) {
+        const uint32_t n = ld(&d.range_winners[row0 + r]);
+        post_fire(n, ld(&d.range_winner_act[row0 + r]), ld(&d.fatigue[n]), ld(&d.adapt[n]), ld(&d.adapt[N + n]),
+                  ld(&d.adapt[2 * N + n]), ld(&d.membrane[n]), ld(&d.p.threshold[n]), c.a->m.neuron_type[n]);
+    }
+    for (uint32_t item = lane + kWaveSize; item < items; item += kWaveSize) {
+        const uint32_t r = fast_div(item, c.a->div_synapses), j = item - r * S;
+        const uint32_t n = r < kWaveSize ? w.entry[r] : ld(&d.range_winners[row0 + r]);
+        const float act = r < kWaveSize ? __uint_as_float(w.pos[r]) : ld(&d.range_winner_act[row0 + r]);
+        const uint64_t slot = static_cast<uint64_t>(n) * S + j;
+        snapshot(r, j, act, ld(&d.p.rec_weight[slot]), c.a->m.rec_edge[slot]);
+    }
+    if (ahead) deliver_items(c, next, np, c.gtid + np.stride, delivered);
     add_count(&c.ctl->tick_ainh[c.tick & 1], inhibitory);
     if (threadIdx.x == 0) {  // the next deliveries read this tick's ring entry from LDS
         sh.ring_tick[rs] = c.tick;
@@ -1158,7 +1295,7 @@ __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, 
     const uint32_t tick = c.tick, rot = tick % N;
     const uint32_t rs = tick % kRing;
     uint64_t* keys = reinterpret_cast<uint64_t*>(step_lds);
-    const uint32_t nwaves = c.P * kWavesPerGroup;
+    const uint32_t nwaves = selecting_waves(c);
     const uint32_t range = (cfg.block_count + nwaves - 1) / nwaves;
     uint32_t running = 0;
     for (uint32_t base = 0; base < nwaves; base += kThreads) {
@@ -2023,23 +2160,20 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         if (!delivered_ahead) {
             // the context (runtime.rs:641-677) is first read by the readout
             if (c.part == c.P - 1) context_resolve(c, sp, sh);
-            phase_deliver(c, sp, sh, false, 0);
+            phase_deliver(c, sp, sh);
             if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 0))) break;
         } else if (threadIdx.x == 0 && pending_events != 0) {
             // the previous step's write_active has rolled this tick's counters
             atomicAdd(&c.ctl->tick_events[c.tick & 1], pending_events);
         }
-        FusedRecord fr{0, 0, 0};
-        if (fused && c.part == 0 && threadIdx.x == 0) {
-            fr.cells = ld(&c.ctl->ctx_count);
-            fr.probes = ld(&c.ctl->ctx_probes);
-            fr.applied = ld(&c.ctl->ctx_applied);
-        }
+        // the context of a step delivered ahead: on the workgroup that owns no
+        // selection blocks, beside the fold (first read by the readout)
+        if (delivered_ahead && c.P > 1 && c.part == c.P - 1) context_resolve(c, sp, sh);
         phase_fold_select(c);
         if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 1))) break;
         // a fused step followed by a frozen one starts the next tick in its
-        // last phase: the next delivery and context resolution run before
-        // this step's closing barrier (one barrier fewer again)
+        // last phase: the next delivery runs before this step's closing
+        // barrier (one barrier fewer again)
         StepParams next{};
         bool pipeline = false;
         if (fused && !learn && s + 1 < steps) {
@@ -2047,11 +2181,11 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             pipeline = (next.flags & kStepLearnTrace) == 0;
         }
         if (redundant) {
-            const uint32_t own = write_active(c, sp, s, sh, fused, fr, pipeline);
+            const uint32_t delivered = write_active(c, sp, s, sh, fused, pipeline, next);
             if (trace) phase_eligibility(c);
             if (pipeline) {
-                if (c.part == c.P - 1) context_resolve(c, next, sh);
-                pending_events = phase_deliver(c, next, sh, true, own);
+                if (c.P == 1) context_resolve(c, next, sh);
+                pending_events = wg_total(delivered);
             }
         } else {
             if (c.part == 0) global_select(c, sh, s);

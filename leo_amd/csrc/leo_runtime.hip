@@ -407,8 +407,9 @@ uint32_t choose_wgs_per_lane(LeoHipRuntime* h, uint32_t lanes, bool canonical) {
     } else if (h->wgs_override) {
         want = h->wgs_override;
     } else {
-        // one selecting wave per block, and about one workgroup per 32K edges
-        uint64_t by_blocks = (h->z.blocks + kWavesPerGroup - 1) / kWavesPerGroup;
+        // one selecting wave per block (the last workgroup selects nothing),
+        // and about one workgroup per 32K edges
+        uint64_t by_blocks = (h->z.blocks + kWavesPerGroup - 1) / kWavesPerGroup + 1;
         uint64_t by_edges = h->z.ns / 32768;
         want = static_cast<uint32_t>(std::max<uint64_t>(1, std::max(by_blocks, by_edges)));
         want = std::min<uint32_t>(want, 64);
