@@ -202,7 +202,7 @@ struct LaneDesc {
     uint32_t LEO_GLOBAL* last_tick;
     float LEO_GLOBAL* adapt;            // 3*N (fast, medium, slow)
     uint32_t LEO_GLOBAL* touched_epoch; // == tick+1 when touched this tick
-    uint32_t LEO_GLOBAL* touched_list;  // N
+    uint32_t LEO_GLOBAL* touched_list;  // N: per selecting wave, its range's touched neurons (see wave_touched)
     uint32_t LEO_GLOBAL* selected_epoch;
     uint32_t LEO_GLOBAL* dest_epoch;
     float LEO_GLOBAL* learning_signal;
@@ -216,6 +216,8 @@ struct LaneDesc {
     uint32_t LEO_GLOBAL* block_epoch;   // blocks: tick+1 when the block's selection above is current
     uint32_t LEO_GLOBAL* touched_bits;  // blocks * block_words: neurons touched this tick, cleared by phase 2
     uint32_t LEO_GLOBAL* wave_total;    // kMaxWaves: block winners of each selecting wave's block range
+    uint32_t LEO_GLOBAL* wave_touched;  // kMaxWaves: touched neurons of each selecting wave's range, listed in
+                                        // touched_list from the range's first neuron on
     // ring: per slot, up to max_active_global active neurons, activation, and S snapshot values each
     uint32_t LEO_GLOBAL* ring_active;   // kRing * cap
     float LEO_GLOBAL* ring_act;         // kRing * cap

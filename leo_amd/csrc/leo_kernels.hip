@@ -959,7 +959,10 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
     w.cands[lane] = 0;
     w.cut[lane] = ~0ULL;
     const uint64_t row0 = static_cast<uint64_t>(b0) * limit;
-    uint32_t supra = 0, staged = 0;
+    // this wave's touched neurons are listed from its range's first neuron on
+    // (no shared counter to wait for)
+    const uint32_t first_listed = b0 * nb;
+    uint32_t supra = 0, staged = 0, listed_before = 0;
     for (uint32_t gb = b0; gb < b1; gb += group) {
         const uint32_t gn = min(group, b1 - gb), gw = gn * wpb;
         uint32_t* bits = d.touched_bits + static_cast<uint64_t>(gb) * wpb;
@@ -989,8 +992,6 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
         wave_sync();
         if (lane < gn) w.start[lane] = w.pos[lane * wpb];
         if (lane == 0) w.start[gn] = total;
-        uint32_t list_at = 0;
-        if (lane == 0 && total) list_at = atomicAdd(&c.ctl->tick_touched[tick & 1], total);
         wave_sync();
         for (uint32_t lo = 0; lo < total;) {
             uint32_t hi = total;
@@ -1018,7 +1019,7 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
             }
             wave_sync();
             const uint32_t cnt = hi - lo;
-            const uint32_t listed = __builtin_amdgcn_readfirstlane(list_at) + lo;
+            const uint32_t listed = first_listed + listed_before + lo;
             for (uint32_t i = lane; i < cnt; i += kWaveSize) {
                 const uint32_t e = w.entry[i];
                 const uint32_t g = e >> 16;
@@ -1074,13 +1075,16 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
         }
         w.cands[lane] = 0;
         w.cut[lane] = ~0ULL;
+        listed_before += total;
         wave_sync();
     }
     supra = wave_sum_u32(supra);
     if (lane == 0) {
         if (supra) atomicAdd(&c.ctl->tick_supra[tick & 1], supra);
         d.wave_total[wv] = staged;
+        d.wave_touched[wv] = listed_before;
     }
+    add_count(&c.ctl->tick_touched[tick & 1], lane == 0 ? listed_before : 0u);
 }
 
 // ---------------------------------------------------------------------------
@@ -2025,16 +2029,23 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
     if (!(sp.flags & kStepFrozen)) {
         const float N = static_cast<float>(cfg.neuron_count);
         const float pop_err = static_cast<float>(A) / N - cfg.target_activity;
-        const uint32_t touched = ld(&ctl->tick_touched[tick & 1]);
-        for (uint32_t i = c.gtid; i < touched; i += c.gstride) {
-            const uint32_t n = ld(&d.touched_list[i]);
-            const float local = ld(&d.activation[n]) > 0.0f ? 1.0f : 0.0f;
-            const float local_err = local - cfg.target_activity;
-            const float delta = cfg.threshold_homeostasis_rate * (local_err + pop_err);
-            const float old_t = ld(&d.p.threshold[n]);
-            const float nt = clampf(old_t + delta, 0.05f, 2.0f);
-            if (nt != old_t) mark_bit(d.ch_threshold, n);
-            d.p.threshold[n] = nt;
+        // the touched list is kept in one segment per selecting wave (at the
+        // first neuron of its block range): one wave per segment
+        const uint32_t nwaves = selecting_waves(c), lane = __lane_id();
+        const uint32_t range = (cfg.block_count + nwaves - 1) / nwaves;
+        for (uint32_t w = c.part * kWavesPerGroup + wave_index(); w < nwaves; w += c.P * kWavesPerGroup) {
+            const uint32_t count = ld(&d.wave_touched[w]);
+            const uint32_t first = min(cfg.block_count, w * range) * cfg.neurons_per_block;
+            for (uint32_t i = lane; i < count; i += kWaveSize) {
+                const uint32_t n = ld(&d.touched_list[first + i]);
+                const float local = ld(&d.activation[n]) > 0.0f ? 1.0f : 0.0f;
+                const float local_err = local - cfg.target_activity;
+                const float delta = cfg.threshold_homeostasis_rate * (local_err + pop_err);
+                const float old_t = ld(&d.p.threshold[n]);
+                const float nt = clampf(old_t + delta, 0.05f, 2.0f);
+                if (nt != old_t) mark_bit(d.ch_threshold, n);
+                d.p.threshold[n] = nt;
+            }
         }
     }
 }
@@ -2314,7 +2325,10 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
     for (uint64_t i = t0; i < cfg.context_embedding_dim; i += ts) d.ctx_latent[i] = 0.0f;
     fill_u32(d.block_epoch, cfg.block_count, 0u, t0, ts);
     fill_u32(d.touched_bits, static_cast<uint64_t>(cfg.block_count) * block_words(cfg.neurons_per_block), 0u, t0, ts);
-    for (uint64_t i = t0; i < kMaxWaves; i += ts) d.wave_total[i] = 0;
+    for (uint64_t i = t0; i < kMaxWaves; i += ts) {
+        d.wave_total[i] = 0;
+        d.wave_touched[i] = 0;
+    }
     if (part == 0 && threadIdx.x == 0) {
         LaneControl* ctl = d.ctl;
         ctl->tick = tick;

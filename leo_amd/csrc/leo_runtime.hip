@@ -281,7 +281,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     size_t o_ls = l.add<float>(z.n), o_bc = l.add<uint32_t>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
     size_t o_bw = l.add<uint32_t>(z.blocks * z.limit), o_bcut = l.add<float>(z.blocks);
     size_t o_bwa = l.add<float>(z.blocks * z.limit);
-    size_t o_wt = l.add<uint32_t>(kMaxWaves);
+    size_t o_wt = l.add<uint32_t>(kMaxWaves), o_wtt = l.add<uint32_t>(kMaxWaves);
     size_t o_bep = l.add<uint32_t>(z.blocks), o_tb = l.add<uint32_t>(z.blocks * z.block_words);
     size_t o_ra = l.add<uint32_t>(kRing * z.cap), o_rv = l.add<float>(kRing * z.cap), o_rval = l.add<float>(kRing * z.cap * z.s);
     size_t o_redge = l.add<uint32_t>(kRing * z.cap * z.s);
@@ -314,6 +314,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     d.range_winner_act = reinterpret_cast<float*>(b + o_bwa);
     d.block_cutoff = reinterpret_cast<float*>(b + o_bcut);
     d.wave_total = reinterpret_cast<uint32_t*>(b + o_wt);
+    d.wave_touched = reinterpret_cast<uint32_t*>(b + o_wtt);
     d.block_epoch = reinterpret_cast<uint32_t*>(b + o_bep);
     d.touched_bits = reinterpret_cast<uint32_t*>(b + o_tb);
     d.ring_active = reinterpret_cast<uint32_t*>(b + o_ra);
@@ -1771,9 +1772,13 @@ int32_t leo_hip_read_list(LeoHipRuntime* h, int32_t which, uint64_t* out, uint64
                 break;
             }
             case LEO_LIST_TOUCHED: {
-                uint32_t n = ctl.tick > 0 ? ctl.tick_touched[last & 1] : 0;
-                v.resize(n);
-                leo::download(v.data(), d.touched_list, n * 4, h->stream);
+                // neurons whose touched epoch is the last tick's (tick + 1)
+                if (ctl.tick == 0) break;
+                std::vector<uint32_t> epoch(h->z.n);
+                leo::download(epoch.data(), d.touched_epoch, h->z.n * 4, h->stream);
+                leo::sync(h->stream);
+                for (uint32_t n = 0; n < h->z.n; ++n)
+                    if (epoch[n] == ctl.tick) v.push_back(n);
                 break;
             }
             case LEO_LIST_ELIGIBLE_REC: {
