@@ -1557,58 +1557,71 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
     const uint32_t ctx_count = ld(&ctl->ctx_count);
     const uint32_t wave = wave_index(), lane = __lane_id();
     float* lat = sh.aux;
-    // context latent (runtime.rs:1120-1136): serial over active slots per dimension
+    // context latent (runtime.rs:1120-1136): serial over active slots per
+    // dimension; the slots and scales, then the embeddings, in one round each
     for (uint32_t e = threadIdx.x; e < E; e += kThreads) {
-        float v = 0.0f;
-        for (uint32_t i = 0; i < ctx_count; ++i) {
-            const float scale = ld(&ctl->ctx_scales[i]);
-            if (scale <= 0.0f) continue;
-            v += ld(&d.p.ctx_emb[static_cast<uint64_t>(ld(&ctl->ctx_slots[i])) * E + e]) * scale;
+        uint32_t slot[kMaxOrder];
+        float scale[kMaxOrder], emb[kMaxOrder];
+#pragma unroll
+        for (uint32_t i = 0; i < kMaxOrder; ++i) {
+            slot[i] = i < ctx_count ? ld(&ctl->ctx_slots[i]) : 0u;
+            scale[i] = i < ctx_count ? ld(&ctl->ctx_scales[i]) : 0.0f;
         }
+#pragma unroll
+        for (uint32_t i = 0; i < kMaxOrder; ++i)
+            emb[i] = i < ctx_count && scale[i] > 0.0f ? ld(&d.p.ctx_emb[static_cast<uint64_t>(slot[i]) * E + e]) : 0.0f;
+        float v = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < kMaxOrder; ++i)
+            if (i < ctx_count && scale[i] > 0.0f) v += emb[i] * scale[i];
         lat[e] = v;
         d.ctx_latent[e] = v;
     }
     __syncthreads();
     // logits[o] = bias[o] + sum over active in order of W[n][o]*a_n (+ context once):
-    // thread t owns outputs t and t+256; the row loads of four active neurons are
-    // issued ahead of their serial adds
+    // thread t owns outputs t and t+256; per chunk of 16 active neurons their
+    // ids and activations, then the 16 row loads, go out together ahead of the
+    // serial adds
     const uint32_t o1 = threadIdx.x, o2 = threadIdx.x + kThreads;
     const bool has2 = o2 < kOutputs;
     float l1 = ld(&d.p.bias[o1]), l2 = has2 ? ld(&d.p.bias[o2]) : 0.0f;
-    uint32_t r = 0;
-    for (; r + 4 <= A; r += 4) {
-        const uint64_t n0 = ld(&act_list[r]), n1 = ld(&act_list[r + 1]), n2 = ld(&act_list[r + 2]),
-                       n3 = ld(&act_list[r + 3]);
-        const float a0 = ld(&act_val[r]), a1 = ld(&act_val[r + 1]), a2 = ld(&act_val[r + 2]), a3 = ld(&act_val[r + 3]);
-        const float w10 = ld(&d.p.out_w[n0 * kOutStride + o1]), w11 = ld(&d.p.out_w[n1 * kOutStride + o1]);
-        const float w12 = ld(&d.p.out_w[n2 * kOutStride + o1]), w13 = ld(&d.p.out_w[n3 * kOutStride + o1]);
-        float w20 = 0.0f, w21 = 0.0f, w22 = 0.0f, w23 = 0.0f;
-        if (has2) {
-            w20 = ld(&d.p.out_w[n0 * kOutStride + o2]);
-            w21 = ld(&d.p.out_w[n1 * kOutStride + o2]);
-            w22 = ld(&d.p.out_w[n2 * kOutStride + o2]);
-            w23 = ld(&d.p.out_w[n3 * kOutStride + o2]);
+    constexpr uint32_t kRows = 16;
+    for (uint32_t r0 = 0; r0 < A; r0 += kRows) {
+        uint64_t n[kRows];
+        float av[kRows], w1[kRows], w2[kRows];
+#pragma unroll
+        for (uint32_t k = 0; k < kRows; ++k) {
+            n[k] = r0 + k < A ? ld(&act_list[r0 + k]) : 0u;
+            av[k] = r0 + k < A ? ld(&act_val[r0 + k]) : 0.0f;
         }
-        l1 += w10 * a0;
-        l1 += w11 * a1;
-        l1 += w12 * a2;
-        l1 += w13 * a3;
-        l2 += w20 * a0;
-        l2 += w21 * a1;
-        l2 += w22 * a2;
-        l2 += w23 * a3;
-    }
-    for (; r < A; ++r) {
-        const uint64_t n = ld(&act_list[r]);
-        const float av = ld(&act_val[r]);
-        l1 += ld(&d.p.out_w[n * kOutStride + o1]) * av;
-        if (has2) l2 += ld(&d.p.out_w[n * kOutStride + o2]) * av;
+#pragma unroll
+        for (uint32_t k = 0; k < kRows; ++k) {
+            w1[k] = r0 + k < A ? ld(&d.p.out_w[n[k] * kOutStride + o1]) : 0.0f;
+            w2[k] = r0 + k < A && has2 ? ld(&d.p.out_w[n[k] * kOutStride + o2]) : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kRows; ++k) {
+            if (r0 + k >= A) break;
+            l1 += w1[k] * av[k];
+            l2 += w2[k] * av[k];
+        }
     }
     if (ctx_count > 0) {
+        constexpr uint32_t kDims = 16;
         float c1 = 0.0f, c2 = 0.0f;
-        for (uint32_t e = 0; e < E; ++e) {
-            c1 += ld(&d.p.ctx_out[o1 * E + e]) * lat[e];
-            if (has2) c2 += ld(&d.p.ctx_out[o2 * E + e]) * lat[e];
+        for (uint32_t e0 = 0; e0 < E; e0 += kDims) {
+            float x1[kDims], x2[kDims];
+#pragma unroll
+            for (uint32_t k = 0; k < kDims; ++k) {
+                x1[k] = e0 + k < E ? ld(&d.p.ctx_out[o1 * E + e0 + k]) : 0.0f;
+                x2[k] = e0 + k < E && has2 ? ld(&d.p.ctx_out[o2 * E + e0 + k]) : 0.0f;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < kDims; ++k) {
+                if (e0 + k >= E) break;
+                c1 += x1[k] * lat[e0 + k];
+                c2 += x2[k] * lat[e0 + k];
+            }
         }
         l1 += c1;
         l2 += c2;
@@ -1889,20 +1902,42 @@ __device__ __forceinline__ void context_update(const StepCtx& c, const StepParam
     const float lr = cfg.context_learning_rate, mu = cfg.max_update, wmin = cfg.weight_min, wmax = cfg.weight_max;
     const float strength = sp.supervised_strength;
     float* grad = sh.aux;
+    // serial in output order; the weights of 32 outputs are loaded at a time
+    constexpr uint32_t kChunk = 32;
     for (uint32_t e = threadIdx.x; e < E; e += kThreads) {
         float g = 0.0f;
-        for (uint32_t o = 0; o < kOutputs; ++o) g += ld(&d.p.ctx_out[o * E + e]) * sh.err[o];
+        for (uint32_t o0 = 0; o0 < kOutputs; o0 += kChunk) {
+            float w[kChunk];
+#pragma unroll
+            for (uint32_t k = 0; k < kChunk; ++k) w[k] = o0 + k < kOutputs ? ld(&d.p.ctx_out[(o0 + k) * E + e]) : 0.0f;
+#pragma unroll
+            for (uint32_t k = 0; k < kChunk; ++k)
+                if (o0 + k < kOutputs) g += w[k] * sh.err[o0 + k];
+        }
         grad[e] = g;
     }
     __syncthreads();
     if (threadIdx.x == 0) ctl->ctx_out_dirty = 1;
-    for (uint32_t i = threadIdx.x; i < kOutputs * E; i += kThreads) {
-        const uint32_t o = i / E, e = i % E;
-        const float gradient = sh.err[o] * ld(&d.ctx_latent[e]);
-        const float delta = bounded(-lr * strength * gradient, mu);
-        const float updated = clampf(ld(&d.p.ctx_out[i]) + delta, wmin, wmax);
-        if (!finitef(updated)) set_error(ctl, kErrContextProjection);
-        d.p.ctx_out[i] = updated;
+    // four elements per thread at a time, their loads together
+    constexpr uint32_t kBatch = 4;
+    for (uint32_t i0 = threadIdx.x; i0 < kOutputs * E; i0 += kBatch * kThreads) {
+        float old[kBatch], latent[kBatch];
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k) {
+            const uint32_t i = i0 + k * kThreads;
+            old[k] = i < kOutputs * E ? ld(&d.p.ctx_out[i]) : 0.0f;
+            latent[k] = i < kOutputs * E ? ld(&d.ctx_latent[i % E]) : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k) {
+            const uint32_t i = i0 + k * kThreads;
+            if (i >= kOutputs * E) continue;
+            const float gradient = sh.err[i / E] * latent[k];
+            const float delta = bounded(-lr * strength * gradient, mu);
+            const float updated = clampf(old[k] + delta, wmin, wmax);
+            if (!finitef(updated)) set_error(ctl, kErrContextProjection);
+            d.p.ctx_out[i] = updated;
+        }
     }
     for (uint32_t i = threadIdx.x; i < count * E; i += kThreads) {
         const uint32_t k = i / E, e = i % E;
