@@ -983,10 +983,13 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
                 const uint32_t p = total + incl - cnt;
                 w.bits[at] = word[k];
                 w.pos[at] = p;
-
-                if (word[k]) bits[at] = 0u;
                 total += __builtin_amdgcn_readlane(incl, kWaveSize - 1);
             }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kWordsPerLane; ++k) {
+            const uint32_t at = k * kWaveSize + lane;
+            if (at < gw && word[k]) bits[at] = 0u;
         }
         // block starts: the list position of each block's first word
         wave_sync();
