@@ -986,6 +986,8 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
                 total += __builtin_amdgcn_readlane(incl, kWaveSize - 1);
             }
         }
+        // the words are cleared after the scan: a store issued between the
+        // rows would be waited for together with the next row's words
 #pragma unroll
         for (uint32_t k = 0; k < kWordsPerLane; ++k) {
             const uint32_t at = k * kWaveSize + lane;
