@@ -1122,8 +1122,9 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     const uint32_t slots = (b1 - b0) * limit;
     // round 1: the per-wave totals, the first 64 staged winners of this
     // wave's range, and this thread's first item of the next tick
-    // the recording thread's loads go out in the same round
-    const bool recorder = c.part == 0 && threadIdx.x == 0;
+    // the recording thread's loads go out in the same round; it runs on the
+    // workgroup that selects nothing (the least work in this phase)
+    const bool recorder = c.part == c.P - 1 && threadIdx.x == 0;
     float pi_old = 0.0f;
     uint32_t supra = 0, rec_n = 0, in_n = 0, cells = 0, probes = 0, applied = 0;
     LateCounters late{};
