@@ -1,7 +1,8 @@
 // Device-side data layout shared by the HIP kernels (leo_kernels.hip) and the
 // host runtime (leo_runtime.hip). One "lane" is one independent runtime
 // trajectory: a logical story worker (training.rs:1669-1683) or the canonical
-// runtime itself. Every array is structure-of-arrays in HBM.
+// runtime itself. Arrays are structure-of-arrays in HBM, except the per-neuron
+// state, which is one 64-byte record per neuron (NeuronField).
 #ifndef LEO_DEVICE_H
 #define LEO_DEVICE_H
 
@@ -184,6 +185,22 @@ struct LaneParams {
     float LEO_GLOBAL* ctx_out;          // 257 * E, output-major
 };
 
+// Words of a neuron's state record.
+enum NeuronField : uint32_t {
+    kNMembrane = 0,
+    kNActivation = 1,
+    kNFatigue = 2,
+    kNAdapt0 = 3,       // fast, medium, slow adaptation
+    kNBranch0 = 6,      // branch accumulators 0..3 (excitatory, inhibitory, temporal, gate)
+    kNLastTick = 10,
+    kNRefractory = 11,  // refractory_until
+    kNTouched = 12,     // touched epoch: tick+1 when touched this tick
+    kNSelected = 13,    // selected epoch: tick+1 when selected this tick
+    kNBucketCount = 14, // deliveries in the neuron's bucket this tick
+    kNDestEpoch = 15,   // learning-destination claim epoch
+};
+constexpr uint32_t kNeuronWords = 16;
+
 // Trace slot marks: a clean slot (0) has not been written since the last
 // reset and holds zeros; a listed slot is on the eligible list; a dropped
 // slot has left the list and keeps its (sub-epsilon) values.
@@ -194,19 +211,11 @@ struct LaneDesc {
     LaneParams p;
     LaneControl LEO_GLOBAL* ctl;
     // neuron state (N)
-    float LEO_GLOBAL* membrane;
-    float LEO_GLOBAL* activation;
-    float LEO_GLOBAL* fatigue;
-    uint32_t LEO_GLOBAL* refractory_until;
-    float LEO_GLOBAL* branches;         // N*4
-    uint32_t LEO_GLOBAL* last_tick;
-    float LEO_GLOBAL* adapt;            // 3*N (fast, medium, slow)
-    uint32_t LEO_GLOBAL* touched_epoch; // == tick+1 when touched this tick
+    // neuron state (N records of kNeuronWords words, fields NeuronField): what
+    // one touched neuron needs shares one 64-byte record
+    uint32_t LEO_GLOBAL* neuron;
     uint32_t LEO_GLOBAL* touched_list;  // N: per selecting wave, its range's touched neurons (see wave_touched)
-    uint32_t LEO_GLOBAL* selected_epoch;
-    uint32_t LEO_GLOBAL* dest_epoch;
     float LEO_GLOBAL* learning_signal;
-    uint32_t LEO_GLOBAL* bucket_count;  // N
     uint64_t LEO_GLOBAL* bucket;        // 2 words per entry: delivery-order key, value bits
     // block selection
     uint32_t LEO_GLOBAL* range_winners; // blocks * max_active_per_block: winners of each selecting wave's block

@@ -203,6 +203,37 @@ __device__ __forceinline__ T ld(const T* p) {
     return __hip_atomic_load(g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A word of neuron n's state record.
+__device__ __forceinline__ float LEO_GLOBAL* nf(const LaneDesc& d, uint64_t n, uint32_t field) {
+    return reinterpret_cast<float LEO_GLOBAL*>(d.neuron) + n * kNeuronWords + field;
+}
+__device__ __forceinline__ uint32_t LEO_GLOBAL* nu(const LaneDesc& d, uint64_t n, uint32_t field) {
+    return d.neuron + n * kNeuronWords + field;
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Coherent (device-scope, L1-bypassing) buffer loads of lane state written by
+// other workgroups, 16 or 4 bytes at a time.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ f32x4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 16));
+}
+__device__ __forceinline__ float ld4(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, 0, 16));
+}
+
+// The four 16-byte quarters of neuron n's record (the host limits N * 64
+// bytes to below 2^31).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t neuron_rsrc(const LaneDesc& d, uint32_t neurons) {
+    return coherent_rsrc(d.neuron, neurons * kNeuronWords * 4);
+}
+__device__ __forceinline__ f32x4 ld_quarter(__amdgpu_buffer_rsrc_t r, uint32_t n, uint32_t quarter) {
+    return ld16(r, n * (kNeuronWords * 4) + quarter * 16);
+}
+
 // XCD (accelerator complex die) this wave runs on.
 __device__ __forceinline__ uint32_t xcc_id() {
     uint32_t v;
@@ -433,7 +464,7 @@ __device__ __forceinline__ uint64_t bucket_entry(uint64_t overflow, uint32_t n, 
 __device__ __forceinline__ bool scatter_event(const StepCtx& c, uint32_t target, uint64_t key, float value) {
     // the overflow offset is loaded with the counter increment (one round trip)
     const uint64_t overflow = c.a->m.bucket_offset[target];
-    const uint32_t p = atomicAdd(&c.d.bucket_count[target], 1u);
+    const uint32_t p = atomicAdd(nu(c.d, target, kNBucketCount), 1u);
     const uint64_t at = bucket_entry(overflow, target, p);
     c.d.bucket[2 * at] = key;
     c.d.bucket[2 * at + 1] = __float_as_uint(value);
@@ -447,7 +478,7 @@ __device__ __forceinline__ bool scatter_event(const StepCtx& c, uint32_t target,
 __device__ __forceinline__ void touch_neuron(const StepCtx& c, uint32_t n, uint32_t tick) {
     const uint32_t nb = c.a->cfg.neurons_per_block;
     const uint32_t blk = fast_div(n, c.a->div_block), off = n - blk * nb;
-    c.d.touched_epoch[n] = tick + 1;
+    (*nu(c.d, n, kNTouched)) = tick + 1;
     atomicOr(&c.d.touched_bits[blk * block_words(nb) + off / 32], 1u << (off & 31));
 }
 
@@ -567,7 +598,7 @@ __device__ __forceinline__ void deliver_commit(const StepCtx& c, const StepParam
             scatter = true;
         }
     } else if (it.touch_n != 0xffffffffu) {
-        d.activation[it.touch_n] = 0.0f;
+        (*nf(d, it.touch_n, kNActivation)) = 0.0f;
     }
     if (scatter && scatter_event(c, it.target, it.key, it.value)) it.touch_n = it.target;
     if (it.touch_n != 0xffffffffu) touch_neuron(c, it.touch_n, p.tick);
@@ -783,17 +814,22 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
     const uint32_t N = cfg.neuron_count, tick = c.tick;
-    float b0 = ld(&d.branches[4 * n]), b1 = ld(&d.branches[4 * n + 1]);
-    float b2 = ld(&d.branches[4 * n + 2]), b3 = ld(&d.branches[4 * n + 3]);
-    float mem = ld(&d.membrane[n]), fat = ld(&d.fatigue[n]);
-    float ad0 = ld(&d.adapt[n]), ad1 = ld(&d.adapt[N + n]), ad2 = ld(&d.adapt[2 * N + n]);
-    const uint32_t last = ld(&d.last_tick[n]);
-    const uint32_t cnt = ld(&d.bucket_count[n]);
+    // the record in three 16-byte loads (membrane .. bucket count)
+    static_assert(kNMembrane == 0 && kNFatigue == 2 && kNAdapt0 == 3 && kNBranch0 == 6 && kNLastTick == 10 &&
+                      kNRefractory == 11 && kNBucketCount == 14,
+                  "record layout");
+    const __amdgpu_buffer_rsrc_t rec = neuron_rsrc(d, N);
+    const f32x4 q0 = ld_quarter(rec, n, 0), q1 = ld_quarter(rec, n, 1), q2 = ld_quarter(rec, n, 2);
+    const f32x4 q3 = ld_quarter(rec, n, 3);
+    float mem = q0.x, fat = q0.z, ad0 = q0.w, ad1 = q1.x, ad2 = q1.y;
+    float b0 = q1.z, b1 = q1.w, b2 = q2.x, b3 = q2.y;
+    const uint32_t last = __float_as_uint(q2.z);
+    const uint32_t cnt = __float_as_uint(q3.z);
     const uint64_t overflow = a.m.bucket_offset[n];  // loaded with the state (used when cnt > 2)
     // the two fixed bucket entries are read with the state
     const uint64_t* fixed = d.bucket + 4ull * n;
     const uint64_t k0 = ld(&fixed[0]), v0 = ld(&fixed[1]), k1 = ld(&fixed[2]), v1 = ld(&fixed[3]);
-    const bool refr = ld(&d.refractory_until[n]) > tick;
+    const bool refr = __float_as_uint(q2.w) > tick;
     const float threshold = ld(&d.p.threshold[n]);
     const uint32_t e = tick - last;
     if (e > 0) {
@@ -807,11 +843,11 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
         ad0 *= k.fast;
         ad1 *= k.medium;
         ad2 *= k.slow;
-        d.fatigue[n] = fat;
-        d.adapt[n] = ad0;
-        d.adapt[N + n] = ad1;
-        d.adapt[2 * N + n] = ad2;
-        d.last_tick[n] = tick;
+        (*nf(d, n, kNFatigue)) = fat;
+        (*nf(d, n, kNAdapt0)) = ad0;
+        (*nf(d, n, kNAdapt0 + 1)) = ad1;
+        (*nf(d, n, kNAdapt0 + 2)) = ad2;
+        (*nu(d, n, kNLastTick)) = tick;
     }
     if (cnt > 0) {
         // selects, not an indexed array (which would live in scratch)
@@ -871,12 +907,12 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
                 started = true;
             }
         }
-        d.bucket_count[n] = 0;
+        (*nu(d, n, kNBucketCount)) = 0;
     }
-    d.branches[4 * n] = b0;
-    d.branches[4 * n + 1] = b1;
-    d.branches[4 * n + 2] = b2;
-    d.branches[4 * n + 3] = b3;
+    (*nf(d, n, kNBranch0)) = b0;
+    (*nf(d, n, kNBranch0 + 1)) = b1;
+    (*nf(d, n, kNBranch0 + 2)) = b2;
+    (*nf(d, n, kNBranch0 + 3)) = b3;
     *refractory = refr;
     if (!refr) {
         const float gate = clampf(b3, 0.0f, 1.0f);
@@ -885,7 +921,7 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
         const float drive = a.m.excitability[n] * net - fat - adaptation - pi;
         mem = mem + drive;
     }
-    if (e > 0 || !refr) d.membrane[n] = mem;
+    if (e > 0 || !refr) (*nf(d, n, kNMembrane)) = mem;
     return mem - threshold;
 }
 
@@ -1060,8 +1096,8 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
                     d.range_winners[at] = n;
                     d.range_winner_act[at] = act;
                     if (a.redundant_global) {  // the global cap cannot bind (runtime.rs:1060-1067)
-                        d.activation[n] = act;
-                        d.selected_epoch[n] = tick + 1;
+                        (*nf(d, n, kNActivation)) = act;
+                        (*nu(d, n, kNSelected)) = tick + 1;
                     }
                 } else if (rank == limit) {
                     w.cut[g] = mine;
@@ -1218,14 +1254,14 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     auto post_fire = [&](uint32_t n, float act, float fat, float ad0, float ad1, float ad2, float mem, float thr,
                          uint8_t type) {
         inhibitory += type != 0 ? 1u : 0u;
-        d.fatigue[n] = fat + cfg.fatigue_gain * act;
-        d.adapt[n] = ad0 + cfg.adaptation_fast_gain * act;
-        d.adapt[N + n] = ad1 + cfg.adaptation_medium_gain * act;
-        d.adapt[2 * N + n] = ad2 + cfg.adaptation_slow_gain * act;
-        d.membrane[n] = mem - thr * cfg.membrane_reset_fraction;
-        d.refractory_until[n] = refractory;
+        (*nf(d, n, kNFatigue)) = fat + cfg.fatigue_gain * act;
+        (*nf(d, n, kNAdapt0)) = ad0 + cfg.adaptation_fast_gain * act;
+        (*nf(d, n, kNAdapt0 + 1)) = ad1 + cfg.adaptation_medium_gain * act;
+        (*nf(d, n, kNAdapt0 + 2)) = ad2 + cfg.adaptation_slow_gain * act;
+        (*nf(d, n, kNMembrane)) = mem - thr * cfg.membrane_reset_fraction;
+        (*nu(d, n, kNRefractory)) = refractory;
         if (ahead) {
-            d.activation[n] = 0.0f;
+            (*nf(d, n, kNActivation)) = 0.0f;
             touch_neuron(c, n, c.tick + 1);
         }
     };
@@ -1249,11 +1285,11 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     float fat = 0.0f, ad0 = 0.0f, ad1 = 0.0f, ad2 = 0.0f, mem = 0.0f, thr = 0.0f;
     uint8_t type = 0;
     if (pf) {
-        fat = ld(&d.fatigue[first_n]);
-        ad0 = ld(&d.adapt[first_n]);
-        ad1 = ld(&d.adapt[N + first_n]);
-        ad2 = ld(&d.adapt[2 * N + first_n]);
-        mem = ld(&d.membrane[first_n]);
+        fat = ld(nf(d, first_n, kNFatigue));
+        ad0 = ld(nf(d, first_n, kNAdapt0));
+        ad1 = ld(nf(d, first_n, kNAdapt0 + 1));
+        ad2 = ld(nf(d, first_n, kNAdapt0 + 2));
+        mem = ld(nf(d, first_n, kNMembrane));
         thr = ld(&d.p.threshold[first_n]);
         type = c.a->m.neuron_type[first_n];
     }
@@ -1276,8 +1312,8 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     // next-tick items than delivering threads
     for (uint32_t r = lane + kWaveSize; r < mine; r += kWaveSize) {
         const uint32_t n = ld(&d.range_winners[row0 + r]);
-        post_fire(n, ld(&d.range_winner_act[row0 + r]), ld(&d.fatigue[n]), ld(&d.adapt[n]), ld(&d.adapt[N + n]),
-                  ld(&d.adapt[2 * N + n]), ld(&d.membrane[n]), ld(&d.p.threshold[n]), c.a->m.neuron_type[n]);
+        post_fire(n, ld(&d.range_winner_act[row0 + r]), ld(nf(d, n, kNFatigue)), ld(nf(d, n, kNAdapt0)), ld(nf(d, n, kNAdapt0 + 1)),
+                  ld(nf(d, n, kNAdapt0 + 2)), ld(nf(d, n, kNMembrane)), ld(&d.p.threshold[n]), c.a->m.neuron_type[n]);
     }
     for (uint32_t item = lane + kWaveSize; item < items; item += kWaveSize) {
         const uint32_t r = fast_div(item, c.a->div_synapses), j = item - r * S;
@@ -1351,8 +1387,8 @@ __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, 
             const float act = key_activation(key);
             act_list[i] = n;
             act_val[i] = act;
-            d.activation[n] = act;
-            d.selected_epoch[n] = tick + 1;
+            (*nf(d, n, kNActivation)) = act;
+            (*nu(d, n, kNSelected)) = tick + 1;
         }
     }
     __syncthreads();
@@ -1399,19 +1435,19 @@ __device__ __forceinline__ void load_slot(SlotInputs& in, const float LEO_GLOBAL
 }
 
 __device__ __forceinline__ void load_epochs(SlotInputs& in, const StepCtx& c, uint32_t dst) {
-    in.touched_epoch = ld(&c.d.touched_epoch[dst]);
-    in.selected_epoch = ld(&c.d.selected_epoch[dst]);
+    in.touched_epoch = ld(nu(c.d, dst, kNTouched));
+    in.selected_epoch = ld(nu(c.d, dst, kNSelected));
 }
 
 __device__ __forceinline__ void load_destination(SlotInputs& in, const StepCtx& c, uint32_t dst) {
     const LaneDesc& d = c.d;
     const uint32_t blk = fast_div(dst, c.a->div_block);
-    in.refractory_until = ld(&d.refractory_until[dst]);
-    in.temporal = ld(&d.branches[4 * dst + BR_TEMP]);
-    in.gate_acc = ld(&d.branches[4 * dst + BR_GATE]);
+    in.refractory_until = ld(nu(d, dst, kNRefractory));
+    in.temporal = ld(nf(d, dst, kNBranch0 + BR_TEMP));
+    in.gate_acc = ld(nf(d, dst, kNBranch0 + BR_GATE));
     in.block_epoch = ld(&d.block_epoch[blk]);
     in.block_cut = ld(&d.block_cutoff[blk]);
-    in.membrane = ld(&d.membrane[dst]);
+    in.membrane = ld(nf(d, dst, kNMembrane));
     in.threshold = ld(&d.p.threshold[dst]);
     in.excitability = c.a->m.excitability[dst];
 }
@@ -1704,14 +1740,14 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
     for (uint32_t item = c.gtid; item < total; item += c.gstride) {
         if (item < A) {
             const uint32_t n = ld(&act_list[item]);
-            const float act = ld(&d.activation[n]);
+            const float act = ld(nf(d, n, kNActivation));
             inhibitory += a.m.neuron_type[n] != 0 ? 1u : 0u;
-            d.fatigue[n] = ld(&d.fatigue[n]) + cfg.fatigue_gain * act;
-            d.adapt[n] = ld(&d.adapt[n]) + cfg.adaptation_fast_gain * act;
-            d.adapt[N + n] = ld(&d.adapt[N + n]) + cfg.adaptation_medium_gain * act;
-            d.adapt[2 * N + n] = ld(&d.adapt[2 * N + n]) + cfg.adaptation_slow_gain * act;
-            d.membrane[n] = ld(&d.membrane[n]) - ld(&d.p.threshold[n]) * cfg.membrane_reset_fraction;
-            d.refractory_until[n] = refractory;
+            (*nf(d, n, kNFatigue)) = ld(nf(d, n, kNFatigue)) + cfg.fatigue_gain * act;
+            (*nf(d, n, kNAdapt0)) = ld(nf(d, n, kNAdapt0)) + cfg.adaptation_fast_gain * act;
+            (*nf(d, n, kNAdapt0 + 1)) = ld(nf(d, n, kNAdapt0 + 1)) + cfg.adaptation_medium_gain * act;
+            (*nf(d, n, kNAdapt0 + 2)) = ld(nf(d, n, kNAdapt0 + 2)) + cfg.adaptation_slow_gain * act;
+            (*nf(d, n, kNMembrane)) = ld(nf(d, n, kNMembrane)) - ld(&d.p.threshold[n]) * cfg.membrane_reset_fraction;
+            (*nu(d, n, kNRefractory)) = refractory;
         } else {
             const uint32_t local = item - A;
             const uint32_t r = fast_div(local, a.div_synapses), j = local - r * S;
@@ -1767,17 +1803,6 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
 // Device-scope 16-byte loads through a buffer resource (cache policy sc1: the
 // load misses the CU's L1 like ld()); the resource is wave-uniform and covers
 // `bytes` from `base` (loads beyond it return 0).
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
-}
-__device__ __forceinline__ f32x4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
-    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 16));
-}
-__device__ __forceinline__ float ld4(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, 0, 16));
-}
-
 // Serial 257-term dot of one output row with the errors, in output order
 // (runtime.rs:1245-1250); eight 16-byte row loads are in flight at a time.
 // Learning signals of up to 64 destinations, one per lane (`dst` on lanes
@@ -1863,7 +1888,7 @@ __device__ __forceinline__ void phase_signals(const StepCtx& c, StepShared& sh) 
             if (item < rec_n) dst = a.m.rec_target[ld(&rec_cur[item])];
             else if (item < rec_n + in_n) dst = a.m.in_target[ld(&in_cur[item - rec_n])];
             else dst = ld(&act_list[item - rec_n - in_n]);
-            won = atomicExch(&d.dest_epoch[dst], c.dest_epoch) != c.dest_epoch;
+            won = atomicExch(nu(d, dst, kNDestEpoch), c.dest_epoch) != c.dest_epoch;
         }
         const unsigned long long mask = __ballot(won);
         if (won) queue[queued + __popcll(mask & below)] = dst;
@@ -2024,9 +2049,9 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
                 nw = excitatory ? maxnum(nw, 0.0f) : fminf(nw, 0.0f);
                 if (!finitef(nw)) set_error(ctl, kErrRecurrent);
                 bool changed = nw != old_w;
-                if (!excitatory && ld(&d.selected_epoch[src]) == tick + 1) {
-                    const float tgt_act = ld(&d.activation[dst]) > 0.0f ? 1.0f : 0.0f;
-                    const float nw2 = inhibitory_step(cfg, nw, ld(&d.activation[src]), tgt_act, sp.strength);
+                if (!excitatory && ld(nu(d, src, kNSelected)) == tick + 1) {
+                    const float tgt_act = ld(nf(d, dst, kNActivation)) > 0.0f ? 1.0f : 0.0f;
+                    const float nw2 = inhibitory_step(cfg, nw, ld(nf(d, src, kNActivation)), tgt_act, sp.strength);
                     if (!finitef(nw2)) set_error(ctl, kErrInhibitory);
                     changed = changed || nw2 != nw;
                     nw = nw2;
@@ -2059,9 +2084,9 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
             const uint64_t slot = static_cast<uint64_t>(src) * S + j;
             if (plastic && ld(&d.rec_mark[slot]) == kMarkListed) continue;
             const uint32_t dst = a.m.rec_target[slot];
-            const float tgt_act = ld(&d.activation[dst]) > 0.0f ? 1.0f : 0.0f;
+            const float tgt_act = ld(nf(d, dst, kNActivation)) > 0.0f ? 1.0f : 0.0f;
             const float old_w = ld(&d.p.rec_weight[slot]);
-            const float nw = inhibitory_step(cfg, old_w, ld(&d.activation[src]), tgt_act, sp.strength);
+            const float nw = inhibitory_step(cfg, old_w, ld(nf(d, src, kNActivation)), tgt_act, sp.strength);
             if (!finitef(nw)) set_error(ctl, kErrInhibitory);
             if (nw != old_w) mark_bit(d.ch_rec, static_cast<uint32_t>(slot));
             d.p.rec_weight[slot] = nw;
@@ -2079,7 +2104,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
             const uint32_t first = min(cfg.block_count, w * range) * cfg.neurons_per_block;
             for (uint32_t i = lane; i < count; i += kWaveSize) {
                 const uint32_t n = ld(&d.touched_list[first + i]);
-                const float local = ld(&d.activation[n]) > 0.0f ? 1.0f : 0.0f;
+                const float local = ld(nf(d, n, kNActivation)) > 0.0f ? 1.0f : 0.0f;
                 const float local_err = local - cfg.target_activity;
                 const float delta = cfg.threshold_homeostasis_rate * (local_err + pop_err);
                 const float old_t = ld(&d.p.threshold[n]);
@@ -2341,16 +2366,14 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
     const uint64_t N = cfg.neuron_count, S = cfg.synapses_per_neuron;
     const uint64_t NS = N * S, NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
     const uint64_t t0 = static_cast<uint64_t>(part) * kThreads + threadIdx.x, ts = static_cast<uint64_t>(parts) * kThreads;
-    fill_f32(d.membrane, N, t0, ts);
-    fill_f32(d.activation, N, t0, ts);
-    fill_f32(d.fatigue, N, t0, ts);
-    fill_u32(d.refractory_until, N, 0u, t0, ts);
-    fill_f32(d.branches, 4 * N, t0, ts);
-    fill_f32(d.adapt, 3 * N, t0, ts);
-    fill_u32(d.last_tick, N, tick, t0, ts);
-    fill_u32(d.touched_epoch, N, 0u, t0, ts);
-    fill_u32(d.selected_epoch, N, 0u, t0, ts);
-    fill_u32(d.bucket_count, N, 0u, t0, ts);
+    // neuron records: zero state, last tick = tick, epochs and claims 0
+    // (claim epochs in use are >= 1)
+    static_assert(kNeuronWords == 16 && kNLastTick == 10, "record layout");
+    {
+        uint4 LEO_GLOBAL* rec = reinterpret_cast<uint4 LEO_GLOBAL*>(d.neuron);
+        const uint4 zero = make_uint4(0u, 0u, 0u, 0u), with_tick = make_uint4(0u, 0u, tick, 0u);
+        for (uint64_t i = t0; i < 4 * N; i += ts) rec[i] = (i & 3) == 2 ? with_tick : zero;
+    }
     const uint64_t groups = NS / 16;
     for (uint64_t g = t0; g < groups; g += ts) clear_trace_group(d, NS, g, tick, set_tick != 0);
     for (uint64_t i = 16 * groups + t0; i < NS; i += ts) {

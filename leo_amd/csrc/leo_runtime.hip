@@ -274,11 +274,8 @@ void copy_params(const LaneParams& dst, const LaneParams& src, const Sizes& z, h
 void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     Layout l;
     size_t o_ctl = l.add<LaneControl>(1);
-    size_t o_mem = l.add<float>(z.n), o_act = l.add<float>(z.n), o_fat = l.add<float>(z.n);
-    size_t o_ref = l.add<uint32_t>(z.n), o_br = l.add<float>(4 * z.n), o_last = l.add<uint32_t>(z.n);
-    size_t o_ad = l.add<float>(3 * z.n), o_te = l.add<uint32_t>(z.n), o_tl = l.add<uint32_t>(z.n);
-    size_t o_se = l.add<uint32_t>(z.n), o_de = l.add<uint32_t>(z.n);
-    size_t o_ls = l.add<float>(z.n), o_bc = l.add<uint32_t>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
+    size_t o_neu = l.add<uint32_t>(kNeuronWords * z.n), o_tl = l.add<uint32_t>(z.n);
+    size_t o_ls = l.add<float>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
     size_t o_bw = l.add<uint32_t>(z.blocks * z.limit), o_bcut = l.add<float>(z.blocks);
     size_t o_bwa = l.add<float>(z.blocks * z.limit);
     size_t o_wt = l.add<uint32_t>(kMaxWaves), o_wtt = l.add<uint32_t>(kMaxWaves);
@@ -296,19 +293,10 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     char* b = lane.state.base;
     LaneDesc& d = lane.desc;
     d.ctl = reinterpret_cast<LaneControl*>(b + o_ctl);
-    d.membrane = reinterpret_cast<float*>(b + o_mem);
-    d.activation = reinterpret_cast<float*>(b + o_act);
-    d.fatigue = reinterpret_cast<float*>(b + o_fat);
-    d.refractory_until = reinterpret_cast<uint32_t*>(b + o_ref);
-    d.branches = reinterpret_cast<float*>(b + o_br);
-    d.last_tick = reinterpret_cast<uint32_t*>(b + o_last);
-    d.adapt = reinterpret_cast<float*>(b + o_ad);
-    d.touched_epoch = reinterpret_cast<uint32_t*>(b + o_te);
+    d.neuron = reinterpret_cast<uint32_t*>(b + o_neu);
     d.touched_list = reinterpret_cast<uint32_t*>(b + o_tl);
-    d.selected_epoch = reinterpret_cast<uint32_t*>(b + o_se);
-    d.dest_epoch = reinterpret_cast<uint32_t*>(b + o_de);
+
     d.learning_signal = reinterpret_cast<float*>(b + o_ls);
-    d.bucket_count = reinterpret_cast<uint32_t*>(b + o_bc);
     d.bucket = reinterpret_cast<uint64_t*>(b + o_bk);
     d.range_winners = reinterpret_cast<uint32_t*>(b + o_bw);
     d.range_winner_act = reinterpret_cast<float*>(b + o_bwa);
@@ -1774,11 +1762,11 @@ int32_t leo_hip_read_list(LeoHipRuntime* h, int32_t which, uint64_t* out, uint64
             case LEO_LIST_TOUCHED: {
                 // neurons whose touched epoch is the last tick's (tick + 1)
                 if (ctl.tick == 0) break;
-                std::vector<uint32_t> epoch(h->z.n);
-                leo::download(epoch.data(), d.touched_epoch, h->z.n * 4, h->stream);
+                std::vector<uint32_t> rec(h->z.n * leo::kNeuronWords);
+                leo::download(rec.data(), d.neuron, rec.size() * 4, h->stream);
                 leo::sync(h->stream);
                 for (uint32_t n = 0; n < h->z.n; ++n)
-                    if (epoch[n] == ctl.tick) v.push_back(n);
+                    if (rec[static_cast<size_t>(n) * leo::kNeuronWords + leo::kNTouched] == ctl.tick) v.push_back(n);
                 break;
             }
             case LEO_LIST_ELIGIBLE_REC: {
@@ -1810,6 +1798,8 @@ int32_t leo_hip_read_state(LeoHipRuntime* h, int32_t which, float* out, uint64_t
         const leo::Sizes& z = h->z;
         const float* src = nullptr;
         uint64_t n = 0;
+        // per-neuron state: `words` consecutive words of each neuron's record
+        uint32_t field = 0, words = 0;
         if (which >= LEO_STATE_REC_BS && which <= LEO_STATE_REC_E) {
             src = d.rec_trace + static_cast<uint64_t>(which - LEO_STATE_REC_BS) * z.ns;
             n = z.ns;
@@ -1818,13 +1808,13 @@ int32_t leo_hip_read_state(LeoHipRuntime* h, int32_t which, float* out, uint64_t
             n = z.ni;
         } else {
             switch (which) {
-                case LEO_STATE_MEMBRANE: src = d.membrane; n = z.n; break;
-                case LEO_STATE_ACTIVATION: src = d.activation; n = z.n; break;
-                case LEO_STATE_FATIGUE: src = d.fatigue; n = z.n; break;
-                case LEO_STATE_BRANCHES: src = d.branches; n = 4 * z.n; break;
-                case LEO_STATE_ADAPT0: src = d.adapt; n = z.n; break;
-                case LEO_STATE_ADAPT1: src = d.adapt + z.n; n = z.n; break;
-                case LEO_STATE_ADAPT2: src = d.adapt + 2 * z.n; n = z.n; break;
+                case LEO_STATE_MEMBRANE: field = leo::kNMembrane; words = 1; break;
+                case LEO_STATE_ACTIVATION: field = leo::kNActivation; words = 1; break;
+                case LEO_STATE_FATIGUE: field = leo::kNFatigue; words = 1; break;
+                case LEO_STATE_BRANCHES: field = leo::kNBranch0; words = 4; break;
+                case LEO_STATE_ADAPT0: field = leo::kNAdapt0; words = 1; break;
+                case LEO_STATE_ADAPT1: field = leo::kNAdapt0 + 1; words = 1; break;
+                case LEO_STATE_ADAPT2: field = leo::kNAdapt0 + 2; words = 1; break;
                 case LEO_STATE_SURROGATE:
                     throw Error(LEO_ERR_UNSUPPORTED, "surrogates are evaluated where the eligibility update uses them, not stored");
                 case LEO_STATE_LOGITS: src = d.logits; n = leo::kOutputs; break;
@@ -1834,7 +1824,16 @@ int32_t leo_hip_read_state(LeoHipRuntime* h, int32_t which, float* out, uint64_t
                 default: throw Error(LEO_ERR_INVALID_ARGUMENT, "unknown state selector");
             }
         }
+        if (words) n = static_cast<uint64_t>(words) * z.n;
         if (count != n) throw Error(LEO_ERR_INVALID_ARGUMENT, "state size mismatch: expected " + std::to_string(n));
+        if (words) {
+            std::vector<float> rec(z.n * leo::kNeuronWords);
+            leo::download(rec.data(), d.neuron, rec.size() * 4, h->stream);
+            leo::sync(h->stream);
+            for (uint64_t i = 0; i < z.n; ++i)
+                for (uint32_t w = 0; w < words; ++w) out[i * words + w] = rec[i * leo::kNeuronWords + field + w];
+            return;
+        }
         leo::download(out, src, n * 4, h->stream);
         leo::sync(h->stream);
     });
