@@ -1285,11 +1285,14 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     float fat = 0.0f, ad0 = 0.0f, ad1 = 0.0f, ad2 = 0.0f, mem = 0.0f, thr = 0.0f;
     uint8_t type = 0;
     if (pf) {
-        fat = ld(nf(d, first_n, kNFatigue));
-        ad0 = ld(nf(d, first_n, kNAdapt0));
-        ad1 = ld(nf(d, first_n, kNAdapt0 + 1));
-        ad2 = ld(nf(d, first_n, kNAdapt0 + 2));
-        mem = ld(nf(d, first_n, kNMembrane));
+        // quarters 0 and 1 of the record: membrane, fatigue, adaptations
+        const __amdgpu_buffer_rsrc_t rec = neuron_rsrc(d, N);
+        const f32x4 q0 = ld_quarter(rec, first_n, 0), q1 = ld_quarter(rec, first_n, 1);
+        mem = q0.x;
+        fat = q0.z;
+        ad0 = q0.w;
+        ad1 = q1.x;
+        ad2 = q1.y;
         thr = ld(&d.p.threshold[first_n]);
         type = c.a->m.neuron_type[first_n];
     }
@@ -1434,20 +1437,29 @@ __device__ __forceinline__ void load_slot(SlotInputs& in, const float LEO_GLOBAL
     in.last = ld(&last[slot]);
 }
 
+// The destination's epochs: quarter 3 of its record.
 __device__ __forceinline__ void load_epochs(SlotInputs& in, const StepCtx& c, uint32_t dst) {
-    in.touched_epoch = ld(nu(c.d, dst, kNTouched));
-    in.selected_epoch = ld(nu(c.d, dst, kNSelected));
+    static_assert(kNTouched == 12 && kNSelected == 13, "record layout");
+    const f32x4 q3 = ld_quarter(neuron_rsrc(c.d, c.a->cfg.neuron_count), dst, 3);
+    in.touched_epoch = __float_as_uint(q3.x);
+    in.selected_epoch = __float_as_uint(q3.y);
 }
 
+// The destination's state: quarters 0 and 2 of its record, its block's
+// selection and its threshold and excitability.
 __device__ __forceinline__ void load_destination(SlotInputs& in, const StepCtx& c, uint32_t dst) {
+    static_assert(kNMembrane == 0 && kNBranch0 + BR_TEMP == 8 && kNBranch0 + BR_GATE == 9 && kNRefractory == 11,
+                  "record layout");
     const LaneDesc& d = c.d;
     const uint32_t blk = fast_div(dst, c.a->div_block);
-    in.refractory_until = ld(nu(d, dst, kNRefractory));
-    in.temporal = ld(nf(d, dst, kNBranch0 + BR_TEMP));
-    in.gate_acc = ld(nf(d, dst, kNBranch0 + BR_GATE));
+    const __amdgpu_buffer_rsrc_t rec = neuron_rsrc(d, c.a->cfg.neuron_count);
+    const f32x4 q0 = ld_quarter(rec, dst, 0), q2 = ld_quarter(rec, dst, 2);
+    in.refractory_until = __float_as_uint(q2.w);
+    in.temporal = q2.x;
+    in.gate_acc = q2.y;
     in.block_epoch = ld(&d.block_epoch[blk]);
     in.block_cut = ld(&d.block_cutoff[blk]);
-    in.membrane = ld(nf(d, dst, kNMembrane));
+    in.membrane = q0.x;
     in.threshold = ld(&d.p.threshold[dst]);
     in.excitability = c.a->m.excitability[dst];
 }
