@@ -201,6 +201,15 @@ enum NeuronField : uint32_t {
 };
 constexpr uint32_t kNeuronWords = 16;
 
+// Words of a synapse slot's trace record: the branch, membrane and fatigue
+// sensitivities, the three adaptation sensitivities, the eligibility, and the
+// tick they were last brought to (u32 bits). One slot's trace is two 16-byte
+// quarters of one record.
+enum TraceField : uint32_t {
+    kTBranch = 0, kTMembrane = 1, kTFatigue = 2, kTAdapt0 = 3, kTEligibility = 6, kTLast = 7,
+};
+constexpr uint32_t kTraceWords = 8;
+
 // Trace slot marks: a clean slot (0) has not been written since the last
 // reset and holds zeros; a listed slot is on the eligible list; a dropped
 // slot has left the list and keeps its (sub-epsilon) values.
@@ -233,13 +242,11 @@ struct LaneDesc {
     float LEO_GLOBAL* ring_value;       // kRing * cap * S
     uint32_t LEO_GLOBAL* ring_edge;     // kRing * cap * S: packed synapse of each snapshot value (target, delay, branch)
     // recurrent traces (N*S): branch, membrane, fatigue, 3 adaptation sensitivities, eligibility
-    float LEO_GLOBAL* rec_trace;        // 7 * NS (SoA planes)
-    uint32_t LEO_GLOBAL* rec_last;      // NS
+    float LEO_GLOBAL* rec_trace;        // NS records of kTraceWords (TraceField)
     uint8_t LEO_GLOBAL* rec_mark;       // NS: kMark*
     uint32_t LEO_GLOBAL* rec_list;      // 2 * NS
     // input traces (258*F)
-    float LEO_GLOBAL* in_trace;         // 7 * NI
-    uint32_t LEO_GLOBAL* in_last;
+    float LEO_GLOBAL* in_trace;         // NI records of kTraceWords (TraceField)
     uint8_t LEO_GLOBAL* in_mark;        // NI: kMark*
     uint32_t LEO_GLOBAL* in_list;       // 2 * NI
     // readout

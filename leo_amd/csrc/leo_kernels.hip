@@ -379,25 +379,28 @@ __device__ __forceinline__ uint32_t selecting_waves(const StepCtx& c) {
 // (runtime.rs:710-766) is slot-local; branch adds go to per-target buckets
 // keyed by CPU delivery order and are folded in phase 2.
 // ---------------------------------------------------------------------------
-// Brings one trace slot to `tick` (runtime.rs:710-766) and returns its
-// decayed branch-sensitivity plane value (the caller adds the activation).
-__device__ __forceinline__ float advance_trace(float* planes, uint64_t plane, uint32_t* last, uint32_t slot,
-                                               uint32_t tick, const LeoConfig& cfg) {
-    // every plane in one round of loads
-    float bs = ld(&planes[slot]);
-    const float ms = ld(&planes[plane + slot]), fs = ld(&planes[2 * plane + slot]);
-    const float f0 = ld(&planes[3 * plane + slot]), f1 = ld(&planes[4 * plane + slot]), f2 = ld(&planes[5 * plane + slot]);
-    const uint32_t e = tick - ld(&last[slot]);
-    if (e == 0) return bs;
+// Coherent loads of a trace record's two quarters (the host limits the trace
+// arrays to below 2^32 bytes).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t trace_rsrc(const float LEO_GLOBAL* trace, uint64_t slots) {
+    return coherent_rsrc(trace, static_cast<uint32_t>(slots * kTraceWords * 4));
+}
+
+// Brings one trace slot to `tick` and adds `activation` to its branch
+// sensitivity (runtime.rs:710-766).
+__device__ __forceinline__ void activate_trace(float LEO_GLOBAL* trace, __amdgpu_buffer_rsrc_t rsrc, uint32_t slot,
+                                               uint32_t tick, float activation, const LeoConfig& cfg) {
+    static_assert(kTBranch == 0 && kTAdapt0 == 3 && kTEligibility == 6 && kTLast == 7, "trace layout");
+    const f32x4 q0 = ld16(rsrc, slot * (kTraceWords * 4)), q1 = ld16(rsrc, slot * (kTraceWords * 4) + 16);
+    f32x4 LEO_GLOBAL* rec = reinterpret_cast<f32x4 LEO_GLOBAL*>(trace + static_cast<uint64_t>(slot) * kTraceWords);
+    const uint32_t e = tick - __float_as_uint(q1.w);
+    if (e == 0) {
+        trace[static_cast<uint64_t>(slot) * kTraceWords + kTBranch] = q0.x + activation;
+        return;
+    }
     const StateDecays k = state_decays(cfg, e);
-    bs *= k.branch;
-    planes[plane + slot] = ms * k.membrane;
-    planes[2 * plane + slot] = fs * k.fatigue;
-    planes[3 * plane + slot] = f0 * k.fast;
-    planes[4 * plane + slot] = f1 * k.medium;
-    planes[5 * plane + slot] = f2 * k.slow;
-    last[slot] = tick;
-    return bs;
+    const float bs = q0.x * k.branch;
+    rec[0] = f32x4{bs + activation, q0.y * k.membrane, q0.z * k.fatigue, q0.w * k.fast};
+    rec[1] = f32x4{q1.x * k.medium, q1.y * k.slow, q1.z, __uint_as_float(tick)};
 }
 
 // Late fields of a step record: work counters complete only after the step's
@@ -610,16 +613,14 @@ __device__ __forceinline__ void deliver_commit(const StepCtx& c, const StepParam
     if (it.ring) {
         const float act = ld(&d.ring_act[it.rbase]);
         const uint64_t slot = it.slot + static_cast<uint64_t>(ld(&d.ring_active[it.rbase])) * S;
-        const float bs = advance_trace(d.rec_trace, NS, d.rec_last, static_cast<uint32_t>(slot), p.tick, cfg);
-        d.rec_trace[slot] = bs + act;
+        activate_trace(d.rec_trace, trace_rsrc(d.rec_trace, NS), static_cast<uint32_t>(slot), p.tick, act, cfg);
         if (ld(&d.rec_mark[slot]) != kMarkListed) {
             d.rec_mark[slot] = kMarkListed;
             new_rec = true;
             eslot = static_cast<uint32_t>(slot);
         }
     } else if (it.inj) {
-        const float bs = advance_trace(d.in_trace, NI, d.in_last, static_cast<uint32_t>(it.slot), p.tick, cfg);
-        d.in_trace[it.slot] = bs + 1.0f;
+        activate_trace(d.in_trace, trace_rsrc(d.in_trace, NI), static_cast<uint32_t>(it.slot), p.tick, 1.0f, cfg);
         if (ld(&d.in_mark[it.slot]) != kMarkListed) {
             d.in_mark[it.slot] = kMarkListed;
             new_in = true;
@@ -1412,12 +1413,11 @@ __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, 
 }
 
 // One eligible slot's update (runtime.rs:805-918) in parts, so that a lane
-// can keep the loads of two slots in flight together: the slot's trace planes
-// and last tick with the destination's touched and selected epochs, then --
-// only for a destination touched this tick (a few percent of the eligible
-// slots of a large model) -- the rest of the destination's state, then the
-// update and its stores. Each destination field lives in its own array, so a
-// load that is not needed would still fetch a whole cache line.
+// can keep the loads of two slots in flight together: the slot's trace record
+// (two 16-byte loads) with the destination's touched and selected epochs,
+// then -- only for a destination touched this tick (a few percent of the
+// eligible slots of a large model) -- the rest of the destination's state,
+// then the update and its two 16-byte stores.
 struct SlotInputs {
     float bs, ms, fs, as0, as1, as2, e;
     uint32_t last;
@@ -1425,16 +1425,16 @@ struct SlotInputs {
     float temporal, gate_acc, block_cut, membrane, threshold, excitability;
 };
 
-__device__ __forceinline__ void load_slot(SlotInputs& in, const float LEO_GLOBAL* planes, uint64_t plane,
-                                          const uint32_t LEO_GLOBAL* last, uint32_t slot) {
-    in.bs = ld(&planes[slot]);
-    in.ms = ld(&planes[plane + slot]);
-    in.fs = ld(&planes[2 * plane + slot]);
-    in.as0 = ld(&planes[3 * plane + slot]);
-    in.as1 = ld(&planes[4 * plane + slot]);
-    in.as2 = ld(&planes[5 * plane + slot]);
-    in.e = ld(&planes[6 * plane + slot]);
-    in.last = ld(&last[slot]);
+__device__ __forceinline__ void load_slot(SlotInputs& in, __amdgpu_buffer_rsrc_t rsrc, uint32_t slot) {
+    const f32x4 q0 = ld16(rsrc, slot * (kTraceWords * 4)), q1 = ld16(rsrc, slot * (kTraceWords * 4) + 16);
+    in.bs = q0.x;
+    in.ms = q0.y;
+    in.fs = q0.z;
+    in.as0 = q0.w;
+    in.as1 = q1.x;
+    in.as2 = q1.y;
+    in.e = q1.z;
+    in.last = __float_as_uint(q1.w);
 }
 
 // The destination's epochs: quarter 3 of its record.
@@ -1464,9 +1464,8 @@ __device__ __forceinline__ void load_destination(SlotInputs& in, const StepCtx& 
     in.excitability = c.a->m.excitability[dst];
 }
 
-__device__ __forceinline__ bool finish_slot(const StepCtx& c, const SlotInputs& in, float LEO_GLOBAL* planes,
-                                            uint64_t plane, uint32_t LEO_GLOBAL* last, uint32_t slot, uint8_t br,
-                                            float pop_cutoff) {
+__device__ __forceinline__ bool finish_slot(const StepCtx& c, const SlotInputs& in, float LEO_GLOBAL* trace,
+                                            uint32_t slot, uint8_t br, float pop_cutoff) {
     const LeoConfig& cfg = c.a->cfg;
     const uint32_t tick = c.tick;
     float bs = in.bs, ms = in.ms, fs = in.fs, as0 = in.as0, as1 = in.as1, as2 = in.as2;
@@ -1479,7 +1478,6 @@ __device__ __forceinline__ bool finish_slot(const StepCtx& c, const SlotInputs& 
         as0 *= k.fast;
         as1 *= k.medium;
         as2 *= k.slow;
-        last[slot] = tick;
     }
     const bool touched = in.touched_epoch == tick + 1;
     const bool selected = in.selected_epoch == tick + 1;
@@ -1503,13 +1501,10 @@ __device__ __forceinline__ bool finish_slot(const StepCtx& c, const SlotInputs& 
         as1 += cfg.adaptation_medium_gain * elig;
         as2 += cfg.adaptation_slow_gain * elig;
     }
-    planes[slot] = bs;
-    planes[plane + slot] = ms;
-    planes[2 * plane + slot] = fs;
-    planes[3 * plane + slot] = as0;
-    planes[4 * plane + slot] = as1;
-    planes[5 * plane + slot] = as2;
-    planes[6 * plane + slot] = elig;
+    // the record in two 16-byte stores (the last tick moves only when it was behind)
+    f32x4 LEO_GLOBAL* rec = reinterpret_cast<f32x4 LEO_GLOBAL*>(trace + static_cast<uint64_t>(slot) * kTraceWords);
+    rec[0] = f32x4{bs, ms, fs, as0};
+    rec[1] = f32x4{as1, as2, elig, __uint_as_float(el > 0 ? tick : in.last)};
     float mag = maxnum(maxnum(maxnum(fabsf(bs), fabsf(ms)), fabsf(fs)), fabsf(elig));
     mag = maxnum(mag, fabsf(as0));
     mag = maxnum(mag, fabsf(as1));
@@ -1535,12 +1530,13 @@ __device__ __forceinline__ void wave_append2(uint32_t LEO_GLOBAL* counter, bool 
 
 // Eligible slots of one list, two per lane per iteration (their loads in
 // flight together); kept slots are compacted into the next list.
-__device__ __forceinline__ void eligibility_list(const StepCtx& c, float LEO_GLOBAL* planes, uint64_t plane,
-                                                 uint32_t LEO_GLOBAL* last, uint8_t LEO_GLOBAL* marks,
+__device__ __forceinline__ void eligibility_list(const StepCtx& c, float LEO_GLOBAL* trace, uint64_t slots,
+                                                 uint8_t LEO_GLOBAL* marks,
                                                  const uint32_t LEO_GLOBAL* cur, uint32_t cur_n,
                                                  uint32_t LEO_GLOBAL* next, uint32_t LEO_GLOBAL* next_count,
                                                  const uint32_t* targets, const uint8_t* branches, float pop_cutoff) {
     const uint32_t lane = __lane_id();
+    const __amdgpu_buffer_rsrc_t rsrc = trace_rsrc(trace, slots);
     for (uint32_t base = c.gtid - lane; base < cur_n; base += 2 * c.gstride) {
         const uint32_t i0 = base + lane, i1 = base + c.gstride + lane;
         const bool v0 = i0 < cur_n, v1 = i1 < cur_n;
@@ -1552,19 +1548,19 @@ __device__ __forceinline__ void eligibility_list(const StepCtx& c, float LEO_GLO
         if (v0) {
             t0 = targets[s0];
             r0 = branches[s0];
-            load_slot(a0, planes, plane, last, s0);
+            load_slot(a0, rsrc, s0);
         }
         if (v1) {
             t1 = targets[s1];
             r1 = branches[s1];
-            load_slot(a1, planes, plane, last, s1);
+            load_slot(a1, rsrc, s1);
         }
         if (v0) load_epochs(a0, c, t0);
         if (v1) load_epochs(a1, c, t1);
         if (v0 && a0.touched_epoch == c.tick + 1) load_destination(a0, c, t0);
         if (v1 && a1.touched_epoch == c.tick + 1) load_destination(a1, c, t1);
-        const bool k0 = v0 && finish_slot(c, a0, planes, plane, last, s0, r0, pop_cutoff);
-        const bool k1 = v1 && finish_slot(c, a1, planes, plane, last, s1, r1, pop_cutoff);
+        const bool k0 = v0 && finish_slot(c, a0, trace, s0, r0, pop_cutoff);
+        const bool k1 = v1 && finish_slot(c, a1, trace, s1, r1, pop_cutoff);
         if (v0 && !k0) marks[s0] = kMarkDropped;
         if (v1 && !k1) marks[s1] = kMarkDropped;
         uint32_t p0, p1;
@@ -1587,9 +1583,9 @@ __device__ __forceinline__ void phase_eligibility(const StepCtx& c) {
         c.ctl->tick_scan_in[c.tick & 1] = in_n;
     }
     const float pop_cutoff = a.redundant_global ? 0.0f : ld(&c.ctl->pop_cutoff);
-    eligibility_list(c, d.rec_trace, NS, d.rec_last, d.rec_mark, d.rec_list + p * NS, rec_n, d.rec_list + q * NS,
+    eligibility_list(c, d.rec_trace, NS, d.rec_mark, d.rec_list + p * NS, rec_n, d.rec_list + q * NS,
                      &c.ctl->rec_count[q], a.m.rec_target, a.m.rec_branch, pop_cutoff);
-    eligibility_list(c, d.in_trace, NI, d.in_last, d.in_mark, d.in_list + p * NI, in_n, d.in_list + q * NI,
+    eligibility_list(c, d.in_trace, NI, d.in_mark, d.in_list + p * NI, in_n, d.in_list + q * NI,
                      &c.ctl->in_count[q], a.m.in_target, a.m.in_branch, pop_cutoff);
 }
 
@@ -2052,7 +2048,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
                 const uint32_t slot = ld(&rec_cur[i]);
                 const uint32_t dst = a.m.rec_target[slot];
                 const uint32_t src = fast_div(slot, a.div_synapses);
-                const float e = ld(&d.rec_trace[6 * NS + slot]);
+                const float e = ld(&d.rec_trace[static_cast<uint64_t>(slot) * kTraceWords + kTEligibility]);
                 const float gradient = ld(&d.learning_signal[dst]) * e;
                 const float delta = bounded(-lr * cs * gradient, mu);
                 const float old_w = ld(&d.p.rec_weight[slot]);
@@ -2076,7 +2072,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
             for (uint32_t i = c.gtid; i < in_n; i += c.gstride) {
                 const uint32_t slot = ld(&in_cur[i]);
                 const uint32_t dst = a.m.in_target[slot];
-                const float e = ld(&d.in_trace[6 * NI + slot]);
+                const float e = ld(&d.in_trace[static_cast<uint64_t>(slot) * kTraceWords + kTEligibility]);
                 const float gradient = ld(&d.learning_signal[dst]) * e;
                 const float delta = bounded(-lr * cs * gradient, mu);
                 const float old_w = ld(&d.p.in_weight[slot]);
@@ -2324,10 +2320,10 @@ __global__ void __launch_bounds__(kThreads) leo_lane_steps_profiled(const Kernel
 // Recurrent trace slots are cleared from their marks: a slot whose mark is 0
 // has not been written since the last reset, so its seven values are still
 // zero (1 = listed as eligible, 2 = dropped from the list with its values
-// kept). Every group of 16 slots with a nonzero mark is zeroed whole with
-// vector stores; a clean slot keeps its last tick, which only scales zeros,
-// unless the tick is set (a new tick may lie below it, so every last tick is
-// rewritten).
+// kept). Every group of 16 slots with a nonzero mark has its 16 trace
+// records (512 contiguous bytes) rewritten; a clean slot keeps its last tick,
+// which only scales zeros, unless the tick is set (a new tick may lie below
+// it, so every record is rewritten).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void fill_u32(uint32_t LEO_GLOBAL* p, uint64_t n, uint32_t v, uint64_t t0, uint64_t ts) {
     // p is 256-byte aligned (lane-state layout)
@@ -2342,30 +2338,20 @@ __device__ __forceinline__ void fill_f32(float LEO_GLOBAL* p, uint64_t n, uint64
     fill_u32(reinterpret_cast<uint32_t LEO_GLOBAL*>(p), n, 0u, t0, ts);
 }
 
-__device__ __forceinline__ void clear_trace_group(const LaneDesc& d, uint64_t NS, uint64_t g, uint32_t tick,
-                                                  bool set_tick) {
+__device__ __forceinline__ void clear_trace_group(const LaneDesc& d, uint64_t g, uint32_t tick, bool set_tick) {
     uint4 LEO_GLOBAL* marks = reinterpret_cast<uint4 LEO_GLOBAL*>(d.rec_mark);
     const uint4 m = marks[g];  // a launch of its own: plain loads see the previous kernels' stores
-    const uint4 zero = make_uint4(0u, 0u, 0u, 0u), t = make_uint4(tick, tick, tick, tick);
-    uint4 LEO_GLOBAL* last = reinterpret_cast<uint4 LEO_GLOBAL*>(d.rec_last + 16 * g);
     const bool dirty = (m.x | m.y | m.z | m.w) != 0u;
-    if (dirty) {
+    if (!dirty && !set_tick) return;
+    // 16 records of 32 bytes: zero sensitivities, last tick = tick
+    uint4 LEO_GLOBAL* rec = reinterpret_cast<uint4 LEO_GLOBAL*>(d.rec_trace + 16 * g * kTraceWords);
+    const uint4 zero = make_uint4(0u, 0u, 0u, 0u), with_tick = make_uint4(0u, 0u, 0u, tick);
 #pragma unroll
-        for (uint64_t p = 0; p < 7; ++p) {
-            uint4 LEO_GLOBAL* plane = reinterpret_cast<uint4 LEO_GLOBAL*>(d.rec_trace + p * NS + 16 * g);
-            plane[0] = zero;
-            plane[1] = zero;
-            plane[2] = zero;
-            plane[3] = zero;
-        }
-        marks[g] = zero;
+    for (uint32_t k = 0; k < 16; ++k) {
+        rec[2 * k] = zero;
+        rec[2 * k + 1] = with_tick;
     }
-    if (dirty || set_tick) {
-        last[0] = t;
-        last[1] = t;
-        last[2] = t;
-        last[3] = t;
-    }
+    if (dirty) marks[g] = zero;
 }
 
 __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uint32_t set_tick, uint32_t new_tick) {
@@ -2387,16 +2373,19 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
         for (uint64_t i = t0; i < 4 * N; i += ts) rec[i] = (i & 3) == 2 ? with_tick : zero;
     }
     const uint64_t groups = NS / 16;
-    for (uint64_t g = t0; g < groups; g += ts) clear_trace_group(d, NS, g, tick, set_tick != 0);
+    for (uint64_t g = t0; g < groups; g += ts) clear_trace_group(d, g, tick, set_tick != 0);
+    auto clear_record = [&](float LEO_GLOBAL* trace, uint64_t i) {
+        uint4 LEO_GLOBAL* rec = reinterpret_cast<uint4 LEO_GLOBAL*>(trace + i * kTraceWords);
+        rec[0] = make_uint4(0u, 0u, 0u, 0u);
+        rec[1] = make_uint4(0u, 0u, 0u, tick);
+    };
     for (uint64_t i = 16 * groups + t0; i < NS; i += ts) {
         if (d.rec_mark[i] != 0 || set_tick) {
-            for (uint64_t p = 0; p < 7; ++p) d.rec_trace[p * NS + i] = 0.0f;
-            d.rec_last[i] = tick;
+            clear_record(d.rec_trace, i);
             d.rec_mark[i] = 0;
         }
     }
-    fill_f32(d.in_trace, 7 * NI, t0, ts);
-    fill_u32(d.in_last, NI, tick, t0, ts);
+    for (uint64_t i = t0; i < NI; i += ts) clear_record(d.in_trace, i);
     for (uint64_t i = t0; i < NI; i += ts) d.in_mark[i] = 0;
     for (uint64_t i = t0; i < cfg.context_embedding_dim; i += ts) d.ctx_latent[i] = 0.0f;
     fill_u32(d.block_epoch, cfg.block_count, 0u, t0, ts);

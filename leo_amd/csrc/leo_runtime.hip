@@ -282,8 +282,8 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     size_t o_bep = l.add<uint32_t>(z.blocks), o_tb = l.add<uint32_t>(z.blocks * z.block_words);
     size_t o_ra = l.add<uint32_t>(kRing * z.cap), o_rv = l.add<float>(kRing * z.cap), o_rval = l.add<float>(kRing * z.cap * z.s);
     size_t o_redge = l.add<uint32_t>(kRing * z.cap * z.s);
-    size_t o_rt = l.add<float>(7 * z.ns), o_rl = l.add<uint32_t>(z.ns), o_rm = l.add<uint8_t>(z.ns), o_rlist = l.add<uint32_t>(2 * z.ns);
-    size_t o_it = l.add<float>(7 * z.ni), o_il = l.add<uint32_t>(z.ni), o_im = l.add<uint8_t>(z.ni), o_ilist = l.add<uint32_t>(2 * z.ni);
+    size_t o_rt = l.add<float>(kTraceWords * z.ns), o_rm = l.add<uint8_t>(z.ns), o_rlist = l.add<uint32_t>(2 * z.ns);
+    size_t o_it = l.add<float>(kTraceWords * z.ni), o_im = l.add<uint8_t>(z.ni), o_ilist = l.add<uint32_t>(2 * z.ni);
     size_t o_lg = l.add<float>(kOutStride), o_pr = l.add<float>(kOutStride), o_er = l.add<float>(kOutStride);
     size_t o_lat = l.add<float>(std::max<uint64_t>(z.e, 1));
     size_t o_cth = l.add<uint32_t>(z.words(z.n)), o_crec = l.add<uint32_t>(z.words(z.ns)), o_cin = l.add<uint32_t>(z.words(z.ni));
@@ -310,11 +310,9 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     d.ring_value = reinterpret_cast<float*>(b + o_rval);
     d.ring_edge = reinterpret_cast<uint32_t*>(b + o_redge);
     d.rec_trace = reinterpret_cast<float*>(b + o_rt);
-    d.rec_last = reinterpret_cast<uint32_t*>(b + o_rl);
     d.rec_mark = reinterpret_cast<uint8_t*>(b + o_rm);
     d.rec_list = reinterpret_cast<uint32_t*>(b + o_rlist);
     d.in_trace = reinterpret_cast<float*>(b + o_it);
-    d.in_last = reinterpret_cast<uint32_t*>(b + o_il);
     d.in_mark = reinterpret_cast<uint8_t*>(b + o_im);
     d.in_list = reinterpret_cast<uint32_t*>(b + o_ilist);
     d.logits = reinterpret_cast<float*>(b + o_lg);
@@ -1435,6 +1433,10 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         leo::model_validate(*config, *model);
         if (static_cast<uint64_t>(config->device.neuron_count) * config->device.synapses_per_neuron >= (1ull << 31))
             throw Error(LEO_ERR_UNSUPPORTED, "neuron_count * synapses_per_neuron at or above 2^31 is not supported");
+        // trace records are read with 32-bit buffer offsets
+        if (static_cast<uint64_t>(config->device.neuron_count) * config->device.synapses_per_neuron * leo::kTraceWords * 4 >=
+            (1ull << 32))
+            throw Error(LEO_ERR_UNSUPPORTED, "recurrent trace records at or above 4 GiB per lane are not supported");
         if (config->device.neuron_count > leo::kMaxPackedNeurons)
             throw Error(LEO_ERR_UNSUPPORTED, "neuron_count above 2^28 is not supported by the packed synapse layout");
         if (config->device.neurons_per_block > leo::kMaxBlockNeurons)
@@ -1800,12 +1802,17 @@ int32_t leo_hip_read_state(LeoHipRuntime* h, int32_t which, float* out, uint64_t
         uint64_t n = 0;
         // per-neuron state: `words` consecutive words of each neuron's record
         uint32_t field = 0, words = 0;
-        if (which >= LEO_STATE_REC_BS && which <= LEO_STATE_REC_E) {
-            src = d.rec_trace + static_cast<uint64_t>(which - LEO_STATE_REC_BS) * z.ns;
-            n = z.ns;
-        } else if (which >= LEO_STATE_IN_BS && which <= LEO_STATE_IN_E) {
-            src = d.in_trace + static_cast<uint64_t>(which - LEO_STATE_IN_BS) * z.ni;
-            n = z.ni;
+        if ((which >= LEO_STATE_REC_BS && which <= LEO_STATE_REC_E) || (which >= LEO_STATE_IN_BS && which <= LEO_STATE_IN_E)) {
+            // one word of each slot's trace record
+            const bool rec = which <= LEO_STATE_REC_E;
+            const uint64_t slots = rec ? z.ns : z.ni;
+            const uint32_t word = static_cast<uint32_t>(which - (rec ? LEO_STATE_REC_BS : LEO_STATE_IN_BS));
+            if (count != slots) throw Error(LEO_ERR_INVALID_ARGUMENT, "state size mismatch: expected " + std::to_string(slots));
+            std::vector<float> all(slots * leo::kTraceWords);
+            leo::download(all.data(), rec ? d.rec_trace : d.in_trace, all.size() * 4, h->stream);
+            leo::sync(h->stream);
+            for (uint64_t i = 0; i < slots; ++i) out[i] = all[i * leo::kTraceWords + word];
+            return;
         } else {
             switch (which) {
                 case LEO_STATE_MEMBRANE: field = leo::kNMembrane; words = 1; break;
