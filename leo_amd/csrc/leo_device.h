@@ -143,6 +143,7 @@ struct LaneControl {
     uint32_t rec_count[2];
     uint32_t in_count[2];
     uint32_t dest_epoch;             // learning-destination epoch
+    uint32_t dest_count;             // entries of this step's destination list
     uint32_t history_len;
     uint32_t history[kMaxOrder];
     uint32_t ctx_count;
@@ -225,6 +226,7 @@ struct LaneDesc {
     uint32_t LEO_GLOBAL* neuron;
     uint32_t LEO_GLOBAL* touched_list;  // N: per selecting wave, its range's touched neurons (see wave_touched)
     float LEO_GLOBAL* learning_signal;
+    uint32_t LEO_GLOBAL* dest_list;     // N: this step's claimed learning destinations (LaneControl dest_count)
     uint64_t LEO_GLOBAL* bucket;        // 2 words per entry: delivery-order key, value bits
     // block selection
     uint32_t LEO_GLOBAL* range_winners; // blocks * max_active_per_block: winners of each selecting wave's block

@@ -1732,6 +1732,44 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
     __syncthreads();
 }
 
+// Learning destinations of this step (runtime.rs:1214-1243): the targets of
+// the eligible recurrent and input slots and the active neurons, each claimed
+// once with an epoch exchange and listed (one append per wave). They need no
+// errors, so the workgroups that do not compute the readout claim them in
+// the readout's phase.
+__device__ __forceinline__ void signal_claims(const StepCtx& c) {
+    const KernelArgs& a = *c.a;
+    const LaneDesc& d = c.d;
+    const LeoConfig& cfg = a.cfg;
+    const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * cfg.synapses_per_neuron;
+    const uint64_t NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
+    const uint32_t rec_n = ld(&c.ctl->rec_count[c.parity]), in_n = ld(&c.ctl->in_count[c.parity]);
+    const uint32_t A = ld(&c.ctl->active_count);
+    const uint32_t rs = c.tick % kRing;
+    const uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cfg.max_active_global;
+    const uint32_t* rec_cur = d.rec_list + c.parity * NS;
+    const uint32_t* in_cur = d.in_list + c.parity * NI;
+    const uint32_t total = rec_n + in_n + A;
+    const uint32_t lane = __lane_id();
+    const uint32_t workers = c.P > 1 ? c.P - 1 : 1;
+    uint32_t claimed = 0;
+    for (uint32_t base = c.part * kThreads + threadIdx.x - lane; base < total; base += workers * kThreads) {
+        const uint32_t item = base + lane;
+        bool won = false;
+        uint32_t dst = 0;
+        if (item < total) {
+            if (item < rec_n) dst = a.m.rec_target[ld(&rec_cur[item])];
+            else if (item < rec_n + in_n) dst = a.m.in_target[ld(&in_cur[item - rec_n])];
+            else dst = ld(&act_list[item - rec_n - in_n]);
+            won = atomicExch(nu(d, dst, kNDestEpoch), c.dest_epoch) != c.dest_epoch;
+        }
+        const uint32_t pos = wave_append(&c.ctl->dest_count, won);
+        if (won) d.dest_list[pos] = dst;
+        claimed += won ? 1u : 0u;
+    }
+    add_count(&c.ctl->tick_dest[c.tick & 1], claimed);
+}
+
 __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step_index, StepShared& sh) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
@@ -1800,6 +1838,7 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
             readout(c, sp, sh, step_index);
         }
     }
+    if ((sp.flags & kStepLearn) && sp.plasticity_scale > 0.0f && (c.part < readout_wg || c.P == 1)) signal_claims(c);
 }
 
 // ---------------------------------------------------------------------------
@@ -1865,60 +1904,25 @@ __device__ __forceinline__ float signal_rows(__amdgpu_buffer_rsrc_t rows, uint32
     return acc;
 }
 
+// The listed destinations' signals (runtime.rs:1245-1250), 64 at a time per
+// wave, the batches dealt round-robin over every wave of the lane.
 __device__ __forceinline__ void phase_signals(const StepCtx& c, StepShared& sh) {
-    const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
-    const LeoConfig& cfg = a.cfg;
-    const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * cfg.synapses_per_neuron;
-    const uint64_t NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
+    const LeoConfig& cfg = c.a->cfg;
     for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = ld(&d.errors[o]);
     __syncthreads();
-    const uint32_t rec_n = ld(&c.ctl->rec_count[c.parity]), in_n = ld(&c.ctl->in_count[c.parity]);
-    const uint32_t A = ld(&c.ctl->active_count);
-    const uint32_t rs = c.tick % kRing;
-    const uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cfg.max_active_global;
-    const uint32_t* rec_cur = d.rec_list + c.parity * NS;
-    const uint32_t* in_cur = d.in_list + c.parity * NI;
-    const uint32_t total = rec_n + in_n + A;
+    const uint32_t count = ld(&c.ctl->dest_count);
     const uint32_t wave = wave_index(), lane = __lane_id();
-    const unsigned long long below = (1ULL << lane) - 1ULL;
-    uint32_t* queue = sh.queue[wave];
-    uint32_t queued = 0, claimed = 0;
+    const uint32_t waves = c.P * kWavesPerGroup;
     // the host limits N * kOutStride * 4 to below 2^31 bytes
     const __amdgpu_buffer_rsrc_t rows = coherent_rsrc(d.p.out_w, cfg.neuron_count * kOutStride * 4);
     float* stage = reinterpret_cast<float*>(step_lds + static_cast<size_t>(wave) * wave_lds_bytes(cfg.neurons_per_block));
-    // claimed destinations are queued per wave and computed 64 at a time, one row per lane
-    for (uint32_t base = c.gtid - lane; base < total; base += c.gstride) {
-        const uint32_t item = base + lane;
-        bool won = false;
-        uint32_t dst = 0;
-        if (item < total) {
-            if (item < rec_n) dst = a.m.rec_target[ld(&rec_cur[item])];
-            else if (item < rec_n + in_n) dst = a.m.in_target[ld(&in_cur[item - rec_n])];
-            else dst = ld(&act_list[item - rec_n - in_n]);
-            won = atomicExch(nu(d, dst, kNDestEpoch), c.dest_epoch) != c.dest_epoch;
-        }
-        const unsigned long long mask = __ballot(won);
-        if (won) queue[queued + __popcll(mask & below)] = dst;
-        queued += static_cast<uint32_t>(__popcll(mask));
-        claimed += won ? 1u : 0u;
-        if (queued >= kWaveSize) {
-            wave_sync();
-            const uint32_t mine = queue[lane];
-            const uint32_t rest = lane + kWaveSize < queued ? queue[lane + kWaveSize] : 0u;
-            wave_sync();
-            if (lane + kWaveSize < queued) queue[lane] = rest;
-            queued -= kWaveSize;
-            d.learning_signal[mine] = signal_rows(rows, mine, kWaveSize, sh.err, stage);
-        }
+    for (uint32_t b = c.part * kWavesPerGroup + wave; b * kWaveSize < count; b += waves) {
+        const uint32_t n = min(kWaveSize, count - b * kWaveSize);
+        const uint32_t dst = lane < n ? ld(&d.dest_list[b * kWaveSize + lane]) : 0u;
+        const float sig = signal_rows(rows, dst, n, sh.err, stage);
+        if (lane < n) d.learning_signal[dst] = sig;
     }
-    wave_sync();
-    if (queued > 0) {
-        const uint32_t mine = lane < queued ? queue[lane] : 0u;
-        const float sig = signal_rows(rows, mine, queued, sh.err, stage);
-        if (lane < queued) d.learning_signal[mine] = sig;
-    }
-    add_count(&c.ctl->tick_dest[c.tick & 1], claimed);
 }
 
 // ---------------------------------------------------------------------------
@@ -2251,6 +2255,8 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             // the previous step's write_active has rolled this tick's counters
             atomicAdd(&c.ctl->tick_events[c.tick & 1], pending_events);
         }
+        // this step's destination list starts empty (filled in the post phase)
+        if (learn && c.part == 0 && threadIdx.x == 0) c.ctl->dest_count = 0;
         // the context of a step delivered ahead: on the workgroup that owns no
         // selection blocks, beside the fold (first read by the readout)
         if (delivered_ahead && c.P > 1 && c.part == c.P - 1) context_resolve(c, sp, sh);
@@ -2280,13 +2286,14 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             }
         }
         if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 2))) break;
+        const bool plastic = learn && sp.plasticity_scale > 0.0f;
         if (!fused) {
             if (trace) c.parity ^= 1;
+            if (plastic) c.dest_epoch += 1;  // the destinations are claimed in the post phase
             phase_post(c, sp, s, sh);
             if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 3))) break;
         }
-        if (learn && sp.plasticity_scale > 0.0f) {
-            c.dest_epoch += 1;
+        if (plastic) {
             phase_signals(c, sh);
             if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 4))) break;
         }

@@ -275,7 +275,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     Layout l;
     size_t o_ctl = l.add<LaneControl>(1);
     size_t o_neu = l.add<uint32_t>(kNeuronWords * z.n), o_tl = l.add<uint32_t>(z.n);
-    size_t o_ls = l.add<float>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
+    size_t o_ls = l.add<float>(z.n), o_dl = l.add<uint32_t>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
     size_t o_bw = l.add<uint32_t>(z.blocks * z.limit), o_bcut = l.add<float>(z.blocks);
     size_t o_bwa = l.add<float>(z.blocks * z.limit);
     size_t o_wt = l.add<uint32_t>(kMaxWaves), o_wtt = l.add<uint32_t>(kMaxWaves);
@@ -297,6 +297,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     d.touched_list = reinterpret_cast<uint32_t*>(b + o_tl);
 
     d.learning_signal = reinterpret_cast<float*>(b + o_ls);
+    d.dest_list = reinterpret_cast<uint32_t*>(b + o_dl);
     d.bucket = reinterpret_cast<uint64_t*>(b + o_bk);
     d.range_winners = reinterpret_cast<uint32_t*>(b + o_bw);
     d.range_winner_act = reinterpret_cast<float*>(b + o_bwa);
