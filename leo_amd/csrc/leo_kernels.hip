@@ -347,6 +347,10 @@ struct alignas(16) StepShared {
     // this workgroup's copy of the emission ring bookkeeping (LaneControl ring_*)
     uint32_t ring_tick[kRing];
     uint32_t ring_count[kRing];
+    // each selecting wave's winner count and first 64 winners (phase 2 to 3)
+    uint32_t win_count[kWavesPerGroup];
+    uint32_t win_n[kWavesPerGroup][kWaveSize];
+    float win_act[kWavesPerGroup][kWaveSize];
 };
 
 // Dynamic LDS (step_lds_bytes): one phase-2 window per wave (Window below);
@@ -977,7 +981,7 @@ __device__ __forceinline__ Window wave_window(uint32_t wave, uint32_t nb) {
 // 1010-1013), compacted from the range's first block row, so that phase 3
 // reads them in one round. A group with more touched neurons than the window
 // holds is taken in windows of whole blocks.
-__device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
+__device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& sh) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -1093,9 +1097,14 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
                 if (rank < limit) {
                     const uint32_t n = add_mod(static_cast<uint32_t>(mine), rot, N);
                     const float act = key_activation(mine);
-                    const uint64_t at = row0 + w.woff[g] + rank;
+                    const uint32_t k = w.woff[g] + rank;  // staged position in the wave's range
+                    const uint64_t at = row0 + k;
                     d.range_winners[at] = n;
                     d.range_winner_act[at] = act;
+                    if (k < kWaveSize) {  // kept for phase 3 in the wave's LDS
+                        sh.win_n[wave][k] = n;
+                        sh.win_act[wave][k] = act;
+                    }
                     if (a.redundant_global) {  // the global cap cannot bind (runtime.rs:1060-1067)
                         (*nf(d, n, kNActivation)) = act;
                         (*nu(d, n, kNSelected)) = tick + 1;
@@ -1123,6 +1132,7 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c) {
     supra = wave_sum_u32(supra);
     if (lane == 0) {
         if (supra) atomicAdd(&c.ctl->tick_supra[tick & 1], supra);
+        sh.win_count[wave] = staged;
         d.wave_total[wv] = staged;
         d.wave_touched[wv] = listed_before;
     }
@@ -1154,11 +1164,10 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     const uint32_t wv = c.part * kWavesPerGroup + wave;
     const uint32_t range = (cfg.block_count + nwaves - 1) / nwaves;
     const uint32_t rs = c.tick % kRing;
-    const uint32_t b0 = min(cfg.block_count, wv * range), b1 = min(cfg.block_count, b0 + range);
+    const uint32_t b0 = min(cfg.block_count, wv * range);
     const uint64_t row0 = static_cast<uint64_t>(b0) * limit;
-    const uint32_t slots = (b1 - b0) * limit;
-    // round 1: the per-wave totals, the first 64 staged winners of this
-    // wave's range, and this thread's first item of the next tick
+    // round 1: the per-wave totals, this wave's winners' state and first
+    // synapses, and this thread's first item of the next tick
     // the recording thread's loads go out in the same round; it runs on the
     // workgroup that selects nothing (the least work in this phase)
     const bool recorder = c.part == c.P - 1 && threadIdx.x == 0;
@@ -1184,13 +1193,39 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     const bool deliver_next = ahead && np.delivers;
     DeliverItem item0 = deliver_fetch(c, next, np, deliver_next ? c.gtid : np.total);
     if (ahead) reset_next_lists(c);
-    uint32_t first_n = 0;
-    float first_act = 0.0f;
-    if (lane < slots) {
-        first_n = ld(&d.range_winners[row0 + lane]);
-        first_act = ld(&d.range_winner_act[row0 + lane]);
+    // this wave's winners are in its LDS since phase 2: their state and
+    // synapses are loaded in the same round as the totals
+    const uint32_t mine = sh.win_count[wave];
+    const uint32_t first_n = lane < mine ? sh.win_n[wave][lane] : 0u;
+    const float first_act = lane < mine ? sh.win_act[wave][lane] : 0.0f;
+    const uint32_t S = cfg.synapses_per_neuron, N = cfg.neuron_count;
+    const uint32_t items = mine * S;
+    const bool pf = fuse_post && lane < mine, sn = fuse_post && lane < items;
+    float fat = 0.0f, ad0 = 0.0f, ad1 = 0.0f, ad2 = 0.0f, mem = 0.0f, thr = 0.0f;
+    uint8_t type = 0;
+    if (pf) {
+        // quarters 0 and 1 of the record: membrane, fatigue, adaptations
+        const __amdgpu_buffer_rsrc_t rec = neuron_rsrc(d, N);
+        const f32x4 q0 = ld_quarter(rec, first_n, 0), q1 = ld_quarter(rec, first_n, 1);
+        mem = q0.x;
+        fat = q0.z;
+        ad0 = q0.w;
+        ad1 = q1.x;
+        ad2 = q1.y;
+        thr = ld(&d.p.threshold[first_n]);
+        type = c.a->m.neuron_type[first_n];
     }
-    const uint32_t mine = ld(&d.wave_total[wv]);
+    uint32_t r0 = 0, j0 = 0, edge0 = 0;
+    float act0 = 0.0f, weight0 = 0.0f;
+    if (sn) {
+        r0 = fast_div(lane, c.a->div_synapses);
+        j0 = lane - r0 * S;
+        const uint32_t n = sh.win_n[wave][r0];
+        act0 = sh.win_act[wave][r0];
+        const uint64_t slot = static_cast<uint64_t>(n) * S + j0;
+        weight0 = ld(&d.p.rec_weight[slot]);
+        edge0 = c.a->m.rec_edge[slot];
+    }
     uint32_t before = 0, all = 0;
     for (uint32_t base = 0; base < nwaves; base += kWaveSize) {
         const uint32_t w = base + lane;
@@ -1243,14 +1278,8 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     // Post-fire updates of this wave's winners and their emission snapshots
     // (the post phase, runtime.rs:920-938, 1084-1106), folded in here when no
     // eligibility update or readout of this step reads the state in between.
-    // The wave's first 64 winners are shared through its phase-2 LDS window.
-    const uint32_t S = cfg.synapses_per_neuron, N = cfg.neuron_count;
-    const Window w = wave_window(wave, cfg.neurons_per_block);
-    w.entry[lane] = first_n;
-    w.pos[lane] = __float_as_uint(first_act);
-    wave_sync();
+    // The wave's first 64 winners are in its LDS since phase 2.
     const uint32_t refractory = c.tick + cfg.refractory_ticks + 1;
-    const uint32_t items = mine * S;
     uint32_t inhibitory = 0, delivered = 0;
     auto post_fire = [&](uint32_t n, float act, float fat, float ad0, float ad1, float ad2, float mem, float thr,
                          uint8_t type) {
@@ -1280,34 +1309,8 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
             delivered += 1;
         }
     };
-    // round 2: the first winner and synapse of each lane, and the bucket
-    // increment of this thread's first next-tick item
-    const bool pf = lane < mine, sn = lane < items;
-    float fat = 0.0f, ad0 = 0.0f, ad1 = 0.0f, ad2 = 0.0f, mem = 0.0f, thr = 0.0f;
-    uint8_t type = 0;
-    if (pf) {
-        // quarters 0 and 1 of the record: membrane, fatigue, adaptations
-        const __amdgpu_buffer_rsrc_t rec = neuron_rsrc(d, N);
-        const f32x4 q0 = ld_quarter(rec, first_n, 0), q1 = ld_quarter(rec, first_n, 1);
-        mem = q0.x;
-        fat = q0.z;
-        ad0 = q0.w;
-        ad1 = q1.x;
-        ad2 = q1.y;
-        thr = ld(&d.p.threshold[first_n]);
-        type = c.a->m.neuron_type[first_n];
-    }
-    uint32_t r0 = 0, j0 = 0, edge0 = 0;
-    float act0 = 0.0f, weight0 = 0.0f;
-    if (sn) {
-        r0 = fast_div(lane, c.a->div_synapses);
-        j0 = lane - r0 * S;
-        const uint32_t n = w.entry[r0];
-        act0 = __uint_as_float(w.pos[r0]);
-        const uint64_t slot = static_cast<uint64_t>(n) * S + j0;
-        weight0 = ld(&d.p.rec_weight[slot]);
-        edge0 = c.a->m.rec_edge[slot];
-    }
+    // round 2: the bucket increment of this thread's first next-tick item
+    // (the winners' state and first synapses are loaded with the totals)
     if (deliver_next) deliver_commit(c, next, np, item0, delivered);
     // round 3: the delay-1 bucket increments
     if (pf) post_fire(first_n, first_act, fat, ad0, ad1, ad2, mem, thr, type);
@@ -1321,8 +1324,8 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     }
     for (uint32_t item = lane + kWaveSize; item < items; item += kWaveSize) {
         const uint32_t r = fast_div(item, c.a->div_synapses), j = item - r * S;
-        const uint32_t n = r < kWaveSize ? w.entry[r] : ld(&d.range_winners[row0 + r]);
-        const float act = r < kWaveSize ? __uint_as_float(w.pos[r]) : ld(&d.range_winner_act[row0 + r]);
+        const uint32_t n = r < kWaveSize ? sh.win_n[wave][r] : ld(&d.range_winners[row0 + r]);
+        const float act = r < kWaveSize ? sh.win_act[wave][r] : ld(&d.range_winner_act[row0 + r]);
         const uint64_t slot = static_cast<uint64_t>(n) * S + j;
         snapshot(r, j, act, ld(&d.p.rec_weight[slot]), c.a->m.rec_edge[slot]);
     }
@@ -1780,7 +1783,6 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
     const uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
     const float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
     const uint32_t total = A + A * S;
-    const uint32_t N = cfg.neuron_count;
     const uint32_t refractory = c.tick + cfg.refractory_ticks + 1;
     uint32_t inhibitory = 0;
     for (uint32_t item = c.gtid; item < total; item += c.gstride) {
@@ -2260,7 +2262,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         // the context of a step delivered ahead: on the workgroup that owns no
         // selection blocks, beside the fold (first read by the readout)
         if (delivered_ahead && c.P > 1 && c.part == c.P - 1) context_resolve(c, sp, sh);
-        phase_fold_select(c);
+        phase_fold_select(c, sh);
         if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 1))) break;
         // a fused step followed by a frozen one starts the next tick in its
         // last phase: the next delivery runs before this step's closing
