@@ -219,6 +219,27 @@ def test_chunked_launches_and_agent_barriers_parity(require_gpu, oracle, monkeyp
 
 
 @pytest.mark.parametrize("wgs", ["1", "2"])
+def test_replay_with_few_workgroups_parity(require_gpu, oracle, monkeypatch, wgs):
+    # one workgroup per lane (selection, context and readout on the same
+    # workgroup) and two (one selecting, one resolving the context): the
+    # frozen replay prefixes run the fused steps that start the next tick
+    # early on both layouts
+    monkeypatch.setenv("LEO_HIP_WGS_PER_LANE", wgs)
+    model = Model.initialize(small_redundant_config())
+    cpu = oracle.OracleRuntime(model)
+    gpu = _runtime(model)
+    stories = [story(700 + k, 60 + 13 * k) for k in range(3)]
+    crep, closs = cpu.train_story_batch(stories, oracle.TRAINING, replay=True)
+    grep, gloss = gpu.train_batch(stories, native.TRAINING, replay=True)
+    for a, b in zip(gloss, closs):
+        assert np.array_equal(a, b)
+    assert grep.replay_prefix_steps == crep.replay_prefix_steps > 0
+    assert grep.mean_loss == crep.mean_loss
+    assert_models_equal(gpu.model(), cpu.model(), f"{wgs} workgroups")
+    gpu.close()
+
+
+@pytest.mark.parametrize("wgs", ["1", "2"])
 def test_dense_touch_multi_window_parity(require_gpu, oracle, monkeypatch, wgs):
     # one or two workgroups per lane make every selecting wave own several
     # blocks, and an input fan-out of three quarters of the units touches well
