@@ -47,6 +47,10 @@ inline __host__ __device__ uint32_t block_words(uint32_t neurons_per_block) { re
 // once (at least one whole block, so a block never spans two windows).
 constexpr uint32_t kGroupBlocks = 64;    // blocks per bitmap load round
 constexpr uint32_t kWordsPerLane = 8;    // bitmap words per lane per load round
+// Delivery entries per target at fixed places (one 64-byte run per target,
+// read with the neuron record); further entries go to the target's overflow
+// range. Four covers nearly every target of a sparse tick.
+constexpr uint32_t kFixedEntries = 4;
 inline __host__ __device__ uint32_t window_capacity(uint32_t neurons_per_block) {
     return neurons_per_block > 256 ? neurons_per_block : 256;
 }
@@ -227,7 +231,8 @@ struct LaneDesc {
     uint32_t LEO_GLOBAL* touched_list;  // N: per selecting wave, its range's touched neurons (see wave_touched)
     float LEO_GLOBAL* learning_signal;
     uint32_t LEO_GLOBAL* dest_list;     // N: this step's claimed learning destinations (LaneControl dest_count)
-    uint64_t LEO_GLOBAL* bucket;        // 2 words per entry: delivery-order key, value bits
+    uint64_t LEO_GLOBAL* bucket;        // 2 words per entry: delivery-order key, value bits; kFixedEntries
+                                        // per target first, then the overflow ranges
     // block selection
     uint32_t LEO_GLOBAL* range_winners; // blocks * max_active_per_block: winners of each selecting wave's block
                              // range in block order, compacted from the row of its first block

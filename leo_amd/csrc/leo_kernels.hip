@@ -460,10 +460,10 @@ __device__ __forceinline__ void roll_counters(const StepCtx& c, uint32_t step_in
     clear_counters(ctl, c.tick);
 }
 
-// Entry p of target n's delivery bucket: the first two at fixed places
-// (2n, 2n+1), the rest in the target's overflow range.
+// Entry p of target n's delivery bucket: the first kFixedEntries at fixed
+// places (kFixedEntries*n + p), the rest in the target's overflow range.
 __device__ __forceinline__ uint64_t bucket_entry(uint64_t overflow, uint32_t n, uint32_t p) {
-    return p < 2 ? 2ull * n + p : overflow + (p - 2);
+    return p < kFixedEntries ? static_cast<uint64_t>(kFixedEntries) * n + p : overflow + (p - kFixedEntries);
 }
 
 // One delivery into target's bucket (the fold of phase 2 orders the bucket
@@ -830,10 +830,19 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
     float b0 = q1.z, b1 = q1.w, b2 = q2.x, b3 = q2.y;
     const uint32_t last = __float_as_uint(q2.z);
     const uint32_t cnt = __float_as_uint(q3.z);
-    const uint64_t overflow = a.m.bucket_offset[n];  // loaded with the state (used when cnt > 2)
-    // the two fixed bucket entries are read with the state
-    const uint64_t* fixed = d.bucket + 4ull * n;
-    const uint64_t k0 = ld(&fixed[0]), v0 = ld(&fixed[1]), k1 = ld(&fixed[2]), v1 = ld(&fixed[3]);
+    const uint64_t overflow = a.m.bucket_offset[n];  // loaded with the state (used when cnt > kFixedEntries)
+    // the fixed bucket entries (one 64-byte run, 16 bytes each: key, value)
+    // are read with the state; N * 64 bytes fits a buffer like the records
+    static_assert(kFixedEntries == 4, "the fold reads four fixed entries");
+    const __amdgpu_buffer_rsrc_t fixed = coherent_rsrc(d.bucket, N * kFixedEntries * 16);
+    f32x4 fe[kFixedEntries];
+#pragma unroll
+    for (uint32_t x = 0; x < kFixedEntries; ++x) fe[x] = ld16(fixed, (n * kFixedEntries + x) * 16);
+    auto entry_key = [](const f32x4& e) {
+        return (static_cast<uint64_t>(__float_as_uint(e.y)) << 32) | __float_as_uint(e.x);
+    };
+    const uint64_t k0 = entry_key(fe[0]), k1 = entry_key(fe[1]);
+    const uint32_t v0 = __float_as_uint(fe[0].z), v1 = __float_as_uint(fe[1].z);
     const bool refr = __float_as_uint(q2.w) > tick;
     const float threshold = ld(&d.p.threshold[n]);
     const uint32_t e = tick - last;
@@ -865,27 +874,28 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
             b3 = br == 3 ? b3 + v : b3;
         };
         if (cnt == 1) {
-            add(k0, static_cast<uint32_t>(v0));
+            add(k0, v0);
         } else if (cnt == 2) {
             if (k1 < k0) {
-                add(k1, static_cast<uint32_t>(v1));
-                add(k0, static_cast<uint32_t>(v0));
+                add(k1, v1);
+                add(k0, v0);
             } else {
-                add(k0, static_cast<uint32_t>(v0));
-                add(k1, static_cast<uint32_t>(v1));
+                add(k0, v0);
+                add(k1, v1);
             }
         } else if (cnt <= 8) {
             uint64_t k[8];
             uint32_t v[8];
-            k[0] = k0;
-            v[0] = static_cast<uint32_t>(v0);
-            k[1] = k1;
-            v[1] = static_cast<uint32_t>(v1);
+#pragma unroll
+            for (uint32_t x = 0; x < kFixedEntries; ++x) {
+                k[x] = x < cnt ? entry_key(fe[x]) : ~0ULL;
+                v[x] = x < cnt ? __float_as_uint(fe[x].z) : 0u;
+            }
             const uint64_t LEO_GLOBAL* over = d.bucket + 2 * overflow;
 #pragma unroll
-            for (uint32_t x = 2; x < 8; ++x) {
-                k[x] = x < cnt ? ld(&over[2 * (x - 2)]) : ~0ULL;
-                v[x] = x < cnt ? static_cast<uint32_t>(ld(&over[2 * (x - 2) + 1])) : 0u;
+            for (uint32_t x = kFixedEntries; x < 8; ++x) {
+                k[x] = x < cnt ? ld(&over[2 * (x - kFixedEntries)]) : ~0ULL;
+                v[x] = x < cnt ? static_cast<uint32_t>(ld(&over[2 * (x - kFixedEntries) + 1])) : 0u;
             }
             sort8(k, v);
 #pragma unroll
@@ -1654,9 +1664,10 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
         }
 #pragma unroll
         for (uint32_t k = 0; k < kRows; ++k) {
-            if (r0 + k >= A) break;
-            l1 += w1[k] * av[k];
-            l2 += w2[k] * av[k];
+            if (r0 + k < A) {  // rows in order, the ragged last chunk stops at A
+                l1 += w1[k] * av[k];
+                l2 += w2[k] * av[k];
+            }
         }
     }
     if (ctx_count > 0) {

@@ -775,13 +775,13 @@ void upload_topology(LeoHipRuntime* h, const LeoModelView& m) {
         }
         for (uint64_t i = 0; i < z.f; ++i) row_count[m.in_target[sym * z.f + i]] = 0;
     }
-    // entries 0 and 1 of target n live at 2n and 2n+1; the rest at
-    // offsets[n] + (p - 2), after the 2N fixed entries
+    // entries p < kFixedEntries of target n live at kFixedEntries*n + p; the
+    // rest at offsets[n] + (p - kFixedEntries), after the fixed entries
     std::vector<uint64_t> offsets(z.n + 1, 0);
-    offsets[0] = 2 * z.n;
+    offsets[0] = kFixedEntries * z.n;
     for (uint64_t n = 0; n < z.n; ++n) {
         const uint64_t need = cap[n] + row_max[n];
-        offsets[n + 1] = offsets[n] + (need > 2 ? need - 2 : 0);
+        offsets[n + 1] = offsets[n] + (need > kFixedEntries ? need - kFixedEntries : 0);
     }
     h->z.bucket_total = offsets[z.n];
     Layout l;
