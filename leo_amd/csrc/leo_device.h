@@ -162,12 +162,15 @@ struct LaneControl {
     uint32_t bias_dirty;
     uint32_t ctx_out_dirty;
     uint32_t error_code;
-    uint32_t barrier;                // lane-group barrier arrival counter
-    uint32_t abort;
-    uint32_t xcc_mask;               // XCDs the lane's workgroups run on (bit per XCD)
     uint32_t ring_tick[kRing];       // tick whose active set ring slot holds (UINT32_MAX = empty)
     uint32_t ring_count[kRing];      // active count of that tick
-    uint32_t tick_touched[2];        // touched count, indexed by tick parity
+    // The barrier counter has a 128-byte L2 line of its own: its polls and
+    // arrivals would otherwise queue behind the per-step counter atomics and
+    // the step record's stores to the same line.
+    alignas(128) uint32_t barrier;   // lane-group barrier arrival counter
+    uint32_t abort;
+    uint32_t xcc_mask;               // XCDs the lane's workgroups run on (bit per XCD)
+    alignas(128) uint32_t tick_touched[2];  // touched count, indexed by tick parity
     uint32_t tick_supra[2];          // suprathreshold count, indexed by tick parity
     uint32_t tick_events[2];         // delivered events, indexed by tick parity
     uint32_t tick_dest[2];           // learning destinations, indexed by tick parity

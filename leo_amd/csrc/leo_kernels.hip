@@ -273,12 +273,12 @@ __device__ __forceinline__ bool lane_barrier(LaneControl* ctl, uint32_t P, uint3
         uint32_t spins = 0;
         uint32_t aborted = 0;
         for (;;) {
-            // the counter and the abort flag are polled in one round trip
-            const uint32_t abort_flag = ld(&ctl->abort);
+            // one poll in flight per workgroup (more load the counter's L2
+            // channel and slow the arrivals); the abort flag every 16th
             const uint32_t arrived = local ? ld(&ctl->barrier)
                                            : __hip_atomic_load(&ctl->barrier, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
             if (arrived >= target) break;
-            if (abort_flag != 0) {
+            if ((spins & 15) == 15 && ld(&ctl->abort) != 0) {
                 aborted = 1;
                 break;
             }

@@ -524,6 +524,7 @@ void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
             lane.schedule.base + ((static_cast<size_t>(lane.schedule_capacity) * sizeof(StepParams) + 255) & ~size_t(255)));
         lane.desc.step_count = static_cast<uint32_t>(r.steps.size());
         upload(const_cast<StepParams*>(lane.desc.steps), r.steps.data(), r.steps.size() * sizeof(StepParams), h->stream);
+        static_assert(offsetof(LaneControl, xcc_mask) == offsetof(LaneControl, barrier) + 8, "cleared together");
         LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->barrier, 0, 12, h->stream));  // barrier, abort, xcc_mask
         LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->error_code, 0, 4, h->stream));
     }
