@@ -337,6 +337,7 @@ void clear_changes(const Lane& lane, const Sizes& z, hipStream_t s) {
     LEO_HIP_CHECK(hipMemsetAsync(d.ch_in, 0, z.words(z.ni) * 4, s));
     LEO_HIP_CHECK(hipMemsetAsync(d.ch_out, 0, z.words(z.n) * 4, s));
     LEO_HIP_CHECK(hipMemsetAsync(d.ch_ctx, 0, z.words(z.slots) * 4, s));
+    static_assert(offsetof(LaneControl, ctx_out_dirty) == offsetof(LaneControl, bias_dirty) + 4, "cleared together");
     LEO_HIP_CHECK(hipMemsetAsync(&d.ctl->bias_dirty, 0, 8, s));  // bias_dirty, ctx_out_dirty
 }
 
