@@ -1886,25 +1886,33 @@ __device__ __forceinline__ float signal_rows(__amdgpu_buffer_rsrc_t rows, uint32
         off[k] = static_cast<uint32_t>(__shfl(static_cast<int>(dst), static_cast<int>(row))) * (kOutStride * 4) + seg * 16;
     }
     const float tail = lane < count ? ld4(rows, dst * (kOutStride * 4) + 4 * kEndIndex) : 0.0f;
-    f32x4 v[8];
+    // two lines in flight (even lines in v, odd lines in w; the unrolled loop
+    // names the buffers statically, so no register copy waits for a load)
+    static_assert(kLines % 2 == 0, "lines are taken in pairs");
+    f32x4 v[8], w[8];
 #pragma unroll
-    for (uint32_t k = 0; k < 8; ++k) v[k] = live[k] ? ld16(rows, off[k]) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t k = 0; k < 8; ++k) {
+        v[k] = live[k] ? ld16(rows, off[k]) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        w[k] = live[k] ? ld16(rows, off[k] + 128) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
     float acc = 0.0f;
+#pragma unroll
     for (uint32_t line = 0; line < kLines; ++line) {
+        f32x4(&cur)[8] = (line & 1) ? w : v;
         wave_sync();
 #pragma unroll
         for (uint32_t k = 0; k < 8; ++k) {
             float* st = stage + (8 * k + sub) * kStageRowFloats + seg * 4;
-            st[0] = v[k].x;
-            st[1] = v[k].y;
-            st[2] = v[k].z;
-            st[3] = v[k].w;
+            st[0] = cur[k].x;
+            st[1] = cur[k].y;
+            st[2] = cur[k].z;
+            st[3] = cur[k].w;
         }
         wave_sync();
-        if (line + 1 < kLines) {
+        if (line + 2 < kLines) {
 #pragma unroll
             for (uint32_t k = 0; k < 8; ++k)
-                v[k] = live[k] ? ld16(rows, off[k] + (line + 1) * 128) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                cur[k] = live[k] ? ld16(rows, off[k] + (line + 2) * 128) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
         if (lane < count) {
             const float* r = stage + lane * kStageRowFloats;
@@ -2032,11 +2040,15 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
     if (learn) {
         for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = ld(&d.errors[o]);
         __syncthreads();
+        // the readout workgroup updates the bias and the context projection;
+        // the other workgroups share the output rows and the synapse slots
+        const uint32_t sharers = c.P > 1 ? c.P - 1 : 1;
+        const uint32_t first = c.part < sharers ? c.gtid : ~0u, stride = sharers * kThreads;
         const float ss = sp.supervised_strength;
         const float olr = cfg.output_learning_rate;
         // output rows of active neurons
         const uint32_t out_items = A * kOutputs;
-        for (uint32_t item = c.gtid; item < out_items; item += c.gstride) {
+        for (uint32_t item = first; item < out_items; item += stride) {
             const uint32_t r = item / kOutputs, o = item % kOutputs;
             const uint32_t n = ld(&act_list[r]);
             const float act = ld(&act_val[r]);
@@ -2061,7 +2073,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
             const float lr = cfg.recurrent_learning_rate;
             const uint32_t rec_n = ld(&ctl->rec_count[c.parity]);
             const uint32_t* rec_cur = d.rec_list + c.parity * NS;
-            for (uint32_t i = c.gtid; i < rec_n; i += c.gstride) {
+            for (uint32_t i = first; i < rec_n; i += stride) {
                 const uint32_t slot = ld(&rec_cur[i]);
                 const uint32_t dst = a.m.rec_target[slot];
                 const uint32_t src = fast_div(slot, a.div_synapses);
@@ -2086,7 +2098,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
             }
             const uint32_t in_n = ld(&ctl->in_count[c.parity]);
             const uint32_t* in_cur = d.in_list + c.parity * NI;
-            for (uint32_t i = c.gtid; i < in_n; i += c.gstride) {
+            for (uint32_t i = first; i < in_n; i += stride) {
                 const uint32_t slot = ld(&in_cur[i]);
                 const uint32_t dst = a.m.in_target[slot];
                 const float e = ld(&d.in_trace[static_cast<uint64_t>(slot) * kTraceWords + kTEligibility]);
@@ -2102,7 +2114,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
         // inhibitory homeostasis on the rows of active inhibitory sources not
         // already handled with their eligible slot above
         const uint32_t inh_items = A * S;
-        for (uint32_t item = c.gtid; item < inh_items; item += c.gstride) {
+        for (uint32_t item = first; item < inh_items; item += stride) {
             const uint32_t r = fast_div(item, a.div_synapses), j = item - r * S;
             const uint32_t src = ld(&act_list[r]);
             if (a.m.neuron_type[src] == 0) continue;
