@@ -1864,12 +1864,12 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
 // load misses the CU's L1 like ld()); the resource is wave-uniform and covers
 // `bytes` from `base` (loads beyond it return 0).
 // Serial 257-term dot of one output row with the errors, in output order
-// (runtime.rs:1245-1250); eight 16-byte row loads are in flight at a time.
+// (runtime.rs:1245-1250).
 // Learning signals of up to 64 destinations, one per lane (`dst` on lanes
 // below `count`; every lane of the wave calls): the output rows are streamed
 // through the wave's LDS stage one 128-byte line at a time, 8 whole lines per
-// load instruction, with the next line in flight while the current one is
-// summed; each lane then adds its row's 257 products in the reference's
+// load instruction, with the next two lines in flight while the current one
+// is summed; each lane then adds its row's 257 products in the reference's
 // order (runtime.rs:1214-1263).
 __device__ __forceinline__ float signal_rows(__amdgpu_buffer_rsrc_t rows, uint32_t dst, uint32_t count, const float* err,
                                              float* stage) {
