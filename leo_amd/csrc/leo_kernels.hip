@@ -2401,8 +2401,9 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
     static_assert(kNeuronWords == 16 && kNLastTick == 10, "record layout");
     {
         uint4 LEO_GLOBAL* rec = reinterpret_cast<uint4 LEO_GLOBAL*>(d.neuron);
-        const uint4 zero = make_uint4(0u, 0u, 0u, 0u), with_tick = make_uint4(0u, 0u, tick, 0u);
-        for (uint64_t i = t0; i < 4 * N; i += ts) rec[i] = (i & 3) == 2 ? with_tick : zero;
+        // a select of the word, not of two vectors (which becomes an indexed
+        // private array)
+        for (uint64_t i = t0; i < 4 * N; i += ts) rec[i] = make_uint4(0u, 0u, (i & 3) == 2 ? tick : 0u, 0u);
     }
     const uint64_t groups = NS / 16;
     for (uint64_t g = t0; g < groups; g += ts) clear_trace_group(d, g, tick, set_tick != 0);
