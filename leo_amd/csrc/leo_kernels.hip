@@ -1930,17 +1930,23 @@ __device__ __forceinline__ float signal_rows(__amdgpu_buffer_rsrc_t rows, uint32
 __device__ __forceinline__ void phase_signals(const StepCtx& c, StepShared& sh) {
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = c.a->cfg;
+    // one round: the errors, the destination count and this wave's first
+    // batch of the list (read before the count is known; entries past it are
+    // masked below)
+    const uint32_t wave = wave_index(), lane = __lane_id();
+    const uint32_t waves = c.P * kWavesPerGroup, b0 = c.part * kWavesPerGroup + wave;
+    const uint32_t N = cfg.neuron_count;
+    const uint32_t count = ld(&c.ctl->dest_count);
+    const uint32_t first_at = b0 * kWaveSize + lane;
+    const uint32_t first_dst = first_at < N ? ld(&d.dest_list[first_at]) : 0u;
     for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = ld(&d.errors[o]);
     __syncthreads();
-    const uint32_t count = ld(&c.ctl->dest_count);
-    const uint32_t wave = wave_index(), lane = __lane_id();
-    const uint32_t waves = c.P * kWavesPerGroup;
     // the host limits N * kOutStride * 4 to below 2^31 bytes
-    const __amdgpu_buffer_rsrc_t rows = coherent_rsrc(d.p.out_w, cfg.neuron_count * kOutStride * 4);
+    const __amdgpu_buffer_rsrc_t rows = coherent_rsrc(d.p.out_w, N * kOutStride * 4);
     float* stage = reinterpret_cast<float*>(step_lds + static_cast<size_t>(wave) * wave_lds_bytes(cfg.neurons_per_block));
-    for (uint32_t b = c.part * kWavesPerGroup + wave; b * kWaveSize < count; b += waves) {
+    for (uint32_t b = b0; b * kWaveSize < count; b += waves) {
         const uint32_t n = min(kWaveSize, count - b * kWaveSize);
-        const uint32_t dst = lane < n ? ld(&d.dest_list[b * kWaveSize + lane]) : 0u;
+        const uint32_t dst = lane < n ? (b == b0 ? first_dst : ld(&d.dest_list[b * kWaveSize + lane])) : 0u;
         const float sig = signal_rows(rows, dst, n, sh.err, stage);
         if (lane < n) d.learning_signal[dst] = sig;
     }
