@@ -2044,12 +2044,21 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
     const float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
     const float mu = cfg.max_update, wmin = cfg.weight_min, wmax = cfg.weight_max;
     if (learn) {
-        for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = ld(&d.errors[o]);
-        __syncthreads();
         // the readout workgroup updates the bias and the context projection;
         // the other workgroups share the output rows and the synapse slots
         const uint32_t sharers = c.P > 1 ? c.P - 1 : 1;
         const uint32_t first = c.part < sharers ? c.gtid : ~0u, stride = sharers * kThreads;
+        // the list lengths and this thread's first eligible slots go out with
+        // the errors (slots read before the lengths are known are masked by
+        // the loops below)
+        const uint32_t* rec_cur = d.rec_list + c.parity * NS;
+        const uint32_t* in_cur = d.in_list + c.parity * NI;
+        const uint32_t rec_n = plastic ? ld(&ctl->rec_count[c.parity]) : 0u;
+        const uint32_t in_n = plastic ? ld(&ctl->in_count[c.parity]) : 0u;
+        const uint32_t rec_first = plastic && first < NS ? ld(&rec_cur[first]) : 0u;
+        const uint32_t in_first = plastic && first < NI ? ld(&in_cur[first]) : 0u;
+        for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = ld(&d.errors[o]);
+        __syncthreads();
         const float ss = sp.supervised_strength;
         const float olr = cfg.output_learning_rate;
         // output rows of active neurons
@@ -2077,10 +2086,8 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
         if (plastic) {
             const float cs = ss * sp.plasticity_scale;
             const float lr = cfg.recurrent_learning_rate;
-            const uint32_t rec_n = ld(&ctl->rec_count[c.parity]);
-            const uint32_t* rec_cur = d.rec_list + c.parity * NS;
             for (uint32_t i = first; i < rec_n; i += stride) {
-                const uint32_t slot = ld(&rec_cur[i]);
+                const uint32_t slot = i == first ? rec_first : ld(&rec_cur[i]);
                 const uint32_t dst = a.m.rec_target[slot];
                 const uint32_t src = fast_div(slot, a.div_synapses);
                 const float e = ld(&d.rec_trace[static_cast<uint64_t>(slot) * kTraceWords + kTEligibility]);
@@ -2102,10 +2109,8 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
                 if (changed) mark_bit(d.ch_rec, slot);
                 d.p.rec_weight[slot] = nw;
             }
-            const uint32_t in_n = ld(&ctl->in_count[c.parity]);
-            const uint32_t* in_cur = d.in_list + c.parity * NI;
             for (uint32_t i = first; i < in_n; i += stride) {
-                const uint32_t slot = ld(&in_cur[i]);
+                const uint32_t slot = i == first ? in_first : ld(&in_cur[i]);
                 const uint32_t dst = a.m.in_target[slot];
                 const float e = ld(&d.in_trace[static_cast<uint64_t>(slot) * kTraceWords + kTEligibility]);
                 const float gradient = ld(&d.learning_signal[dst]) * e;
