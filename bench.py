@@ -8,14 +8,18 @@ runtime -- the reference benchmark's input_bytes_per_second definition
 replay and merge). Synthetic seeded stories and a seeded synthetic model of the
 workload's shape; nothing is skipped inside the timed region.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload B] [--no-replay]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload D] [--no-replay]
 
-Prints one JSON line. The roofline object prices the step kernel's work
+The default workload is D (1,048,576 units, fan-in 64,
+64 story lanes, 30% replay), the configuration the headline metric is quoted
+on. Prints one JSON line. The roofline object prices the step kernel's work
 counters with the per-lane-step byte model of leo_runtime.hip (step_bytes) and
-divides by the summed HIP-event time of its launches inside the timed region.
+divides by the summed HIP-event time of its launches inside the timed region;
+roofline.sections splits the same figures into the story pass (story lanes),
+the replay (canonical runtime) and the batch-end mean (merge kernel).
 cpu_baseline times the CPU oracle (this repository's restatement of Leo's CPU
-executor, one thread per story as in training.rs:1669-1683) on one batch of the
-same workload.
+executor, one thread per story as in training.rs:1669-1683) on a bounded sample
+of one batch of the same workload.
 """
 from __future__ import annotations
 
@@ -33,9 +37,14 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 
 
+_HIP = None
+
+
 def _device_sync() -> None:
-    hip = ctypes.CDLL("libamdhip64.so")
-    if hip.hipDeviceSynchronize() != 0:
+    global _HIP
+    if _HIP is None:
+        _HIP = ctypes.CDLL("libamdhip64.so")
+    if _HIP.hipDeviceSynchronize() != 0:
         raise RuntimeError("hipDeviceSynchronize failed")
 
 
@@ -104,7 +113,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--workload", default="B")
+    ap.add_argument("--workload", default="D")
     ap.add_argument("--no-replay", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -154,6 +163,19 @@ def main() -> int:
 
     kernel_s = ks["kernel_ms"] / 1e3
     achieved = ks["algorithmic_bytes"] / kernel_s / 1e9 if kernel_s > 0 else 0.0
+
+    def section(name, launches, ms, nbytes, steps):
+        gbs = nbytes / (ms / 1e3) / 1e9 if ms > 0 else 0.0
+        return {"kernel": name, "launches": launches, "kernel_ms": ms, "algorithmic_bytes": nbytes,
+                "lane_steps": steps, "achieved": gbs, "frac": gbs / HBM_PEAK_GBS}
+
+    sections = {
+        "story": section("leo_lane_steps (story lanes)", ks["section_launches"][0], ks["section_kernel_ms"][0],
+                         ks["section_bytes"][0], ks["section_lane_steps"][0]),
+        "replay": section("leo_lane_steps (canonical runtime)", ks["section_launches"][1],
+                          ks["section_kernel_ms"][1], ks["section_bytes"][1], ks["section_lane_steps"][1]),
+        "merge": section("leo_merge_fixed", ks["merge_launches"], ks["merge_ms"], ks["merge_bytes"], 0),
+    }
     line = {
         "metric": "trained bytes/sec (FP32, 1 MI355X)",
         "value": trained / elapsed,
@@ -190,12 +212,14 @@ def main() -> int:
             "algorithmic_bytes": ks["algorithmic_bytes"],
             "lane_steps": ks["lane_steps"],
             "merge_ms": ks["merge_ms"],
+            "sections": sections,
         },
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
         d, o = batches[args.warmup]
         line["cpu_baseline"] = cpu_baseline(w, model, d, o, replay)
+        line["config"]["cpu_baseline_sample"] = line["cpu_baseline"]["sample"]
     print(json.dumps(line), flush=True)
     return 0
 

@@ -169,6 +169,21 @@ typedef struct LeoKernelStats {
     /* Story lanes resident on the device at once; larger batches run in
      * groups of this many lanes (sized from free device memory at creation). */
     uint64_t resident_lanes;
+    /* The step-kernel figures above split by the lanes a launch served:
+     * [0] story lanes of a logical batch, [1] the canonical runtime (replay,
+     * in-place single-story passes and single steps). */
+    uint64_t section_launches[2];
+    uint64_t section_lane_steps[2];
+    double section_kernel_ms[2];
+    double section_bytes[2];
+    /* Batch-end mean: (element, lane) pairs whose lane value differs from the
+     * base, merged elements, and the algorithmic bytes they imply (24 B per
+     * changed lane value -- lane value, base and the f64 accumulator
+     * read-modify-write -- plus 4 (L+1) B per merged element for the
+     * canonical write and the lane scatters). */
+    uint64_t merge_lane_changes;
+    uint64_t merge_elements;
+    double merge_bytes;
 } LeoKernelStats;
 
 /* Selectors for leo_hip_parameter_changes (ParameterChanges, runtime.rs:37-46). */

@@ -337,7 +337,8 @@ struct MergeArgs {
     uint32_t synapses_per_neuron;
     const uint8_t LEO_GLOBAL* neuron_type;
     float weight_min, weight_max;
-    unsigned long long LEO_GLOBAL* updates;
+    unsigned long long LEO_GLOBAL* updates;       // merged elements
+    unsigned long long LEO_GLOBAL* lane_changes;  // (element, lane) pairs with a nonzero delta
     uint32_t LEO_GLOBAL* error;
     // Lane groups (batches larger than the resident lanes): kMergeAccumulate
     // continues the lane-ordered f64 sum of each element in acc (and the

@@ -2489,7 +2489,7 @@ __device__ __forceinline__ float merge_project(const MergeArgs& m, uint64_t i, f
 }
 
 __global__ void __launch_bounds__(kThreads) leo_merge_fixed(MergeArgs m) {
-    unsigned long long local = 0;
+    unsigned long long local = 0, changes = 0;
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < m.count;
          i += static_cast<uint64_t>(gridDim.x) * kThreads) {
         uint64_t at = m.row ? (i / m.row) * m.stride + (i % m.row) : i;
@@ -2514,6 +2514,7 @@ __global__ void __launch_bounds__(kThreads) leo_merge_fixed(MergeArgs m) {
             float delta = m.lanes[l][at] - base;
             if (delta != 0.0f) {
                 any = true;
+                changes += 1;
                 if (!finitef(delta)) atomicCAS(m.error, 0u, 1u);
                 sum += static_cast<double>(delta);
             }
@@ -2532,6 +2533,7 @@ __global__ void __launch_bounds__(kThreads) leo_merge_fixed(MergeArgs m) {
         local += 1;
     }
     if (local) atomicAdd(m.updates, local);
+    if (changes) atomicAdd(m.lane_changes, changes);
 }
 
 }  // namespace leo

@@ -24,6 +24,7 @@
 #include <utility>
 #include <vector>
 
+#include "launch_plan.h"
 #include "leo_device.h"
 #include "leo_hip.h"
 #include "leo_host.h"
@@ -386,10 +387,9 @@ void reset_lane_objects(LeoHipRuntime* h, const std::vector<Lane*>& lanes, bool 
     }
 }
 
-uint32_t choose_wgs_per_lane(LeoHipRuntime* h, uint32_t lanes, bool canonical) {
-    uint32_t coop = static_cast<uint32_t>(h->cus * h->coop_blocks_per_cu);
-    uint32_t limit = std::max<uint32_t>(1, coop / std::max<uint32_t>(lanes, 1));
-    limit = std::min<uint32_t>(limit, kMaxWaves / kWavesPerGroup);
+// Launch shape of `lanes` lanes: the wanted workgroups per lane, capped by the
+// cooperative capacity (launch_plan.h).
+LanePlan choose_wgs_per_lane(LeoHipRuntime* h, uint32_t lanes, bool canonical) {
     uint32_t want;
     if (canonical && h->canonical_wgs_override) {
         want = h->canonical_wgs_override;
@@ -410,7 +410,8 @@ uint32_t choose_wgs_per_lane(LeoHipRuntime* h, uint32_t lanes, bool canonical) {
             want = std::min<uint32_t>(want, per_xcd);
         }
     }
-    return std::max<uint32_t>(1, std::min(want, limit));
+    return plan_lanes(lanes, want, static_cast<uint32_t>(h->cus), static_cast<uint32_t>(h->coop_blocks_per_cu),
+                      kMaxWaves / kWavesPerGroup, kXcds);
 }
 
 StepParams make_step(const LeoHostConfig& c, Lane& lane, uint32_t symbol, int32_t target, int32_t permission,
@@ -482,15 +483,21 @@ double step_bytes(const LeoHostConfig& c, const StepParams& sp, const StepRecord
     return b;
 }
 
-void account_launch(LeoHipRuntime* h, const std::vector<LaneRun>& runs, float ms) {
+void account_launch(LeoHipRuntime* h, const std::vector<LaneRun>& runs, float ms, bool canonical) {
     LeoKernelStats& t = h->telemetry;
+    const int section = canonical ? 1 : 0;
     t.launches += 1;
     t.kernel_ms += ms;
+    t.section_launches[section] += 1;
+    t.section_kernel_ms[section] += ms;
     for (const LaneRun& run : runs) {
         for (size_t i = 0; i < run.steps.size(); ++i) {
             const StepRecord& r = run.records[i];
+            const double bytes = step_bytes(h->cfg, run.steps[i], r);
             t.lane_steps += 1;
-            t.algorithmic_bytes += step_bytes(h->cfg, run.steps[i], r);
+            t.algorithmic_bytes += bytes;
+            t.section_lane_steps[section] += 1;
+            t.section_bytes[section] += bytes;
             t.events += r.events;
             t.touched += r.touched;
             t.active += r.active;
@@ -534,9 +541,11 @@ void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     stage_descs(h, lanes);
     // lanes are padded to a multiple of the XCD count so that each lane's
     // workgroups land on one XCD (see lane_steps)
-    const uint32_t padded = (count + kXcds - 1) / kXcds * kXcds;
-    const uint32_t P = choose_wgs_per_lane(h, padded, count == 1 && runs[0].lane == h->canonical.get());
-    const uint32_t stride = P > 1 ? padded : count;
+    const bool canonical = count == 1 && runs[0].lane == h->canonical.get();
+    const LanePlan plan = choose_wgs_per_lane(h, count, canonical);
+    const uint32_t P = plan.P, stride = plan.stride;
+    if (static_cast<uint64_t>(plan.grid) > cooperative_capacity(h->cus, h->coop_blocks_per_cu))
+        throw Error(LEO_ERR_INTERNAL, "cooperative launch exceeds the resident workgroup capacity");
     KernelArgs a = kernel_args(h, reinterpret_cast<LaneDesc*>(h->lane_descs.base), count, P);
     a.lane_stride = stride;
     if (!h->kernel_args_buf.base) h->kernel_args_buf.allocate(sizeof(KernelArgs));
@@ -561,7 +570,7 @@ void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     float ms = 0.0f;
     LEO_HIP_CHECK(hipEventElapsedTime(&ms, h->ev_start, h->ev_stop));
     h->last_launch_ms = ms;
-    account_launch(h, runs, ms);
+    account_launch(h, runs, ms, canonical);
     if (h->phase_profile) {
         // lane 0 of the launch is representative (lanes run the same phase sequence)
         unsigned long long prof[2 * kPhases];
@@ -1059,7 +1068,7 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes, uint32_t
     const Sizes& z = h->z;
     const uint32_t L = static_cast<uint32_t>(lanes.size());
     // scratch: 6 pointer tables of L entries + 1 counter + error word
-    size_t need = 6 * L * sizeof(float*) + 256;
+    size_t need = 6 * L * sizeof(float*) + 256;  // + counters
     if (h->merge_scratch.bytes < need) {
         h->merge_scratch.allocate(need);
     }
@@ -1075,9 +1084,10 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes, uint32_t
     }
     char* base = h->merge_scratch.base;
     upload(base, tables.data(), tables.size() * sizeof(float*), h->stream);
+    // counters: merged elements, changed lane values, then the error word
     auto* counter = reinterpret_cast<unsigned long long*>(base + 6 * L * sizeof(float*));
-    auto* error = reinterpret_cast<uint32_t*>(counter + 1);
-    LEO_HIP_CHECK(hipMemsetAsync(counter, 0, 16, h->stream));
+    auto* error = reinterpret_cast<uint32_t*>(counter + 2);
+    LEO_HIP_CHECK(hipMemsetAsync(counter, 0, 24, h->stream));
     LEO_HIP_CHECK(hipEventRecord(h->ev_start, h->stream));
     struct Job {
         float* canonical;
@@ -1119,6 +1129,7 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes, uint32_t
         m.weight_min = h->cfg.device.weight_min;
         m.weight_max = h->cfg.device.weight_max;
         m.updates = counter;
+        m.lane_changes = counter + 1;
         m.error = error;
         uint64_t blocks = std::min<uint64_t>((m.count + kThreads - 1) / kThreads, 4096);
         hipLaunchKernelGGL(leo_merge_fixed, dim3(static_cast<uint32_t>(std::max<uint64_t>(blocks, 1))), dim3(kThreads), 0,
@@ -1126,15 +1137,26 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes, uint32_t
         LEO_HIP_CHECK(hipGetLastError());
     }
     LEO_HIP_CHECK(hipEventRecord(h->ev_stop, h->stream));
-    unsigned long long updates = 0;
+    unsigned long long counts[2] = {0, 0};
     uint32_t err = 0;
-    download(&updates, counter, 8, h->stream);
+    download(counts, counter, 16, h->stream);
     download(&err, error, 4, h->stream);
     sync(h->stream);
+    const unsigned long long updates = counts[0];
     float ms = 0.0f;
     LEO_HIP_CHECK(hipEventElapsedTime(&ms, h->ev_start, h->ev_stop));
-    h->telemetry.merge_launches += 6;
-    h->telemetry.merge_ms += ms;
+    LeoKernelStats& t = h->telemetry;
+    t.merge_launches += 6;
+    t.merge_ms += ms;
+    // algorithmic bytes of the mean: 24 per changed lane value, 4 (L+1) per
+    // merged element (canonical write and the lane scatters)
+    t.merge_lane_changes += counts[1];
+    t.merge_bytes += 24.0 * static_cast<double>(counts[1]);
+    if (mode != kMergeAccumulate) {
+        const double lanes_total = mode == kMergeFinalize ? total_lanes : L;
+        t.merge_elements += updates;
+        t.merge_bytes += 4.0 * (lanes_total + 1.0) * static_cast<double>(updates);
+    }
     if (err) throw Error(LEO_ERR_INTERNAL, "merged parameter became non-finite");
     return updates;
 }
@@ -1444,6 +1466,14 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
             throw Error(LEO_ERR_UNSUPPORTED, "neuron_count above 2^28 is not supported by the packed synapse layout");
         if (config->device.neurons_per_block > leo::kMaxBlockNeurons)
             throw Error(LEO_ERR_UNSUPPORTED, "neurons_per_block above 1024 is not supported by the device selection");
+        {
+            // a binding global cap sorts every block winner of a tick in one
+            // workgroup's LDS (runtime.rs:1047-1074)
+            const uint64_t winners = static_cast<uint64_t>(config->device.block_count) * config->device.max_active_per_block;
+            if (winners > config->device.max_active_global && winners > leo::kMaxBlockNeurons)
+                throw Error(LEO_ERR_UNSUPPORTED, "a binding max_active_global with more than 1024 block winners per tick "
+                                                 "(block_count * max_active_per_block) is not supported");
+        }
         if (static_cast<uint64_t>(config->device.neuron_count) * leo::kOutStride * 4 >= (1ULL << 31))
             throw Error(LEO_ERR_UNSUPPORTED, "output projection above 2 GiB per lane is not supported");
         int devices = 0;
@@ -1467,10 +1497,15 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         LEO_HIP_CHECK(hipEventCreate(&h->ev_start));
         LEO_HIP_CHECK(hipEventCreate(&h->ev_stop));
         h->cus = prop.multiProcessorCount;
-        LEO_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&h->coop_blocks_per_cu,
-                                                                   reinterpret_cast<const void*>(&leo::leo_lane_steps),
-                                                                   leo::kThreads,
-                                                                   leo::step_lds_bytes(config->device.neurons_per_block)));
+        // cooperative capacity: the smaller occupancy of the step kernel and
+        // its phase-profiling build (either may be launched on the same grid)
+        int occupancy[2] = {0, 0};
+        const void* step_kernels[2] = {reinterpret_cast<const void*>(&leo::leo_lane_steps),
+                                       reinterpret_cast<const void*>(&leo::leo_lane_steps_profiled)};
+        for (int k = 0; k < 2; ++k)
+            LEO_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &occupancy[k], step_kernels[k], leo::kThreads, leo::step_lds_bytes(config->device.neurons_per_block)));
+        h->coop_blocks_per_cu = std::min(occupancy[0], occupancy[1]);
         if (h->coop_blocks_per_cu <= 0) throw Error(LEO_ERR_DEVICE, "step kernel cannot be resident");
         if (const char* env = std::getenv("LEO_HIP_WGS_PER_LANE")) h->wgs_override = static_cast<uint32_t>(std::atoi(env));
         if (const char* env = std::getenv("LEO_HIP_CANONICAL_WGS"))
@@ -1501,6 +1536,11 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         const size_t reserve = leo::merge_accumulator_bytes(h->z) + (size_t(1) << 30);
         const size_t fit = free_bytes > reserve ? (free_bytes - reserve) / std::max<size_t>(per_lane, 1) : 0;
         h->resident_lanes = static_cast<uint32_t>(std::min<size_t>(h->max_lanes, 1 + fit));
+        // one cooperative launch holds at most cus * coop_blocks_per_cu
+        // workgroups, one per lane at the least (lanes padded to the XCDs)
+        h->resident_lanes = std::min(h->resident_lanes, leo::cooperative_lane_limit(static_cast<uint32_t>(h->cus),
+                                                                                static_cast<uint32_t>(h->coop_blocks_per_cu),
+                                                                                leo::kXcds));
         if (const char* env = std::getenv("LEO_HIP_RESIDENT_LANES"))
             h->resident_lanes = std::max<uint32_t>(1, std::min<uint32_t>(h->resident_lanes, std::atoi(env)));
         *out = h.release();
@@ -1543,7 +1583,10 @@ int32_t leo_hip_reset_transient_state(LeoHipRuntime* h) {
 int32_t leo_hip_enable_parameter_tracking(LeoHipRuntime* h) {
     return guarded([&] {
         leo::BusyGuard g(h);
-        if (h->tracking) return;
+        // the GPU adapter starts a fresh change set on every call
+        // (cuda.rs:2827-2837; the coordinator calls it before each batch's
+        // replay, training.rs:1628), unlike the CPU Runtime's no-op when
+        // tracking is already on (runtime.rs:310-320)
         h->tracking = true;
         leo::clear_changes(*h->canonical, h->z, h->stream);
         leo::sync(h->stream);

@@ -124,6 +124,10 @@ class LeoKernelStats(ctypes.Structure):
         ("active_inhibitory", ctypes.c_uint64), ("merge_launches", ctypes.c_uint64), ("merge_ms", ctypes.c_double),
         ("phase_work_us", ctypes.c_double * 8), ("phase_wait_us", ctypes.c_double * 8),
         ("resident_lanes", ctypes.c_uint64),
+        ("section_launches", ctypes.c_uint64 * 2), ("section_lane_steps", ctypes.c_uint64 * 2),
+        ("section_kernel_ms", ctypes.c_double * 2), ("section_bytes", ctypes.c_double * 2),
+        ("merge_lane_changes", ctypes.c_uint64), ("merge_elements", ctypes.c_uint64),
+        ("merge_bytes", ctypes.c_double),
     ]
 
 

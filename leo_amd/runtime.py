@@ -261,7 +261,7 @@ class HipRuntime:
         out = {}
         for name, _ in native.LeoKernelStats._fields_:
             v = getattr(st, name)
-            out[name] = list(v) if name.startswith("phase_") else v
+            out[name] = list(v) if isinstance(v, ctypes.Array) else v
         return out
 
     @property
