@@ -184,6 +184,10 @@ typedef struct LeoKernelStats {
     uint64_t merge_lane_changes;
     uint64_t merge_elements;
     double merge_bytes;
+    /* Eligible slots whose weight update a plasticity step applied: the kept
+     * slots with nonzero eligibility (with zero eligibility the update leaves
+     * the weight unchanged, bit for bit). */
+    uint64_t learning_slots;
 } LeoKernelStats;
 
 /* Selectors for leo_hip_parameter_changes (ParameterChanges, runtime.rs:37-46). */
@@ -294,6 +298,59 @@ int32_t leo_hip_train_batch(LeoHipRuntime* runtime, const uint8_t* bytes, const 
 /* RuntimeBackend::synchronize_model + model() (backend.rs:355-356): copy the
  * canonical model into caller-owned arrays (host layouts). */
 int32_t leo_hip_download_model(LeoHipRuntime* runtime, LeoModelView* out);
+/* RuntimeBackend::synchronize_model (backend.rs:356) as the GPU adapter does
+ * it (cuda.rs:2817-2825 -> sync_changed_model_to_host, cuda.rs:5657-5760):
+ * `mirror` is the caller's host model, current as of its last synchronisation
+ * (leo_hip_download_model, this call, or the model the runtime was created or
+ * uploaded with); only the elements of the canonical model changed since then
+ * -- by steps, the batch-end mean, the keyed context merge -- are written into
+ * it, plus the whole bias / context output projection when they changed, and
+ * the generation, revision and statistics. The Rust adapter calls it in
+ * parameter_changes() before returning, so that
+ * PackedSparseModelUpdate::from_model reads current values (training.rs:1558-1562,
+ * 1644-1648). */
+int32_t leo_hip_synchronize_model(LeoHipRuntime* runtime, LeoModelView* mirror);
+
+/* PackedSparseModelUpdate (crates/leo-core/src/parallel.rs:79-97): canonical
+ * values of changed elements in packed layouts -- output rows neuron by
+ * neuron (257 values each), context rows slot by slot (E values each). The
+ * bias (257 values) and the context output projection (257*E, output-major)
+ * are whole or NULL. */
+typedef struct LeoPackedUpdate {
+    const uint32_t* threshold_indices;
+    const float* threshold_values;
+    uint64_t threshold_count;
+    const uint32_t* recurrent_indices;
+    const float* recurrent_values;
+    uint64_t recurrent_count;
+    const uint32_t* input_indices;
+    const float* input_values;
+    uint64_t input_count;
+    const uint32_t* output_neurons;
+    const float* output_values_by_neuron;
+    uint64_t output_count;
+    const uint32_t* context_slots;
+    const uint64_t* context_keys;
+    const uint32_t* context_observations;
+    const float* context_embeddings;
+    uint64_t context_count;
+    const float* output_bias;
+    const float* context_output_weights;
+    uint64_t generation;
+    uint64_t parameter_revision;
+    LeoStatistics statistics;
+} LeoPackedUpdate;
+
+/* RuntimeBackend::synchronize_packed_model (backend.rs:374-376, GPU adapter
+ * cuda.rs:2844-2857 -> 2869-3080): scatter the packed rows into the canonical
+ * device image (PackedSparseModelUpdate::apply_to_model, parallel.rs:186-302,
+ * with its index and size checks) and take the update's generation, revision
+ * and statistics; parameter tracking ends. Story lanes need no scatter: each
+ * logical batch forks its lanes from the canonical image. */
+int32_t leo_hip_synchronize_packed_model(LeoHipRuntime* runtime, const LeoPackedUpdate* update);
+/* RuntimeBackend::commit_packed_host_model (backend.rs:378-387, cuda.rs:2859-2868):
+ * the same scatter, keeping parameter tracking as it is. */
+int32_t leo_hip_commit_packed_host_model(LeoHipRuntime* runtime, const LeoPackedUpdate* update);
 /* RuntimeBackend::model_mut (backend.rs:357): replace the canonical model. */
 int32_t leo_hip_upload_model(LeoHipRuntime* runtime, const LeoModelView* model);
 /* RuntimeBackend::parameter_changes (backend.rs:359): the tracked index set

@@ -129,7 +129,8 @@ struct StepRecord {
     uint32_t scanned_in;        // eligible input slots updated
     uint32_t destinations;      // learning destinations
     uint32_t active_inhibitory; // active inhibitory sources
-    uint32_t pad[2];
+    uint32_t learning_slots;    // eligible slots whose update the step applies (nonzero eligibility)
+    uint32_t pad;
 };
 
 // Device numerical guard codes (the reference's sticky error_flag 1-7,
@@ -148,6 +149,8 @@ struct LaneControl {
     uint32_t in_count[2];
     uint32_t dest_epoch;             // learning-destination epoch
     uint32_t dest_count;             // entries of this step's destination list
+    uint32_t rec_learn_count;        // entries of this step's recurrent learning-slot list
+    uint32_t in_learn_count;         // entries of this step's input learning-slot list
     uint32_t history_len;
     uint32_t history[kMaxOrder];
     uint32_t ctx_count;
@@ -177,6 +180,7 @@ struct LaneControl {
     uint32_t tick_ainh[2];           // active inhibitory sources, indexed by tick parity
     uint32_t tick_scan_rec[2];       // eligible recurrent slots scanned, indexed by tick parity
     uint32_t tick_scan_in[2];        // eligible input slots scanned, indexed by tick parity
+    uint32_t tick_learn[2];          // learning slots listed, indexed by tick parity
 };
 
 // Learned parameters of a lane (private copy for story lanes, the canonical
@@ -234,6 +238,10 @@ struct LaneDesc {
     uint32_t LEO_GLOBAL* touched_list;  // N: per selecting wave, its range's touched neurons (see wave_touched)
     float LEO_GLOBAL* learning_signal;
     uint32_t LEO_GLOBAL* dest_list;     // N: this step's claimed learning destinations (LaneControl dest_count)
+    // this step's learning slots: kept eligible slots whose weight update can
+    // change the weight (nonzero eligibility), listed by the eligibility phase
+    uint32_t LEO_GLOBAL* rec_learn;     // NS (LaneControl rec_learn_count)
+    uint32_t LEO_GLOBAL* in_learn;      // NI (LaneControl in_learn_count)
     uint64_t LEO_GLOBAL* bucket;        // 2 words per entry: delivery-order key, value bits; kFixedEntries
                                         // per target first, then the overflow ranges
     // block selection
@@ -318,6 +326,15 @@ struct KernelArgs {
     uint32_t spin_limit;
     uint32_t lane_stride;            // workgroup b serves lane b % lane_stride (>= lane_count)
     uint32_t local_sync;             // allow XCD-local lane barriers
+    // Learning slots are the kept eligible slots with nonzero eligibility:
+    // with e == 0 the update -lr*s*(signal*e) is a signed zero, and adding it
+    // to a valid weight that is not -0.0 returns the weight unchanged, bit for
+    // bit, through the clamp and the sign projection (model.rs:343-380 keeps
+    // every weight in bounds and of its source's sign). The host clears this
+    // flag when a recurrent or input weight is -0.0 (learning and the merge
+    // never produce one from another value); every kept slot is then a
+    // learning slot.
+    uint32_t skip_zero_eligibility;
     FastDiv div_synapses;            // synapses_per_neuron
     FastDiv div_block;               // neurons_per_block
     FastDiv div_block_words;         // block_words(neurons_per_block)
@@ -349,6 +366,32 @@ struct MergeArgs {
     uint32_t total_lanes;
     double LEO_GLOBAL* acc;
     uint8_t LEO_GLOBAL* any;
+    // Host-stale marks of the canonical image: one bit per merged element
+    // (per merged neuron row for the output projection: element / row), or,
+    // with stale_flag, one word set when any element of the tensor merges.
+    uint32_t LEO_GLOBAL* stale;
+    uint32_t stale_flag;
+};
+
+// Sparse moves between a canonical tensor and a packed buffer: element
+// index[k] (row index[k], `row` elements from index*stride, when row > 0)
+// of `tensor` to or from packed[k] (packed[k*row .. k*row+row)).
+struct SparseMove {
+    float LEO_GLOBAL* tensor;
+    const uint32_t LEO_GLOBAL* index;
+    float LEO_GLOBAL* packed;
+    uint64_t count;              // indices
+    uint32_t row;                // 0: single elements
+    uint32_t stride;
+    uint32_t to_tensor;          // 1: scatter packed -> tensor, 0: gather tensor -> packed
+};
+
+// Folds a lane's change bitmaps into the host-stale bitmaps and clears them
+// (words[i] bitmaps of words each; the last pair holds the dirty flags).
+struct FoldArgs {
+    uint32_t LEO_GLOBAL* changes[6];
+    uint32_t LEO_GLOBAL* stale[6];
+    uint64_t words[6];
 };
 enum : uint32_t { kMergeDirect = 0, kMergeAccumulate = 1, kMergeFinalize = 2 };
 

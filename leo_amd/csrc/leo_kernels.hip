@@ -410,7 +410,7 @@ __device__ __forceinline__ void activate_trace(float LEO_GLOBAL* trace, __amdgpu
 // Late fields of a step record: work counters complete only after the step's
 // last barrier, so the record is finished by the next step (or kernel end).
 struct LateCounters {
-    uint32_t events, touched, scanned_rec, scanned_in, destinations, inhibitory;
+    uint32_t events, touched, scanned_rec, scanned_in, destinations, inhibitory, learning;
 };
 
 __device__ __forceinline__ LateCounters load_late_counters(LaneControl LEO_GLOBAL* ctl, uint32_t tick) {
@@ -422,6 +422,7 @@ __device__ __forceinline__ LateCounters load_late_counters(LaneControl LEO_GLOBA
     v.scanned_in = ld(&ctl->tick_scan_in[k]);
     v.destinations = ld(&ctl->tick_dest[k]);
     v.inhibitory = ld(&ctl->tick_ainh[k]);
+    v.learning = ld(&ctl->tick_learn[k]);
     return v;
 }
 
@@ -433,6 +434,7 @@ __device__ __forceinline__ void store_late_record(const LaneDesc& d, uint32_t st
     rec.scanned_in = v.scanned_in;
     rec.destinations = v.destinations;
     rec.active_inhibitory = v.inhibitory;
+    rec.learning_slots = v.learning;
 }
 
 // all loads first (one round trip), then the stores
@@ -451,6 +453,7 @@ __device__ __forceinline__ void clear_counters(LaneControl LEO_GLOBAL* ctl, uint
     ctl->tick_ainh[n] = 0;
     ctl->tick_scan_rec[n] = 0;
     ctl->tick_scan_in[n] = 0;
+    ctl->tick_learn[n] = 0;
 }
 // Once tick-1 is complete (phase 3 of `tick`, by one thread): its record is
 // finished and its per-tick counters, which tick+1 reuses, are cleared.
@@ -1478,7 +1481,7 @@ __device__ __forceinline__ void load_destination(SlotInputs& in, const StepCtx& 
 }
 
 __device__ __forceinline__ bool finish_slot(const StepCtx& c, const SlotInputs& in, float LEO_GLOBAL* trace,
-                                            uint32_t slot, uint8_t br, float pop_cutoff) {
+                                            uint32_t slot, uint8_t br, float pop_cutoff, float& eligibility) {
     const LeoConfig& cfg = c.a->cfg;
     const uint32_t tick = c.tick;
     float bs = in.bs, ms = in.ms, fs = in.fs, as0 = in.as0, as1 = in.as1, as2 = in.as2;
@@ -1522,6 +1525,7 @@ __device__ __forceinline__ bool finish_slot(const StepCtx& c, const SlotInputs& 
     mag = maxnum(mag, fabsf(as0));
     mag = maxnum(mag, fabsf(as1));
     mag = maxnum(mag, fabsf(as2));
+    eligibility = elig;
     return mag > cfg.eligibility_epsilon;
 }
 
@@ -1541,13 +1545,32 @@ __device__ __forceinline__ void wave_append2(uint32_t LEO_GLOBAL* counter, bool 
     pos1 = base + n0 + static_cast<uint32_t>(__popcll(m1 & below));
 }
 
+// Where a plasticity step lists its learning slots and claims their
+// destinations (runtime.rs:1214-1243).
+struct LearnOut {
+    uint32_t LEO_GLOBAL* list;   // learning slots of this list
+    uint32_t LEO_GLOBAL* count;
+    bool plastic;                // the step commits recurrent/input plasticity
+    uint32_t claimed;            // this thread's destinations claimed
+    uint32_t listed;             // this thread's learning slots listed
+};
+
 // Eligible slots of one list, two per lane per iteration (their loads in
-// flight together); kept slots are compacted into the next list.
+// flight together); kept slots are compacted into the next list. On a
+// plasticity step the kept slots whose update can change their weight
+// (nonzero eligibility; every kept slot when skip_zero_eligibility is off) are
+// listed as learning slots, and their destinations are claimed once each
+// with an epoch exchange: the learning signal is computed for exactly those.
+// The reference also computes signals for the other destinations (the
+// targets of zero-eligibility slots and the active neurons); no update reads
+// them.
 __device__ __forceinline__ void eligibility_list(const StepCtx& c, float LEO_GLOBAL* trace, uint64_t slots,
                                                  uint8_t LEO_GLOBAL* marks,
                                                  const uint32_t LEO_GLOBAL* cur, uint32_t cur_n,
                                                  uint32_t LEO_GLOBAL* next, uint32_t LEO_GLOBAL* next_count,
-                                                 const uint32_t* targets, const uint8_t* branches, float pop_cutoff) {
+                                                 const uint32_t* targets, const uint8_t* branches, float pop_cutoff,
+                                                 LearnOut& learn) {
+    const bool skip_zero = c.a->skip_zero_eligibility != 0;
     const uint32_t lane = __lane_id();
     const __amdgpu_buffer_rsrc_t rsrc = trace_rsrc(trace, slots);
     for (uint32_t base = c.gtid - lane; base < cur_n; base += 2 * c.gstride) {
@@ -1572,18 +1595,32 @@ __device__ __forceinline__ void eligibility_list(const StepCtx& c, float LEO_GLO
         if (v1) load_epochs(a1, c, t1);
         if (v0 && a0.touched_epoch == c.tick + 1) load_destination(a0, c, t0);
         if (v1 && a1.touched_epoch == c.tick + 1) load_destination(a1, c, t1);
-        const bool k0 = v0 && finish_slot(c, a0, trace, s0, r0, pop_cutoff);
-        const bool k1 = v1 && finish_slot(c, a1, trace, s1, r1, pop_cutoff);
+        float e0 = 0.0f, e1 = 0.0f;
+        const bool k0 = v0 && finish_slot(c, a0, trace, s0, r0, pop_cutoff, e0);
+        const bool k1 = v1 && finish_slot(c, a1, trace, s1, r1, pop_cutoff, e1);
         if (v0 && !k0) marks[s0] = kMarkDropped;
         if (v1 && !k1) marks[s1] = kMarkDropped;
         uint32_t p0, p1;
         wave_append2(next_count, k0, k1, p0, p1);
         if (k0) next[p0] = s0;
         if (k1) next[p1] = s1;
+        if (learn.plastic) {  // wave-uniform
+            const bool l0 = k0 && (e0 != 0.0f || !skip_zero), l1 = k1 && (e1 != 0.0f || !skip_zero);
+            wave_append2(learn.count, l0, l1, p0, p1);
+            if (l0) learn.list[p0] = s0;
+            if (l1) learn.list[p1] = s1;
+            const bool w0 = l0 && atomicExch(nu(c.d, t0, kNDestEpoch), c.dest_epoch) != c.dest_epoch;
+            const bool w1 = l1 && atomicExch(nu(c.d, t1, kNDestEpoch), c.dest_epoch) != c.dest_epoch;
+            wave_append2(&c.ctl->dest_count, w0, w1, p0, p1);
+            if (w0) c.d.dest_list[p0] = t0;
+            if (w1) c.d.dest_list[p1] = t1;
+            learn.listed += (l0 ? 1u : 0u) + (l1 ? 1u : 0u);
+            learn.claimed += (w0 ? 1u : 0u) + (w1 ? 1u : 0u);
+        }
     }
 }
 
-__device__ __forceinline__ void phase_eligibility(const StepCtx& c) {
+__device__ __forceinline__ void phase_eligibility(const StepCtx& c, bool plastic) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -1596,10 +1633,16 @@ __device__ __forceinline__ void phase_eligibility(const StepCtx& c) {
         c.ctl->tick_scan_in[c.tick & 1] = in_n;
     }
     const float pop_cutoff = a.redundant_global ? 0.0f : ld(&c.ctl->pop_cutoff);
+    LearnOut rec{d.rec_learn, &c.ctl->rec_learn_count, plastic, 0, 0};
     eligibility_list(c, d.rec_trace, NS, d.rec_mark, d.rec_list + p * NS, rec_n, d.rec_list + q * NS,
-                     &c.ctl->rec_count[q], a.m.rec_target, a.m.rec_branch, pop_cutoff);
+                     &c.ctl->rec_count[q], a.m.rec_target, a.m.rec_branch, pop_cutoff, rec);
+    LearnOut in{d.in_learn, &c.ctl->in_learn_count, plastic, rec.claimed, rec.listed};
     eligibility_list(c, d.in_trace, NI, d.in_mark, d.in_list + p * NI, in_n, d.in_list + q * NI,
-                     &c.ctl->in_count[q], a.m.in_target, a.m.in_branch, pop_cutoff);
+                     &c.ctl->in_count[q], a.m.in_target, a.m.in_branch, pop_cutoff, in);
+    if (plastic) {
+        add_count(&c.ctl->tick_dest[c.tick & 1], in.claimed);
+        add_count(&c.ctl->tick_learn[c.tick & 1], in.listed);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1746,44 +1789,6 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
     __syncthreads();
 }
 
-// Learning destinations of this step (runtime.rs:1214-1243): the targets of
-// the eligible recurrent and input slots and the active neurons, each claimed
-// once with an epoch exchange and listed (one append per wave). They need no
-// errors, so the workgroups that do not compute the readout claim them in
-// the readout's phase.
-__device__ __forceinline__ void signal_claims(const StepCtx& c) {
-    const KernelArgs& a = *c.a;
-    const LaneDesc& d = c.d;
-    const LeoConfig& cfg = a.cfg;
-    const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * cfg.synapses_per_neuron;
-    const uint64_t NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
-    const uint32_t rec_n = ld(&c.ctl->rec_count[c.parity]), in_n = ld(&c.ctl->in_count[c.parity]);
-    const uint32_t A = ld(&c.ctl->active_count);
-    const uint32_t rs = c.tick % kRing;
-    const uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cfg.max_active_global;
-    const uint32_t* rec_cur = d.rec_list + c.parity * NS;
-    const uint32_t* in_cur = d.in_list + c.parity * NI;
-    const uint32_t total = rec_n + in_n + A;
-    const uint32_t lane = __lane_id();
-    const uint32_t workers = c.P > 1 ? c.P - 1 : 1;
-    uint32_t claimed = 0;
-    for (uint32_t base = c.part * kThreads + threadIdx.x - lane; base < total; base += workers * kThreads) {
-        const uint32_t item = base + lane;
-        bool won = false;
-        uint32_t dst = 0;
-        if (item < total) {
-            if (item < rec_n) dst = a.m.rec_target[ld(&rec_cur[item])];
-            else if (item < rec_n + in_n) dst = a.m.in_target[ld(&in_cur[item - rec_n])];
-            else dst = ld(&act_list[item - rec_n - in_n]);
-            won = atomicExch(nu(d, dst, kNDestEpoch), c.dest_epoch) != c.dest_epoch;
-        }
-        const uint32_t pos = wave_append(&c.ctl->dest_count, won);
-        if (won) d.dest_list[pos] = dst;
-        claimed += won ? 1u : 0u;
-    }
-    add_count(&c.ctl->tick_dest[c.tick & 1], claimed);
-}
-
 __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& sp, uint32_t step_index, StepShared& sh) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
@@ -1851,7 +1856,6 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
             readout(c, sp, sh, step_index);
         }
     }
-    if ((sp.flags & kStepLearn) && sp.plasticity_scale > 0.0f && (c.part < readout_wg || c.P == 1)) signal_claims(c);
 }
 
 // ---------------------------------------------------------------------------
@@ -2048,13 +2052,13 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
         // the other workgroups share the output rows and the synapse slots
         const uint32_t sharers = c.P > 1 ? c.P - 1 : 1;
         const uint32_t first = c.part < sharers ? c.gtid : ~0u, stride = sharers * kThreads;
-        // the list lengths and this thread's first eligible slots go out with
-        // the errors (slots read before the lengths are known are masked by
-        // the loops below)
-        const uint32_t* rec_cur = d.rec_list + c.parity * NS;
-        const uint32_t* in_cur = d.in_list + c.parity * NI;
-        const uint32_t rec_n = plastic ? ld(&ctl->rec_count[c.parity]) : 0u;
-        const uint32_t in_n = plastic ? ld(&ctl->in_count[c.parity]) : 0u;
+        // the learning-slot list lengths and this thread's first learning
+        // slots go out with the errors (slots read before the lengths are
+        // known are masked by the loops below)
+        const uint32_t* rec_cur = d.rec_learn;
+        const uint32_t* in_cur = d.in_learn;
+        const uint32_t rec_n = plastic ? ld(&ctl->rec_learn_count) : 0u;
+        const uint32_t in_n = plastic ? ld(&ctl->in_learn_count) : 0u;
         const uint32_t rec_first = plastic && first < NS ? ld(&rec_cur[first]) : 0u;
         const uint32_t in_first = plastic && first < NI ? ld(&in_cur[first]) : 0u;
         for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = ld(&d.errors[o]);
@@ -2123,14 +2127,19 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
             }
         }
         // inhibitory homeostasis on the rows of active inhibitory sources not
-        // already handled with their eligible slot above
+        // already handled with their learning slot above (a kept eligible
+        // slot with nonzero eligibility, or any kept slot without the zero
+        // skip)
         const uint32_t inh_items = A * S;
+        const bool skip_zero = a.skip_zero_eligibility != 0;
         for (uint32_t item = first; item < inh_items; item += stride) {
             const uint32_t r = fast_div(item, a.div_synapses), j = item - r * S;
             const uint32_t src = ld(&act_list[r]);
             if (a.m.neuron_type[src] == 0) continue;
             const uint64_t slot = static_cast<uint64_t>(src) * S + j;
-            if (plastic && ld(&d.rec_mark[slot]) == kMarkListed) continue;
+            if (plastic && ld(&d.rec_mark[slot]) == kMarkListed &&
+                (!skip_zero || ld(&d.rec_trace[slot * kTraceWords + kTEligibility]) != 0.0f))
+                continue;
             const uint32_t dst = a.m.rec_target[slot];
             const float tgt_act = ld(nf(d, dst, kNActivation)) > 0.0f ? 1.0f : 0.0f;
             const float old_w = ld(&d.p.rec_weight[slot]);
@@ -2291,8 +2300,17 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             // the previous step's write_active has rolled this tick's counters
             atomicAdd(&c.ctl->tick_events[c.tick & 1], pending_events);
         }
-        // this step's destination list starts empty (filled in the post phase)
-        if (learn && c.part == 0 && threadIdx.x == 0) c.ctl->dest_count = 0;
+        // this step's destination and learning-slot lists start empty (filled
+        // by the eligibility phase) under a new claim epoch
+        const bool plastic = learn && sp.plasticity_scale > 0.0f;
+        if (plastic) {
+            c.dest_epoch += 1;
+            if (c.part == 0 && threadIdx.x == 0) {
+                c.ctl->dest_count = 0;
+                c.ctl->rec_learn_count = 0;
+                c.ctl->in_learn_count = 0;
+            }
+        }
         // the context of a step delivered ahead: on the workgroup that owns no
         // selection blocks, beside the fold (first read by the readout)
         if (delivered_ahead && c.P > 1 && c.part == c.P - 1) context_resolve(c, sp, sh);
@@ -2309,7 +2327,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         }
         if (redundant) {
             const uint32_t delivered = write_active(c, sp, s, sh, fused, pipeline, next);
-            if (trace) phase_eligibility(c);
+            if (trace) phase_eligibility(c, plastic);
             if (pipeline) {
                 if (c.P == 1) context_resolve(c, next, sh);
                 pending_events = wg_total(delivered);
@@ -2318,14 +2336,12 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             if (c.part == 0) global_select(c, sh, s);
             if (trace) {
                 if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 7))) break;
-                phase_eligibility(c);
+                phase_eligibility(c, plastic);
             }
         }
         if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 2))) break;
-        const bool plastic = learn && sp.plasticity_scale > 0.0f;
         if (!fused) {
             if (trace) c.parity ^= 1;
-            if (plastic) c.dest_epoch += 1;  // the destinations are claimed in the post phase
             phase_post(c, sp, s, sh);
             if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 3))) break;
         }
@@ -2453,6 +2469,9 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
         ctl->clipped = 0;
         ctl->pop_cutoff = 0.0f;
         ctl->active_count = 0;
+        ctl->dest_count = 0;
+        ctl->rec_learn_count = 0;
+        ctl->in_learn_count = 0;
         ctl->error_code = 0;
         ctl->barrier = 0;
         ctl->abort = 0;
@@ -2463,6 +2482,7 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
         for (int k = 0; k < 2; ++k) {
             ctl->tick_touched[k] = ctl->tick_supra[k] = ctl->tick_events[k] = 0;
             ctl->tick_dest[k] = ctl->tick_ainh[k] = ctl->tick_scan_rec[k] = ctl->tick_scan_in[k] = 0;
+            ctl->tick_learn[k] = 0;
         }
     }
 }
@@ -2488,6 +2508,18 @@ __device__ __forceinline__ float merge_project(const MergeArgs& m, uint64_t i, f
     }
 }
 
+// Host-stale mark of a merged element: its bit (its neuron row's for the
+// output projection), or the tensor's flag word.
+__device__ __forceinline__ void mark_stale(const MergeArgs& m, uint64_t i) {
+    if (!m.stale) return;
+    if (m.stale_flag) {
+        m.stale[0] = 1u;
+        return;
+    }
+    const uint64_t bit = m.kind == kMergeOutput ? i / m.row : i;
+    atomicOr(&m.stale[bit >> 5], 1u << (bit & 31));
+}
+
 __global__ void __launch_bounds__(kThreads) leo_merge_fixed(MergeArgs m) {
     unsigned long long local = 0, changes = 0;
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < m.count;
@@ -2501,6 +2533,7 @@ __global__ void __launch_bounds__(kThreads) leo_merge_fixed(MergeArgs m) {
             v = merge_project(m, i, v);
             if (!finitef(v)) atomicCAS(m.error, 0u, 3u);
             m.canonical[at] = v;
+            mark_stale(m, i);
             local += 1;
             continue;
         }
@@ -2530,10 +2563,43 @@ __global__ void __launch_bounds__(kThreads) leo_merge_fixed(MergeArgs m) {
         v = merge_project(m, i, v);
         if (!finitef(v)) atomicCAS(m.error, 0u, 3u);
         m.canonical[at] = v;
+        mark_stale(m, i);
         local += 1;
     }
     if (local) atomicAdd(m.updates, local);
     if (changes) atomicAdd(m.lane_changes, changes);
+}
+
+// ---------------------------------------------------------------------------
+// Host synchronisation of the canonical image (cuda.rs:5657-5760) and packed
+// sparse updates (parallel.rs:186-302, cuda.rs:2869-3080).
+// ---------------------------------------------------------------------------
+// One tensor's elements (or rows) between the canonical image and a packed
+// buffer, one element per thread.
+__global__ void __launch_bounds__(kThreads) leo_sparse_move(SparseMove mv) {
+    const uint64_t per = mv.row ? mv.row : 1u;
+    const uint64_t total = mv.count * per;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < total;
+         i += static_cast<uint64_t>(gridDim.x) * kThreads) {
+        const uint64_t k = i / per, e = i - k * per;
+        const uint64_t at = mv.row ? static_cast<uint64_t>(mv.index[k]) * mv.stride + e : mv.index[k];
+        if (mv.to_tensor) mv.tensor[at] = mv.packed[i];
+        else mv.packed[i] = mv.tensor[at];
+    }
+}
+
+// stale |= changes, changes = 0, for each bitmap (and the dirty-flag words).
+__global__ void __launch_bounds__(kThreads) leo_fold_changes(FoldArgs f) {
+    for (uint32_t b = 0; b < 6; ++b) {
+        for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < f.words[b];
+             i += static_cast<uint64_t>(gridDim.x) * kThreads) {
+            const uint32_t v = f.changes[b][i];
+            if (v) {
+                f.stale[b][i] |= v;
+                f.changes[b][i] = 0u;
+            }
+        }
+    }
 }
 
 }  // namespace leo

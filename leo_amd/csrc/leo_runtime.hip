@@ -36,6 +36,8 @@ __global__ void leo_lane_steps_profiled(const KernelArgs* args);
 __global__ void leo_reset_lanes(KernelArgs args, uint32_t set_tick, uint32_t new_tick);
 
 __global__ void leo_merge_fixed(MergeArgs m);
+__global__ void leo_sparse_move(SparseMove mv);
+__global__ void leo_fold_changes(FoldArgs f);
 
 namespace {
 
@@ -170,6 +172,15 @@ struct LeoHipRuntime {
     uint32_t max_steps_override = 0;
     float last_launch_ms = 0.0f;  // duration of the latest lane-steps launch (HIP events)
     leo::Arena merge_scratch;  // lane pointer table + counters
+    // Host-stale marks of the canonical image: elements changed since the
+    // caller's host mirror was last synchronised that the change bitmaps no
+    // longer hold (tracking restarts fold them in here; the batch-end mean and
+    // the keyed context merge mark them directly). Sets: threshold, recurrent,
+    // input, output rows, context slots; then the bias / context output flags.
+    leo::Arena stale;
+    uint32_t* stale_bits[5] = {};
+    uint32_t* stale_flags = nullptr;  // [0] bias, [1] context output projection
+    leo::Arena move_scratch;          // packed indices and values of sparse moves
     // host copies of the read-only topology (device copies are immutable)
     std::vector<float> excitability;
     std::vector<uint8_t> neuron_type, rec_branch, rec_delay, in_branch;
@@ -178,6 +189,9 @@ struct LeoHipRuntime {
     uint64_t generation = 0, revision = 0;
     LeoStatistics stats{};
     bool tracking = false;
+    // a recurrent or input weight of the canonical model is -0.0 (see
+    // KernelArgs::skip_zero_eligibility)
+    bool negative_zero_weights = false;
     std::atomic<bool> busy{false};
     uint32_t wgs_override = 0;
     uint32_t canonical_wgs_override = 0;
@@ -277,6 +291,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     size_t o_ctl = l.add<LaneControl>(1);
     size_t o_neu = l.add<uint32_t>(kNeuronWords * z.n), o_tl = l.add<uint32_t>(z.n);
     size_t o_ls = l.add<float>(z.n), o_dl = l.add<uint32_t>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
+    size_t o_rl = l.add<uint32_t>(z.ns), o_il = l.add<uint32_t>(z.ni);
     size_t o_bw = l.add<uint32_t>(z.blocks * z.limit), o_bcut = l.add<float>(z.blocks);
     size_t o_bwa = l.add<float>(z.blocks * z.limit);
     size_t o_wt = l.add<uint32_t>(kMaxWaves), o_wtt = l.add<uint32_t>(kMaxWaves);
@@ -299,6 +314,8 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
 
     d.learning_signal = reinterpret_cast<float*>(b + o_ls);
     d.dest_list = reinterpret_cast<uint32_t*>(b + o_dl);
+    d.rec_learn = reinterpret_cast<uint32_t*>(b + o_rl);
+    d.in_learn = reinterpret_cast<uint32_t*>(b + o_il);
     d.bucket = reinterpret_cast<uint64_t*>(b + o_bk);
     d.range_winners = reinterpret_cast<uint32_t*>(b + o_bw);
     d.range_winner_act = reinterpret_cast<float*>(b + o_bwa);
@@ -342,6 +359,84 @@ void clear_changes(const Lane& lane, const Sizes& z, hipStream_t s) {
     LEO_HIP_CHECK(hipMemsetAsync(&d.ctl->bias_dirty, 0, 8, s));  // bias_dirty, ctx_out_dirty
 }
 
+// ---------------------------------------------------------------------------
+// Host-stale marks of the canonical image and sparse moves (the reference GPU
+// adapter's change lists and gather/scatter kernels, cuda.rs:5657-5760,
+// 2869-3080).
+// ---------------------------------------------------------------------------
+uint64_t set_size(const Sizes& z, int set) {
+    const uint64_t counts[5] = {z.n, z.ns, z.ni, z.n, z.slots};
+    return counts[set];
+}
+
+void allocate_stale(LeoHipRuntime* h) {
+    const Sizes& z = h->z;
+    Layout l;
+    size_t at[5];
+    for (int i = 0; i < 5; ++i) at[i] = l.add<uint32_t>(z.words(set_size(z, i)));
+    const size_t flags = l.add<uint32_t>(2);
+    h->stale.allocate(l.cursor);
+    for (int i = 0; i < 5; ++i) h->stale_bits[i] = reinterpret_cast<uint32_t*>(h->stale.base + at[i]);
+    h->stale_flags = reinterpret_cast<uint32_t*>(h->stale.base + flags);
+    LEO_HIP_CHECK(hipMemsetAsync(h->stale.base, 0, h->stale.bytes, h->stream));
+}
+
+void clear_stale(LeoHipRuntime* h) { LEO_HIP_CHECK(hipMemsetAsync(h->stale.base, 0, h->stale.bytes, h->stream)); }
+
+uint32_t* change_bits(const LaneDesc& d, int set) {
+    uint32_t* bits[5] = {d.ch_threshold, d.ch_rec, d.ch_in, d.ch_out, d.ch_ctx};
+    return bits[set];
+}
+
+// Tracking restart of the canonical runtime: its change sets and dirty flags
+// move into the host-stale marks and start empty.
+void fold_changes(LeoHipRuntime* h) {
+    const LaneDesc& d = h->canonical->desc;
+    FoldArgs f{};
+    uint64_t widest = 2;
+    for (int i = 0; i < 5; ++i) {
+        f.changes[i] = change_bits(d, i);
+        f.stale[i] = h->stale_bits[i];
+        f.words[i] = h->z.words(set_size(h->z, i));
+        widest = std::max(widest, f.words[i]);
+    }
+    static_assert(offsetof(LaneControl, ctx_out_dirty) == offsetof(LaneControl, bias_dirty) + 4, "flag pair");
+    f.changes[5] = &d.ctl->bias_dirty;
+    f.stale[5] = h->stale_flags;
+    f.words[5] = 2;
+    const uint64_t blocks = std::min<uint64_t>((widest + kThreads - 1) / kThreads, 2048);
+    hipLaunchKernelGGL(leo_fold_changes, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, h->stream, f);
+    LEO_HIP_CHECK(hipGetLastError());
+}
+
+// Moves `count` elements (rows of `row` elements at `stride` when row > 0)
+// between a canonical tensor and the host: gathers into `values` when
+// to_tensor is false, scatters `values` when true.
+void sparse_move(LeoHipRuntime* h, float* tensor, const uint32_t* index, uint64_t count, uint32_t row, uint32_t stride,
+                 float* values, bool to_tensor) {
+    if (count == 0) return;
+    const uint64_t per = row ? row : 1;
+    const size_t index_bytes = (count * 4 + 255) & ~size_t(255);
+    const size_t need = index_bytes + count * per * 4;
+    if (h->move_scratch.bytes < need) h->move_scratch.allocate(need);
+    char* base = h->move_scratch.base;
+    upload(base, index, count * 4, h->stream);
+    if (to_tensor) upload(base + index_bytes, values, count * per * 4, h->stream);
+    SparseMove mv{};
+    mv.tensor = tensor;
+    mv.index = reinterpret_cast<const uint32_t*>(base);
+    mv.packed = reinterpret_cast<float*>(base + index_bytes);
+    mv.count = count;
+    mv.row = row;
+    mv.stride = stride;
+    mv.to_tensor = to_tensor ? 1u : 0u;
+    const uint64_t blocks = std::min<uint64_t>((count * per + kThreads - 1) / kThreads, 4096);
+    hipLaunchKernelGGL(leo_sparse_move, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, h->stream, mv);
+    LEO_HIP_CHECK(hipGetLastError());
+    if (!to_tensor) download(values, base + index_bytes, count * per * 4, h->stream);
+    sync(h->stream);
+}
+
 KernelArgs kernel_args(LeoHipRuntime* h, LaneDesc* lanes, uint32_t count, uint32_t P) {
     KernelArgs a{};
     a.cfg = h->cfg.device;
@@ -356,6 +451,7 @@ KernelArgs kernel_args(LeoHipRuntime* h, LaneDesc* lanes, uint32_t count, uint32
     a.div_synapses = make_fast_div(h->cfg.device.synapses_per_neuron);
     a.div_block = make_fast_div(h->cfg.device.neurons_per_block);
     a.div_block_words = make_fast_div(block_words(h->cfg.device.neurons_per_block));
+    a.skip_zero_eligibility = h->negative_zero_weights ? 0u : 1u;
     return a;
 }
 
@@ -463,10 +559,12 @@ struct LaneRun {
 //   60 per active neuron        post-activation state RMW + ring entry
 //    8 per active edge          emission snapshot weight read + value write
 // 1028 per active neuron        readout row gather (output computed)
-// 1032 per destination          learning-signal row read + signal write
+// 1032 per destination          learning-signal row read + signal write (destinations: the
+//                               targets of learning slots, the kept eligible slots whose
+//                               eligibility is nonzero; no update reads another signal)
 // 2056 per active neuron        output row RMW (learning step)
-//   37 per kept eligible slot   weight RMW 8 + eligibility 4 + target 4 + signal 4 + list 4 + marks/type 13
-//   24 per inhibitory edge      target activation 4 + weight RMW 8 + target 4 + mark 8
+//   37 per learning slot        weight RMW 8 + eligibility 4 + target 4 + signal 4 + list 4 + marks/type 13
+//   28 per inhibitory edge      target activation 4 + weight RMW 8 + target 4 + mark 8 + eligibility 4
 //    4 per context cell * E     embedding row read
 double step_bytes(const LeoHostConfig& c, const StepParams& sp, const StepRecord& r) {
     const double S = c.device.synapses_per_neuron, F = c.device.input_fanout, E = c.device.context_embedding_dim;
@@ -478,8 +576,8 @@ double step_bytes(const LeoHostConfig& c, const StepParams& sp, const StepRecord
                4.0 * r.context_cells * E;
     if (lam) b += 72.0 * (static_cast<double>(r.events) + F) + 140.0 * (static_cast<double>(r.scanned_rec) + r.scanned_in);
     if (out) b += 1028.0 * r.active;
-    if (pi) b += 1032.0 * r.destinations + 37.0 * (static_cast<double>(r.eligible_rec) + r.eligible_in);
-    if (sig) b += 2056.0 * r.active + 24.0 * r.active_inhibitory * S;
+    if (pi) b += 1032.0 * r.destinations + 37.0 * r.learning_slots;
+    if (sig) b += 2056.0 * r.active + 28.0 * r.active_inhibitory * S;
     return b;
 }
 
@@ -505,6 +603,7 @@ void account_launch(LeoHipRuntime* h, const std::vector<LaneRun>& runs, float ms
             t.scanned_in += r.scanned_in;
             t.kept_rec += r.eligible_rec;
             t.kept_in += r.eligible_in;
+            t.learning_slots += r.learning_slots;
             t.destinations += r.destinations;
             t.active_inhibitory += r.active_inhibitory;
         }
@@ -740,10 +839,20 @@ std::vector<HostStep> document_steps(const uint8_t* story, size_t len) {  // tra
     return steps;
 }
 
+bool has_negative_zero(const float* v, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) {
+        uint32_t bits;
+        std::memcpy(&bits, v + i, 4);
+        if (bits == 0x80000000u) return true;
+    }
+    return false;
+}
+
 // Host layouts <-> device layouts.
 void upload_model(LeoHipRuntime* h, const LeoModelView& m) {
     const Sizes& z = h->z;
     hipStream_t s = h->stream;
+    h->negative_zero_weights = has_negative_zero(m.rec_weight, z.ns) || has_negative_zero(m.in_weight, z.ni);
     upload(h->canon.threshold, m.threshold, z.n * 4, s);
     upload(h->canon.rec_weight, m.rec_weight, z.ns * 4, s);
     upload(h->canon.in_weight, m.in_weight, z.ni * 4, s);
@@ -960,6 +1069,7 @@ size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<HostContext>
     const uint64_t spo = h->cfg.device.context_slots_per_order;
     HostContext master = download_context(h, h->canon);
     sync(h->stream);
+    const HostContext before = master;
     const size_t lanes = lane_ctx.size();
     // per-lane deltas against the pre-merge canonical (context_deltas_for_slots)
     std::vector<std::vector<ContextDelta>> deltas(lanes);
@@ -1049,6 +1159,16 @@ size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<HostContext>
     upload(h->canon.ctx_keys, master.keys.data(), z.slots * 8, h->stream);
     upload(h->canon.ctx_obs, master.obs.data(), z.slots * 4, h->stream);
     upload(h->canon.ctx_emb, master.emb.data(), z.slots * z.e * 4, h->stream);
+    // the slots the merge rewrote are host-stale
+    std::vector<uint32_t> stale = download_bits(h, h->stale_bits[4], z.slots);
+    sync(h->stream);
+    for (uint64_t slot = 0; slot < z.slots; ++slot) {
+        const bool changed = master.keys[slot] != before.keys[slot] || master.obs[slot] != before.obs[slot] ||
+                             !std::equal(master.emb.begin() + slot * E, master.emb.begin() + (slot + 1) * E,
+                                         before.emb.begin() + slot * E);
+        if (changed) stale[slot >> 5] |= 1u << (slot & 31);
+    }
+    upload(h->stale_bits[4], stale.data(), stale.size() * 4, h->stream);
     sync(h->stream);
     return merged.size();
 }
@@ -1131,6 +1251,11 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes, uint32_t
         m.updates = counter;
         m.lane_changes = counter + 1;
         m.error = error;
+        // merged canonical elements are host-stale (bias and context output: whole)
+        m.stale = jobs[j].kind == kMergeBias ? h->stale_flags
+                  : jobs[j].kind == kMergeContextOut ? h->stale_flags + 1
+                  : h->stale_bits[jobs[j].kind];
+        m.stale_flag = (jobs[j].kind == kMergeBias || jobs[j].kind == kMergeContextOut) ? 1u : 0u;
         uint64_t blocks = std::min<uint64_t>((m.count + kThreads - 1) / kThreads, 4096);
         hipLaunchKernelGGL(leo_merge_fixed, dim3(static_cast<uint32_t>(std::max<uint64_t>(blocks, 1))), dim3(kThreads), 0,
                            h->stream, m);
@@ -1278,6 +1403,110 @@ void story_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets
     rep.merge_context_keys = ctx;
     rep.story_seconds += run_seconds;
     rep.merge_seconds += merge_seconds;
+}
+
+// synchronize_model on a host mirror (cuda.rs:2817-2825, 5657-5760): every
+// element marked changed (tracked) or host-stale is gathered from the
+// canonical image into the mirror; then nothing is stale.
+void synchronize_host(LeoHipRuntime* h, LeoModelView& m) {
+    const Sizes& z = h->z;
+    const LaneDesc& d = h->canonical->desc;
+    std::vector<std::vector<uint32_t>> bits(5), stale(5);
+    for (int i = 0; i < 5; ++i) {
+        bits[i] = download_bits(h, change_bits(d, i), set_size(z, i));
+        stale[i] = download_bits(h, h->stale_bits[i], set_size(z, i));
+    }
+    uint32_t flags[2] = {0, 0}, stale_flags[2] = {0, 0};
+    download(flags, &d.ctl->bias_dirty, 8, h->stream);
+    download(stale_flags, h->stale_flags, 8, h->stream);
+    sync(h->stream);
+    std::vector<uint32_t> index[5];
+    for (int i = 0; i < 5; ++i) {
+        for (size_t w = 0; w < bits[i].size(); ++w) bits[i][w] |= stale[i][w];
+        for (uint64_t v : bits_to_indices(bits[i], set_size(z, i))) index[i].push_back(static_cast<uint32_t>(v));
+    }
+    float* single_targets[3] = {m.threshold, m.rec_weight, m.in_weight};
+    float* single_sources[3] = {h->canon.threshold, h->canon.rec_weight, h->canon.in_weight};
+    for (int i = 0; i < 3; ++i) {
+        std::vector<float> values(index[i].size());
+        sparse_move(h, single_sources[i], index[i].data(), index[i].size(), 0, 0, values.data(), false);
+        for (size_t k = 0; k < index[i].size(); ++k) single_targets[i][index[i][k]] = values[k];
+    }
+    {
+        // output rows: neuron-major on the device, output-major on the host
+        const std::vector<uint32_t>& rows = index[3];
+        std::vector<float> values(rows.size() * kOutputs);
+        sparse_move(h, h->canon.out_w, rows.data(), rows.size(), kOutputs, kOutStride, values.data(), false);
+        for (size_t k = 0; k < rows.size(); ++k)
+            for (uint64_t o = 0; o < kOutputs; ++o) m.out_weight[o * z.n + rows[k]] = values[k * kOutputs + o];
+    }
+    if (!index[4].empty()) {
+        // the context tables are small: read whole, copy the marked slots
+        HostContext c = download_context(h, h->canon);
+        sync(h->stream);
+        for (uint32_t slot : index[4]) {
+            m.ctx_keys[slot] = c.keys[slot];
+            m.ctx_obs[slot] = c.obs[slot];
+            std::copy(c.emb.begin() + slot * z.e, c.emb.begin() + (slot + 1) * z.e, m.ctx_emb + slot * z.e);
+        }
+    }
+    if (flags[0] | stale_flags[0]) download(m.bias, h->canon.bias, kOutputs * 4, h->stream);
+    if (flags[1] | stale_flags[1]) download(m.ctx_out, h->canon.ctx_out, kOutputs * z.e * 4, h->stream);
+    clear_stale(h);
+    sync(h->stream);
+    m.generation = h->generation;
+    m.parameter_revision = h->revision;
+    m.statistics = h->stats;
+}
+
+// PackedSparseModelUpdate::apply_to_model (parallel.rs:186-302) on the
+// canonical device image, with the reference's index and size checks.
+void apply_packed(LeoHipRuntime* h, const LeoPackedUpdate& u, bool end_tracking) {
+    const Sizes& z = h->z;
+    auto need = [](bool ok, const char* what) {
+        if (!ok) throw Error(LEO_ERR_INVALID_ARGUMENT, what);
+    };
+    auto check_indices = [&](const uint32_t* idx, const void* values, uint64_t count, uint64_t limit, const char* label) {
+        need(count == 0 || (idx && values), label);
+        for (uint64_t k = 0; k < count; ++k)
+            if (idx[k] >= limit) throw Error(LEO_ERR_INVALID_ARGUMENT, std::string(label) + " packed sparse index is outside model");
+    };
+    check_indices(u.threshold_indices, u.threshold_values, u.threshold_count, z.n, "threshold");
+    check_indices(u.recurrent_indices, u.recurrent_values, u.recurrent_count, z.ns, "recurrent");
+    check_indices(u.input_indices, u.input_values, u.input_count, z.ni, "input");
+    check_indices(u.output_neurons, u.output_values_by_neuron, u.output_count, z.n, "packed output neuron");
+    check_indices(u.context_slots, u.context_embeddings, u.context_count, z.slots, "packed context slot");
+    need(u.context_count == 0 || (u.context_keys && u.context_observations), "packed context rows have invalid dimensions");
+    sparse_move(h, h->canon.threshold, u.threshold_indices, u.threshold_count, 0, 0,
+                const_cast<float*>(u.threshold_values), true);
+    sparse_move(h, h->canon.rec_weight, u.recurrent_indices, u.recurrent_count, 0, 0,
+                const_cast<float*>(u.recurrent_values), true);
+    sparse_move(h, h->canon.in_weight, u.input_indices, u.input_count, 0, 0, const_cast<float*>(u.input_values), true);
+    sparse_move(h, h->canon.out_w, u.output_neurons, u.output_count, kOutputs, kOutStride,
+                const_cast<float*>(u.output_values_by_neuron), true);
+    if (u.context_count) {
+        // keys as rows of two 32-bit words, observations as words, embeddings as rows of E
+        std::vector<float> keys(u.context_count * 2), obs(u.context_count);
+        std::memcpy(keys.data(), u.context_keys, u.context_count * 8);
+        std::memcpy(obs.data(), u.context_observations, u.context_count * 4);
+        sparse_move(h, reinterpret_cast<float*>(h->canon.ctx_keys), u.context_slots, u.context_count, 2, 2, keys.data(), true);
+        sparse_move(h, reinterpret_cast<float*>(h->canon.ctx_obs), u.context_slots, u.context_count, 0, 0, obs.data(), true);
+        sparse_move(h, h->canon.ctx_emb, u.context_slots, u.context_count, static_cast<uint32_t>(z.e),
+                    static_cast<uint32_t>(z.e), const_cast<float*>(u.context_embeddings), true);
+    }
+    if (u.output_bias) upload(h->canon.bias, u.output_bias, kOutputs * 4, h->stream);
+    if (u.context_output_weights) upload(h->canon.ctx_out, u.context_output_weights, kOutputs * z.e * 4, h->stream);
+    // the mirror that packed this update holds the bias / projection it carries
+    uint32_t carried[2] = {u.output_bias ? 1u : 0u, u.context_output_weights ? 1u : 0u};
+    for (int k = 0; k < 2; ++k)
+        if (carried[k]) LEO_HIP_CHECK(hipMemsetAsync(h->stale_flags + k, 0, 4, h->stream));
+    sync(h->stream);
+    if (has_negative_zero(u.recurrent_values, u.recurrent_count) || has_negative_zero(u.input_values, u.input_count))
+        h->negative_zero_weights = true;
+    h->generation = u.generation;
+    h->revision = u.parameter_revision;
+    h->stats = u.statistics;
+    if (end_tracking) h->tracking = false;
 }
 
 // training.rs:1782-1830
@@ -1523,6 +1752,7 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         h->canonical = std::make_unique<leo::Lane>();
         leo::allocate_lane_state(*h->canonical, h->z, h->stream);
         h->canonical->desc.p = h->canon;
+        leo::allocate_stale(h.get());
         h->lane_descs.allocate(sizeof(leo::LaneDesc) * std::max<uint32_t>(h->max_lanes, 1));
         std::vector<leo::Lane*> lanes{h->canonical.get()};
         leo::reset_lane_objects(h.get(), lanes, true, 0);  // Runtime::new: tick 0, empty state
@@ -1588,7 +1818,7 @@ int32_t leo_hip_enable_parameter_tracking(LeoHipRuntime* h) {
         // replay, training.rs:1628), unlike the CPU Runtime's no-op when
         // tracking is already on (runtime.rs:310-320)
         h->tracking = true;
-        leo::clear_changes(*h->canonical, h->z, h->stream);
+        leo::fold_changes(h);  // the changes so far stay marked for the host mirror
         leo::sync(h->stream);
     });
 }
@@ -1725,6 +1955,8 @@ int32_t leo_hip_download_model(LeoHipRuntime* h, LeoModelView* out) {
         leo::BusyGuard g(h);
         if (!out) throw Error(LEO_ERR_INVALID_ARGUMENT, "null model view");
         leo::download_model(h, *out);
+        leo::clear_stale(h);
+        leo::sync(h->stream);
     });
 }
 
@@ -1743,8 +1975,34 @@ int32_t leo_hip_upload_model(LeoHipRuntime* h, const LeoModelView* model) {
         h->canonical->desc.p = p;
         std::vector<leo::Lane*> lanes{h->canonical.get()};
         leo::reset_lane_objects(h, lanes, true, tick);
-        if (h->tracking) leo::clear_changes(*h->canonical, h->z, h->stream);
+        // the caller's mirror is the model just uploaded
+        leo::clear_changes(*h->canonical, h->z, h->stream);
+        leo::clear_stale(h);
         leo::sync(h->stream);
+    });
+}
+
+int32_t leo_hip_synchronize_model(LeoHipRuntime* h, LeoModelView* mirror) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (!mirror) throw Error(LEO_ERR_INVALID_ARGUMENT, "null model view");
+        leo::synchronize_host(h, *mirror);
+    });
+}
+
+int32_t leo_hip_synchronize_packed_model(LeoHipRuntime* h, const LeoPackedUpdate* update) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (!update) throw Error(LEO_ERR_INVALID_ARGUMENT, "null packed update");
+        leo::apply_packed(h, *update, true);
+    });
+}
+
+int32_t leo_hip_commit_packed_host_model(LeoHipRuntime* h, const LeoPackedUpdate* update) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (!update) throw Error(LEO_ERR_INVALID_ARGUMENT, "null packed update");
+        leo::apply_packed(h, *update, false);
     });
 }
 

@@ -127,7 +127,21 @@ class LeoKernelStats(ctypes.Structure):
         ("section_launches", ctypes.c_uint64 * 2), ("section_lane_steps", ctypes.c_uint64 * 2),
         ("section_kernel_ms", ctypes.c_double * 2), ("section_bytes", ctypes.c_double * 2),
         ("merge_lane_changes", ctypes.c_uint64), ("merge_elements", ctypes.c_uint64),
-        ("merge_bytes", ctypes.c_double),
+        ("merge_bytes", ctypes.c_double), ("learning_slots", ctypes.c_uint64),
+    ]
+
+
+class LeoPackedUpdate(ctypes.Structure):
+    _fields_ = [
+        ("threshold_indices", _P), ("threshold_values", _P), ("threshold_count", ctypes.c_uint64),
+        ("recurrent_indices", _P), ("recurrent_values", _P), ("recurrent_count", ctypes.c_uint64),
+        ("input_indices", _P), ("input_values", _P), ("input_count", ctypes.c_uint64),
+        ("output_neurons", _P), ("output_values_by_neuron", _P), ("output_count", ctypes.c_uint64),
+        ("context_slots", _P), ("context_keys", _P), ("context_observations", _P), ("context_embeddings", _P),
+        ("context_count", ctypes.c_uint64),
+        ("output_bias", _P), ("context_output_weights", _P),
+        ("generation", ctypes.c_uint64), ("parameter_revision", ctypes.c_uint64),
+        ("statistics", LeoStatistics),
     ]
 
 
@@ -155,6 +169,9 @@ SIGNATURES = {
     "leo_hip_train_batch": (_I32, [_P, _P, _P, _U32, _I32, _U32, _P, _P]),
     "leo_hip_download_model": (_I32, [_P, _P]),
     "leo_hip_upload_model": (_I32, [_P, _P]),
+    "leo_hip_synchronize_model": (_I32, [_P, _P]),
+    "leo_hip_synchronize_packed_model": (_I32, [_P, _P]),
+    "leo_hip_commit_packed_host_model": (_I32, [_P, _P]),
     "leo_hip_parameter_changes": (_I32, [_P, _I32, _P, _U64, _P, _P, _P]),
     "leo_hip_probabilities": (_I32, [_P, _P]),
     "leo_hip_read_list": (_I32, [_P, _I32, _P, _U64, _P]),

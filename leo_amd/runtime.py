@@ -78,6 +78,63 @@ class BatchReport:
         return cls(**{name: getattr(r, name) for name, _ in native.LeoBatchReport._fields_})
 
 
+class PackedUpdate:
+    """PackedSparseModelUpdate (crates/leo-core/src/parallel.rs:79-183): the
+    canonical values of a change set, packed once per logical batch."""
+
+    def __init__(self, model: Model, changes: Dict[str, object]):
+        n = model.neuron_count
+        dim = model.config.context.embedding_dim
+        self.threshold_indices = np.asarray(changes["threshold"], dtype=np.uint32)
+        self.threshold_values = model.threshold[self.threshold_indices].astype(np.float32)
+        self.recurrent_indices = np.asarray(changes["recurrent_weight"], dtype=np.uint32)
+        self.recurrent_values = model.rec_weight[self.recurrent_indices].astype(np.float32)
+        self.input_indices = np.asarray(changes["input_weight"], dtype=np.uint32)
+        self.input_values = model.in_weight[self.input_indices].astype(np.float32)
+        self.output_neurons = np.asarray(changes["output_neurons"], dtype=np.uint32)
+        # one contiguous row of the 257 outputs per changed neuron
+        out = model.out_weight.reshape(257, n)
+        self.output_values_by_neuron = np.ascontiguousarray(out[:, self.output_neurons].T).reshape(-1)
+        self.context_slots = np.asarray(changes["context_slots"], dtype=np.uint32)
+        self.context_keys = model.ctx_keys[self.context_slots].astype(np.uint64)
+        self.context_observations = model.ctx_obs[self.context_slots].astype(np.uint32)
+        emb = model.ctx_emb.reshape(-1, dim)
+        self.context_embeddings = np.ascontiguousarray(emb[self.context_slots]).reshape(-1)
+        self.output_bias = model.bias.copy() if changes["output_bias_dirty"] else None
+        self.context_output_weights = model.ctx_out.copy() if changes["context_output_dirty"] else None
+        self.generation = model.generation
+        self.parameter_revision = model.parameter_revision
+        self.statistics = dict(model.statistics)
+
+    @classmethod
+    def from_model(cls, model: Model, changes: Dict[str, object]) -> "PackedUpdate":
+        return cls(model, changes)
+
+    def to_c(self) -> native.LeoPackedUpdate:
+        u = native.LeoPackedUpdate()
+        for name in ("threshold", "recurrent", "input"):
+            idx, val = getattr(self, f"{name}_indices"), getattr(self, f"{name}_values")
+            setattr(u, f"{name}_indices", idx.ctypes.data)
+            setattr(u, f"{name}_values", val.ctypes.data)
+            setattr(u, f"{name}_count", idx.size)
+        u.output_neurons = self.output_neurons.ctypes.data
+        u.output_values_by_neuron = self.output_values_by_neuron.ctypes.data
+        u.output_count = self.output_neurons.size
+        u.context_slots = self.context_slots.ctypes.data
+        u.context_keys = self.context_keys.ctypes.data
+        u.context_observations = self.context_observations.ctypes.data
+        u.context_embeddings = self.context_embeddings.ctypes.data
+        u.context_count = self.context_slots.size
+        u.output_bias = self.output_bias.ctypes.data if self.output_bias is not None else None
+        u.context_output_weights = (self.context_output_weights.ctypes.data
+                                    if self.context_output_weights is not None else None)
+        u.generation = self.generation
+        u.parameter_revision = self.parameter_revision
+        for k, v in self.statistics.items():
+            setattr(u.statistics, k, v)
+        return u
+
+
 def pack_stories(stories: Sequence[bytes]) -> Tuple[np.ndarray, np.ndarray]:
     """Concatenate stories into (bytes, offsets[count+1])."""
     offsets = np.zeros(len(stories) + 1, dtype=np.uint64)
@@ -135,6 +192,23 @@ class HipRuntime:
         """model_mut() replacement: upload a whole model (backend.rs:357)."""
         view = model.view()
         self._call("leo_hip_upload_model", ctypes.byref(view))
+
+    def synchronize_model(self, mirror: Model) -> None:
+        """synchronize_model() on a host mirror (cuda.rs:2817-2825): only the
+        elements changed since the mirror's last synchronisation are copied."""
+        view = mirror.view()
+        self._call("leo_hip_synchronize_model", ctypes.byref(view))
+        mirror._absorb(view)
+
+    def synchronize_packed_model(self, update: PackedUpdate) -> None:
+        """backend.rs:374-376 / cuda.rs:2844-2857: scatter; tracking ends."""
+        u = update.to_c()
+        self._call("leo_hip_synchronize_packed_model", ctypes.byref(u))
+
+    def commit_packed_host_model(self, update: PackedUpdate) -> None:
+        """backend.rs:378-387 / cuda.rs:2859-2868: scatter; tracking kept."""
+        u = update.to_c()
+        self._call("leo_hip_commit_packed_host_model", ctypes.byref(u))
 
     def begin_document(self) -> None:
         self._call("leo_hip_begin_document")

@@ -125,6 +125,7 @@ def load() -> ctypes.CDLL:
         "oracle_finish_document": (ctypes.c_int32, [_P]),
         "oracle_reset_transient_state": (ctypes.c_int32, [_P]),
         "oracle_enable_parameter_tracking": (ctypes.c_int32, [_P]),
+        "oracle_restart_parameter_tracking": (ctypes.c_int32, [_P]),
         "oracle_changes_flags": (ctypes.c_int32, [_P, _P, _P]),
         "oracle_step": (ctypes.c_int32, [_P, ctypes.c_uint32, ctypes.c_int32, ctypes.c_int32, _P]),
         "oracle_current_tick": (ctypes.c_uint64, [_P]),
@@ -269,6 +270,10 @@ class OracleRuntime:
 
     def enable_parameter_tracking(self):
         _check(self.lib.oracle_enable_parameter_tracking(self.handle))
+
+    def restart_parameter_tracking(self):
+        """The GPU adapter's enable_parameter_tracking: fresh change sets on every call."""
+        _check(self.lib.oracle_restart_parameter_tracking(self.handle))
 
     def step(self, symbol: int, target: Optional[int], permission: int) -> OracleStepMetrics:
         m = OracleStepMetrics()

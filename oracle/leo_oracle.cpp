@@ -471,6 +471,20 @@ struct Runtime {
         ch_ctx_mark.assign(model.ctx_keys.size(), 0);
     }
 
+    // The GPU adapter's enable_parameter_tracking (cuda.rs:2827-2837): a fresh
+    // change set and clean dirty flags on every call, also when tracking is on.
+    void restart_parameter_tracking() {
+        track = false;
+        enable_parameter_tracking();
+        ch_threshold.clear();
+        ch_rec.clear();
+        ch_in.clear();
+        ch_out.clear();
+        ch_ctx.clear();
+        output_bias_dirty = false;
+        context_output_dirty = false;
+    }
+
     ParameterChanges parameter_changes() const {
         ParameterChanges c;
         c.threshold = ch_threshold;
@@ -1809,6 +1823,7 @@ int32_t oracle_begin_document(OracleRuntime* r) { return guard([&] { r->rt->rese
 int32_t oracle_finish_document(OracleRuntime* r) { return guard([&] { r->rt->finish_document(); }); }
 int32_t oracle_reset_transient_state(OracleRuntime* r) { return guard([&] { r->rt->reset_transient_state(); }); }
 int32_t oracle_enable_parameter_tracking(OracleRuntime* r) { return guard([&] { r->rt->enable_parameter_tracking(); }); }
+int32_t oracle_restart_parameter_tracking(OracleRuntime* r) { return guard([&] { r->rt->restart_parameter_tracking(); }); }
 int32_t oracle_changes_flags(const OracleRuntime* r, uint32_t* bias_dirty, uint32_t* ctx_dirty) {
     *bias_dirty = r->rt->output_bias_dirty;
     *ctx_dirty = r->rt->context_output_dirty;

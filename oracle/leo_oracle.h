@@ -208,6 +208,9 @@ int32_t oracle_begin_document(OracleRuntime* runtime);
 int32_t oracle_finish_document(OracleRuntime* runtime);
 int32_t oracle_reset_transient_state(OracleRuntime* runtime);
 int32_t oracle_enable_parameter_tracking(OracleRuntime* runtime);
+/* The GPU adapter's tracking restart (cuda.rs:2827-2837): empty change sets
+ * and clean dirty flags on every call. */
+int32_t oracle_restart_parameter_tracking(OracleRuntime* runtime);
 int32_t oracle_changes_flags(const OracleRuntime* runtime, uint32_t* bias_dirty,
                              uint32_t* context_output_dirty);
 int32_t oracle_step(OracleRuntime* runtime, uint32_t symbol, int32_t target, int32_t permission,

@@ -1,13 +1,26 @@
-"""Writes tests/golden/workloadA_batches.npz and .json: the CPU oracle's results
-for two logical batches of workload A (1,024 units) with 30% replay, from the
-seeded synthetic model and the first three seeded stories.
+"""Writes the CPU oracle's golden fixtures for workload A (1,024 units, one
+logical worker, 30% replay), from the seeded synthetic model and seeded
+stories:
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py          # workloadA_batches.npz / .json
+    python tests/golden/make_golden.py --long   # workloadA_1M.json
 
-The fixture holds the inputs (story bytes, offsets), every per-step loss, the
-replay schedule counts, the full threshold and bias vectors, and SHA-256
-digests of every learned tensor. tests/test_golden.py checks that the oracle
-still reproduces it (CPU) and that the HIP path matches it bit for bit (GPU).
+workloadA_batches holds two logical batches: the inputs (story bytes,
+offsets), every per-step loss, the replay schedule counts, the full threshold
+and bias vectors, and SHA-256 digests of every learned tensor.
+
+workloadA_1M holds a run over the first stories of the workload until more
+than 2^20 bytes are trained, one story per logical batch (the workload's single
+worker trains in place, training.rs:1548-1582) with replay: at checkpoints
+after 2^16, 2^18, 2^19 and 2^20 trained bytes, the running bits per byte, the
+statistics, the parameter revision, the digests of every learned tensor and
+how many slots of each context order are taken. The six context orders of
+4,096 slots fill within the first checkpoints, so every later allocation
+evicts the weakest slot of its probe window.
+
+tests/test_golden.py checks that the oracle still reproduces them (CPU; the
+long run up to its first checkpoint) and that the HIP path matches them bit
+for bit (GPU).
 """
 from __future__ import annotations
 
@@ -73,5 +86,56 @@ def main() -> None:
     print("wrote", HERE / "workloadA_batches.npz", "and .json")
 
 
+LONG_CHECKPOINTS = (1 << 16, 1 << 18, 1 << 19, 1 << 20)
+LONG_STORIES = 2000  # more than enough stories of U[256,1024] bytes for 2^20 bytes
+
+
+def long_run(runtime, train, stories, checkpoints=LONG_CHECKPOINTS, on_checkpoint=None):
+    """Trains one story per logical batch until the last checkpoint is passed;
+    returns the checkpoint records (the first story boundary at or past each)."""
+    records, trained, pending = [], 0, list(checkpoints)
+    for index, story in enumerate(stories):
+        train(runtime, story)
+        trained += len(story)
+        if pending and trained >= pending[0]:
+            pending.pop(0)
+            model = runtime.model()
+            spo = model.config.context.slots_per_order
+            rec = model_record(model)
+            rec.update(stories=index + 1, trained_bytes=trained, bits_per_byte=float(model.bits_per_byte()),
+                       context_slots_taken=[int((model.ctx_keys[o * spo:(o + 1) * spo] != 0).sum())
+                                            for o in range(model.config.context.max_order)])
+            records.append(rec)
+            if on_checkpoint:
+                on_checkpoint(rec)
+            if not pending:
+                break
+    return records
+
+
+def long_stories():
+    w = WORKLOADS["A"]
+    data, offsets = synthetic_stories(w, LONG_STORIES)
+    return w, [data[int(offsets[i]):int(offsets[i + 1])].tobytes() for i in range(LONG_STORIES)]
+
+
+def main_long() -> None:
+    from oracle import binding
+
+    w, stories = long_stories()
+    model = workload_model(w)
+    rt = binding.OracleRuntime(model)
+    records = long_run(rt, lambda r, s: r.train_story_batch([s], binding.TRAINING, replay=True), stories,
+                       on_checkpoint=lambda rec: print("checkpoint", rec["trained_bytes"], rec["bits_per_byte"],
+                                                       flush=True))
+    out = {"workload": "A", "checkpoints": list(LONG_CHECKPOINTS), "initial": model_record(model),
+           "records": records}
+    (HERE / "workloadA_1M.json").write_text(json.dumps(out, indent=1, sort_keys=True) + "\n")
+    print("wrote", HERE / "workloadA_1M.json")
+
+
 if __name__ == "__main__":
-    main()
+    if "--long" in sys.argv[1:]:
+        main_long()
+    else:
+        main()

@@ -85,3 +85,69 @@ def test_hip_path_matches_fixture(require_gpu):
         _check_model(final, record["final"], "hip")
     finally:
         rt.close()
+
+
+# --- the long run (tests/golden/make_golden.py --long) -----------------------------------
+def _long_fixture():
+    return json.loads((GOLDEN / "workloadA_1M.json").read_text())
+
+
+def _check_long_record(got, want, label):
+    assert got["stories"] == want["stories"] and got["trained_bytes"] == want["trained_bytes"], label
+    assert got["digests"] == want["digests"], f"{label}: tensor digests"
+    assert got["statistics"] == want["statistics"], f"{label}: statistics"
+    assert got["parameter_revision"] == want["parameter_revision"], label
+    assert got["context_slots_taken"] == want["context_slots_taken"], label
+    # the north star's criterion is running bits per byte within 1e-3; the
+    # path is bit-exact, so the figure is identical
+    assert abs(got["bits_per_byte"] - want["bits_per_byte"]) <= 1e-3, label
+    assert got["bits_per_byte"] == want["bits_per_byte"], label
+
+
+def test_long_fixture_fills_the_context_tables():
+    record = _long_fixture()
+    last = record["records"][-1]
+    assert last["trained_bytes"] >= 1 << 20
+    spo = 4096
+    # orders 3-6 are full from the second checkpoint on: their allocations evict
+    for rec in record["records"][1:]:
+        assert all(taken == spo for taken in rec["context_slots_taken"][2:]), rec["context_slots_taken"]
+
+
+def test_oracle_reproduces_long_fixture_first_checkpoint(oracle):
+    import sys
+
+    sys.path.insert(0, str(GOLDEN))
+    import make_golden
+
+    record = _long_fixture()
+    w, stories = make_golden.long_stories()
+    rt = oracle.OracleRuntime(workload_model(w))
+    got = make_golden.long_run(rt, lambda r, s: r.train_story_batch([s], oracle.TRAINING, replay=True), stories,
+                               checkpoints=record["checkpoints"][:1])
+    _check_long_record(got[0], record["records"][0], "oracle, first checkpoint")
+
+
+@pytest.mark.gpu
+def test_hip_path_matches_long_fixture(require_gpu):
+    import sys
+
+    from leo_amd.runtime import HipRuntime
+
+    sys.path.insert(0, str(GOLDEN))
+    import make_golden
+
+    record = _long_fixture()
+    w, stories = make_golden.long_stories()
+    rt = HipRuntime(workload_model(w), device=0, max_lanes=1)
+    try:
+        print("golden: workload A, one story per batch with replay, past 2^20 trained bytes", flush=True)
+        got = make_golden.long_run(rt, lambda r, s: r.train_batch([s], native.TRAINING, replay=True), stories,
+                                   checkpoints=record["checkpoints"],
+                                   on_checkpoint=lambda rec: print("checkpoint", rec["trained_bytes"],
+                                                                   rec["bits_per_byte"], flush=True))
+    finally:
+        rt.close()
+    assert len(got) == len(record["records"])
+    for g, want in zip(got, record["records"]):
+        _check_long_record(g, want, f"hip at {want['trained_bytes']} bytes")

@@ -265,3 +265,47 @@ def test_dense_touch_multi_window_parity(require_gpu, oracle, monkeypatch, wgs):
     assert stats["touched"] / max(stats["lane_steps"], 1) > int(wgs) * 4 * 256
     assert_models_equal(gpu.model(), cpu.model(), "after document")
     gpu.close()
+
+
+def _bitwise_weights_equal(got, want, label):
+    # np.array_equal treats -0.0 and +0.0 alike; the bit patterns must match too
+    for name in ("rec_weight", "in_weight"):
+        g = getattr(got, name).view(np.uint32)
+        c = getattr(want, name).view(np.uint32)
+        assert np.array_equal(g, c), f"{label}: {name} bits differ at {np.nonzero(g != c)[0][:8]}"
+
+
+@pytest.mark.parametrize("negative_zero", [False, True])
+def test_learning_slots_and_negative_zero_weights(require_gpu, oracle, negative_zero):
+    # Learning slots are the kept eligible slots with nonzero eligibility;
+    # a -0.0 recurrent or input weight switches every kept slot back to a
+    # learning slot, and the weights must then match the oracle bit for bit
+    # (an update with zero eligibility turns an excitatory -0.0 into +0.0).
+    cfg = small_redundant_config()
+    model = Model.initialize(cfg)
+    if negative_zero:
+        S = cfg.model.synapses_per_neuron
+        excitatory = np.nonzero(model.neuron_type == 0)[0][:64]
+        for n in excitatory:
+            model.rec_weight[n * S:(n + 1) * S] = np.float32(-0.0)
+        model.in_weight[::3] = np.float32(-0.0)
+        model.validate()
+    cpu = oracle.OracleRuntime(model)
+    gpu = _runtime(model)
+    try:
+        for batch in ([story(700, 120)], [story(701 + k, 60 + 9 * k) for k in range(3)]):
+            crep, closs = cpu.train_story_batch(batch, oracle.TRAINING, replay=True)
+            grep, gloss = gpu.train_batch(batch, native.TRAINING, replay=True)
+            for a, b in zip(gloss, closs):
+                assert np.array_equal(a, b)
+            assert grep.replay_steps == crep.replay_steps
+        got, want = gpu.model(), cpu.model()
+        assert_models_equal(got, want, f"negative zero {negative_zero}")
+        _bitwise_weights_equal(got, want, f"negative zero {negative_zero}")
+        stats = gpu.kernel_stats()
+        assert stats["learning_slots"] > 0
+        if not negative_zero:
+            # far fewer learning slots than kept eligible slots
+            assert stats["learning_slots"] < stats["kept_rec"] + stats["kept_in"]
+    finally:
+        gpu.close()
