@@ -351,6 +351,16 @@ int32_t leo_hip_synchronize_packed_model(LeoHipRuntime* runtime, const LeoPacked
 /* RuntimeBackend::commit_packed_host_model (backend.rs:378-387, cuda.rs:2859-2868):
  * the same scatter, keeping parameter tracking as it is. */
 int32_t leo_hip_commit_packed_host_model(LeoHipRuntime* runtime, const LeoPackedUpdate* update);
+/* No counterpart in the reference: leo_hip_commit_packed_host_model for
+ * callers that cannot allocate device memory (code under graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). It stages the packed rows
+ * in a fixed 8 MiB device scratch array per GPU instead of the runtime's
+ * growable buffer, and calls no device allocation. An update one of whose
+ * tensors needs more than 8 MiB of staging (indices and values, e.g. more
+ * than about 8,100 output rows or 1M recurrent elements) is refused with
+ * LEO_ERR_INVALID_ARGUMENT before anything is written. All runtimes on a GPU
+ * share its scratch: calls that overlap on one GPU race. */
+int32_t leo_hip_commit_packed_host_model_no_alloc(LeoHipRuntime* runtime, const LeoPackedUpdate* update);
 /* RuntimeBackend::model_mut (backend.rs:357): replace the canonical model. */
 int32_t leo_hip_upload_model(LeoHipRuntime* runtime, const LeoModelView* model);
 /* RuntimeBackend::parameter_changes (backend.rs:359): the tracked index set

@@ -20,6 +20,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
@@ -409,19 +410,67 @@ void fold_changes(LeoHipRuntime* h) {
     LEO_HIP_CHECK(hipGetLastError());
 }
 
+// Scratch of the allocation-free packed commit
+// (leo_hip_commit_packed_host_model_no_alloc): a file-scope device array, one
+// copy per GPU, held until the process ends. Host code uses its per-device
+// address from hipGetSymbolAddress, never the array's name. Every call on a
+// GPU shares that GPU's copy: calls that overlap on one GPU race.
+constexpr size_t kStaticScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+char* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The device address of `scratch` on `device` (which must be current),
+// looked up once per device.
+char* static_scratch(int device) {
+    if (device < 0 || device >= kMaxScratchDevices)
+        throw Error(LEO_ERR_DEVICE, "device index beyond the static scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[device]) {
+        void* ptr = nullptr;
+        LEO_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (!ptr) throw Error(LEO_ERR_DEVICE, "static scratch has no device address");
+        g_scratch_ptr[device] = static_cast<char*>(ptr);
+    }
+    return g_scratch_ptr[device];
+}
+
+// Bytes a sparse move of `count` elements (rows of `per`) stages: the u32
+// indices (256-byte aligned) and the values.
+size_t move_bytes(uint64_t count, uint64_t per) {
+    return count ? ((count * 4 + 255) & ~size_t(255)) + count * per * 4 : 0;
+}
+
+// Device staging of sparse moves: the runtime's growable scratch, or a
+// fixed buffer that must not grow (the allocation-free entry point).
+struct Staging {
+    char* fixed = nullptr;   // non-null: use this buffer of `capacity` bytes, never allocate
+    size_t capacity = 0;
+};
+
 // Moves `count` elements (rows of `row` elements at `stride` when row > 0)
 // between a canonical tensor and the host: gathers into `values` when
 // to_tensor is false, scatters `values` when true.
 void sparse_move(LeoHipRuntime* h, float* tensor, const uint32_t* index, uint64_t count, uint32_t row, uint32_t stride,
-                 float* values, bool to_tensor) {
+                 const float* values_in, float* values_out, bool to_tensor, const Staging& staging = Staging{}) {
     if (count == 0) return;
     const uint64_t per = row ? row : 1;
     const size_t index_bytes = (count * 4 + 255) & ~size_t(255);
     const size_t need = index_bytes + count * per * 4;
-    if (h->move_scratch.bytes < need) h->move_scratch.allocate(need);
-    char* base = h->move_scratch.base;
+    char* base = staging.fixed;
+    if (base) {
+        if (need > staging.capacity)
+            throw Error(LEO_ERR_INVALID_ARGUMENT, "sparse move of " + std::to_string(need) +
+                                                      " bytes exceeds the fixed scratch of " +
+                                                      std::to_string(staging.capacity) + " bytes");
+    } else {
+        if (h->move_scratch.bytes < need) h->move_scratch.allocate(need);
+        base = h->move_scratch.base;
+    }
     upload(base, index, count * 4, h->stream);
-    if (to_tensor) upload(base + index_bytes, values, count * per * 4, h->stream);
+    if (to_tensor) upload(base + index_bytes, values_in, count * per * 4, h->stream);
     SparseMove mv{};
     mv.tensor = tensor;
     mv.index = reinterpret_cast<const uint32_t*>(base);
@@ -433,7 +482,7 @@ void sparse_move(LeoHipRuntime* h, float* tensor, const uint32_t* index, uint64_
     const uint64_t blocks = std::min<uint64_t>((count * per + kThreads - 1) / kThreads, 4096);
     hipLaunchKernelGGL(leo_sparse_move, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, h->stream, mv);
     LEO_HIP_CHECK(hipGetLastError());
-    if (!to_tensor) download(values, base + index_bytes, count * per * 4, h->stream);
+    if (!to_tensor) download(values_out, base + index_bytes, count * per * 4, h->stream);
     sync(h->stream);
 }
 
@@ -1429,14 +1478,14 @@ void synchronize_host(LeoHipRuntime* h, LeoModelView& m) {
     float* single_sources[3] = {h->canon.threshold, h->canon.rec_weight, h->canon.in_weight};
     for (int i = 0; i < 3; ++i) {
         std::vector<float> values(index[i].size());
-        sparse_move(h, single_sources[i], index[i].data(), index[i].size(), 0, 0, values.data(), false);
+        sparse_move(h, single_sources[i], index[i].data(), index[i].size(), 0, 0, nullptr, values.data(), false);
         for (size_t k = 0; k < index[i].size(); ++k) single_targets[i][index[i][k]] = values[k];
     }
     {
         // output rows: neuron-major on the device, output-major on the host
         const std::vector<uint32_t>& rows = index[3];
         std::vector<float> values(rows.size() * kOutputs);
-        sparse_move(h, h->canon.out_w, rows.data(), rows.size(), kOutputs, kOutStride, values.data(), false);
+        sparse_move(h, h->canon.out_w, rows.data(), rows.size(), kOutputs, kOutStride, nullptr, values.data(), false);
         for (size_t k = 0; k < rows.size(); ++k)
             for (uint64_t o = 0; o < kOutputs; ++o) m.out_weight[o * z.n + rows[k]] = values[k * kOutputs + o];
     }
@@ -1461,7 +1510,7 @@ void synchronize_host(LeoHipRuntime* h, LeoModelView& m) {
 
 // PackedSparseModelUpdate::apply_to_model (parallel.rs:186-302) on the
 // canonical device image, with the reference's index and size checks.
-void apply_packed(LeoHipRuntime* h, const LeoPackedUpdate& u, bool end_tracking) {
+void apply_packed(LeoHipRuntime* h, const LeoPackedUpdate& u, bool end_tracking, const Staging& staging = Staging{}) {
     const Sizes& z = h->z;
     auto need = [](bool ok, const char* what) {
         if (!ok) throw Error(LEO_ERR_INVALID_ARGUMENT, what);
@@ -1477,22 +1526,32 @@ void apply_packed(LeoHipRuntime* h, const LeoPackedUpdate& u, bool end_tracking)
     check_indices(u.output_neurons, u.output_values_by_neuron, u.output_count, z.n, "packed output neuron");
     check_indices(u.context_slots, u.context_embeddings, u.context_count, z.slots, "packed context slot");
     need(u.context_count == 0 || (u.context_keys && u.context_observations), "packed context rows have invalid dimensions");
-    sparse_move(h, h->canon.threshold, u.threshold_indices, u.threshold_count, 0, 0,
-                const_cast<float*>(u.threshold_values), true);
-    sparse_move(h, h->canon.rec_weight, u.recurrent_indices, u.recurrent_count, 0, 0,
-                const_cast<float*>(u.recurrent_values), true);
-    sparse_move(h, h->canon.in_weight, u.input_indices, u.input_count, 0, 0, const_cast<float*>(u.input_values), true);
-    sparse_move(h, h->canon.out_w, u.output_neurons, u.output_count, kOutputs, kOutStride,
-                const_cast<float*>(u.output_values_by_neuron), true);
+    if (staging.fixed) {
+        // every move must fit before the first one writes
+        const size_t largest = std::max({move_bytes(u.threshold_count, 1), move_bytes(u.recurrent_count, 1),
+                                         move_bytes(u.input_count, 1), move_bytes(u.output_count, kOutputs),
+                                         move_bytes(u.context_count, std::max<uint64_t>(z.e, 2))});
+        if (largest > staging.capacity)
+            throw Error(LEO_ERR_INVALID_ARGUMENT, "packed update needs " + std::to_string(largest) +
+                                                      " bytes of scratch for one tensor; the allocation-free entry "
+                                                      "point holds " + std::to_string(staging.capacity));
+    }
+    sparse_move(h, h->canon.threshold, u.threshold_indices, u.threshold_count, 0, 0, u.threshold_values, nullptr, true,
+                staging);
+    sparse_move(h, h->canon.rec_weight, u.recurrent_indices, u.recurrent_count, 0, 0, u.recurrent_values, nullptr, true,
+                staging);
+    sparse_move(h, h->canon.in_weight, u.input_indices, u.input_count, 0, 0, u.input_values, nullptr, true, staging);
+    sparse_move(h, h->canon.out_w, u.output_neurons, u.output_count, kOutputs, kOutStride, u.output_values_by_neuron,
+                nullptr, true, staging);
     if (u.context_count) {
-        // keys as rows of two 32-bit words, observations as words, embeddings as rows of E
-        std::vector<float> keys(u.context_count * 2), obs(u.context_count);
-        std::memcpy(keys.data(), u.context_keys, u.context_count * 8);
-        std::memcpy(obs.data(), u.context_observations, u.context_count * 4);
-        sparse_move(h, reinterpret_cast<float*>(h->canon.ctx_keys), u.context_slots, u.context_count, 2, 2, keys.data(), true);
-        sparse_move(h, reinterpret_cast<float*>(h->canon.ctx_obs), u.context_slots, u.context_count, 0, 0, obs.data(), true);
+        // keys as rows of two 32-bit words, observations as words, embeddings
+        // as rows of E (moves copy the bits)
+        sparse_move(h, reinterpret_cast<float*>(h->canon.ctx_keys), u.context_slots, u.context_count, 2, 2,
+                    reinterpret_cast<const float*>(u.context_keys), nullptr, true, staging);
+        sparse_move(h, reinterpret_cast<float*>(h->canon.ctx_obs), u.context_slots, u.context_count, 0, 0,
+                    reinterpret_cast<const float*>(u.context_observations), nullptr, true, staging);
         sparse_move(h, h->canon.ctx_emb, u.context_slots, u.context_count, static_cast<uint32_t>(z.e),
-                    static_cast<uint32_t>(z.e), const_cast<float*>(u.context_embeddings), true);
+                    static_cast<uint32_t>(z.e), u.context_embeddings, nullptr, true, staging);
     }
     if (u.output_bias) upload(h->canon.bias, u.output_bias, kOutputs * 4, h->stream);
     if (u.context_output_weights) upload(h->canon.ctx_out, u.context_output_weights, kOutputs * z.e * 4, h->stream);
@@ -1753,6 +1812,7 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         leo::allocate_lane_state(*h->canonical, h->z, h->stream);
         h->canonical->desc.p = h->canon;
         leo::allocate_stale(h.get());
+        (void)leo::static_scratch(device);  // set-up of the allocation-free entry point on this device
         h->lane_descs.allocate(sizeof(leo::LaneDesc) * std::max<uint32_t>(h->max_lanes, 1));
         std::vector<leo::Lane*> lanes{h->canonical.get()};
         leo::reset_lane_objects(h.get(), lanes, true, 0);  // Runtime::new: tick 0, empty state
@@ -2003,6 +2063,17 @@ int32_t leo_hip_commit_packed_host_model(LeoHipRuntime* h, const LeoPackedUpdate
         leo::BusyGuard g(h);
         if (!update) throw Error(LEO_ERR_INVALID_ARGUMENT, "null packed update");
         leo::apply_packed(h, *update, false);
+    });
+}
+
+int32_t leo_hip_commit_packed_host_model_no_alloc(LeoHipRuntime* h, const LeoPackedUpdate* update) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (!update) throw Error(LEO_ERR_INVALID_ARGUMENT, "null packed update");
+        leo::Staging staging;
+        staging.fixed = leo::static_scratch(h->device);
+        staging.capacity = leo::kStaticScratchBytes;
+        leo::apply_packed(h, *update, false, staging);
     });
 }
 

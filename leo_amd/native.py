@@ -172,6 +172,7 @@ SIGNATURES = {
     "leo_hip_synchronize_model": (_I32, [_P, _P]),
     "leo_hip_synchronize_packed_model": (_I32, [_P, _P]),
     "leo_hip_commit_packed_host_model": (_I32, [_P, _P]),
+    "leo_hip_commit_packed_host_model_no_alloc": (_I32, [_P, _P]),
     "leo_hip_parameter_changes": (_I32, [_P, _I32, _P, _U64, _P, _P, _P]),
     "leo_hip_probabilities": (_I32, [_P, _P]),
     "leo_hip_read_list": (_I32, [_P, _I32, _P, _U64, _P]),
