@@ -14,9 +14,9 @@ than 2^20 bytes are trained, one story per logical batch (the workload's single
 worker trains in place, training.rs:1548-1582) with replay: at checkpoints
 after 2^16, 2^18, 2^19 and 2^20 trained bytes, the running bits per byte, the
 statistics, the parameter revision, the digests of every learned tensor and
-how many slots of each context order are taken. The six context orders of
-4,096 slots fill within the first checkpoints, so every later allocation
-evicts the weakest slot of its probe window.
+how many slots of each context order are taken. Context orders 4 to 6
+(4,096 slots each) are full by the second checkpoint, so from there on every
+allocation at those orders evicts the weakest slot of its probe window.
 
 tests/test_golden.py checks that the oracle still reproduces them (CPU; the
 long run up to its first checkpoint) and that the HIP path matches them bit

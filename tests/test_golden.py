@@ -109,9 +109,9 @@ def test_long_fixture_fills_the_context_tables():
     last = record["records"][-1]
     assert last["trained_bytes"] >= 1 << 20
     spo = 4096
-    # orders 3-6 are full from the second checkpoint on: their allocations evict
+    # orders 4-6 are full from the second checkpoint on: their allocations evict
     for rec in record["records"][1:]:
-        assert all(taken == spo for taken in rec["context_slots_taken"][2:]), rec["context_slots_taken"]
+        assert all(taken == spo for taken in rec["context_slots_taken"][3:]), rec["context_slots_taken"]
 
 
 def test_oracle_reproduces_long_fixture_first_checkpoint(oracle):
