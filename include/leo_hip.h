@@ -139,6 +139,36 @@ typedef struct LeoBatchReport {
     double replay_seconds;
 } LeoBatchReport;
 
+/* EvaluationMetrics with its ActivityDiagnostics
+ * (crates/leo-cli/src/training/metrics.rs:6-24, 182-191). */
+typedef struct LeoEvaluationReport {
+    double loss;                       /* mean loss over targets */
+    double bits_per_byte;              /* loss / ln 2 */
+    double accuracy;                   /* predicted == target, over targets */
+    uint64_t targets;
+    uint64_t processed_stories;
+    uint64_t processed_bytes;
+    uint64_t neuron_count;
+    uint64_t steps;
+    uint64_t active_neurons_sum;
+    uint64_t active_neurons_peak;
+    uint64_t emitted_events;
+    uint64_t suprathreshold_sum;
+    uint64_t block_selected_sum;
+    uint64_t cap_clipped_sum;
+    uint64_t cap_hit_steps;
+    double population_inhibition_sum;
+    float population_inhibition_peak;
+    uint32_t pad0;
+    double eligibility_sum;
+    uint64_t eligibility_count;
+    uint64_t context_cells_sum;
+    uint64_t context_probes_sum;
+    uint64_t context_applied_steps;
+    double context_loss_gain_sum;      /* neural-only loss minus loss, summed */
+    uint64_t output_madds_sum;
+} LeoEvaluationReport;
+
 /* Device telemetry of the step kernel (the role of the reference's sampled
  * batch telemetry, cuda_plan.rs:67-103 / cuda.rs:8671-9022). kernel_ms is the
  * summed HIP-event time of the step-kernel launches on the runtime's stream;
@@ -188,6 +218,11 @@ typedef struct LeoKernelStats {
      * slots with nonzero eligibility (with zero eligibility the update leaves
      * the weight unchanged, bit for bit). */
     uint64_t learning_slots;
+    /* Delivery buckets of more than 8 entries in one tick, folded by a whole
+     * wave after a sort: ranked in registers (up to 128 entries) or radix
+     * sorted through the target's shadow range. */
+    uint64_t deep_register_folds;
+    uint64_t deep_radix_folds;
 } LeoKernelStats;
 
 /* Selectors for leo_hip_parameter_changes (ParameterChanges, runtime.rs:37-46). */
@@ -294,6 +329,19 @@ int32_t leo_hip_training_story_batch(LeoHipRuntime* runtime, const uint8_t* byte
 int32_t leo_hip_train_batch(LeoHipRuntime* runtime, const uint8_t* bytes, const uint64_t* offsets,
                             uint32_t count, int32_t permission, uint32_t replay_enabled,
                             float* losses_out, LeoBatchReport* report);
+
+/* evaluate_model_shard (crates/leo-cli/src/training/validation.rs:65-135):
+ * every non-empty story scored frozen -- begin_document, its document steps
+ * (training.rs:1747-1757) with Permission::Frozen and their targets, then
+ * finish_document -- with no learning and no statistics, accumulated as
+ * record_evaluation_step does (validation.rs:137-154). Stories run on story
+ * lanes that read the canonical image (frozen steps write no parameter), lane
+ * i starting at the tick the sequential loop would reach, so every loss,
+ * prediction and worklist equals one runtime scoring the stories in order;
+ * the canonical runtime ends reset, its tick advanced past every step.
+ * losses_out (optional) receives each non-empty story's len+1 step losses. */
+int32_t leo_hip_evaluate(LeoHipRuntime* runtime, const uint8_t* bytes, const uint64_t* offsets,
+                         uint32_t count, float* losses_out, LeoEvaluationReport* report);
 
 /* RuntimeBackend::synchronize_model + model() (backend.rs:355-356): copy the
  * canonical model into caller-owned arrays (host layouts). */

@@ -70,11 +70,18 @@ inline __host__ __device__ size_t window_bytes(uint32_t neurons_per_block) {
 constexpr uint32_t kStageRowFloats = 33;
 constexpr size_t kStageBytes = 64 * kStageRowFloats * 4;
 
-// Per-wave share of the dynamic LDS: the phase-2 window, reused by the
-// learning-signal staging.
-inline __host__ __device__ size_t wave_lds_bytes(uint32_t neurons_per_block) {
+// Radix counts of a wave's deep-bucket sort, after its window: the current
+// pass's 256 scatter offsets and the next pass's 256 counts.
+constexpr size_t kDeepHistBytes = 2 * 256 * 4;
+
+// Per-wave share of the dynamic LDS: the phase-2 window (reused by the
+// learning-signal staging), then the deep-bucket histogram.
+inline __host__ __device__ size_t wave_window_bytes(uint32_t neurons_per_block) {
     const size_t w = window_bytes(neurons_per_block);
     return ((w > kStageBytes ? w : kStageBytes) + 15) / 16 * 16;
+}
+inline __host__ __device__ size_t wave_lds_bytes(uint32_t neurons_per_block) {
+    return wave_window_bytes(neurons_per_block) + kDeepHistBytes;
 }
 
 // Dynamic LDS of the step kernel: one share per wave; the binding-cap global
@@ -93,6 +100,7 @@ enum : uint32_t {
     kStepAllocate = 1u << 3,      // context allocation allowed
     kStepLearn = 1u << 4,         // target present and strength > 0
     kStepOutput = 1u << 5,        // compute logits/probabilities
+    kStepNeuralLoss = 1u << 6,    // also record the neural-only loss terms (runtime.rs:1119, 1151-1167)
 };
 
 // One scheduled step, prepared by the host from the story bytes
@@ -130,7 +138,14 @@ struct StepRecord {
     uint32_t destinations;      // learning destinations
     uint32_t active_inhibitory; // active inhibitory sources
     uint32_t learning_slots;    // eligible slots whose update the step applies (nonzero eligibility)
-    uint32_t pad;
+    // neural-only loss terms (kStepNeuralLoss): the maximum of the logits
+    // before the context contribution, the serial sum of exp(logit - max),
+    // and the target's logit; the loss is max + ln(sum) - logit
+    float neural_max;
+    float neural_sum;
+    float neural_target;
+    uint32_t deep_folds;        // buckets of more than 8 deliveries: ranked in registers (low 16 bits),
+                                // radix-sorted (high 16 bits)
 };
 
 // Device numerical guard codes (the reference's sticky error_flag 1-7,
@@ -181,6 +196,7 @@ struct LaneControl {
     uint32_t tick_scan_rec[2];       // eligible recurrent slots scanned, indexed by tick parity
     uint32_t tick_scan_in[2];        // eligible input slots scanned, indexed by tick parity
     uint32_t tick_learn[2];          // learning slots listed, indexed by tick parity
+    uint32_t tick_deep[2];           // deep bucket folds (StepRecord::deep_folds), indexed by tick parity
 };
 
 // Learned parameters of a lane (private copy for story lanes, the canonical
@@ -244,6 +260,7 @@ struct LaneDesc {
     uint32_t LEO_GLOBAL* in_learn;      // NI (LaneControl in_learn_count)
     uint64_t LEO_GLOBAL* bucket;        // 2 words per entry: delivery-order key, value bits; kFixedEntries
                                         // per target first, then the overflow ranges
+    uint64_t LEO_GLOBAL* shadow;        // 2 words per entry: the radix sort's second buffer (shadow_offset)
     // block selection
     uint32_t LEO_GLOBAL* range_winners; // blocks * max_active_per_block: winners of each selecting wave's block
                              // range in block order, compacted from the row of its first block
@@ -300,6 +317,7 @@ struct SharedModel {
     const uint32_t LEO_GLOBAL* in_target;
     const uint8_t LEO_GLOBAL* in_branch;
     const uint64_t LEO_GLOBAL* bucket_offset;   // N+1
+    const uint64_t LEO_GLOBAL* shadow_offset;   // N+1: each deep-capable target's shadow range (entries)
     const uint32_t LEO_GLOBAL* rec_edge;        // N*S: pack_edge(target, delay, branch) of each recurrent slot
 };
 
@@ -315,6 +333,53 @@ inline __host__ __device__ uint32_t pack_edge(uint32_t target, uint32_t delay, u
 inline __host__ __device__ uint32_t edge_target(uint32_t e) { return e & (kMaxPackedNeurons - 1); }
 inline __host__ __device__ uint32_t edge_delay(uint32_t e) { return 1u << ((e >> kEdgeTargetBits) & 3u); }
 inline __host__ __device__ uint32_t edge_branch(uint32_t e) { return e >> (kEdgeTargetBits + 2); }
+
+// Deep delivery buckets (more entries in one tick than the in-register
+// sort network takes) are folded by the whole wave after a sort of the
+// bucket by delivery key (delay class, the emitting neuron's active rank, its
+// synapse slot; or class 4 and the input slot), which is unique per entry, so
+// each branch's accumulator receives its values in the reference's delivery
+// order (runtime.rs:605-639). Up to kDeepRegisterEntries entries are ranked in
+// registers; larger buckets, which only targets of that capacity can have, go
+// through an LSD radix sort with 8-bit digits between the bucket and the
+// target's shadow range, on a compacted key of the significant fields.
+constexpr uint32_t kDeepRegisterEntries = 128;
+constexpr uint32_t kDeepMaxPasses = 8;
+struct DeepSortPlan {
+    uint32_t rank_bits;                   // bits of the rank field (active rank or input slot)
+    uint32_t slot_bits;                   // bits of the synapse-slot field
+    uint32_t passes;                      // radix passes
+    uint32_t shift[kDeepMaxPasses];       // digit positions in the sort key, least significant first
+    uint32_t bits[kDeepMaxPasses];        // digit widths (<= 8)
+};
+// Compacted sort key of a bucket entry, ordered as the delivery key: class,
+// rank, slot from the most significant bits down (the input items of class 4
+// carry their slot in the rank field).
+inline __host__ __device__ uint64_t deep_sort_key(uint64_t key, uint32_t rank_bits, uint32_t slot_bits) {
+    const uint64_t cls = key >> 61;
+    const uint64_t rank = cls < 4 ? (key >> 32) & 0x1fffffffu : (key >> 2) & 0x3fffffffu;
+    const uint64_t slot = cls < 4 ? (key >> 2) & 0x3fffffffu : 0u;
+    return ((cls << rank_bits | rank) << slot_bits) | slot;
+}
+// Plan for active ranks below max_active_global, input slots below
+// input_fanout and synapse slots below synapses_per_neuron.
+inline DeepSortPlan deep_sort_plan(uint32_t cap, uint32_t fanout, uint32_t synapses) {
+    auto bits_for = [](uint32_t limit) {
+        uint32_t b = 1;
+        while (b < 30 && (1ull << b) < limit) ++b;
+        return b;
+    };
+    DeepSortPlan p{};
+    p.rank_bits = bits_for(cap > fanout ? cap : fanout);
+    p.slot_bits = bits_for(synapses);
+    const uint32_t total = p.rank_bits + p.slot_bits + 3;  // + class
+    for (uint32_t at = 0; at < total && p.passes < kDeepMaxPasses; at += 8) {
+        p.shift[p.passes] = at;
+        p.bits[p.passes] = total - at < 8 ? total - at : 8;
+        ++p.passes;
+    }
+    return p;
+}
 
 struct KernelArgs {
     LeoConfig cfg;
@@ -335,6 +400,7 @@ struct KernelArgs {
     // never produce one from another value); every kept slot is then a
     // learning slot.
     uint32_t skip_zero_eligibility;
+    DeepSortPlan deep;
     FastDiv div_synapses;            // synapses_per_neuron
     FastDiv div_block;               // neurons_per_block
     FastDiv div_block_words;         // block_words(neurons_per_block)

@@ -323,6 +323,10 @@ __device__ __forceinline__ uint32_t next_pow2(uint32_t v) {
     return p;
 }
 
+// Window key of a neuron whose deep bucket the wave folds after the others
+// (above every selection key, whose high word is at most 0xfffffffe).
+constexpr uint64_t kDeepPending = ~1ULL;
+
 // Selection key: ascending order == (activation desc, rotated tie key asc)
 // (runtime.rs:987-1009); activation > 0 so its bit pattern is monotone.
 __device__ __forceinline__ uint64_t selection_key(float act, uint32_t tie) {
@@ -410,7 +414,7 @@ __device__ __forceinline__ void activate_trace(float LEO_GLOBAL* trace, __amdgpu
 // Late fields of a step record: work counters complete only after the step's
 // last barrier, so the record is finished by the next step (or kernel end).
 struct LateCounters {
-    uint32_t events, touched, scanned_rec, scanned_in, destinations, inhibitory, learning;
+    uint32_t events, touched, scanned_rec, scanned_in, destinations, inhibitory, learning, deep;
 };
 
 __device__ __forceinline__ LateCounters load_late_counters(LaneControl LEO_GLOBAL* ctl, uint32_t tick) {
@@ -423,6 +427,7 @@ __device__ __forceinline__ LateCounters load_late_counters(LaneControl LEO_GLOBA
     v.destinations = ld(&ctl->tick_dest[k]);
     v.inhibitory = ld(&ctl->tick_ainh[k]);
     v.learning = ld(&ctl->tick_learn[k]);
+    v.deep = ld(&ctl->tick_deep[k]);
     return v;
 }
 
@@ -435,6 +440,7 @@ __device__ __forceinline__ void store_late_record(const LaneDesc& d, uint32_t st
     rec.destinations = v.destinations;
     rec.active_inhibitory = v.inhibitory;
     rec.learning_slots = v.learning;
+    rec.deep_folds = v.deep;
 }
 
 // all loads first (one round trip), then the stores
@@ -454,6 +460,7 @@ __device__ __forceinline__ void clear_counters(LaneControl LEO_GLOBAL* ctl, uint
     ctl->tick_scan_rec[n] = 0;
     ctl->tick_scan_in[n] = 0;
     ctl->tick_learn[n] = 0;
+    ctl->tick_deep[n] = 0;
 }
 // Once tick-1 is complete (phase 3 of `tick`, by one thread): its record is
 // finished and its per-tick counters, which tick+1 reuses, are cleared.
@@ -817,7 +824,9 @@ __device__ __forceinline__ void sort8(uint64_t (&k)[8], uint32_t (&v)[8]) {
 // delivered values in CPU delivery order (runtime.rs:605-639, 701-708), and,
 // unless refractory, applies the drive (runtime.rs:940-975). Returns the
 // margin membrane - threshold; *refractory tells whether the neuron skipped.
-__device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float pi, bool* refractory) {
+// A neuron with more than 8 deliveries this tick is left untouched and
+// *deferred set: the wave folds it with deep_fold.
+__device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float pi, bool* refractory, bool* deferred) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -848,6 +857,8 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
     const uint32_t v0 = __float_as_uint(fe[0].z), v1 = __float_as_uint(fe[1].z);
     const bool refr = __float_as_uint(q2.w) > tick;
     const float threshold = ld(&d.p.threshold[n]);
+    *deferred = cnt > 8;
+    if (cnt > 8) return 0.0f;  // every load above is in flight together; nothing written yet
     const uint32_t e = tick - last;
     if (e > 0) {
         const StateDecays k = state_decays(cfg, e);
@@ -886,7 +897,7 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
                 add(k0, v0);
                 add(k1, v1);
             }
-        } else if (cnt <= 8) {
+        } else {
             uint64_t k[8];
             uint32_t v[8];
 #pragma unroll
@@ -904,26 +915,6 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
 #pragma unroll
             for (uint32_t x = 0; x < 8; ++x)
                 if (x < cnt) add(k[x], v[x]);
-        } else {
-            // many deliveries: fold in key order by repeated minimum search
-            // (keys are unique; nothing is written back)
-            uint64_t last = 0;
-            bool started = false;
-            for (uint32_t t = 0; t < cnt; ++t) {
-                uint64_t best = ~0ULL;
-                uint32_t best_v = 0;
-                for (uint32_t x = 0; x < cnt; ++x) {
-                    const uint64_t at = bucket_entry(overflow, n, x);
-                    const uint64_t kx = ld(&d.bucket[2 * at]);
-                    if ((!started || kx > last) && kx < best) {
-                        best = kx;
-                        best_v = static_cast<uint32_t>(ld(&d.bucket[2 * at + 1]));
-                    }
-                }
-                add(best, best_v);
-                last = best;
-                started = true;
-            }
         }
         (*nu(d, n, kNBucketCount)) = 0;
     }
@@ -940,6 +931,238 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
         mem = mem + drive;
     }
     if (e > 0 || !refr) (*nf(d, n, kNMembrane)) = mem;
+    return mem - threshold;
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, uint32_t lane) {
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), static_cast<int>(lane));
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(v >> 32), static_cast<int>(lane));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// One entry (key, value bits) of a deep bucket in its current array: the
+// target's bucket (entries by bucket_entry) or its shadow range.
+struct DeepArray {
+    uint64_t LEO_GLOBAL* base;
+    uint64_t overflow;   // the bucket's overflow offset (bucket) or the shadow range's start (shadow)
+    uint32_t n;
+    bool bucket;
+    __device__ __forceinline__ uint64_t at(uint32_t p) const {
+        return bucket ? bucket_entry(overflow, n, p) : overflow + p;
+    }
+};
+
+constexpr uint32_t kDeepTiles = 8;  // 64-entry tiles a lane has in flight
+
+// fold_drive of a neuron with more than 8 deliveries, by the whole wave (all
+// lanes active, n uniform): the bucket is sorted by delivery key -- ranked in
+// registers up to kDeepRegisterEntries entries, else by an LSD radix sort
+// between the bucket and the target's shadow range with the histogram in
+// `hist` (256 words of LDS) -- and every lane adds the entries in that order
+// (uniform values, so every lane holds the same sums). Lane 0 writes the
+// state.
+__device__ float deep_fold(const StepCtx& c, uint32_t n, float pi, bool* refractory, uint32_t* hist) {
+    const KernelArgs& a = *c.a;
+    const LaneDesc& d = c.d;
+    const LeoConfig& cfg = a.cfg;
+    const uint32_t N = cfg.neuron_count, tick = c.tick, lane = __lane_id();
+    const __amdgpu_buffer_rsrc_t rec = neuron_rsrc(d, N);
+    const f32x4 q0 = ld_quarter(rec, n, 0), q1 = ld_quarter(rec, n, 1), q2 = ld_quarter(rec, n, 2);
+    const f32x4 q3 = ld_quarter(rec, n, 3);
+    const uint64_t overflow = a.m.bucket_offset[n];
+    const float threshold = ld(&d.p.threshold[n]);
+    float mem = q0.x, fat = q0.z, ad0 = q0.w, ad1 = q1.x, ad2 = q1.y;
+    float b0 = q1.z, b1 = q1.w, b2 = q2.x, b3 = q2.y;
+    // every lane read the same record: the count is uniform
+    const uint32_t last = __float_as_uint(q2.z), cnt = __builtin_amdgcn_readfirstlane(__float_as_uint(q3.z));
+    const bool refr = __float_as_uint(q2.w) > tick;
+    const uint32_t e = tick - last;
+    if (e > 0) {
+        const StateDecays k = state_decays(cfg, e);
+        b0 *= k.branch;
+        b1 *= k.branch;
+        b2 *= k.branch;
+        b3 *= k.branch;
+        mem *= k.membrane;
+        fat *= k.fatigue;
+        ad0 *= k.fast;
+        ad1 *= k.medium;
+        ad2 *= k.slow;
+    }
+    auto add = [&](uint32_t key_lo, uint32_t bits) {
+        const float v = __uint_as_float(bits);
+        const uint32_t br = key_lo & 3u;
+        b0 = br == 0 ? b0 + v : b0;
+        b1 = br == 1 ? b1 + v : b1;
+        b2 = br == 2 ? b2 + v : b2;
+        b3 = br == 3 ? b3 + v : b3;
+    };
+    DeepArray bucket{d.bucket, overflow, n, true};
+    if (cnt <= kDeepRegisterEntries) {
+        // two entries per lane; rank = number of smaller keys (keys unique)
+        uint64_t k0 = ~0ULL, k1 = ~0ULL;
+        uint32_t v0 = 0, v1 = 0;
+        if (lane < cnt) {
+            const uint64_t at = bucket.at(lane);
+            k0 = ld(&d.bucket[2 * at]);
+            v0 = static_cast<uint32_t>(ld(&d.bucket[2 * at + 1]));
+        }
+        if (lane + kWaveSize < cnt) {
+            const uint64_t at = bucket.at(lane + kWaveSize);
+            k1 = ld(&d.bucket[2 * at]);
+            v1 = static_cast<uint32_t>(ld(&d.bucket[2 * at + 1]));
+        }
+        uint32_t r0 = 0, r1 = 0;
+        for (uint32_t q = 0; q < cnt; ++q) {
+            const uint64_t kq = readlane_u64(q < kWaveSize ? k0 : k1, q & (kWaveSize - 1));
+            r0 += kq < k0 ? 1u : 0u;
+            r1 += kq < k1 ? 1u : 0u;
+        }
+        for (uint32_t r = 0; r < cnt; ++r) {
+            const uint64_t m0 = __ballot(lane < cnt && r0 == r);
+            const uint64_t m1 = __ballot(lane + kWaveSize < cnt && r1 == r);
+            const bool first = m0 != 0;
+            const uint32_t src = static_cast<uint32_t>(__ffsll(static_cast<long long>(first ? m0 : m1)) - 1);
+            const uint32_t key_lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(first ? k0 : k1), static_cast<int>(src));
+            const uint32_t bits = __builtin_amdgcn_readlane(first ? v0 : v1, static_cast<int>(src));
+            add(key_lo, bits);
+        }
+    } else {
+        // LSD radix sort, 8-bit digits; each pass reads its source in order
+        // (kDeepTiles tiles of 64 entries in flight per lane), counts the
+        // next digit while scattering the current one stably
+        const DeepSortPlan& plan = a.deep;
+        const DeepArray shadow{d.shadow, a.m.shadow_offset[n], n, false};
+        auto digit_of = [&](uint64_t key, uint32_t pass) {
+            const uint64_t sk = deep_sort_key(key, plan.rank_bits, plan.slot_bits);
+            return static_cast<uint32_t>(sk >> plan.shift[pass]) & ((1u << plan.bits[pass]) - 1u);
+        };
+        auto zero_hist = [&]() {
+            for (uint32_t b = lane; b < 256; b += kWaveSize) hist[b] = 0u;
+            wave_sync();
+        };
+        auto exclusive_scan_hist = [&]() {
+            uint32_t h[4];
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k) h[k] = hist[4 * lane + k];
+            const uint32_t local = h[0] + h[1] + h[2] + h[3];
+            uint32_t run = wave_incl_scan_u32(local) - local;
+            wave_sync();
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k) {
+                hist[4 * lane + k] = run;
+                run += h[k];
+            }
+            wave_sync();
+        };
+        // counts of the first digit
+        zero_hist();
+        for (uint32_t t0 = 0; t0 < cnt; t0 += kDeepTiles * kWaveSize) {
+            uint64_t keys[kDeepTiles];
+#pragma unroll
+            for (uint32_t k = 0; k < kDeepTiles; ++k) {
+                const uint32_t p = t0 + k * kWaveSize + lane;
+                keys[k] = p < cnt ? ld(&d.bucket[2 * bucket.at(p)]) : 0ULL;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < kDeepTiles; ++k)
+                if (t0 + k * kWaveSize + lane < cnt) atomicAdd(&hist[digit_of(keys[k], 0)], 1u);
+        }
+        wave_sync();
+        for (uint32_t pass = 0; pass < plan.passes; ++pass) {
+            // selects, not an indexed pair (which would live in scratch)
+            const DeepArray src = (pass & 1) ? shadow : bucket;
+            const DeepArray dst = (pass & 1) ? bucket : shadow;
+            const bool more = pass + 1 < plan.passes;
+            exclusive_scan_hist();
+            // the next pass's counts go to the second half of the stage: the
+            // scatter offsets stay in the first
+            uint32_t* next = hist + 256;
+            if (more) {
+                for (uint32_t b = lane; b < 256; b += kWaveSize) next[b] = 0u;
+                wave_sync();
+            }
+            const uint32_t bits = plan.bits[pass];
+            const uint64_t below = (1ULL << lane) - 1ULL;
+            for (uint32_t t0 = 0; t0 < cnt; t0 += kDeepTiles * kWaveSize) {
+                uint64_t keys[kDeepTiles];
+                uint32_t vals[kDeepTiles];
+#pragma unroll
+                for (uint32_t k = 0; k < kDeepTiles; ++k) {
+                    const uint32_t p = t0 + k * kWaveSize + lane;
+                    const uint64_t at = p < cnt ? src.at(p) : 0u;
+                    keys[k] = p < cnt ? ld(&src.base[2 * at]) : 0ULL;
+                    vals[k] = p < cnt ? static_cast<uint32_t>(ld(&src.base[2 * at + 1])) : 0u;
+                }
+#pragma unroll
+                for (uint32_t k = 0; k < kDeepTiles; ++k) {
+                    const bool tile = t0 + k * kWaveSize < cnt;  // uniform
+                    const bool valid = t0 + k * kWaveSize + lane < cnt;
+                    const uint32_t dig = valid ? digit_of(keys[k], pass) : 0u;
+                    uint64_t peers = __ballot(valid);
+                    for (uint32_t b = 0; b < bits; ++b) {
+                        const bool bit = ((dig >> b) & 1u) != 0;
+                        const uint64_t ones = __ballot(bit);
+                        peers &= bit ? ones : ~ones;
+                    }
+                    const uint32_t rank = static_cast<uint32_t>(__popcll(peers & below));
+                    const uint32_t group = static_cast<uint32_t>(__popcll(peers));
+                    const uint32_t pos = tile ? hist[dig] + rank : 0u;
+                    wave_sync();
+                    if (valid) {
+                        const uint64_t at = dst.at(pos);
+                        dst.base[2 * at] = keys[k];
+                        dst.base[2 * at + 1] = vals[k];
+                        if (rank + 1 == group) hist[dig] += group;
+                        if (more) atomicAdd(&next[digit_of(keys[k], pass + 1)], 1u);
+                    }
+                    wave_sync();
+                }
+            }
+            // the stores are complete before the next pass reads them
+            __builtin_amdgcn_s_waitcnt(0);
+            wave_sync();
+            if (more) {
+                for (uint32_t b = lane; b < 256; b += kWaveSize) hist[b] = next[b];
+                wave_sync();
+            }
+        }
+        // fold in sorted order, tile by tile
+        const DeepArray sorted = (plan.passes & 1) ? shadow : bucket;
+        for (uint32_t t0 = 0; t0 < cnt; t0 += kWaveSize) {
+            const uint32_t p = t0 + lane;
+            const uint64_t at = p < cnt ? sorted.at(p) : 0u;
+            const uint32_t key_lo = p < cnt ? static_cast<uint32_t>(ld(&sorted.base[2 * at])) : 0u;
+            const uint32_t val = p < cnt ? static_cast<uint32_t>(ld(&sorted.base[2 * at + 1])) : 0u;
+            const uint32_t m = min(kWaveSize, cnt - t0);
+            for (uint32_t j = 0; j < m; ++j)
+                add(__builtin_amdgcn_readlane(key_lo, static_cast<int>(j)), __builtin_amdgcn_readlane(val, static_cast<int>(j)));
+        }
+    }
+    *refractory = refr;
+    if (!refr) {
+        const float gate = clampf(b3, 0.0f, 1.0f);
+        const float net = b0 + b2 * gate + b1;
+        const float adaptation = ad0 + ad1 + ad2;
+        const float drive = a.m.excitability[n] * net - fat - adaptation - pi;
+        mem = mem + drive;
+    }
+    if (lane == 0) {
+        atomicAdd(&c.ctl->tick_deep[tick & 1], cnt <= kDeepRegisterEntries ? 1u : 0x10000u);
+        if (e > 0) {
+            (*nf(d, n, kNFatigue)) = fat;
+            (*nf(d, n, kNAdapt0)) = ad0;
+            (*nf(d, n, kNAdapt0 + 1)) = ad1;
+            (*nf(d, n, kNAdapt0 + 2)) = ad2;
+            (*nu(d, n, kNLastTick)) = tick;
+        }
+        (*nu(d, n, kNBucketCount)) = 0;
+        (*nf(d, n, kNBranch0)) = b0;
+        (*nf(d, n, kNBranch0 + 1)) = b1;
+        (*nf(d, n, kNBranch0 + 2)) = b2;
+        (*nf(d, n, kNBranch0 + 3)) = b3;
+        if (e > 0 || !refr) (*nf(d, n, kNMembrane)) = mem;
+    }
     return mem - threshold;
 }
 
@@ -1079,18 +1302,43 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
             wave_sync();
             const uint32_t cnt = hi - lo;
             const uint32_t listed = first_listed + listed_before + lo;
+            bool any_deep = false;
             for (uint32_t i = lane; i < cnt; i += kWaveSize) {
                 const uint32_t e = w.entry[i];
                 const uint32_t g = e >> 16;
                 const uint32_t n = (gb + g) * nb + (e & 0xffffu);
-                bool refractory = false;
-                const float act = clampf(fold_drive(c, n, pi, &refractory), 0.0f, 1.0f);
-                const bool candidate = !refractory && act > 0.0f;
-                w.key[i] = candidate ? selection_key(act, add_mod(n, N - rot, N)) : ~0ULL;
+                bool refractory = false, deep = false;
+                const float act = clampf(fold_drive(c, n, pi, &refractory, &deep), 0.0f, 1.0f);
+                const bool candidate = !deep && !refractory && act > 0.0f;
+                w.key[i] = deep ? kDeepPending : candidate ? selection_key(act, add_mod(n, N - rot, N)) : ~0ULL;
+                any_deep |= deep;
                 if (candidate) atomicAdd(&w.cands[g], 1u);
                 d.touched_list[listed + i] = n;
             }
             wave_sync();
+            if (__ballot(any_deep)) {
+                // neurons with more than 8 deliveries: the whole wave folds each
+                uint32_t* hist = reinterpret_cast<uint32_t*>(reinterpret_cast<unsigned char*>(w.key) +
+                                                             wave_window_bytes(nb));
+                for (uint32_t i0 = 0; i0 < cnt; i0 += kWaveSize) {
+                    uint64_t pending = __ballot(i0 + lane < cnt && w.key[i0 + lane] == kDeepPending);
+                    while (pending) {
+                        const uint32_t i = i0 + static_cast<uint32_t>(__ffsll(static_cast<long long>(pending)) - 1);
+                        pending &= pending - 1;
+                        const uint32_t e = __builtin_amdgcn_readfirstlane(w.entry[i]);
+                        const uint32_t g = e >> 16;
+                        const uint32_t n = (gb + g) * nb + (e & 0xffffu);
+                        bool refractory = false;
+                        const float act = clampf(deep_fold(c, n, pi, &refractory, hist), 0.0f, 1.0f);
+                        const bool candidate = !refractory && act > 0.0f;
+                        if (lane == 0) {
+                            w.key[i] = candidate ? selection_key(act, add_mod(n, N - rot, N)) : ~0ULL;
+                            if (candidate) atomicAdd(&w.cands[g], 1u);
+                        }
+                        wave_sync();
+                    }
+                }
+            }
             {
                 // staged positions of this window's blocks (block order)
                 const bool in = lane < gn && w.start[lane] >= lo && w.start[lane] < hi;
@@ -1713,9 +1961,11 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
             }
         }
     }
+    // the context contribution (read from the latent in sh.aux) is computed
+    // before the neural-loss pass reuses sh.aux, and added after it
+    float c1 = 0.0f, c2 = 0.0f;
     if (ctx_count > 0) {
         constexpr uint32_t kDims = 16;
-        float c1 = 0.0f, c2 = 0.0f;
         for (uint32_t e0 = 0; e0 < E; e0 += kDims) {
             float x1[kDims], x2[kDims];
 #pragma unroll
@@ -1730,6 +1980,31 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
                 c2 += x2[k] * lat[e0 + k];
             }
         }
+    }
+    if (sp.flags & kStepNeuralLoss) {
+        // loss_from_logits on the neural logits, before the context is added
+        // (runtime.rs:1119, 1151-1167): f32::max fold, exp, serial sum
+        float nm = has2 ? maxnum(l1, l2) : l1;
+        for (int off = 32; off > 0; off >>= 1) nm = maxnum(nm, __shfl_xor(nm, off));
+        if (lane == 0) sh.redf[wave] = nm;
+        __syncthreads();
+        nm = sh.redf[0];
+        for (uint32_t w = 1; w < kWavesPerGroup; ++w) nm = maxnum(nm, sh.redf[w]);
+        sh.aux[o1] = glibc_expf_nonpositive(l1 - nm);
+        if (has2) sh.aux[o2] = glibc_expf_nonpositive(l2 - nm);
+        __syncthreads();
+        StepRecord LEO_GLOBAL& rec = d.records[step_index];
+        if (threadIdx.x == 0) {
+            float sum = 0.0f;
+            for (uint32_t o = 0; o < kOutputs; ++o) sum += sh.aux[o];
+            rec.neural_max = nm;
+            rec.neural_sum = sum;
+        }
+        if (sp.target_index >= 0 && static_cast<uint32_t>(sp.target_index) == o1) rec.neural_target = l1;
+        if (sp.target_index >= 0 && has2 && static_cast<uint32_t>(sp.target_index) == o2) rec.neural_target = l2;
+        __syncthreads();
+    }
+    if (ctx_count > 0) {
         l1 += c1;
         l2 += c2;
     }
@@ -2483,6 +2758,7 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
             ctl->tick_touched[k] = ctl->tick_supra[k] = ctl->tick_events[k] = 0;
             ctl->tick_dest[k] = ctl->tick_ainh[k] = ctl->tick_scan_rec[k] = ctl->tick_scan_in[k] = 0;
             ctl->tick_learn[k] = 0;
+            ctl->tick_deep[k] = 0;
         }
     }
 }

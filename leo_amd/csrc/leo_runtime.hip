@@ -88,7 +88,7 @@ struct Layout {
 };
 
 struct Sizes {
-    uint64_t n, s, f, ns, ni, slots, e, blocks, block_words, limit, cap, bucket_total;
+    uint64_t n, s, f, ns, ni, slots, e, blocks, block_words, limit, cap, bucket_total, shadow_total;
     uint64_t words(uint64_t count) const { return (count + 31) / 32; }
 };
 
@@ -293,6 +293,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     size_t o_neu = l.add<uint32_t>(kNeuronWords * z.n), o_tl = l.add<uint32_t>(z.n);
     size_t o_ls = l.add<float>(z.n), o_dl = l.add<uint32_t>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
     size_t o_rl = l.add<uint32_t>(z.ns), o_il = l.add<uint32_t>(z.ni);
+    size_t o_sh = l.add<uint64_t>(2 * std::max<uint64_t>(z.shadow_total, 1));
     size_t o_bw = l.add<uint32_t>(z.blocks * z.limit), o_bcut = l.add<float>(z.blocks);
     size_t o_bwa = l.add<float>(z.blocks * z.limit);
     size_t o_wt = l.add<uint32_t>(kMaxWaves), o_wtt = l.add<uint32_t>(kMaxWaves);
@@ -315,6 +316,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
 
     d.learning_signal = reinterpret_cast<float*>(b + o_ls);
     d.dest_list = reinterpret_cast<uint32_t*>(b + o_dl);
+    d.shadow = reinterpret_cast<uint64_t*>(b + o_sh);
     d.rec_learn = reinterpret_cast<uint32_t*>(b + o_rl);
     d.in_learn = reinterpret_cast<uint32_t*>(b + o_il);
     d.bucket = reinterpret_cast<uint64_t*>(b + o_bk);
@@ -501,6 +503,8 @@ KernelArgs kernel_args(LeoHipRuntime* h, LaneDesc* lanes, uint32_t count, uint32
     a.div_block = make_fast_div(h->cfg.device.neurons_per_block);
     a.div_block_words = make_fast_div(block_words(h->cfg.device.neurons_per_block));
     a.skip_zero_eligibility = h->negative_zero_weights ? 0u : 1u;
+    a.deep = deep_sort_plan(h->cfg.device.max_active_global, h->cfg.device.input_fanout,
+                            h->cfg.device.synapses_per_neuron);
     return a;
 }
 
@@ -653,6 +657,8 @@ void account_launch(LeoHipRuntime* h, const std::vector<LaneRun>& runs, float ms
             t.kept_rec += r.eligible_rec;
             t.kept_in += r.eligible_in;
             t.learning_slots += r.learning_slots;
+            t.deep_register_folds += r.deep_folds & 0xffffu;
+            t.deep_radix_folds += r.deep_folds >> 16;
             t.destinations += r.destinations;
             t.active_inhibitory += r.active_inhibitory;
         }
@@ -953,10 +959,20 @@ void upload_topology(LeoHipRuntime* h, const LeoModelView& m) {
         offsets[n + 1] = offsets[n] + (need > kFixedEntries ? need - kFixedEntries : 0);
     }
     h->z.bucket_total = offsets[z.n];
+    // sort space of the deep buckets: every target whose bucket can hold
+    // more entries than the in-register sort takes gets a range of its
+    // capacity (the radix sort's second buffer)
+    std::vector<uint64_t> shadow(z.n + 1, 0);
+    for (uint64_t n = 0; n < z.n; ++n) {
+        const uint64_t need = cap[n] + row_max[n];
+        shadow[n + 1] = shadow[n] + (need > kDeepRegisterEntries ? need : 0);
+    }
+    h->z.shadow_total = shadow[z.n];
     Layout l;
     size_t o_ex = l.add<float>(z.n), o_ty = l.add<uint8_t>(z.n), o_rt = l.add<uint32_t>(z.ns);
     size_t o_rb = l.add<uint8_t>(z.ns), o_rd = l.add<uint8_t>(z.ns), o_it = l.add<uint32_t>(z.ni);
     size_t o_ib = l.add<uint8_t>(z.ni), o_off = l.add<uint64_t>(z.n + 1), o_edge = l.add<uint32_t>(z.ns);
+    size_t o_sho = l.add<uint64_t>(z.n + 1);
     h->shared.allocate(l.cursor);
     char* b = h->shared.base;
     h->sm.excitability = reinterpret_cast<const float*>(b + o_ex);
@@ -968,6 +984,7 @@ void upload_topology(LeoHipRuntime* h, const LeoModelView& m) {
     h->sm.in_branch = reinterpret_cast<const uint8_t*>(b + o_ib);
     h->sm.bucket_offset = reinterpret_cast<const uint64_t*>(b + o_off);
     h->sm.rec_edge = reinterpret_cast<const uint32_t*>(b + o_edge);
+    h->sm.shadow_offset = reinterpret_cast<const uint64_t*>(b + o_sho);
     std::vector<uint32_t> edges(z.ns);
     for (uint64_t i = 0; i < z.ns; ++i) edges[i] = pack_edge(m.rec_target[i], m.rec_delay[i], m.rec_branch[i]);
     hipStream_t s = h->stream;
@@ -979,6 +996,7 @@ void upload_topology(LeoHipRuntime* h, const LeoModelView& m) {
     upload(b + o_it, m.in_target, z.ni * 4, s);
     upload(b + o_ib, m.in_branch, z.ni, s);
     upload(b + o_off, offsets.data(), offsets.size() * 8, s);
+    upload(b + o_sho, shadow.data(), shadow.size() * 8, s);
     upload(b + o_edge, edges.data(), z.ns * 4, s);
     sync(s);
 }
@@ -1452,6 +1470,104 @@ void story_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets
     rep.merge_context_keys = ctx;
     rep.story_seconds += run_seconds;
     rep.merge_seconds += merge_seconds;
+}
+
+// Frozen evaluation (validation.rs:65-154). Story lanes borrow the canonical
+// parameters for the launch: frozen steps allocate no context slot and run no
+// learning or homeostasis, so nothing writes them.
+struct BorrowedParams {
+    std::vector<std::pair<Lane*, LaneParams>> saved;
+    ~BorrowedParams() {
+        for (auto& [lane, p] : saved) lane->desc.p = p;
+    }
+};
+
+void evaluate_stories(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets, uint32_t count,
+                      float* losses_out, LeoEvaluationReport& rep) {
+    std::vector<uint32_t> stories;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (offsets[i + 1] < offsets[i]) throw Error(LEO_ERR_INVALID_ARGUMENT, "story offsets must not decrease");
+        if (offsets[i + 1] > offsets[i]) stories.push_back(i);  // validation.rs:86-88 skips empty stories
+    }
+    const uint32_t S = h->cfg.device.synapses_per_neuron, E = h->cfg.device.context_embedding_dim;
+    const uint32_t resident = std::max<uint32_t>(1, std::min(h->resident_lanes, h->max_lanes));
+    const float uniform_loss = std::log(static_cast<float>(kOutputs));  // loss_from_logits fallback
+    uint32_t tick = h->canonical->tick;
+    double loss_sum = 0.0;
+    uint64_t correct = 0;
+    size_t cursor = 0;
+    rep.neuron_count = h->z.n;
+    for (size_t lo = 0; lo < stories.size(); lo += resident) {
+        const size_t hi = std::min(stories.size(), lo + resident);
+        BorrowedParams borrowed;
+        std::vector<LaneRun> runs;
+        std::vector<std::vector<HostStep>> host_steps;
+        for (size_t k = lo; k < hi; ++k) {
+            Lane& lane = story_lane(h, static_cast<uint32_t>(k - lo));
+            borrowed.saved.push_back({&lane, lane.desc.p});
+            lane.desc.p = h->canon;
+            // begin_document at the tick one runtime scoring the stories in
+            // order would have reached
+            std::vector<Lane*> one{&lane};
+            reset_lane_objects(h, one, true, tick);
+            const uint32_t s = stories[k];
+            host_steps.push_back(document_steps(bytes + offsets[s], static_cast<size_t>(offsets[s + 1] - offsets[s])));
+            LaneRun run{&lane, {}, {}};
+            for (const HostStep& st : host_steps.back()) {
+                StepParams sp = make_step(h->cfg, lane, st.symbol, st.target, LEO_FROZEN, tick++, true);
+                sp.flags |= kStepNeuralLoss;
+                run.steps.push_back(sp);
+            }
+            runs.push_back(std::move(run));
+        }
+        run_lanes(h, runs);
+        // record_evaluation_step + ActivityDiagnostics::record, story by story
+        for (size_t k = 0; k < runs.size(); ++k) {
+            const LaneRun& run = runs[k];
+            for (size_t i = 0; i < run.steps.size(); ++i) {
+                const StepParams& sp = run.steps[i];
+                const StepRecord& r = run.records[i];
+                const float loss = step_loss(sp, r);
+                if (losses_out) losses_out[cursor++] = loss;
+                loss_sum += static_cast<double>(loss);
+                rep.targets += 1;
+                const uint32_t predicted = r.predicted < 256 ? r.predicted : kEnd;
+                if (predicted == static_cast<uint32_t>(host_steps[k][i].target)) correct += 1;
+                rep.steps += 1;
+                rep.active_neurons_sum += r.active;
+                rep.active_neurons_peak = std::max<uint64_t>(rep.active_neurons_peak, r.active);
+                rep.emitted_events += static_cast<uint64_t>(r.active) * S;
+                rep.suprathreshold_sum += r.suprathreshold;
+                rep.block_selected_sum += r.block_selected;
+                rep.cap_clipped_sum += r.clipped;
+                if (r.clipped > 0) rep.cap_hit_steps += 1;
+                rep.population_inhibition_sum += static_cast<double>(r.population_inhibition);
+                rep.population_inhibition_peak = std::max(rep.population_inhibition_peak, r.population_inhibition);
+                // frozen steps apply no learning: mean |eligibility| is 0
+                rep.eligibility_count += static_cast<uint64_t>(r.eligible_rec) + r.eligible_in;
+                rep.context_cells_sum += r.context_cells;
+                rep.context_probes_sum += r.context_probes;
+                if (r.context_applied) rep.context_applied_steps += 1;
+                const bool finite_sum = std::isfinite(r.neural_sum) && r.neural_sum > 0.0f;
+                const float neural = finite_sum ? (r.neural_max + std::log(r.neural_sum)) - r.neural_target : uniform_loss;
+                rep.context_loss_gain_sum += static_cast<double>(neural - loss);
+                rep.output_madds_sum += static_cast<uint64_t>(r.active) * kOutputs +
+                                        static_cast<uint64_t>(r.context_cells) * E +
+                                        (r.context_cells > 0 ? static_cast<uint64_t>(E) * kOutputs : 0);
+            }
+            const uint32_t s = stories[lo + k];
+            rep.processed_bytes += offsets[s + 1] - offsets[s];
+            rep.processed_stories += 1;
+        }
+    }
+    // finish_document of the last story: the canonical runtime ends reset,
+    // its tick past every evaluated step
+    std::vector<Lane*> canonical{h->canonical.get()};
+    reset_lane_objects(h, canonical, true, tick);
+    sync(h->stream);
+    rep.loss = loss_sum / static_cast<double>(std::max<uint64_t>(rep.targets, 1));
+    rep.bits_per_byte = rep.loss / std::log(2.0);
+    rep.accuracy = static_cast<double>(correct) / static_cast<double>(std::max<uint64_t>(rep.targets, 1));
 }
 
 // synchronize_model on a host mirror (cuda.rs:2817-2825, 5657-5760): every
@@ -2006,6 +2122,17 @@ int32_t leo_hip_train_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64
                 leo::replay_story(h, bytes + offsets[i], static_cast<size_t>(offsets[i + 1] - offsets[i]), losses[i],
                                   permission, rep);
         rep.replay_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
+        if (report) *report = rep;
+    });
+}
+
+int32_t leo_hip_evaluate(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets, uint32_t count,
+                         float* losses_out, LeoEvaluationReport* report) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        if (count > 0 && (!bytes || !offsets)) throw Error(LEO_ERR_INVALID_ARGUMENT, "null story arrays");
+        LeoEvaluationReport rep{};
+        leo::evaluate_stories(h, bytes, offsets, count, losses_out, rep);
         if (report) *report = rep;
     });
 }

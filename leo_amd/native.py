@@ -115,6 +115,22 @@ class LeoBatchReport(ctypes.Structure):
     ]
 
 
+class LeoEvaluationReport(ctypes.Structure):
+    _fields_ = [
+        ("loss", ctypes.c_double), ("bits_per_byte", ctypes.c_double), ("accuracy", ctypes.c_double),
+        ("targets", ctypes.c_uint64), ("processed_stories", ctypes.c_uint64), ("processed_bytes", ctypes.c_uint64),
+        ("neuron_count", ctypes.c_uint64), ("steps", ctypes.c_uint64), ("active_neurons_sum", ctypes.c_uint64),
+        ("active_neurons_peak", ctypes.c_uint64), ("emitted_events", ctypes.c_uint64),
+        ("suprathreshold_sum", ctypes.c_uint64), ("block_selected_sum", ctypes.c_uint64),
+        ("cap_clipped_sum", ctypes.c_uint64), ("cap_hit_steps", ctypes.c_uint64),
+        ("population_inhibition_sum", ctypes.c_double), ("population_inhibition_peak", ctypes.c_float),
+        ("pad0", ctypes.c_uint32), ("eligibility_sum", ctypes.c_double), ("eligibility_count", ctypes.c_uint64),
+        ("context_cells_sum", ctypes.c_uint64), ("context_probes_sum", ctypes.c_uint64),
+        ("context_applied_steps", ctypes.c_uint64), ("context_loss_gain_sum", ctypes.c_double),
+        ("output_madds_sum", ctypes.c_uint64),
+    ]
+
+
 class LeoKernelStats(ctypes.Structure):
     _fields_ = [
         ("launches", ctypes.c_uint64), ("lane_steps", ctypes.c_uint64), ("kernel_ms", ctypes.c_double),
@@ -128,6 +144,7 @@ class LeoKernelStats(ctypes.Structure):
         ("section_kernel_ms", ctypes.c_double * 2), ("section_bytes", ctypes.c_double * 2),
         ("merge_lane_changes", ctypes.c_uint64), ("merge_elements", ctypes.c_uint64),
         ("merge_bytes", ctypes.c_double), ("learning_slots", ctypes.c_uint64),
+        ("deep_register_folds", ctypes.c_uint64), ("deep_radix_folds", ctypes.c_uint64),
     ]
 
 
@@ -167,6 +184,7 @@ SIGNATURES = {
     "leo_hip_replay_streaming_batch": (_I32, [_P, _P, _P, _U32, _I32, _P, _P]),
     "leo_hip_training_story_batch": (_I32, [_P, _P, _P, _U32, _I32, _P, _P]),
     "leo_hip_train_batch": (_I32, [_P, _P, _P, _U32, _I32, _U32, _P, _P]),
+    "leo_hip_evaluate": (_I32, [_P, _P, _P, _U32, _P, _P]),
     "leo_hip_download_model": (_I32, [_P, _P]),
     "leo_hip_upload_model": (_I32, [_P, _P]),
     "leo_hip_synchronize_model": (_I32, [_P, _P]),

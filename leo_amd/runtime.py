@@ -275,6 +275,18 @@ class HipRuntime:
                    1 if replay else 0, losses.ctypes.data, ctypes.byref(rep))
         return BatchReport.from_c(rep), _split_losses(losses, stories)
 
+    def evaluate(self, stories: Sequence[bytes]) -> Tuple[Dict[str, float], List[np.ndarray]]:
+        """evaluate_model_shard (crates/leo-cli/src/training/validation.rs:65-135): frozen
+        scoring of the stories; returns EvaluationMetrics (+ ActivityDiagnostics) and each
+        non-empty story's step losses."""
+        data, offsets = pack_stories(stories)
+        losses = np.zeros(int(offsets[-1]) + len(stories), dtype=np.float32)
+        rep = native.LeoEvaluationReport()
+        self._call("leo_hip_evaluate", data.ctypes.data, offsets.ctypes.data, len(stories), losses.ctypes.data,
+                   ctypes.byref(rep))
+        report = {name: getattr(rep, name) for name, _ in native.LeoEvaluationReport._fields_ if name != "pad0"}
+        return report, [l for l in _split_losses(losses, stories) if l.size]
+
     def train_batch_packed(self, data: np.ndarray, offsets: np.ndarray, permission: int, replay: bool = True
                            ) -> BatchReport:
         """train_batch over pre-packed stories (no per-story loss copy-out)."""
