@@ -221,6 +221,24 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base
 __device__ __forceinline__ f32x4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 16));
 }
+// Records of `stride` bytes through a buffer resource in index mode: the
+// address is base + index * stride + offset, computed in 64 bits, and the
+// range check counts records, so arrays of up to 2^32 records (beyond 4 GiB)
+// are addressed with 32-bit indices. Device scope (sc1), like ld16.
+__device__ f32x4 struct_buffer_load_b128(__amdgpu_buffer_rsrc_t rsrc, int vindex, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.v4f32");
+__device__ float struct_buffer_load_b32(__amdgpu_buffer_rsrc_t rsrc, int vindex, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.f32");
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t record_rsrc(const void* base, uint32_t stride, uint32_t records) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(stride), static_cast<int>(records),
+                                             0x00020000);
+}
+__device__ __forceinline__ f32x4 ld16_record(__amdgpu_buffer_rsrc_t r, uint32_t index, uint32_t byte_offset) {
+    return struct_buffer_load_b128(r, static_cast<int>(index), static_cast<int>(byte_offset), 0, 16);
+}
+__device__ __forceinline__ float ld4_record(__amdgpu_buffer_rsrc_t r, uint32_t index, uint32_t byte_offset) {
+    return struct_buffer_load_b32(r, static_cast<int>(index), static_cast<int>(byte_offset), 0, 16);
+}
 __device__ __forceinline__ float ld4(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, 0, 16));
 }
@@ -390,7 +408,7 @@ __device__ __forceinline__ uint32_t selecting_waves(const StepCtx& c) {
 // Coherent loads of a trace record's two quarters (the host limits the trace
 // arrays to below 2^32 bytes).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t trace_rsrc(const float LEO_GLOBAL* trace, uint64_t slots) {
-    return coherent_rsrc(trace, static_cast<uint32_t>(slots * kTraceWords * 4));
+    return record_rsrc(trace, kTraceWords * 4, static_cast<uint32_t>(slots));
 }
 
 // Brings one trace slot to `tick` and adds `activation` to its branch
@@ -398,7 +416,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t trace_rsrc(const float LEO_GLO
 __device__ __forceinline__ void activate_trace(float LEO_GLOBAL* trace, __amdgpu_buffer_rsrc_t rsrc, uint32_t slot,
                                                uint32_t tick, float activation, const LeoConfig& cfg) {
     static_assert(kTBranch == 0 && kTAdapt0 == 3 && kTEligibility == 6 && kTLast == 7, "trace layout");
-    const f32x4 q0 = ld16(rsrc, slot * (kTraceWords * 4)), q1 = ld16(rsrc, slot * (kTraceWords * 4) + 16);
+    const f32x4 q0 = ld16_record(rsrc, slot, 0), q1 = ld16_record(rsrc, slot, 16);
     f32x4 LEO_GLOBAL* rec = reinterpret_cast<f32x4 LEO_GLOBAL*>(trace + static_cast<uint64_t>(slot) * kTraceWords);
     const uint32_t e = tick - __float_as_uint(q1.w);
     if (e == 0) {
@@ -1690,7 +1708,7 @@ struct SlotInputs {
 };
 
 __device__ __forceinline__ void load_slot(SlotInputs& in, __amdgpu_buffer_rsrc_t rsrc, uint32_t slot) {
-    const f32x4 q0 = ld16(rsrc, slot * (kTraceWords * 4)), q1 = ld16(rsrc, slot * (kTraceWords * 4) + 16);
+    const f32x4 q0 = ld16_record(rsrc, slot, 0), q1 = ld16_record(rsrc, slot, 16);
     in.bs = q0.x;
     in.ms = q0.y;
     in.fs = q0.z;
@@ -2156,23 +2174,23 @@ __device__ __forceinline__ float signal_rows(__amdgpu_buffer_rsrc_t rows, uint32
     const uint32_t lane = __lane_id();
     const uint32_t seg = lane & 7, sub = lane >> 3;
     // this lane loads 16 bytes of rows sub, 8 + sub, ..., 56 + sub
-    uint32_t off[8];
+    uint32_t row_of[8];
     bool live[8];
 #pragma unroll
     for (uint32_t k = 0; k < 8; ++k) {
         const uint32_t row = 8 * k + sub;
         live[k] = row < count;
-        off[k] = static_cast<uint32_t>(__shfl(static_cast<int>(dst), static_cast<int>(row))) * (kOutStride * 4) + seg * 16;
+        row_of[k] = static_cast<uint32_t>(__shfl(static_cast<int>(dst), static_cast<int>(row)));
     }
-    const float tail = lane < count ? ld4(rows, dst * (kOutStride * 4) + 4 * kEndIndex) : 0.0f;
+    const float tail = lane < count ? ld4_record(rows, dst, 4 * kEndIndex) : 0.0f;
     // two lines in flight (even lines in v, odd lines in w; the unrolled loop
     // names the buffers statically, so no register copy waits for a load)
     static_assert(kLines % 2 == 0, "lines are taken in pairs");
     f32x4 v[8], w[8];
 #pragma unroll
     for (uint32_t k = 0; k < 8; ++k) {
-        v[k] = live[k] ? ld16(rows, off[k]) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        w[k] = live[k] ? ld16(rows, off[k] + 128) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        v[k] = live[k] ? ld16_record(rows, row_of[k], seg * 16) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        w[k] = live[k] ? ld16_record(rows, row_of[k], seg * 16 + 128) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
     float acc = 0.0f;
 #pragma unroll
@@ -2191,7 +2209,8 @@ __device__ __forceinline__ float signal_rows(__amdgpu_buffer_rsrc_t rows, uint32
         if (line + 2 < kLines) {
 #pragma unroll
             for (uint32_t k = 0; k < 8; ++k)
-                cur[k] = live[k] ? ld16(rows, off[k] + (line + 2) * 128) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                cur[k] = live[k] ? ld16_record(rows, row_of[k], seg * 16 + (line + 2) * 128)
+                                 : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
         if (lane < count) {
             const float* r = stage + lane * kStageRowFloats;
@@ -2220,8 +2239,8 @@ __device__ __forceinline__ void phase_signals(const StepCtx& c, StepShared& sh) 
     const uint32_t first_dst = first_at < N ? ld(&d.dest_list[first_at]) : 0u;
     for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = ld(&d.errors[o]);
     __syncthreads();
-    // the host limits N * kOutStride * 4 to below 2^31 bytes
-    const __amdgpu_buffer_rsrc_t rows = coherent_rsrc(d.p.out_w, N * kOutStride * 4);
+    // rows addressed by index (N records of kOutStride floats)
+    const __amdgpu_buffer_rsrc_t rows = record_rsrc(d.p.out_w, kOutStride * 4, N);
     float* stage = reinterpret_cast<float*>(step_lds + static_cast<size_t>(wave) * wave_lds_bytes(cfg.neurons_per_block));
     for (uint32_t b = b0; b * kWaveSize < count; b += waves) {
         const uint32_t n = min(kWaveSize, count - b * kWaveSize);

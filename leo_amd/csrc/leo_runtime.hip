@@ -1862,10 +1862,6 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         leo::model_validate(*config, *model);
         if (static_cast<uint64_t>(config->device.neuron_count) * config->device.synapses_per_neuron >= (1ull << 31))
             throw Error(LEO_ERR_UNSUPPORTED, "neuron_count * synapses_per_neuron at or above 2^31 is not supported");
-        // trace records are read with 32-bit buffer offsets
-        if (static_cast<uint64_t>(config->device.neuron_count) * config->device.synapses_per_neuron * leo::kTraceWords * 4 >=
-            (1ull << 32))
-            throw Error(LEO_ERR_UNSUPPORTED, "recurrent trace records at or above 4 GiB per lane are not supported");
         if (config->device.neuron_count > leo::kMaxPackedNeurons)
             throw Error(LEO_ERR_UNSUPPORTED, "neuron_count above 2^28 is not supported by the packed synapse layout");
         if (config->device.neurons_per_block > leo::kMaxBlockNeurons)
@@ -1878,8 +1874,10 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
                 throw Error(LEO_ERR_UNSUPPORTED, "a binding max_active_global with more than 1024 block winners per tick "
                                                  "(block_count * max_active_per_block) is not supported");
         }
-        if (static_cast<uint64_t>(config->device.neuron_count) * leo::kOutStride * 4 >= (1ULL << 31))
-            throw Error(LEO_ERR_UNSUPPORTED, "output projection above 2 GiB per lane is not supported");
+        // neuron records and the fixed delivery entries are read with 32-bit
+        // buffer offsets (64 bytes per neuron)
+        if (static_cast<uint64_t>(config->device.neuron_count) * leo::kNeuronWords * 4 >= (1ull << 32))
+            throw Error(LEO_ERR_UNSUPPORTED, "neuron_count above 2^26 is not supported by the neuron records");
         int devices = 0;
         if (hipGetDeviceCount(&devices) != hipSuccess || devices <= 0)
             throw Error(LEO_ERR_DEVICE, "GPU backend requested, but no HIP device is available");
