@@ -36,7 +36,7 @@ HIP_FLAGS = [
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
 ]
-CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wextra",
+CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-pthread", "-ffp-contract=off", "-Wall", "-Wextra",
              f"-I{ROOT / 'include'}", f"-I{CSRC}"]
 
 
@@ -57,7 +57,7 @@ def build_library() -> pathlib.Path:
     _run([os.environ.get("CXX", "g++"), *CXX_FLAGS, "-c", CSRC / "host_model.cpp", "-o", host_obj])
     objects.append(host_obj)
     tmp = LIB.with_suffix(".so.tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objects, "-o", tmp])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", *objects, "-o", tmp])
     os.replace(tmp, LIB)
     return LIB
 

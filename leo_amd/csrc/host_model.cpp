@@ -8,6 +8,7 @@
 #include <cstdint>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "leo_hip.h"
@@ -37,6 +38,10 @@ struct SplitMix64 {
         return static_cast<size_t>(next_u64() % static_cast<uint64_t>(upper));
     }
     float range_f32(float low, float high) { return low + (high - low) * next_f32(); }
+    // The i-th output depends only on seed + i * increment, so a generator
+    // can be positioned anywhere in the stream.
+    static constexpr uint64_t kIncrement = 0x9E3779B97F4A7C15ULL;
+    void skip(uint64_t outputs) { state += outputs * kIncrement; }
     template <class T>
     void shuffle(std::vector<T>& v) {
         for (size_t i = v.size(); i-- > 1;) {
@@ -52,6 +57,33 @@ struct SplitMix64 {
         return std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
     }
 };
+
+// Fills out[i] = range_f32(low, high) for i < count with the generator's next
+// `count` outputs, in parallel chunks (each positioned with skip), and leaves
+// the generator where the sequential loop would: the values are the ones the
+// sequential loop draws.
+void fill_range_f32(SplitMix64& rng, float* out, size_t count, float low, float high) {
+    const size_t kChunk = size_t(1) << 22;
+    const unsigned threads = static_cast<unsigned>(
+        std::min<size_t>({std::max(1u, std::thread::hardware_concurrency()), 16u, (count + kChunk - 1) / kChunk}));
+    auto work = [&](size_t begin, size_t end) {
+        SplitMix64 local = rng;
+        local.skip(begin);
+        for (size_t i = begin; i < end; ++i) out[i] = local.range_f32(low, high);
+    };
+    if (threads <= 1) {
+        work(0, count);
+    } else {
+        std::vector<std::thread> pool;
+        const size_t per = (count + threads - 1) / threads;
+        for (unsigned t = 0; t < threads; ++t) {
+            const size_t begin = std::min(count, t * per), end = std::min(count, begin + per);
+            pool.emplace_back(work, begin, end);
+        }
+        for (auto& th : pool) th.join();
+    }
+    rng.skip(count);
+}
 
 constexpr uint8_t BR_EXC = 0, BR_INH = 1, BR_TEMP = 2, BR_GATE = 3;
 
@@ -124,8 +156,8 @@ void init_input(const LeoHostConfig& c, SplitMix64& rng, LeoModelView& m) {
 // model.rs:126-157: output, context projection, empty context memory.
 void init_projections(const LeoHostConfig& c, SplitMix64& rng, LeoModelView& m) {
     const Sizes z = sizes_of(c);
-    for (size_t i = 0; i < 257 * z.n; ++i) m.out_weight[i] = rng.range_f32(-0.005f, 0.005f);
-    for (size_t i = 0; i < 257 * z.e; ++i) m.ctx_out[i] = rng.range_f32(-0.005f, 0.005f);
+    fill_range_f32(rng, m.out_weight, 257 * z.n, -0.005f, 0.005f);
+    fill_range_f32(rng, m.ctx_out, 257 * z.e, -0.005f, 0.005f);
     std::fill(m.bias, m.bias + 257, 0.0f);
     std::fill(m.ctx_keys, m.ctx_keys + z.slots, 0);
     std::fill(m.ctx_emb, m.ctx_emb + z.slots * z.e, 0.0f);
@@ -204,8 +236,12 @@ void model_initialize_synthetic(const LeoHostConfig& c, uint32_t topology, float
     // Target sampler: uniform, or Zipf(exponent) over a seeded permutation of the
     // neurons (inverse CDF by binary search), so in-degree is heavy-tailed while
     // every row keeps its fixed capacity S.
+    // A guide table narrows each search: with K a power of two, u*K is exact,
+    // so j = floor(u*K) gives j/K <= u < (j+1)/K and the lower bound of u lies
+    // in [guide[j], guide[j+1]], guide[j] being the lower bound of j/K.
     std::vector<double> cdf;
-    std::vector<uint32_t> perm;
+    std::vector<uint32_t> perm, guide;
+    size_t guide_size = 1;
     if (topology != LEO_TOPOLOGY_UNIFORM) {
         if (!(exponent > 0.0f)) throw Error(LEO_ERR_INVALID_ARGUMENT, "power-law exponent must be positive");
         cdf.resize(n);
@@ -218,12 +254,22 @@ void model_initialize_synthetic(const LeoHostConfig& c, uint32_t topology, float
         perm.resize(n);
         for (size_t i = 0; i < n; ++i) perm[i] = static_cast<uint32_t>(i);
         rng.shuffle(perm);
+        while (guide_size < n && guide_size < (size_t(1) << 24)) guide_size <<= 1;
+        guide.resize(guide_size + 1);
+        size_t at = 0;
+        for (size_t j = 0; j <= guide_size; ++j) {
+            const double bound = static_cast<double>(j) / static_cast<double>(guide_size);
+            while (at < n && cdf[at] < bound) ++at;
+            guide[j] = static_cast<uint32_t>(at);
+        }
     }
     std::vector<uint32_t> in_degree(cap ? n : 0, 0);
     auto draw_target = [&]() -> size_t {
         if (topology == LEO_TOPOLOGY_UNIFORM) return rng.range_usize(n);
         double u = rng.next_unit_open();
-        size_t rank = static_cast<size_t>(std::lower_bound(cdf.begin(), cdf.end(), u) - cdf.begin());
+        const size_t j = static_cast<size_t>(u * static_cast<double>(guide_size));
+        size_t rank = static_cast<size_t>(
+            std::lower_bound(cdf.begin() + guide[j], cdf.begin() + guide[j + 1], u) - cdf.begin());
         return perm[std::min(rank, n - 1)];
     };
     std::vector<std::pair<size_t, uint8_t>> used;
