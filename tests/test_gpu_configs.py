@@ -8,7 +8,14 @@
   sample -- the batch's first 8 stories cut to 128 bytes, replay on -- against
   the CPU oracle bit for bit; and one full-size 64-story batch with replay
   (two resident lane groups, the grouped mean) run twice from the same model:
-  identical models, a valid model, and the batch's counters consistent.
+  identical models, a valid model, and the batch's counters consistent;
+
+* E-shaped (E's configuration, heavy-tailed in-degree capped at 4096, 80
+  winners per block, 30% target activity, on 65,536 units driven to the
+  per-block cap): a 4-story batch cut to 40 bytes, replay on, against the
+  oracle bit for bit, with the hub buckets folded by the radix path; and E
+  at full size in the same regime: an 8-story batch run twice, identical and
+  valid.
 """
 from __future__ import annotations
 
@@ -148,4 +155,124 @@ def test_workload_c_full_batch_is_deterministic_and_valid(require_gpu, model_c, 
                   "merge_context_keys", "active_neurons_sum"):
         assert getattr(reports[0], field) == getattr(reports[1], field), field
     assert reports[0].replay_steps > 0 and reports[0].targets == trained + 32
+    finals[0].validate()
+
+
+# --- E-shaped reduced model: heavy-tailed in-degree capped at 4096, 80 winners per
+# block, 30% target activity (E's rules on 65,536 units) ---------------------------
+E_REDUCED_NEURONS = 65_536
+E_REDUCED_THRESHOLD = 0.05  # the lowest canonical threshold
+
+
+def drive_to_e_regime(m):
+    """Drives a synthetic model into workload E's high-activity regime:
+    thresholds at 0.05, excitatory recurrent weights tripled and input weights
+    doubled (clamped to weight_max). Without it the synthetic E model starts
+    nearly silent (a handful of active units a step)."""
+    wmax = np.float32(m.config.learning.weight_max)
+    exc = m.rec_weight > 0
+    m.rec_weight[exc] = np.minimum(m.rec_weight[exc] * np.float32(3.0), wmax)
+    m.in_weight[:] = np.minimum(m.in_weight * np.float32(2.0), wmax)
+    m.threshold[:] = np.float32(E_REDUCED_THRESHOLD)
+    m.validate()
+    return m
+
+
+def e_reduced_model():
+    """Workload E's configuration and topology generator on 65,536 units (256
+    blocks, 80 winners each, max_active_global = blocks * 80 as in E), driven
+    into E's regime, so that the blocks reach their 80-winner cap (31% of the
+    units) within about 40 steps and the capped hubs receive hundreds of
+    events a step."""
+    from leo_amd.model import Model
+    from leo_amd.workload import workload_config
+
+    w = WORKLOADS["E"]
+    cfg = workload_config(w)
+    blocks = E_REDUCED_NEURONS // 256
+    cfg.model.neuron_count = E_REDUCED_NEURONS
+    cfg.model.block_count = blocks
+    cfg.model.max_active_global = blocks * w.per_block
+    m = Model.synthetic(cfg, topology=w.topology, exponent=w.exponent, in_degree_cap=w.in_degree_cap,
+                        weight_sigma=0.05)
+    return drive_to_e_regime(m)
+
+
+@pytest.fixture(scope="module")
+def model_e_reduced():
+    print("building the E-shaped reduced model (65,536 units, heavy-tailed in-degree capped at 4096)", flush=True)
+    return e_reduced_model()
+
+
+def test_workload_e_shaped_batch_matches_oracle(require_gpu, oracle, model_e_reduced):
+    w = WORKLOADS["E"]
+    data, offsets = synthetic_stories(w, 4)
+    stories = [s[:40] for s in story_list(data, offsets)]
+    deg = np.bincount(model_e_reduced.rec_target.astype(np.int64), minlength=E_REDUCED_NEURONS)
+    assert deg.max() == w.in_degree_cap and (deg > 1024).sum() > 100
+    print(f"E-shaped: 4 stories cut to 40 bytes ({sum(map(len, stories))} bytes), replay on", flush=True)
+    cpu = oracle.OracleRuntime(model_e_reduced)
+    crep, closs = cpu.train_story_batch(stories, oracle.TRAINING, replay=True)
+    print("oracle done", flush=True)
+    gpu = _runtime(model_e_reduced, 4)
+    try:
+        gpu.kernel_stats(reset=True)
+        grep, gloss = gpu.train_batch(stories, native.TRAINING, replay=True)
+        stats = gpu.kernel_stats()
+        for i, (g, c) in enumerate(zip(gloss, closs)):
+            assert np.array_equal(g, c), f"story {i}: first differing step {np.nonzero(g != c)[0][:4]}"
+        assert (grep.replay_segments, grep.replay_steps, grep.replay_prefix_steps) == \
+            (crep.replay_segments, crep.replay_steps, crep.replay_prefix_steps)
+        assert grep.merge_fixed_parameter_updates == crep.merge_fixed_parameter_updates
+        assert grep.merge_context_keys == crep.merge_context_keys
+        assert grep.active_neurons_sum == crep.active_neurons_sum
+        got = gpu.model()
+    finally:
+        gpu.close()
+    print(f"active per step {grep.active_neurons_sum / max(1, grep.activity_steps):.0f}; deep folds: register "
+          f"{stats['deep_register_folds']}, radix {stats['deep_radix_folds']}", flush=True)
+    # the batch reaches the per-block cap regime and folds hub buckets by radix sort
+    assert grep.active_neurons_sum > 0.15 * E_REDUCED_NEURONS * grep.activity_steps
+    assert stats["deep_radix_folds"] > 0
+    assert_models_equal(got, cpu.model(), "E-shaped reduced batch")
+
+
+def test_workload_e_full_size_batch_is_deterministic_and_valid(require_gpu):
+    """Workload E at full size (4,194,304 units, 2^27 recurrent synapses,
+    heavy-tailed in-degree capped at 4096) driven into its regime: an 8-story
+    batch cut to 48 bytes with replay (about 400 lane steps and 120 replay
+    steps), run twice from the same model."""
+    w = WORKLOADS["E"]
+    print("building the workload E model (4,194,304 units)", flush=True)
+    model = drive_to_e_regime(workload_model(w))
+    data, offsets = synthetic_stories(w, 8)
+    stories = [s[:48] for s in story_list(data, offsets)]
+    trained = sum(map(len, stories))
+    finals, reports, stats = [], [], []
+    for run in range(2):
+        print(f"workload E: 8-story batch ({trained} bytes) with replay, run {run}", flush=True)
+        rt = _runtime(model, 8)
+        try:
+            rt.kernel_stats(reset=True)
+            rep, losses = rt.train_batch(stories, native.TRAINING, replay=True)
+            stats.append(rt.kernel_stats())
+            finals.append(rt.model())
+            reports.append(rep)
+        finally:
+            rt.close()
+        print(f"run {run}: story {rep.story_seconds:.2f} s, replay {rep.replay_seconds:.2f} s, "
+              f"{rep.active_neurons_sum / max(1, rep.activity_steps):.0f} active per step, "
+              f"{rep.replay_steps} replay steps", flush=True)
+        assert len(losses) == 8 and all(len(l) == len(s) + 1 for l, s in zip(losses, stories))
+        assert all(np.isfinite(l).all() and (l >= 0).all() for l in losses)
+    assert_models_equal(finals[0], finals[1], "two runs of the workload E batch")
+    for field in ("mean_loss", "targets", "replay_steps", "replay_prefix_steps", "merge_fixed_parameter_updates",
+                  "merge_context_keys", "active_neurons_sum", "emitted_events"):
+        assert getattr(reports[0], field) == getattr(reports[1], field), field
+    for key in ("lane_steps", "deep_register_folds", "deep_radix_folds", "learning_slots"):
+        assert stats[0][key] == stats[1][key], key
+    a = reports[0]
+    assert a.targets == trained + 8 and a.replay_steps > 0
+    assert stats[0]["deep_radix_folds"] > 0
+    assert a.active_neurons_sum > 0.02 * w.neurons * a.activity_steps
     finals[0].validate()
