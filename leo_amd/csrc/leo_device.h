@@ -84,12 +84,19 @@ inline __host__ __device__ size_t wave_lds_bytes(uint32_t neurons_per_block) {
     return wave_window_bytes(neurons_per_block) + kDeepHistBytes;
 }
 
-// Dynamic LDS of the step kernel: one share per wave; the binding-cap global
-// sort (up to kMaxBlockNeurons keys) reuses the front.
+// Dynamic LDS of the step kernel: one share per wave. The binding-cap global
+// selection reuses it: the selecting waves' first winner positions
+// (kSelectStartsBytes), then keys -- up to kMaxBlockNeurons sorted in place,
+// or a tile of select_tile_keys() keys streamed past every key of the lane.
+constexpr size_t kSelectStartsBytes = ((kMaxWaves + 1) * 4 + 15) / 16 * 16;
 inline size_t step_lds_bytes(uint32_t neurons_per_block) {
     const size_t lists = static_cast<size_t>(kWavesPerGroup) * wave_lds_bytes(neurons_per_block);
-    const size_t sort = static_cast<size_t>(kMaxBlockNeurons) * 8;
+    const size_t sort = kSelectStartsBytes + static_cast<size_t>(kMaxBlockNeurons) * 8;
     return ((lists > sort ? lists : sort) + 15) / 16 * 16;
+}
+inline uint32_t select_tile_keys(uint32_t neurons_per_block) {
+    const size_t keys = (step_lds_bytes(neurons_per_block) - kSelectStartsBytes) / 8;
+    return static_cast<uint32_t>(keys / kThreads * kThreads);
 }
 
 // Step flags (per scheduled step).
@@ -400,6 +407,7 @@ struct KernelArgs {
     // never produce one from another value); every kept slot is then a
     // learning slot.
     uint32_t skip_zero_eligibility;
+    uint32_t select_tile;            // select_tile_keys(neurons_per_block)
     DeepSortPlan deep;
     FastDiv div_synapses;            // synapses_per_neuron
     FastDiv div_block;               // neurons_per_block

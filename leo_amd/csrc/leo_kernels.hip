@@ -1617,8 +1617,32 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     return delivered;
 }
 
-// Binding global cap (workgroup 0): sort every block winner by
-// (activation desc, tie asc), keep max_active_global (runtime.rs:1029-1057).
+// Binding global cap: every block winner by selection key ascending
+// (activation desc, tie asc); the first max_active_global form the active list
+// (runtime.rs:1029-1057). Every workgroup lists the selecting waves' first
+// winner positions in LDS; up to kMaxBlockNeurons winners are then sorted in
+// workgroup 0's LDS. Beyond that every workgroup ranks its share of the
+// winners by counting the smaller keys (the keys are distinct: they hold the
+// rotated neuron index), with all keys streamed through LDS in tiles, and
+// places each kept winner at its rank.
+__device__ __forceinline__ uint64_t winner_key(const LaneDesc& d, const uint32_t* starts, uint32_t nwaves,
+                                               uint32_t range, uint32_t block_count, uint32_t limit, uint32_t flat,
+                                               uint32_t N, uint32_t rot, uint32_t* n_out, float* act_out) {
+    // the last wave whose first position is <= flat (empty waves come before it)
+    uint32_t lo = 0, hi = nwaves;
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (starts[mid] <= flat) lo = mid;
+        else hi = mid;
+    }
+    const uint64_t at = static_cast<uint64_t>(min(block_count, lo * range)) * limit + (flat - starts[lo]);
+    const uint32_t n = ld(&d.range_winners[at]);
+    const float act = ld(&d.range_winner_act[at]);
+    *n_out = n;
+    *act_out = act;
+    return selection_key(act, add_mod(n, N - rot, N));
+}
+
 __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, uint32_t step_index) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
@@ -1626,13 +1650,13 @@ __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, 
     const uint32_t N = cfg.neuron_count, limit = cfg.max_active_per_block, cap = cfg.max_active_global;
     const uint32_t tick = c.tick, rot = tick % N;
     const uint32_t rs = tick % kRing;
-    uint64_t* keys = reinterpret_cast<uint64_t*>(step_lds);
+    uint32_t* starts = reinterpret_cast<uint32_t*>(step_lds);
+    uint64_t* keys = reinterpret_cast<uint64_t*>(step_lds + kSelectStartsBytes);
     const uint32_t nwaves = selecting_waves(c);
     const uint32_t range = (cfg.block_count + nwaves - 1) / nwaves;
     uint32_t running = 0;
     for (uint32_t base = 0; base < nwaves; base += kThreads) {
         const uint32_t wv = base + threadIdx.x;
-        const uint64_t row0 = static_cast<uint64_t>(min(cfg.block_count, wv * range)) * limit;
         const uint32_t v = wv < nwaves ? ld(&d.wave_total[wv]) : 0;
         sh.scan[threadIdx.x] = v;
         __syncthreads();
@@ -1642,40 +1666,76 @@ __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, 
             sh.scan[threadIdx.x] += add;
             __syncthreads();
         }
-        const uint32_t start = running + sh.scan[threadIdx.x] - v;
-        for (uint32_t i = 0; i < v; ++i) {
-            if (start + i < kMaxBlockNeurons) {
-                const uint32_t n = ld(&d.range_winners[row0 + i]);
-                keys[start + i] = selection_key(ld(&d.range_winner_act[row0 + i]), add_mod(n, N - rot, N));
-            }
-        }
+        if (wv < nwaves) starts[wv] = running + sh.scan[threadIdx.x] - v;
         const uint32_t chunk_total = sh.scan[kThreads - 1];
         __syncthreads();
         running += chunk_total;
     }
-    uint32_t active = 0, clipped = 0;
+    if (threadIdx.x == 0) starts[nwaves] = running;
+    __syncthreads();
+    const uint32_t active = running < cap ? running : cap;
+    uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
+    float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
     float pop_cutoff = 0.0f;
-    if (running > kMaxBlockNeurons) {
-        if (threadIdx.x == 0) set_error(c.ctl, kErrCapacity);
-    } else {
+    // the first winner not kept sets the population cutoff from its margin,
+    // clamped to population_inhibition_max, not from its activation (which
+    // is clamped to 1) (runtime.rs:1045-1050)
+    auto cutoff_of = [&](uint32_t n) {
+        return clampf(ld(nf(d, n, kNMembrane)) - ld(&d.p.threshold[n]), 0.0f, cfg.population_inhibition_max);
+    };
+    auto keep = [&](uint32_t rank, uint32_t n, float act) {
+        act_list[rank] = n;
+        act_val[rank] = act;
+        (*nf(d, n, kNActivation)) = act;
+        (*nu(d, n, kNSelected)) = tick + 1;
+    };
+    if (running <= kMaxBlockNeurons) {
+        if (c.part != 0) return;
+        for (uint32_t f = threadIdx.x; f < running; f += kThreads) {
+            uint32_t n;
+            float act;
+            keys[f] = winner_key(d, starts, nwaves, range, cfg.block_count, limit, f, N, rot, &n, &act);
+        }
         const uint32_t M = next_pow2(running < 2 ? 2 : running);
         for (uint32_t i = running + threadIdx.x; i < M; i += kThreads) keys[i] = ~0ULL;
         __syncthreads();
         bitonic_sort_lds(keys, M);
-        active = running < cap ? running : cap;
-        clipped = running - active;
-        if (running > cap) pop_cutoff = clampf(key_activation(keys[cap]), 0.0f, cfg.population_inhibition_max);
-        uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
-        float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
+        if (running > cap) pop_cutoff = cutoff_of(add_mod(static_cast<uint32_t>(keys[cap]), rot, N));
         for (uint32_t i = threadIdx.x; i < active; i += kThreads) {
             const uint64_t key = keys[i];
-            const uint32_t n = add_mod(static_cast<uint32_t>(key), rot, N);
-            const float act = key_activation(key);
-            act_list[i] = n;
-            act_val[i] = act;
-            (*nf(d, n, kNActivation)) = act;
-            (*nu(d, n, kNSelected)) = tick + 1;
+            keep(i, add_mod(static_cast<uint32_t>(key), rot, N), key_activation(key));
         }
+    } else {
+        // this workgroup's share of the winners, a thread's key at a time
+        const uint32_t tile = a.select_tile;
+        const uint32_t per = (running + c.P - 1) / c.P;
+        const uint32_t mine_lo = min(running, c.part * per), mine_hi = min(running, mine_lo + per);
+        for (uint32_t base = mine_lo; base < mine_hi; base += kThreads) {
+            const uint32_t f = base + threadIdx.x;
+            const bool has = f < mine_hi;
+            uint32_t my_n = 0;
+            float my_act = 0.0f;
+            uint64_t my_key = ~0ULL;
+            if (has) my_key = winner_key(d, starts, nwaves, range, cfg.block_count, limit, f, N, rot, &my_n, &my_act);
+            uint32_t rank = 0;
+            for (uint32_t t0 = 0; t0 < running; t0 += tile) {
+                const uint32_t tn = min(tile, running - t0);
+                __syncthreads();  // the previous tile is consumed
+                for (uint32_t i = threadIdx.x; i < tn; i += kThreads) {
+                    uint32_t n;
+                    float act;
+                    keys[i] = winner_key(d, starts, nwaves, range, cfg.block_count, limit, t0 + i, N, rot, &n, &act);
+                }
+                __syncthreads();
+                if (has)
+                    for (uint32_t i = 0; i < tn; ++i) rank += keys[i] < my_key ? 1u : 0u;
+            }
+            if (has) {
+                if (rank < cap) keep(rank, my_n, my_act);
+                else if (rank == cap) c.ctl->pop_cutoff = cutoff_of(my_n);
+            }
+        }
+        if (c.part != 0) return;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -1683,8 +1743,10 @@ __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, 
         LaneControl* ctl = c.ctl;
         ctl->active_count = active;
         ctl->block_selected = running;
-        ctl->clipped = clipped;
-        ctl->pop_cutoff = pop_cutoff;
+        ctl->clipped = running - active;
+        // beyond kMaxBlockNeurons winners the workgroup that ranks the first
+        // winner not kept stores the cutoff
+        if (running <= kMaxBlockNeurons || running <= cap) ctl->pop_cutoff = pop_cutoff;
         ctl->ring_tick[rs] = tick;
         ctl->ring_count[rs] = active;
         const float activity = static_cast<float>(active) / static_cast<float>(N);
@@ -2627,7 +2689,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
                 pending_events = wg_total(delivered);
             }
         } else {
-            if (c.part == 0) global_select(c, sh, s);
+            global_select(c, sh, s);
             if (trace) {
                 if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 7))) break;
                 phase_eligibility(c, plastic);

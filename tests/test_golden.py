@@ -139,13 +139,24 @@ def test_hip_path_matches_long_fixture(require_gpu):
 
     record = _long_fixture()
     w, stories = make_golden.long_stories()
+    # a run of a few minutes: progress goes to the terminal even when pytest
+    # captures output
+    say = lambda *a: print(*a, file=sys.__stderr__, flush=True)  # noqa: E731
+    done = [0]
+
+    def train(r, s):
+        out = r.train_batch([s], native.TRAINING, replay=True)
+        done[0] += 1
+        if done[0] % 200 == 0:
+            say(f"golden long run: {done[0]} stories trained")
+        return out
+
     rt = HipRuntime(workload_model(w), device=0, max_lanes=1)
     try:
-        print("golden: workload A, one story per batch with replay, past 2^20 trained bytes", flush=True)
-        got = make_golden.long_run(rt, lambda r, s: r.train_batch([s], native.TRAINING, replay=True), stories,
-                                   checkpoints=record["checkpoints"],
-                                   on_checkpoint=lambda rec: print("checkpoint", rec["trained_bytes"],
-                                                                   rec["bits_per_byte"], flush=True))
+        say("golden: workload A, one story per batch with replay, past 2^20 trained bytes")
+        got = make_golden.long_run(rt, train, stories, checkpoints=record["checkpoints"],
+                                   on_checkpoint=lambda rec: say("checkpoint", rec["trained_bytes"],
+                                                                 rec["bits_per_byte"]))
     finally:
         rt.close()
     assert len(got) == len(record["records"])

@@ -276,3 +276,73 @@ def test_workload_e_full_size_batch_is_deterministic_and_valid(require_gpu):
     assert stats[0]["deep_radix_folds"] > 0
     assert a.active_neurons_sum > 0.02 * w.neurons * a.activity_steps
     finals[0].validate()
+
+
+# --- binding global cap beyond 1,024 block winners: 256 blocks of 256 units,
+# 16 winners each (up to 4,096 block winners) against a cap of 2,048 --------
+BINDING_NEURONS = 65_536
+BINDING_CAP = 2048
+
+
+def binding_cap_model():
+    """Workload D's configuration (uniform targets) on 65,536 units with fan-in
+    32, 16 winners per block and max_active_global 2,048 (target_activity
+    0.02), driven to high activity like E's regime (thresholds 0.05,
+    excitatory recurrent weights x3, input weights x2): more than 2,048 of the
+    up to 4,096 block winners compete within a few steps."""
+    from leo_amd.model import Model
+    from leo_amd.workload import workload_config
+
+    w = WORKLOADS["D"]
+    cfg = workload_config(w)
+    cfg.model.neuron_count = BINDING_NEURONS
+    cfg.model.block_count = BINDING_NEURONS // 256
+    cfg.model.synapses_per_neuron = 32
+    cfg.model.input_fanout = 256
+    cfg.model.max_active_per_block = 16
+    cfg.model.max_active_global = BINDING_CAP
+    cfg.dynamics.target_activity = 0.02
+    m = Model.synthetic(cfg, topology=w.topology, weight_sigma=0.05)
+    return drive_to_e_regime(m)
+
+
+def test_binding_global_cap_beyond_1024_winners_matches_oracle(require_gpu, oracle):
+    from leo_amd.runtime import HipRuntime
+
+    print("building a 65,536-unit model with 16 winners per block and max_active_global 2048", flush=True)
+    model = binding_cap_model()
+    w = WORKLOADS["D"]
+    data, offsets = synthetic_stories(w, 4)
+    stories = [s[:36] for s in story_list(data, offsets)]
+    cpu = oracle.OracleRuntime(model)
+    gpu = HipRuntime(model, device=0, max_lanes=4)
+    try:
+        # a document step by step: the step metrics of the global selection
+        cpu.begin_document()
+        gpu.begin_document()
+        text = stories[0]
+        steps = [(256, text[0])] + [(text[i], text[i + 1]) for i in range(len(text) - 1)]
+        widest = clipped = 0
+        for i, (sym, tgt) in enumerate(steps):
+            cm = cpu.step(sym, tgt, oracle.TRAINING)
+            gm = gpu.step(sym, tgt, native.TRAINING)
+            assert (gm.active_neurons, gm.block_selected_neurons, gm.global_cap_clipped_neurons) == \
+                (cm.active_neurons, cm.block_selected_neurons, cm.global_cap_clipped_neurons), i
+            assert gm.population_inhibition == cm.population_inhibition, i
+            assert gm.loss == cm.loss and gm.eligible_recurrent_synapses == cm.eligible_recurrent_synapses, i
+            widest = max(widest, gm.block_selected_neurons)
+            clipped += gm.global_cap_clipped_neurons
+        print(f"document: up to {widest} block winners, {clipped} clipped by the cap", flush=True)
+        assert widest > 1024 and clipped > 0
+        # then a story batch with replay from the trained state
+        crep, closs = cpu.train_story_batch(stories[1:], oracle.TRAINING, replay=True)
+        print("oracle batch done", flush=True)
+        grep, gloss = gpu.train_batch(stories[1:], native.TRAINING, replay=True)
+        for i, (g, c) in enumerate(zip(gloss, closs)):
+            assert np.array_equal(g, c), f"story {i}: first differing step {np.nonzero(g != c)[0][:4]}"
+        assert (grep.replay_steps, grep.replay_prefix_steps, grep.active_neurons_sum) == \
+            (crep.replay_steps, crep.replay_prefix_steps, crep.active_neurons_sum)
+        got = gpu.model()
+    finally:
+        gpu.close()
+    assert_models_equal(got, cpu.model(), "binding global cap")
