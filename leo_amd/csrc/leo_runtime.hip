@@ -77,6 +77,84 @@ struct Arena {
     }
 };
 
+// Pinned host staging of the per-launch transfers (step schedules, lane
+// descriptors and kernel arguments up; step records and lane control words
+// down), on a transfer stream of its own: the step stream waits for the
+// uploads through an event, and the transfer stream waits for the step
+// stream's kernel through another before the downloads. Space is handed out
+// in order and reclaimed only once the transfer stream has drained, so no
+// pending copy's source or destination is reused.
+struct PinnedStaging {
+    char* base = nullptr;
+    size_t capacity = 0, used = 0;
+    hipStream_t xfer = nullptr;
+    hipEvent_t uploaded = nullptr, computed = nullptr;
+    bool pending_uploads = false;
+    PinnedStaging() = default;
+    PinnedStaging(const PinnedStaging&) = delete;
+    PinnedStaging& operator=(const PinnedStaging&) = delete;
+    ~PinnedStaging() {
+        if (xfer) (void)hipStreamSynchronize(xfer);
+        if (base) (void)hipHostFree(base);
+        if (uploaded) (void)hipEventDestroy(uploaded);
+        if (computed) (void)hipEventDestroy(computed);
+        if (xfer) (void)hipStreamDestroy(xfer);
+    }
+    void init() {
+        LEO_HIP_CHECK(hipStreamCreateWithFlags(&xfer, hipStreamNonBlocking));
+        LEO_HIP_CHECK(hipEventCreateWithFlags(&uploaded, hipEventDisableTiming));
+        LEO_HIP_CHECK(hipEventCreateWithFlags(&computed, hipEventDisableTiming));
+    }
+    static size_t rounded(size_t bytes) { return (bytes + 255) & ~static_cast<size_t>(255); }
+    // Room for `bytes` more (in rounded pieces) without reclaiming: drains the
+    // transfer stream and, if needed, grows the buffer first.
+    void reserve(size_t bytes) {
+        if (used + bytes <= capacity) return;
+        drain();
+        if (bytes <= capacity) return;
+        if (base) LEO_HIP_CHECK(hipHostFree(base));
+        base = nullptr;
+        capacity = std::max<size_t>({rounded(bytes), 2 * capacity, size_t(1) << 20});
+        LEO_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&base), capacity, hipHostMallocDefault));
+    }
+    char* take(size_t bytes) {
+        const size_t need = rounded(bytes);
+        reserve(need);
+        char* p = base + used;
+        used += need;
+        return p;
+    }
+    void h2d(void* dst, const void* src, size_t bytes) {
+        if (!bytes) return;
+        char* p = take(bytes);
+        std::memcpy(p, src, bytes);
+        LEO_HIP_CHECK(hipMemcpyAsync(dst, p, bytes, hipMemcpyHostToDevice, xfer));
+        pending_uploads = true;
+    }
+    // the stream `s` waits for every upload issued so far
+    void publish(hipStream_t s) {
+        if (!pending_uploads) return;
+        LEO_HIP_CHECK(hipEventRecord(uploaded, xfer));
+        LEO_HIP_CHECK(hipStreamWaitEvent(s, uploaded, 0));
+        pending_uploads = false;
+    }
+    // later transfers start after the work queued on `s` so far
+    void follow(hipStream_t s) {
+        LEO_HIP_CHECK(hipEventRecord(computed, s));
+        LEO_HIP_CHECK(hipStreamWaitEvent(xfer, computed, 0));
+    }
+    // a download into staging space; valid after drain()
+    const char* d2h(const void* src, size_t bytes) {
+        char* p = take(bytes);
+        if (bytes) LEO_HIP_CHECK(hipMemcpyAsync(p, src, bytes, hipMemcpyDeviceToHost, xfer));
+        return p;
+    }
+    void drain() {
+        if (xfer) LEO_HIP_CHECK(hipStreamSynchronize(xfer));
+        used = 0;
+    }
+};
+
 struct Layout {
     size_t cursor = 0;
     template <class T>
@@ -201,6 +279,7 @@ struct LeoHipRuntime {
     bool phase_profile = false;
     double wall_clock_khz = 0.0;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+    leo::PinnedStaging staging;  // per-launch transfers (transfer stream + pinned buffer)
 };
 
 namespace leo {
@@ -521,10 +600,15 @@ void reset_lanes(LeoHipRuntime* h, uint32_t count, bool set_tick, uint32_t new_t
     LEO_HIP_CHECK(hipGetLastError());
 }
 
+// Lane descriptors go up through the pinned staging; the step stream waits for
+// them, and they wait for the step stream's queued work (which may still read
+// the descriptors they replace).
 void stage_descs(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
     std::vector<LaneDesc> host(lanes.size());
     for (size_t i = 0; i < lanes.size(); ++i) host[i] = lanes[i]->desc;
-    upload(h->lane_descs.base, host.data(), host.size() * sizeof(LaneDesc), h->stream);
+    h->staging.follow(h->stream);
+    h->staging.h2d(h->lane_descs.base, host.data(), host.size() * sizeof(LaneDesc));
+    h->staging.publish(h->stream);
 }
 
 void reset_lane_objects(LeoHipRuntime* h, const std::vector<Lane*>& lanes, bool set_tick, uint32_t new_tick) {
@@ -675,6 +759,14 @@ void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     for (auto& r : runs) max_tick = std::max<uint64_t>(max_tick, static_cast<uint64_t>(r.lane->tick) + r.steps.size());
     if (max_tick + static_cast<uint64_t>(h->cfg.device.refractory_ticks) + 2 >= 0xffffffffULL)
         throw Error(LEO_ERR_UNSUPPORTED, "lane tick would exceed the 32-bit device tick range");
+    // every staged transfer of this launch fits without reclaiming space
+    // (downloads stay valid until the final drain)
+    size_t staged = PinnedStaging::rounded(count * sizeof(LaneDesc)) + PinnedStaging::rounded(sizeof(KernelArgs));
+    for (auto& r : runs)
+        staged += PinnedStaging::rounded(r.steps.size() * sizeof(StepParams)) +
+                  PinnedStaging::rounded(r.steps.size() * sizeof(StepRecord)) + PinnedStaging::rounded(sizeof(LaneControl));
+    h->staging.reserve(staged);
+    h->staging.follow(h->stream);  // the uploads replace what queued work may still read
     for (auto& r : runs) {
         Lane& lane = *r.lane;
         uint32_t need = static_cast<uint32_t>(std::max<size_t>(r.steps.size(), 1));
@@ -687,7 +779,7 @@ void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
         lane.desc.records = reinterpret_cast<StepRecord*>(
             lane.schedule.base + ((static_cast<size_t>(lane.schedule_capacity) * sizeof(StepParams) + 255) & ~size_t(255)));
         lane.desc.step_count = static_cast<uint32_t>(r.steps.size());
-        upload(const_cast<StepParams*>(lane.desc.steps), r.steps.data(), r.steps.size() * sizeof(StepParams), h->stream);
+        h->staging.h2d(const_cast<StepParams*>(lane.desc.steps), r.steps.data(), r.steps.size() * sizeof(StepParams));
         static_assert(offsetof(LaneControl, xcc_mask) == offsetof(LaneControl, barrier) + 8, "cleared together");
         LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->barrier, 0, 12, h->stream));  // barrier, abort, xcc_mask
         LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->error_code, 0, 4, h->stream));
@@ -705,7 +797,8 @@ void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     KernelArgs a = kernel_args(h, reinterpret_cast<LaneDesc*>(h->lane_descs.base), count, P);
     a.lane_stride = stride;
     if (!h->kernel_args_buf.base) h->kernel_args_buf.allocate(sizeof(KernelArgs));
-    upload(h->kernel_args_buf.base, &a, sizeof(KernelArgs), h->stream);
+    h->staging.h2d(h->kernel_args_buf.base, &a, sizeof(KernelArgs));
+    h->staging.publish(h->stream);
     const KernelArgs* device_args = reinterpret_cast<const KernelArgs*>(h->kernel_args_buf.base);
     void* params[] = {&device_args};
     const void* kernel = h->phase_profile ? reinterpret_cast<const void*>(&leo_lane_steps_profiled)
@@ -716,13 +809,20 @@ void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
     LEO_HIP_CHECK(hipLaunchCooperativeKernel(kernel, dim3(stride * P), dim3(kThreads), params,
                                              step_lds_bytes(h->cfg.device.neurons_per_block), h->stream));
     LEO_HIP_CHECK(hipEventRecord(h->ev_stop, h->stream));
+    h->staging.follow(h->stream);
+    std::vector<const char*> staged_records(count), staged_ctl(count);
+    for (uint32_t i = 0; i < count; ++i) {
+        staged_records[i] = h->staging.d2h(runs[i].lane->desc.records, runs[i].steps.size() * sizeof(StepRecord));
+        staged_ctl[i] = h->staging.d2h(runs[i].lane->desc.ctl, sizeof(LaneControl));
+    }
+    LEO_HIP_CHECK(hipStreamSynchronize(h->staging.xfer));  // the kernel and its downloads are complete
     std::vector<LaneControl> ctl(count);
     for (uint32_t i = 0; i < count; ++i) {
         runs[i].records.resize(runs[i].steps.size());
-        download(runs[i].records.data(), runs[i].lane->desc.records, runs[i].steps.size() * sizeof(StepRecord), h->stream);
-        download(&ctl[i], runs[i].lane->desc.ctl, sizeof(LaneControl), h->stream);
+        std::memcpy(runs[i].records.data(), staged_records[i], runs[i].steps.size() * sizeof(StepRecord));
+        std::memcpy(&ctl[i], staged_ctl[i], sizeof(LaneControl));
     }
-    sync(h->stream);
+    h->staging.drain();
     float ms = 0.0f;
     LEO_HIP_CHECK(hipEventElapsedTime(&ms, h->ev_start, h->ev_stop));
     h->last_launch_ms = ms;
@@ -1892,6 +1992,7 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         LEO_HIP_CHECK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
         LEO_HIP_CHECK(hipEventCreate(&h->ev_start));
         LEO_HIP_CHECK(hipEventCreate(&h->ev_stop));
+        h->staging.init();
         h->cus = prop.multiProcessorCount;
         // cooperative capacity: the smaller occupancy of the step kernel and
         // its phase-profiling build (either may be launched on the same grid)
