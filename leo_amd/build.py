@@ -53,9 +53,10 @@ def build_library() -> pathlib.Path:
         obj = BUILD / (src + ".o")
         _run([HIPCC, *HIP_FLAGS, "-c", CSRC / src, "-o", obj])
         objects.append(obj)
-    host_obj = BUILD / "host_model.o"
-    _run([os.environ.get("CXX", "g++"), *CXX_FLAGS, "-c", CSRC / "host_model.cpp", "-o", host_obj])
-    objects.append(host_obj)
+    for src in ("host_model.cpp", "formats.cpp"):
+        obj = BUILD / (pathlib.Path(src).stem + ".o")
+        _run([os.environ.get("CXX", "g++"), *CXX_FLAGS, "-c", CSRC / src, "-o", obj])
+        objects.append(obj)
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", *objects, "-o", tmp])
     os.replace(tmp, LIB)

@@ -99,6 +99,30 @@ class TrainingConfig:
     minimum_relative_improvement: float = 0.005
 
 
+def _toml_value(value: Any, default: Any) -> str:
+    if isinstance(value, bool):
+        return "true" if value else "false"
+    if isinstance(default, float) or isinstance(value, float):
+        v = float(value)
+        if not math.isfinite(v):
+            raise ConfigError("configuration floats must be finite")
+        text = repr(v)
+        return text if any(ch in text for ch in ".eE") else text + ".0"
+    if isinstance(value, int):
+        return str(value)
+    if isinstance(value, str):
+        escaped = []
+        for ch in value:
+            if ch == "\\" or ch == '"':
+                escaped.append("\\" + ch)
+            elif ord(ch) < 0x20 or ord(ch) == 0x7F:
+                escaped.append(f"\\u{ord(ch):04X}")
+            else:
+                escaped.append(ch)
+        return '"' + "".join(escaped) + '"'
+    raise ConfigError(f"cannot write {type(value).__name__} to TOML")
+
+
 def _f32(value: float) -> float:
     import numpy as np
 
@@ -144,6 +168,22 @@ class Config:
 
     def to_dict(self) -> Dict[str, Any]:
         return {s: dataclasses.asdict(getattr(self, s)) for s in self._SECTIONS}
+
+    def to_toml(self) -> str:
+        """Config::to_toml (config.rs:521-523): every section and field in
+        declaration order. Floats are written so that they parse back to the
+        same value (as f64 here, and as f32 where the reference stores f32);
+        the text is not byte-identical to the reference's serializer, and no
+        reader depends on that."""
+        lines = []
+        for section in self._SECTIONS:
+            if lines:
+                lines.append("")
+            lines.append(f"[{section}]")
+            target = getattr(self, section)
+            for f in dataclasses.fields(target):
+                lines.append(f"{f.name} = {_toml_value(getattr(target, f.name), f.default)}")
+        return "\n".join(lines) + "\n"
 
     def copy(self) -> "Config":
         return Config.from_dict(self.to_dict()) if self.is_valid() else dataclasses.replace(self)

@@ -21,6 +21,9 @@ ERR_NUMERICAL = 4
 ERR_UNSUPPORTED = 5
 ERR_INTERNAL = 6
 ERR_BUSY = 7
+ERR_CORRUPT = 8        # include/leo_formats.h: checkpoint / dataset artifact damaged
+ERR_INCOMPATIBLE = 9   # artifact of another format version or semantics
+ERR_IO = 10
 
 FROZEN, PROVISIONAL, TRAINING, VERIFIED = 0, 1, 2, 3
 TOPOLOGY_UNIFORM, TOPOLOGY_POWER_LAW, TOPOLOGY_HEAVY_TAIL = 0, 1, 2
@@ -211,7 +214,7 @@ def load(path: Optional[pathlib.Path] = None) -> ctypes.CDLL:
     if not target.exists():
         raise RuntimeError(f"{target} is missing: build it with `python -m leo_amd.build` (no CPU fallback exists)")
     lib = ctypes.CDLL(str(target))
-    for name, (restype, argtypes) in SIGNATURES.items():
+    for name, (restype, argtypes) in {**SIGNATURES, **FORMAT_SIGNATURES}.items():
         fn = getattr(lib, name)
         fn.restype = restype
         fn.argtypes = argtypes
@@ -220,6 +223,51 @@ def load(path: Optional[pathlib.Path] = None) -> ctypes.CDLL:
     if path is None:
         _lib = lib
     return lib
+
+
+
+# Every symbol include/leo_formats.h declares (the host artifact layer).
+class LeoDigest(ctypes.Structure):
+    _fields_ = [("bytes", ctypes.c_uint8 * 32)]
+
+
+class LeoCheckpointInfo(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_uint64) for name in (
+        "generation", "parameter_revision", "config_offset", "config_length", "neuron_count",
+        "synapses_per_neuron", "input_fanout", "context_slots", "context_embedding_dim")]
+
+
+class LeoStoryIndex(ctypes.Structure):
+    _fields_ = [("offset", ctypes.c_uint64), ("length", ctypes.c_uint32), ("split_flags", ctypes.c_uint32)]
+
+
+class LeoDatasetIdentity(ctypes.Structure):
+    _fields_ = [("schema_version", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+                ("record_count", ctypes.c_uint64), ("bytes_length", ctypes.c_uint64),
+                ("bytes_digest", LeoDigest), ("records_digest", LeoDigest),
+                ("provenance_digest", LeoDigest), ("dataset_id", LeoDigest)]
+
+
+FORMAT_SIGNATURES = {
+    "leo_sha256": (_I32, [_P, _U64, _P]),
+    "leo_sha256_file": (_I32, [ctypes.c_char_p, _P]),
+    "leo_checkpoint_encoded_size": (_I32, [_P, _U64, _P]),
+    "leo_checkpoint_encode": (_I32, [_P, _P, _P, _U64, _P, _U64]),
+    "leo_checkpoint_inspect": (_I32, [_P, _U64, _P]),
+    "leo_checkpoint_decode": (_I32, [_P, _U64, _P, _P]),
+    "leo_checkpoint_save_atomic": (_I32, [ctypes.c_char_p, _P, _P, _P, _U64, _U32]),
+    "leo_checkpoint_read_generation": (_I32, [ctypes.c_char_p, _P]),
+    "leo_checkpoint_prune_generations": (_I32, [ctypes.c_char_p, _U64]),
+    "leo_dataset_compute_id": (_I32, [_U32, _U64, _U64, _P, _P, _P, _P]),
+    "leo_dataset_write_index": (_I32, [ctypes.c_char_p, ctypes.c_char_p, _P, _U64, _P, _P]),
+    "leo_dataset_open": (_I32, [ctypes.c_char_p, ctypes.c_char_p, _P]),
+    "leo_dataset_close": (None, [_P]),
+    "leo_dataset_identity": (_I32, [_P, _P]),
+    "leo_dataset_len": (_U64, [_P]),
+    "leo_dataset_entry": (_I32, [_P, _U64, _P]),
+    "leo_dataset_story": (_I32, [_P, _U64, _P, _U64, _P]),
+    "leo_dataset_pack": (_I32, [_P, _U64, _U64, _P, _U64, _P]),
+}
 
 
 def last_error(lib: ctypes.CDLL) -> str:

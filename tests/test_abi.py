@@ -19,8 +19,8 @@ from tests.helpers import toml_test_config
 ROOT = pathlib.Path(__file__).resolve().parents[1]
 
 
-def _declared_functions():
-    text = (ROOT / "include" / "leo_hip.h").read_text()
+def _declared_functions(header="leo_hip.h"):
+    text = (ROOT / "include" / header).read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return set(re.findall(r"^\s*(?:[A-Za-z_][\w\s\*]*?)\b(leo_\w+)\s*\(", text, flags=re.M))
 
@@ -36,12 +36,14 @@ def test_header_declares_the_backend_surface():
 
 def test_library_exports_every_declared_function():
     lib = ctypes.CDLL(str(native.LIB_PATH))
-    missing = [name for name in sorted(_declared_functions()) if not hasattr(lib, name)]
+    declared = _declared_functions() | _declared_functions("leo_formats.h")
+    missing = [name for name in sorted(declared) if not hasattr(lib, name)]
     assert not missing, f"declared but not exported: {missing}"
 
 
 def test_python_signatures_cover_exactly_the_header():
     assert set(native.SIGNATURES) == _declared_functions()
+    assert set(native.FORMAT_SIGNATURES) == _declared_functions("leo_formats.h")
 
 
 def test_generated_abi_is_current():
