@@ -1372,7 +1372,17 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
                 const uint32_t g = w.entry[i] >> 16;
                 const uint32_t s0 = w.start[g] - lo, s1 = w.start[g + 1] - lo;
                 uint32_t rank = 0;
-                for (uint32_t j = s0; j < s1; ++j) rank += w.key[j] < mine ? 1u : 0u;
+                // eight independent LDS reads in flight per round (one read
+                // at a time waits out the LDS latency on every key)
+                uint32_t j = s0;
+                for (; j + 8 <= s1; j += 8) {
+                    uint64_t k[8];
+#pragma unroll
+                    for (uint32_t x = 0; x < 8; ++x) k[x] = w.key[j + x];
+#pragma unroll
+                    for (uint32_t x = 0; x < 8; ++x) rank += k[x] < mine ? 1u : 0u;
+                }
+                for (; j < s1; ++j) rank += w.key[j] < mine ? 1u : 0u;
                 if (rank < limit) {
                     const uint32_t n = add_mod(static_cast<uint32_t>(mine), rot, N);
                     const float act = key_activation(mine);
