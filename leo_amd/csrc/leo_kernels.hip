@@ -1983,6 +1983,23 @@ __device__ __forceinline__ void phase_eligibility(const StepCtx& c, bool plastic
     }
 }
 
+// The serial sum of kOutputs values in LDS (runtime.rs:1175-1180 order),
+// read sixteen at a time in 16-byte loads (one read at a time would wait out
+// the LDS latency on every term).
+__device__ __forceinline__ float serial_sum_outputs(const float* v) {
+    static_assert(kOutputs == 257, "256 values in sixteen-value groups, then the last");
+    const f32x4* v4 = reinterpret_cast<const f32x4*>(v);
+    float sum = 0.0f;
+    for (uint32_t g = 0; g < 64; g += 4) {
+        const f32x4 a = v4[g], b = v4[g + 1], c = v4[g + 2], e = v4[g + 3];
+        sum += a.x; sum += a.y; sum += a.z; sum += a.w;
+        sum += b.x; sum += b.y; sum += b.z; sum += b.w;
+        sum += c.x; sum += c.y; sum += c.z; sum += c.w;
+        sum += e.x; sum += e.y; sum += e.z; sum += e.w;
+    }
+    return sum + v[256];
+}
+
 // ---------------------------------------------------------------------------
 // Phase 4: post-activation dynamics (runtime.rs:920-938), emission snapshot
 // (runtime.rs:1084-1106), and on the last workgroup the readout, softmax and
@@ -1995,14 +2012,28 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
     LaneControl* ctl = c.ctl;
     const uint32_t cap = cfg.max_active_global, E = cfg.context_embedding_dim;
     const uint32_t rs = c.tick % kRing;
-    const uint32_t A = ld(&ctl->active_count);
     const uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
     const float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
-    const uint32_t ctx_count = ld(&ctl->ctx_count);
     const uint32_t wave = wave_index(), lane = __lane_id();
+    const uint32_t o1 = threadIdx.x, o2 = threadIdx.x + kThreads;
+    const bool has2 = o2 < kOutputs;
     float* lat = sh.aux;
+    // Memory rounds: (1) the active and context counts, the context slots
+    // and scales, the bias and this thread's first 16 context-projection
+    // weights; (2) the first 256 active ids and activations (into LDS) and
+    // the context embeddings; (3) rows of 32 active neurons at a time.
+    const uint32_t A = ld(&ctl->active_count);
+    const uint32_t ctx_count = ld(&ctl->ctx_count);
+    float l1 = ld(&d.p.bias[o1]), l2 = has2 ? ld(&d.p.bias[o2]) : 0.0f;
+    constexpr uint32_t kDims = 16;
+    float x1[kDims], x2[kDims];
+#pragma unroll
+    for (uint32_t k = 0; k < kDims; ++k) {
+        x1[k] = k < E ? ld(&d.p.ctx_out[o1 * E + k]) : 0.0f;
+        x2[k] = k < E && has2 ? ld(&d.p.ctx_out[o2 * E + k]) : 0.0f;
+    }
     // context latent (runtime.rs:1120-1136): serial over active slots per
-    // dimension; the slots and scales, then the embeddings, in one round each
+    // dimension
     for (uint32_t e = threadIdx.x; e < E; e += kThreads) {
         uint32_t slot[kMaxOrder];
         float scale[kMaxOrder], emb[kMaxOrder];
@@ -2021,47 +2052,71 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
         lat[e] = v;
         d.ctx_latent[e] = v;
     }
-    __syncthreads();
-    // logits[o] = bias[o] + sum over active in order of W[n][o]*a_n (+ context once):
-    // thread t owns outputs t and t+256; per chunk of 16 active neurons their
-    // ids and activations, then the 16 row loads, go out together ahead of the
-    // serial adds
-    const uint32_t o1 = threadIdx.x, o2 = threadIdx.x + kThreads;
-    const bool has2 = o2 < kOutputs;
-    float l1 = ld(&d.p.bias[o1]), l2 = has2 ? ld(&d.p.bias[o2]) : 0.0f;
-    constexpr uint32_t kRows = 16;
-    for (uint32_t r0 = 0; r0 < A; r0 += kRows) {
-        uint64_t n[kRows];
-        float av[kRows], w1[kRows], w2[kRows];
+    // logits[o] = bias[o] + sum over active in order of W[n][o]*a_n (+ context
+    // once): thread t owns outputs t and t+256; the active ids and
+    // activations are staged in LDS 256 at a time, then the rows of 32
+    // neurons go out together ahead of the serial adds
+    // (ids past the block's end read row 0 and are not added, so the row
+    // loads carry no conditions and go out back to back)
+    uint32_t* ids = reinterpret_cast<uint32_t*>(step_lds);
+    float* acts = reinterpret_cast<float*>(step_lds) + kThreads;
+    constexpr uint32_t kRows = 32;
+    static_assert(kThreads % kRows == 0, "whole row chunks per block of ids");
+    for (uint32_t b0 = 0; b0 < A; b0 += kThreads) {
+        const uint32_t bn = min(kThreads, A - b0);
+        __syncthreads();  // the previous block's ids are consumed (and the latent is written)
+        ids[threadIdx.x] = threadIdx.x < bn ? ld(&act_list[b0 + threadIdx.x]) : 0u;
+        if (threadIdx.x < bn) acts[threadIdx.x] = ld(&act_val[b0 + threadIdx.x]);
+        __syncthreads();
+        for (uint32_t r0 = 0; r0 < bn; r0 += kRows) {
+            float w1[kRows], w2[kRows];
+            uint32_t n[kRows];
+            const uint4* ids4 = reinterpret_cast<const uint4*>(ids + r0);
 #pragma unroll
-        for (uint32_t k = 0; k < kRows; ++k) {
-            n[k] = r0 + k < A ? ld(&act_list[r0 + k]) : 0u;
-            av[k] = r0 + k < A ? ld(&act_val[r0 + k]) : 0.0f;
-        }
+            for (uint32_t k = 0; k < kRows / 4; ++k) {
+                const uint4 q = ids4[k];
+                n[4 * k] = q.x;
+                n[4 * k + 1] = q.y;
+                n[4 * k + 2] = q.z;
+                n[4 * k + 3] = q.w;
+            }
 #pragma unroll
-        for (uint32_t k = 0; k < kRows; ++k) {
-            w1[k] = r0 + k < A ? ld(&d.p.out_w[n[k] * kOutStride + o1]) : 0.0f;
-            w2[k] = r0 + k < A && has2 ? ld(&d.p.out_w[n[k] * kOutStride + o2]) : 0.0f;
-        }
+            for (uint32_t k = 0; k < kRows; ++k) {
+                const float* row = d.p.out_w + static_cast<uint64_t>(n[k]) * kOutStride;
+                w1[k] = ld(&row[o1]);
+                w2[k] = has2 ? ld(&row[o2]) : 0.0f;
+            }
+            float av[kRows];
+            const f32x4* acts4 = reinterpret_cast<const f32x4*>(acts + r0);
 #pragma unroll
-        for (uint32_t k = 0; k < kRows; ++k) {
-            if (r0 + k < A) {  // rows in order, the ragged last chunk stops at A
-                l1 += w1[k] * av[k];
-                l2 += w2[k] * av[k];
+            for (uint32_t k = 0; k < kRows / 4; ++k) {
+                const f32x4 q = acts4[k];
+                av[4 * k] = q.x;
+                av[4 * k + 1] = q.y;
+                av[4 * k + 2] = q.z;
+                av[4 * k + 3] = q.w;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < kRows; ++k) {
+                if (r0 + k < bn) {  // rows in order, the ragged last chunk stops at A
+                    l1 += w1[k] * av[k];
+                    l2 += w2[k] * av[k];
+                }
             }
         }
     }
+    __syncthreads();  // the latent is visible (A = 0 skips the loop's barriers)
     // the context contribution (read from the latent in sh.aux) is computed
     // before the neural-loss pass reuses sh.aux, and added after it
     float c1 = 0.0f, c2 = 0.0f;
     if (ctx_count > 0) {
-        constexpr uint32_t kDims = 16;
         for (uint32_t e0 = 0; e0 < E; e0 += kDims) {
-            float x1[kDims], x2[kDims];
+            if (e0 > 0) {
 #pragma unroll
-            for (uint32_t k = 0; k < kDims; ++k) {
-                x1[k] = e0 + k < E ? ld(&d.p.ctx_out[o1 * E + e0 + k]) : 0.0f;
-                x2[k] = e0 + k < E && has2 ? ld(&d.p.ctx_out[o2 * E + e0 + k]) : 0.0f;
+                for (uint32_t k = 0; k < kDims; ++k) {
+                    x1[k] = e0 + k < E ? ld(&d.p.ctx_out[o1 * E + e0 + k]) : 0.0f;
+                    x2[k] = e0 + k < E && has2 ? ld(&d.p.ctx_out[o2 * E + e0 + k]) : 0.0f;
+                }
             }
 #pragma unroll
             for (uint32_t k = 0; k < kDims; ++k) {
@@ -2085,8 +2140,7 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
         __syncthreads();
         StepRecord LEO_GLOBAL& rec = d.records[step_index];
         if (threadIdx.x == 0) {
-            float sum = 0.0f;
-            for (uint32_t o = 0; o < kOutputs; ++o) sum += sh.aux[o];
+            const float sum = serial_sum_outputs(sh.aux);
             rec.neural_max = nm;
             rec.neural_sum = sum;
         }
@@ -2115,11 +2169,7 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
     sh.aux[o1] = glibc_expf_nonpositive(l1 - mx);
     if (has2) sh.aux[o2] = glibc_expf_nonpositive(l2 - mx);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float sum = 0.0f;
-        for (uint32_t o = 0; o < kOutputs; ++o) sum += sh.aux[o];
-        sh.redf[0] = sum;
-    }
+    if (threadIdx.x == 0) sh.redf[0] = serial_sum_outputs(sh.aux);
     __syncthreads();
     const float sum = sh.redf[0];
     const bool uniform = !finitef(sum) || sum <= 0.0f;
