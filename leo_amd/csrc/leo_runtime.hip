@@ -279,7 +279,12 @@ struct LeoHipRuntime {
     bool phase_profile = false;
     double wall_clock_khz = 0.0;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+    std::vector<hipEvent_t> launch_events;  // timing events of queued launches (pairs)
     leo::PinnedStaging staging;  // per-launch transfers (transfer stream + pinned buffer)
+    ~LeoHipRuntime() {
+        if (staging.xfer) (void)hipStreamSynchronize(staging.xfer);
+        for (hipEvent_t e : launch_events) (void)hipEventDestroy(e);
+    }
 };
 
 namespace leo {
@@ -752,45 +757,73 @@ void account_launch(LeoHipRuntime* h, const std::vector<LaneRun>& runs, float ms
 }
 
 // One cooperative launch over all given lanes (each with its own schedule).
-void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
+// One launch of the step kernel queued on the runtime's streams: its lanes'
+// schedules, where its step records and control words arrive in pinned
+// memory, its timing events and the ticks its lanes must reach.
+struct QueuedLaunch {
+    std::vector<LaneRun> runs;
+    std::vector<const char*> records, ctl;
+    std::vector<uint32_t> end_tick;
+    hipEvent_t start = nullptr, stop = nullptr;
+    bool canonical = false;
+};
+
+// Pinned staging bytes one launch of these schedules moves (its uploads and
+// downloads; a reset's descriptors take one more rounded LaneDesc group).
+size_t launch_staging_bytes(size_t lanes, const std::vector<size_t>& steps) {
+    size_t staged = PinnedStaging::rounded(lanes * sizeof(LaneDesc)) + PinnedStaging::rounded(sizeof(KernelArgs));
+    for (size_t n : steps)
+        staged += PinnedStaging::rounded(n * sizeof(StepParams)) + PinnedStaging::rounded(n * sizeof(StepRecord)) +
+                  PinnedStaging::rounded(sizeof(LaneControl));
+    return staged;
+}
+
+// Every lane's schedule buffer holds `steps` steps (allocated while nothing
+// queued can be reading the old one).
+void ensure_schedule(Lane& lane, size_t steps) {
+    const uint32_t need = static_cast<uint32_t>(std::max<size_t>(steps, 1));
+    if (need <= lane.schedule_capacity) return;
+    const uint32_t cap = std::max<uint32_t>(need, 256);
+    lane.schedule.allocate(static_cast<size_t>(cap) * (sizeof(StepParams) + sizeof(StepRecord)) + 512);
+    lane.schedule_capacity = cap;
+}
+
+// Queues one launch without waiting for it: uploads through the pinned
+// staging (after the step stream's queued work, which may still read the
+// buffers they replace), the control words' clears and the kernel, then the
+// downloads on the transfer stream. The caller has reserved the staging
+// space of everything it queues before the next drain, and sized the
+// schedule buffers. The lanes' host tick mirrors advance at once.
+QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent_t start, hipEvent_t stop) {
+    QueuedLaunch q;
     const uint32_t count = static_cast<uint32_t>(runs.size());
-    if (count == 0) return;
     uint64_t max_tick = 0;
     for (auto& r : runs) max_tick = std::max<uint64_t>(max_tick, static_cast<uint64_t>(r.lane->tick) + r.steps.size());
     if (max_tick + static_cast<uint64_t>(h->cfg.device.refractory_ticks) + 2 >= 0xffffffffULL)
         throw Error(LEO_ERR_UNSUPPORTED, "lane tick would exceed the 32-bit device tick range");
-    // every staged transfer of this launch fits without reclaiming space
-    // (downloads stay valid until the final drain)
-    size_t staged = PinnedStaging::rounded(count * sizeof(LaneDesc)) + PinnedStaging::rounded(sizeof(KernelArgs));
-    for (auto& r : runs)
-        staged += PinnedStaging::rounded(r.steps.size() * sizeof(StepParams)) +
-                  PinnedStaging::rounded(r.steps.size() * sizeof(StepRecord)) + PinnedStaging::rounded(sizeof(LaneControl));
-    h->staging.reserve(staged);
     h->staging.follow(h->stream);  // the uploads replace what queued work may still read
     for (auto& r : runs) {
         Lane& lane = *r.lane;
-        uint32_t need = static_cast<uint32_t>(std::max<size_t>(r.steps.size(), 1));
-        if (need > lane.schedule_capacity) {
-            uint32_t cap = std::max<uint32_t>(need, 256);
-            lane.schedule.allocate(static_cast<size_t>(cap) * (sizeof(StepParams) + sizeof(StepRecord)) + 512);
-            lane.schedule_capacity = cap;
-        }
+        if (r.steps.size() > lane.schedule_capacity) throw Error(LEO_ERR_INTERNAL, "schedule buffer not sized");
         lane.desc.steps = reinterpret_cast<const StepParams*>(lane.schedule.base);
         lane.desc.records = reinterpret_cast<StepRecord*>(
             lane.schedule.base + ((static_cast<size_t>(lane.schedule_capacity) * sizeof(StepParams) + 255) & ~size_t(255)));
         lane.desc.step_count = static_cast<uint32_t>(r.steps.size());
         h->staging.h2d(const_cast<StepParams*>(lane.desc.steps), r.steps.data(), r.steps.size() * sizeof(StepParams));
+        // cleared on the transfer stream, after the previous launch's
+        // control words have been downloaded there
         static_assert(offsetof(LaneControl, xcc_mask) == offsetof(LaneControl, barrier) + 8, "cleared together");
-        LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->barrier, 0, 12, h->stream));  // barrier, abort, xcc_mask
-        LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->error_code, 0, 4, h->stream));
+        LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->barrier, 0, 12, h->staging.xfer));  // barrier, abort, xcc_mask
+        LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->error_code, 0, 4, h->staging.xfer));
+        h->staging.pending_uploads = true;
     }
     std::vector<Lane*> lanes;
     for (auto& r : runs) lanes.push_back(r.lane);
     stage_descs(h, lanes);
     // lanes are padded to a multiple of the XCD count so that each lane's
     // workgroups land on one XCD (see lane_steps)
-    const bool canonical = count == 1 && runs[0].lane == h->canonical.get();
-    const LanePlan plan = choose_wgs_per_lane(h, count, canonical);
+    q.canonical = count == 1 && runs[0].lane == h->canonical.get();
+    const LanePlan plan = choose_wgs_per_lane(h, count, q.canonical);
     const uint32_t P = plan.P, stride = plan.stride;
     if (static_cast<uint64_t>(plan.grid) > cooperative_capacity(h->cus, h->coop_blocks_per_cu))
         throw Error(LEO_ERR_INTERNAL, "cooperative launch exceeds the resident workgroup capacity");
@@ -805,32 +838,43 @@ void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
                                           : reinterpret_cast<const void*>(&leo_lane_steps);
     if (h->phase_profile)
         for (auto& r : runs) LEO_HIP_CHECK(hipMemsetAsync(r.lane->desc.phase_profile, 0, 2 * kPhases * 8, h->stream));
-    LEO_HIP_CHECK(hipEventRecord(h->ev_start, h->stream));
+    q.start = start;
+    q.stop = stop;
+    LEO_HIP_CHECK(hipEventRecord(start, h->stream));
     LEO_HIP_CHECK(hipLaunchCooperativeKernel(kernel, dim3(stride * P), dim3(kThreads), params,
                                              step_lds_bytes(h->cfg.device.neurons_per_block), h->stream));
-    LEO_HIP_CHECK(hipEventRecord(h->ev_stop, h->stream));
+    LEO_HIP_CHECK(hipEventRecord(stop, h->stream));
     h->staging.follow(h->stream);
-    std::vector<const char*> staged_records(count), staged_ctl(count);
+    q.records.resize(count);
+    q.ctl.resize(count);
     for (uint32_t i = 0; i < count; ++i) {
-        staged_records[i] = h->staging.d2h(runs[i].lane->desc.records, runs[i].steps.size() * sizeof(StepRecord));
-        staged_ctl[i] = h->staging.d2h(runs[i].lane->desc.ctl, sizeof(LaneControl));
+        q.records[i] = h->staging.d2h(runs[i].lane->desc.records, runs[i].steps.size() * sizeof(StepRecord));
+        q.ctl[i] = h->staging.d2h(runs[i].lane->desc.ctl, sizeof(LaneControl));
+        runs[i].lane->tick += static_cast<uint32_t>(runs[i].steps.size());
+        q.end_tick.push_back(runs[i].lane->tick);
     }
-    LEO_HIP_CHECK(hipStreamSynchronize(h->staging.xfer));  // the kernel and its downloads are complete
+    q.runs = std::move(runs);
+    return q;
+}
+
+// Completes a queued launch once the transfer stream has drained past it:
+// records, timing, telemetry, and the device's error and tick checks.
+void complete_launch(LeoHipRuntime* h, QueuedLaunch& q) {
+    const uint32_t count = static_cast<uint32_t>(q.runs.size());
     std::vector<LaneControl> ctl(count);
     for (uint32_t i = 0; i < count; ++i) {
-        runs[i].records.resize(runs[i].steps.size());
-        std::memcpy(runs[i].records.data(), staged_records[i], runs[i].steps.size() * sizeof(StepRecord));
-        std::memcpy(&ctl[i], staged_ctl[i], sizeof(LaneControl));
+        q.runs[i].records.resize(q.runs[i].steps.size());
+        std::memcpy(q.runs[i].records.data(), q.records[i], q.runs[i].steps.size() * sizeof(StepRecord));
+        std::memcpy(&ctl[i], q.ctl[i], sizeof(LaneControl));
     }
-    h->staging.drain();
     float ms = 0.0f;
-    LEO_HIP_CHECK(hipEventElapsedTime(&ms, h->ev_start, h->ev_stop));
+    LEO_HIP_CHECK(hipEventElapsedTime(&ms, q.start, q.stop));
     h->last_launch_ms = ms;
-    account_launch(h, runs, ms, canonical);
+    account_launch(h, q.runs, ms, q.canonical);
     if (h->phase_profile) {
         // lane 0 of the launch is representative (lanes run the same phase sequence)
         unsigned long long prof[2 * kPhases];
-        download(prof, runs[0].lane->desc.phase_profile, sizeof(prof), h->stream);
+        download(prof, q.runs[0].lane->desc.phase_profile, sizeof(prof), h->stream);
         sync(h->stream);
         for (uint32_t p = 0; p < kPhases; ++p) {
             h->telemetry.phase_work_us[p] += static_cast<double>(prof[p]) / h->wall_clock_khz * 1e3;
@@ -838,7 +882,6 @@ void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
         }
     }
     for (uint32_t i = 0; i < count; ++i) {
-        runs[i].lane->tick += static_cast<uint32_t>(runs[i].steps.size());
         if (ctl[i].error_code != 0) {
             uint32_t code = ctl[i].error_code;
             if (code == kErrBarrier) throw Error(LEO_ERR_DEVICE, "device lane barrier timed out");
@@ -846,8 +889,30 @@ void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
                 throw Error(LEO_ERR_UNSUPPORTED, "global selection exceeds the device sort capacity");
             throw Error(LEO_ERR_NUMERICAL, "device numerical guard tripped (code " + std::to_string(code) + ")");
         }
-        if (ctl[i].tick != runs[i].lane->tick) throw Error(LEO_ERR_INTERNAL, "device lane tick diverged from the host mirror");
+        if (ctl[i].tick != q.end_tick[i]) throw Error(LEO_ERR_INTERNAL, "device lane tick diverged from the host mirror");
     }
+}
+
+void run_lanes_once(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
+    const uint32_t count = static_cast<uint32_t>(runs.size());
+    if (count == 0) return;
+    std::vector<size_t> steps;
+    for (auto& r : runs) {
+        steps.push_back(r.steps.size());
+        ensure_schedule(*r.lane, r.steps.size());
+    }
+    h->staging.reserve(launch_staging_bytes(count, steps));
+    QueuedLaunch q = enqueue_lanes(h, std::move(runs), h->ev_start, h->ev_stop);
+    LEO_HIP_CHECK(hipStreamSynchronize(h->staging.xfer));  // the kernel and its downloads are complete
+    try {
+        complete_launch(h, q);
+    } catch (...) {
+        runs = std::move(q.runs);
+        h->staging.drain();
+        throw;
+    }
+    runs = std::move(q.runs);
+    h->staging.drain();
 }
 
 // Steps of the first launch of a long schedule: a launch stays around a
@@ -941,6 +1006,21 @@ LeoStepMetrics to_metrics(const StepParams& sp, const StepRecord& rec, float los
     return m;
 }
 
+// The canonical runtime's host mirrors after its steps ran (statistics,
+// revision, persistent activity, as Runtime::step keeps them), and the steps'
+// metrics appended to `out`.
+void absorb_canonical(LeoHipRuntime* h, const LaneRun& r, std::vector<LeoStepMetrics>& out) {
+    for (size_t i = 0; i < r.steps.size(); ++i) {
+        float loss = step_loss(r.steps[i], r.records[i]);
+        account_step(h->stats, r.steps[i], r.records[i], loss, h->cfg.device.synapses_per_neuron);
+        if (r.steps[i].flags & kStepLearn) h->revision += 1;
+        if (!(r.steps[i].flags & kStepFrozen)) r.lane->persistent_activity = true;
+        LeoStepMetrics m = to_metrics(r.steps[i], r.records[i], loss);
+        m.emitted_events = r.records[i].active * h->cfg.device.synapses_per_neuron;
+        out.push_back(m);
+    }
+}
+
 // Execute steps on the canonical runtime; stats and revision update the
 // canonical mirrors exactly as Runtime::step does.
 // `outputs[i]` asks for the readout of step i even when it does not learn.
@@ -958,16 +1038,7 @@ std::vector<LeoStepMetrics> canonical_steps(LeoHipRuntime* h, const std::vector<
     run_lanes(h, runs);
     std::vector<LeoStepMetrics> out;
     out.reserve(steps.size());
-    const LaneRun& r = runs[0];
-    for (size_t i = 0; i < r.steps.size(); ++i) {
-        float loss = step_loss(r.steps[i], r.records[i]);
-        account_step(h->stats, r.steps[i], r.records[i], loss, h->cfg.device.synapses_per_neuron);
-        if (r.steps[i].flags & kStepLearn) h->revision += 1;
-        if (!(r.steps[i].flags & kStepFrozen)) lane.persistent_activity = true;
-        LeoStepMetrics m = to_metrics(r.steps[i], r.records[i], loss);
-        m.emitted_events = r.records[i].active * h->cfg.device.synapses_per_neuron;
-        out.push_back(m);
-    }
+    absorb_canonical(h, runs[0], out);
     return out;
 }
 
@@ -980,6 +1051,96 @@ void canonical_reset(LeoHipRuntime* h) {
     std::vector<Lane*> lanes{h->canonical.get()};
     reset_lane_objects(h, lanes, false, 0);
     sync(h->stream);
+}
+
+// A run of canonical steps after an optional reset (one replay segment).
+struct CanonicalSegment {
+    bool reset_before = false;
+    std::vector<HostStep> steps;
+    std::vector<int32_t> permissions;
+};
+
+// Runs the segments on the canonical runtime as the sequential executor
+// would (reset, then the steps, segment by segment), with every reset,
+// schedule upload, launch and download queued back to back and one wait at
+// the end instead of one per launch. Launches take the first launch's step
+// count, then four times the previous one (at most 4096); the results do not
+// depend on how the steps are cut into launches. Metrics of the steps are
+// appended to `out` in order.
+void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment>& segments,
+                            std::vector<LeoStepMetrics>& out) {
+    Lane& lane = *h->canonical;
+    if (h->phase_profile) {  // the profiling build reads its clocks launch by launch
+        for (const CanonicalSegment& seg : segments) {
+            if (seg.reset_before) canonical_reset(h);
+            auto m = canonical_steps(h, seg.steps, seg.permissions, false);
+            out.insert(out.end(), m.begin(), m.end());
+        }
+        return;
+    }
+    // launch cuts and the staging they need, known before anything is queued
+    std::vector<std::vector<size_t>> cuts(segments.size());
+    size_t staged = 0, largest = 0, launches = 0;
+    for (size_t k = 0; k < segments.size(); ++k) {
+        if (segments[k].reset_before) staged += PinnedStaging::rounded(sizeof(LaneDesc));
+        size_t chunk = max_steps_per_launch(h, 1);
+        for (size_t at = 0; at < segments[k].steps.size();) {
+            const size_t n = std::min(chunk, segments[k].steps.size() - at);
+            cuts[k].push_back(n);
+            staged += launch_staging_bytes(1, {n});
+            largest = std::max(largest, n);
+            at += n;
+            chunk = std::min<size_t>(4096, chunk * 4);
+        }
+        launches += cuts[k].size();
+    }
+    if (launches == 0) {
+        for (const CanonicalSegment& seg : segments)
+            if (seg.reset_before) canonical_reset(h);
+        return;
+    }
+    sync(h->stream);
+    ensure_schedule(lane, largest);
+    h->staging.reserve(staged);
+    while (h->launch_events.size() < 2 * launches) {
+        hipEvent_t e;
+        LEO_HIP_CHECK(hipEventCreate(&e));
+        h->launch_events.push_back(e);
+    }
+    std::vector<QueuedLaunch> queued;
+    queued.reserve(launches);
+    for (size_t k = 0; k < segments.size(); ++k) {
+        const CanonicalSegment& seg = segments[k];
+        if (seg.reset_before) {
+            std::vector<Lane*> lanes{&lane};
+            reset_lane_objects(h, lanes, false, 0);
+        }
+        size_t at = 0;
+        for (size_t n : cuts[k]) {
+            LaneRun run{&lane, {}, {}};
+            run.steps.reserve(n);
+            uint32_t tick = lane.tick;
+            for (size_t i = at; i < at + n; ++i)
+                run.steps.push_back(make_step(h->cfg, lane, seg.steps[i].symbol, seg.steps[i].target,
+                                              seg.permissions[i], tick++, false));
+            std::vector<LaneRun> runs;
+            runs.push_back(std::move(run));
+            const size_t e = 2 * queued.size();
+            queued.push_back(enqueue_lanes(h, std::move(runs), h->launch_events[e], h->launch_events[e + 1]));
+            at += n;
+        }
+    }
+    LEO_HIP_CHECK(hipStreamSynchronize(h->staging.xfer));  // every queued kernel and download is complete
+    try {
+        for (QueuedLaunch& q : queued) {
+            complete_launch(h, q);
+            absorb_canonical(h, q.runs[0], out);
+        }
+    } catch (...) {
+        h->staging.drain();
+        throw;
+    }
+    h->staging.drain();
 }
 
 void canonical_finish_document(LeoHipRuntime* h) {  // runtime.rs:357-363
@@ -1837,71 +1998,76 @@ void replay_story(LeoHipRuntime* h, const uint8_t* story, size_t len, const std:
         if (supervised) s.target = p < len ? static_cast<int32_t>(story[p]) : static_cast<int32_t>(kEnd);
         return s;
     };
-    auto execute = [&](const std::vector<HostStep>& steps, const std::vector<int32_t>& perms) {
-        auto metrics = canonical_steps(h, steps, perms, false);
-        for (size_t i = 0; i < metrics.size(); ++i) {
-            if (perms[i] == LEO_FROZEN) continue;
-            rep.activity_steps += 1;
-            rep.active_neurons_sum += metrics[i].active_neurons;
-            rep.emitted_events += metrics[i].emitted_events;
-        }
-    };
+    std::vector<CanonicalSegment> segments;
+    // the cleanup after the replay belongs to its last range: a skipped last
+    // range leaves the runtime as the previous range left it
+    // (replay_target_range_impl, training.rs:1848-1870, 1938)
+    bool cleanup = true;
     if (h->cfg.replay_stateful_batch) {
-        canonical_reset(h);
-        std::vector<HostStep> steps;
-        std::vector<int32_t> perms;
+        CanonicalSegment seg;
+        seg.reset_before = true;
         const size_t terminal = len + 1;
         size_t cursor = 0;
         for (auto [rs, re] : ranges) {
             size_t start = std::max(std::min(rs, terminal), cursor);
             size_t end = std::max(std::min(re, terminal), start);
             for (size_t p = cursor; p < start; ++p) {
-                steps.push_back(position_step(p, false));
-                perms.push_back(LEO_FROZEN);
+                seg.steps.push_back(position_step(p, false));
+                seg.permissions.push_back(LEO_FROZEN);
                 rep.replay_prefix_steps += 1;
             }
             for (size_t p = start; p < end; ++p) {
-                steps.push_back(position_step(p, true));
-                perms.push_back(permission);
+                seg.steps.push_back(position_step(p, true));
+                seg.permissions.push_back(permission);
                 rep.replay_steps += 1;
             }
             cursor = end;
         }
-        if (!steps.empty()) execute(steps, perms);
-        canonical_reset(h);
-        return;
-    }
-    for (size_t ri = 0; ri < ranges.size(); ++ri) {
-        auto [rs, re] = ranges[ri];
-        if (rs >= re || rs > len) continue;
-        size_t end = std::min(re, len + 1);
-        canonical_reset(h);  // begin_document_deferred_for_replay
-        std::vector<HostStep> steps;
-        std::vector<int32_t> perms;
-        size_t next = rs;
-        if (next > 0) {
-            steps.push_back({kBegin, -1});
-            perms.push_back(LEO_FROZEN);
-            for (size_t i = 0; i + 1 < next; ++i) {
-                steps.push_back({story[i], -1});
-                perms.push_back(LEO_FROZEN);
+        segments.push_back(std::move(seg));
+    } else {
+        for (auto [rs, re] : ranges) {
+            cleanup = !(rs >= re || rs > len);
+            if (!cleanup) continue;
+            size_t end = std::min(re, len + 1);
+            CanonicalSegment seg;
+            seg.reset_before = true;  // begin_document_deferred_for_replay
+            size_t next = rs;
+            if (next > 0) {
+                seg.steps.push_back({kBegin, -1});
+                seg.permissions.push_back(LEO_FROZEN);
+                for (size_t i = 0; i + 1 < next; ++i) {
+                    seg.steps.push_back({story[i], -1});
+                    seg.permissions.push_back(LEO_FROZEN);
+                }
+                rep.replay_prefix_steps += next;
             }
-            rep.replay_prefix_steps += next;
+            if (next == 0) {
+                seg.steps.push_back({kBegin, story[0]});
+                seg.permissions.push_back(permission);
+                rep.replay_steps += 1;
+                next = 1;
+            }
+            for (size_t p = next; p < end; ++p) {
+                seg.steps.push_back(position_step(p, true));
+                seg.permissions.push_back(permission);
+                rep.replay_steps += 1;
+            }
+            segments.push_back(std::move(seg));
         }
-        if (next == 0) {
-            steps.push_back({kBegin, story[0]});
-            perms.push_back(permission);
-            rep.replay_steps += 1;
-            next = 1;
-        }
-        for (size_t p = next; p < end; ++p) {
-            steps.push_back(position_step(p, true));
-            perms.push_back(permission);
-            rep.replay_steps += 1;
-        }
-        execute(steps, perms);
-        if (ri + 1 == ranges.size()) canonical_reset(h);
+        if (segments.empty()) return;
     }
+    std::vector<LeoStepMetrics> metrics;
+    run_canonical_segments(h, segments, metrics);
+    size_t at = 0;
+    for (const CanonicalSegment& seg : segments)
+        for (int32_t perm : seg.permissions) {
+            const LeoStepMetrics& m = metrics[at++];
+            if (perm == LEO_FROZEN) continue;
+            rep.activity_steps += 1;
+            rep.active_neurons_sum += m.active_neurons;
+            rep.emitted_events += m.emitted_events;
+        }
+    if (cleanup) canonical_reset(h);
 }
 
 }  // namespace
