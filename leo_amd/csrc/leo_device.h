@@ -37,6 +37,8 @@ constexpr uint32_t kMaxBlockNeurons = 1024;
 constexpr uint32_t kWaveSize = 64;
 constexpr uint32_t kWavesPerGroup = kThreads / kWaveSize;
 constexpr uint32_t kMaxWaves = 1024;     // selecting waves per lane (workgroups per lane <= 256)
+constexpr uint32_t kMaxLaneWgs = kMaxWaves / kWavesPerGroup;  // workgroups per lane
+constexpr uint32_t kFlagWords = 32;       // a barrier arrival flag per 128-byte L2 line
 constexpr uint32_t kXcds = 8;            // accelerator complex dies of an MI355X (workgroups dispatched round-robin)
 
 // Touched-neuron bitmap: each block owns ceil(neurons_per_block/32) words,
@@ -254,6 +256,9 @@ constexpr uint8_t kMarkClean = 0, kMarkListed = 1, kMarkDropped = 2;
 struct LaneDesc {
     LaneParams p;
     LaneControl LEO_GLOBAL* ctl;
+    // kMaxLaneWgs * kFlagWords: workgroup p's barrier arrival epoch at word
+    // p * kFlagWords (cleared by workgroup p before the launch's first barrier)
+    uint32_t LEO_GLOBAL* barrier_flags;
     // neuron state (N)
     // neuron state (N records of kNeuronWords words, fields NeuronField): what
     // one touched neuron needs shares one 64-byte record

@@ -259,42 +259,74 @@ __device__ __forceinline__ uint32_t xcc_id() {
     return v;
 }
 
-// Lane-group barrier. Thread 0 of each of the P workgroups arrives on the
-// lane's counter and waits for the others; the wait is bounded, and on
-// timeout the lane is aborted so every workgroup leaves the step loop and the
-// grid drains.
+// Barrier of the P workgroups of one lane; false when the lane aborted
+// (another workgroup's wait timed out or the host's spin limit ran out).
+// Workgroups on one XCD (`local`) share its L2: each stores its arrival epoch
+// to a flag of its own 128-byte line, and the first wave polls the P flags,
+// one lane per flag, so that arrivals and polls spread over the L2 channels
+// (a shared counter queues every arrival atomic and every poll on one
+// channel: measured, a frozen step at 32 workgroups took 10% longer). A lane
+// spread over several XCDs counts arrivals with a device-scope atomic counter
+// between release and acquire fences.
 //
 // Visibility. With `local` (all workgroups of the lane verified to run on one
-// XCD, hence share one L2, and every cross-workgroup read done with ld()),
-// waiting until this thread's stores have completed to L2 is the whole release
-// and nothing needs invalidating. Otherwise agent-scope release/acquire fences
-// write back and invalidate the L2 so other XCDs see the data.
-__device__ __forceinline__ bool lane_barrier(LaneControl* ctl, uint32_t P, uint32_t& target, uint32_t spin_limit, bool local) {
+// XCD, and every cross-workgroup read done with ld()), waiting until this
+// workgroup's stores have completed to L2 is the whole release and nothing
+// needs invalidating. Otherwise agent-scope fences write back and invalidate
+// the L2 so other XCDs see the data. The wait is bounded: on timeout the lane
+// is aborted, so every workgroup leaves the step loop and the grid drains.
+__device__ __forceinline__ bool lane_barrier(const LaneDesc& d, uint32_t part, uint32_t P, uint32_t& target,
+                                             uint32_t spin_limit, bool local) {
     __shared__ uint32_t s_abort;
+    LaneControl* ctl = d.ctl;
     if (P == 1) {
         __syncthreads();
         return true;
     }
     if (local) {
         __builtin_amdgcn_s_waitcnt(0);
-    } else {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        target += P;
-        if (local) {
-            __hip_atomic_fetch_add(&ctl->barrier, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            __hip_atomic_fetch_add(&ctl->barrier, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        target += P;  // every thread keeps the count (the polling wave compares against it)
+        const uint32_t epoch = __builtin_amdgcn_readfirstlane(target / P);
+        if (threadIdx.x < kWaveSize) {
+            const uint32_t lane = threadIdx.x;
+            uint32_t LEO_GLOBAL* flags = d.barrier_flags;
+            if (lane == 0)
+                __hip_atomic_store(&flags[part * kFlagWords], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uint32_t spins = 0, aborted = 0;
+            for (;;) {
+                bool arrived = true;
+                for (uint32_t w = lane; w < P; w += kWaveSize) arrived &= ld(&flags[w * kFlagWords]) >= epoch;
+                if (__all(arrived)) break;
+                if ((spins & 15) == 15 && ld(&ctl->abort) != 0) {
+                    aborted = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                if (++spins > spin_limit) {
+                    if (lane == 0) {
+                        __hip_atomic_store(&ctl->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        set_error(ctl, kErrBarrier);
+                    }
+                    aborted = 1;
+                    break;
+                }
+            }
+            if (lane == 0) s_abort = aborted;
         }
+        __syncthreads();
+        return s_abort == 0;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    target += P;
+    if (threadIdx.x == 0) {
+        __hip_atomic_fetch_add(&ctl->barrier, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         uint32_t spins = 0;
         uint32_t aborted = 0;
         for (;;) {
-            // one poll in flight per workgroup (more load the counter's L2
-            // channel and slow the arrivals); the abort flag every 16th
-            const uint32_t arrived = local ? ld(&ctl->barrier)
-                                           : __hip_atomic_load(&ctl->barrier, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+            // one poll in flight per workgroup; the abort flag every 16th
+            const uint32_t arrived = __hip_atomic_load(&ctl->barrier, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
             if (arrived >= target) break;
             if ((spins & 15) == 15 && ld(&ctl->abort) != 0) {
                 aborted = 1;
@@ -311,7 +343,7 @@ __device__ __forceinline__ bool lane_barrier(LaneControl* ctl, uint32_t P, uint3
         s_abort = aborted;
     }
     __syncthreads();
-    if (!local) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     return s_abort == 0;
 }
 
@@ -875,6 +907,7 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
     const uint32_t v0 = __float_as_uint(fe[0].z), v1 = __float_as_uint(fe[1].z);
     const bool refr = __float_as_uint(q2.w) > tick;
     const float threshold = ld(&d.p.threshold[n]);
+    const float excitability = a.m.excitability[n];  // in the same round, though a refractory neuron skips it
     *deferred = cnt > 8;
     if (cnt > 8) return 0.0f;  // every load above is in flight together; nothing written yet
     const uint32_t e = tick - last;
@@ -945,7 +978,7 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
         const float gate = clampf(b3, 0.0f, 1.0f);
         const float net = b0 + b2 * gate + b1;
         const float adaptation = ad0 + ad1 + ad2;
-        const float drive = a.m.excitability[n] * net - fat - adaptation - pi;
+        const float drive = excitability * net - fat - adaptation - pi;
         mem = mem + drive;
     }
     if (e > 0 || !refr) (*nf(d, n, kNMembrane)) = mem;
@@ -2614,7 +2647,7 @@ __device__ __forceinline__ bool phase_barrier(const StepCtx& c, uint32_t& target
     unsigned long long arrived = 0;
     const bool timer = kProfile && c.part == 0 && threadIdx.x == 0;
     if (timer) clock.arrive(phase, arrived);
-    const bool ok = lane_barrier(c.ctl, c.P, target, spin_limit, c.local);
+    const bool ok = lane_barrier(c.d, c.part, c.P, target, spin_limit, c.local);
     if (timer) clock.release(phase, arrived);
     return ok;
 }
@@ -2664,8 +2697,13 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
     const bool redundant = args.redundant_global != 0;
     const uint32_t spin = args.spin_limit;
     if (P > 1 && args.local_sync) {
-        if (threadIdx.x == 0) atomicOr(&c.ctl->xcc_mask, 1u << xcc_id());
-        if (!lane_barrier(c.ctl, P, target, spin, false)) return;
+        // each workgroup clears its barrier flag (last launch's epochs)
+        // before the launch's first barrier, which counts arrivals instead
+        if (threadIdx.x == 0) {
+            atomicOr(&c.ctl->xcc_mask, 1u << xcc_id());
+            c.d.barrier_flags[c.part * kFlagWords] = 0u;
+        }
+        if (!lane_barrier(c.d, c.part, P, target, spin, false)) return;
         c.local = __popc(ld(&c.ctl->xcc_mask)) == 1;
     }
     if (threadIdx.x < kRing) {

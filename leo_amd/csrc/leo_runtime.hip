@@ -373,7 +373,7 @@ void copy_params(const LaneParams& dst, const LaneParams& src, const Sizes& z, h
 
 void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     Layout l;
-    size_t o_ctl = l.add<LaneControl>(1);
+    size_t o_ctl = l.add<LaneControl>(1), o_flag = l.add<uint32_t>(kMaxLaneWgs * kFlagWords);
     size_t o_neu = l.add<uint32_t>(kNeuronWords * z.n), o_tl = l.add<uint32_t>(z.n);
     size_t o_ls = l.add<float>(z.n), o_dl = l.add<uint32_t>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
     size_t o_rl = l.add<uint32_t>(z.ns), o_il = l.add<uint32_t>(z.ni);
@@ -395,6 +395,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     char* b = lane.state.base;
     LaneDesc& d = lane.desc;
     d.ctl = reinterpret_cast<LaneControl*>(b + o_ctl);
+    d.barrier_flags = reinterpret_cast<uint32_t*>(b + o_flag);
     d.neuron = reinterpret_cast<uint32_t*>(b + o_neu);
     d.touched_list = reinterpret_cast<uint32_t*>(b + o_tl);
 
@@ -801,6 +802,12 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
     for (auto& r : runs) max_tick = std::max<uint64_t>(max_tick, static_cast<uint64_t>(r.lane->tick) + r.steps.size());
     if (max_tick + static_cast<uint64_t>(h->cfg.device.refractory_ticks) + 2 >= 0xffffffffULL)
         throw Error(LEO_ERR_UNSUPPORTED, "lane tick would exceed the 32-bit device tick range");
+    // lanes are padded to a multiple of the XCD count so that each lane's
+    // workgroups land on one XCD (see lane_steps)
+    q.canonical = count == 1 && runs[0].lane == h->canonical.get();
+    const LanePlan plan = choose_wgs_per_lane(h, count, q.canonical);
+    const uint32_t P = plan.P, stride = plan.stride;
+    if (P > kMaxLaneWgs) throw Error(LEO_ERR_INTERNAL, "more workgroups per lane than barrier flags");
     h->staging.follow(h->stream);  // the uploads replace what queued work may still read
     for (auto& r : runs) {
         Lane& lane = *r.lane;
@@ -820,11 +827,6 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
     std::vector<Lane*> lanes;
     for (auto& r : runs) lanes.push_back(r.lane);
     stage_descs(h, lanes);
-    // lanes are padded to a multiple of the XCD count so that each lane's
-    // workgroups land on one XCD (see lane_steps)
-    q.canonical = count == 1 && runs[0].lane == h->canonical.get();
-    const LanePlan plan = choose_wgs_per_lane(h, count, q.canonical);
-    const uint32_t P = plan.P, stride = plan.stride;
     if (static_cast<uint64_t>(plan.grid) > cooperative_capacity(h->cus, h->coop_blocks_per_cu))
         throw Error(LEO_ERR_INTERNAL, "cooperative launch exceeds the resident workgroup capacity");
     KernelArgs a = kernel_args(h, reinterpret_cast<LaneDesc*>(h->lane_descs.base), count, P);
