@@ -197,16 +197,25 @@ struct LaneControl {
     alignas(128) uint32_t barrier;   // lane-group barrier arrival counter
     uint32_t abort;
     uint32_t xcc_mask;               // XCDs the lane's workgroups run on (bit per XCD)
-    alignas(128) uint32_t tick_touched[2];  // touched count, indexed by tick parity
-    uint32_t tick_supra[2];          // suprathreshold count, indexed by tick parity
-    uint32_t tick_events[2];         // delivered events, indexed by tick parity
-    uint32_t tick_dest[2];           // learning destinations, indexed by tick parity
-    uint32_t tick_ainh[2];           // active inhibitory sources, indexed by tick parity
-    uint32_t tick_scan_rec[2];       // eligible recurrent slots scanned, indexed by tick parity
-    uint32_t tick_scan_in[2];        // eligible input slots scanned, indexed by tick parity
-    uint32_t tick_learn[2];          // learning slots listed, indexed by tick parity
-    uint32_t tick_deep[2];           // deep bucket folds (StepRecord::deep_folds), indexed by tick parity
 };
+
+// Per-tick work counters of the step records, kept per workgroup: workgroup p
+// adds to the words of its own 128-byte line (p * kFlagWords + 2 * kind +
+// tick parity), and a recording wave sums the P lines. (One shared line
+// queues every workgroup's atomics on one L2 channel ahead of each barrier.)
+enum CounterKind : uint32_t {
+    kCTouched,      // touched neurons
+    kCSupra,        // suprathreshold neurons
+    kCEvents,       // delivered events
+    kCDest,         // learning destinations
+    kCInhibitory,   // active inhibitory sources
+    kCScanRec,      // eligible recurrent slots scanned
+    kCScanIn,       // eligible input slots scanned
+    kCLearn,        // learning slots listed
+    kCDeep,         // deep bucket folds (StepRecord::deep_folds)
+    kCounterKinds
+};
+static_assert(2 * kCounterKinds <= kFlagWords, "a workgroup's counters fit its line");
 
 // Learned parameters of a lane (private copy for story lanes, the canonical
 // image for the canonical runtime).
@@ -259,6 +268,7 @@ struct LaneDesc {
     // kMaxLaneWgs * kFlagWords: workgroup p's barrier arrival epoch at word
     // p * kFlagWords (cleared by workgroup p before the launch's first barrier)
     uint32_t LEO_GLOBAL* barrier_flags;
+    uint32_t LEO_GLOBAL* wg_counts;  // kMaxLaneWgs * kFlagWords: per-workgroup tick counters (CounterKind)
     // neuron state (N)
     // neuron state (N records of kNeuronWords words, fields NeuronField): what
     // one touched neuron needs shares one 64-byte record

@@ -115,22 +115,6 @@ __device__ uint64_t context_key(const uint32_t* history, uint32_t len, uint32_t 
 __device__ __forceinline__ void set_error(LaneControl* ctl, uint32_t code) { atomicCAS(&ctl->error_code, 0u, code); }
 __device__ __forceinline__ void mark_bit(uint32_t* bits, uint32_t index) { atomicOr(&bits[index >> 5], 1u << (index & 31)); }
 
-// Workgroup-wide sum of a per-thread count, added to *global once.
-// Workgroup total of a per-thread count, valid on thread 0.
-__device__ uint32_t wg_total(uint32_t local) {
-    __shared__ uint32_t s_count;
-    if (threadIdx.x == 0) s_count = 0;
-    __syncthreads();
-    if (local) atomicAdd(&s_count, local);
-    __syncthreads();
-    return s_count;
-}
-
-__device__ void add_count(uint32_t* global, uint32_t local) {
-    const uint32_t total = wg_total(local);
-    if (threadIdx.x == 0 && total) atomicAdd(global, total);
-}
-
 // Wave-aggregated append: one atomic per wave instead of one per lane. Must be
 // reached by every active lane of the wave (wave-uniform control flow).
 __device__ __forceinline__ uint32_t wave_append(uint32_t* counter, bool pred) {
@@ -467,18 +451,43 @@ struct LateCounters {
     uint32_t events, touched, scanned_rec, scanned_in, destinations, inhibitory, learning, deep;
 };
 
-__device__ __forceinline__ LateCounters load_late_counters(LaneControl LEO_GLOBAL* ctl, uint32_t tick) {
-    const uint32_t k = tick & 1;
-    LateCounters v;
-    v.events = ld(&ctl->tick_events[k]);
-    v.touched = ld(&ctl->tick_touched[k]);
-    v.scanned_rec = ld(&ctl->tick_scan_rec[k]);
-    v.scanned_in = ld(&ctl->tick_scan_in[k]);
-    v.destinations = ld(&ctl->tick_dest[k]);
-    v.inhibitory = ld(&ctl->tick_ainh[k]);
-    v.learning = ld(&ctl->tick_learn[k]);
-    v.deep = ld(&ctl->tick_deep[k]);
-    return v;
+__device__ __forceinline__ uint32_t LEO_GLOBAL* counter_word(const StepCtx& c, uint32_t part, uint32_t kind,
+                                                          uint32_t tick) {
+    return c.d.wg_counts + part * kFlagWords + 2 * kind + (tick & 1);
+}
+
+// Adds a wave's count to its workgroup's counter (every lane of the wave calls).
+__device__ __forceinline__ void count_wave(const StepCtx& c, uint32_t kind, uint32_t tick, uint32_t local) {
+    const uint32_t total = wave_sum_u32(local);
+    if (__lane_id() == 0 && total) atomicAdd(counter_word(c, c.part, kind, tick), total);
+}
+
+// One counter of `tick` summed over the lane's workgroups by a whole wave, uniform.
+__device__ __forceinline__ uint32_t counter_total(const StepCtx& c, uint32_t kind, uint32_t tick) {
+    uint32_t v = 0;
+    for (uint32_t w = __lane_id(); w < c.P; w += kWaveSize) v += ld(counter_word(c, w, kind, tick));
+    return wave_sum_u32(v);
+}
+
+// The late counters of `tick` by a whole wave (all loads in one round), uniform.
+__device__ __forceinline__ LateCounters load_late_counters(const StepCtx& c, uint32_t tick) {
+    uint32_t v[kCounterKinds];
+#pragma unroll
+    for (uint32_t k = 0; k < kCounterKinds; ++k) v[k] = 0;
+    for (uint32_t w = __lane_id(); w < c.P; w += kWaveSize) {
+#pragma unroll
+        for (uint32_t k = 0; k < kCounterKinds; ++k) v[k] += ld(counter_word(c, w, k, tick));
+    }
+    LateCounters out;
+    out.events = wave_sum_u32(v[kCEvents]);
+    out.touched = wave_sum_u32(v[kCTouched]);
+    out.scanned_rec = wave_sum_u32(v[kCScanRec]);
+    out.scanned_in = wave_sum_u32(v[kCScanIn]);
+    out.destinations = wave_sum_u32(v[kCDest]);
+    out.inhibitory = wave_sum_u32(v[kCInhibitory]);
+    out.learning = wave_sum_u32(v[kCLearn]);
+    out.deep = wave_sum_u32(v[kCDeep]);
+    return out;
 }
 
 __device__ __forceinline__ void store_late_record(const LaneDesc& d, uint32_t step_index, const LateCounters& v) {
@@ -493,31 +502,25 @@ __device__ __forceinline__ void store_late_record(const LaneDesc& d, uint32_t st
     rec.deep_folds = v.deep;
 }
 
-// all loads first (one round trip), then the stores
-__device__ __forceinline__ void finalize_record(const LaneDesc& d, LaneControl LEO_GLOBAL* ctl, uint32_t step_index,
-                                                uint32_t tick) {
-    store_late_record(d, step_index, load_late_counters(ctl, tick));
+// By a whole wave: all loads first (one round trip), then the stores.
+__device__ __forceinline__ void finalize_record(const StepCtx& c, uint32_t step_index, uint32_t tick) {
+    const LateCounters v = load_late_counters(c, tick);
+    if (__lane_id() == 0) store_late_record(c.d, step_index, v);
 }
 
-// Clears the per-tick counters that tick+1 reuses.
-__device__ __forceinline__ void clear_counters(LaneControl LEO_GLOBAL* ctl, uint32_t tick) {
-    const uint32_t n = (tick + 1) & 1;
-    ctl->tick_touched[n] = 0;
-    ctl->tick_supra[n] = 0;
-    ctl->tick_events[n] = 0;
-    ctl->tick_dest[n] = 0;
-    ctl->tick_ainh[n] = 0;
-    ctl->tick_scan_rec[n] = 0;
-    ctl->tick_scan_in[n] = 0;
-    ctl->tick_learn[n] = 0;
-    ctl->tick_deep[n] = 0;
+// Clears the per-tick counters that tick+1 reuses, by a whole wave (after its
+// loads of tick-1's counters, which share the words).
+__device__ __forceinline__ void clear_counters(const StepCtx& c, uint32_t tick) {
+    for (uint32_t w = __lane_id(); w < c.P; w += kWaveSize) {
+#pragma unroll
+        for (uint32_t k = 0; k < kCounterKinds; ++k) *counter_word(c, w, k, tick + 1) = 0u;
+    }
 }
-// Once tick-1 is complete (phase 3 of `tick`, by one thread): its record is
-// finished and its per-tick counters, which tick+1 reuses, are cleared.
+// Once tick-1 is complete (by one wave): its record is finished and its
+// per-tick counters, which tick+1 reuses, are cleared.
 __device__ __forceinline__ void roll_counters(const StepCtx& c, uint32_t step_index) {
-    LaneControl LEO_GLOBAL* ctl = c.ctl;
-    if (step_index > 0) finalize_record(c.d, ctl, step_index - 1, c.tick - 1);
-    clear_counters(ctl, c.tick);
+    if (step_index > 0) finalize_record(c, step_index - 1, c.tick - 1);
+    clear_counters(c, c.tick);
 }
 
 // Entry p of target n's delivery bucket: the first kFixedEntries at fixed
@@ -720,7 +723,7 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
     const DeliverPlan p = deliver_plan(c, sh, false);
     uint32_t delivered = 0;
     deliver_items(c, sp, p, c.gtid, delivered);
-    add_count(&c.ctl->tick_events[p.tick & 1], delivered);
+    count_wave(c, kCEvents, p.tick, delivered);
 }
 
 // ---------------------------------------------------------------------------
@@ -1199,7 +1202,7 @@ __device__ float deep_fold(const StepCtx& c, uint32_t n, float pi, bool* refract
         mem = mem + drive;
     }
     if (lane == 0) {
-        atomicAdd(&c.ctl->tick_deep[tick & 1], cnt <= kDeepRegisterEntries ? 1u : 0x10000u);
+        atomicAdd(counter_word(c, c.part, kCDeep, tick), cnt <= kDeepRegisterEntries ? 1u : 0x10000u);
         if (e > 0) {
             (*nf(d, n, kNFatigue)) = fat;
             (*nf(d, n, kNAdapt0)) = ad0;
@@ -1453,12 +1456,12 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
     }
     supra = wave_sum_u32(supra);
     if (lane == 0) {
-        if (supra) atomicAdd(&c.ctl->tick_supra[tick & 1], supra);
+        if (supra) atomicAdd(counter_word(c, c.part, kCSupra, tick), supra);
         sh.win_count[wave] = staged;
         d.wave_total[wv] = staged;
         d.wave_touched[wv] = listed_before;
+        if (listed_before) atomicAdd(counter_word(c, c.part, kCTouched, tick), listed_before);
     }
-    add_count(&c.ctl->tick_touched[tick & 1], lane == 0 ? listed_before : 0u);
 }
 
 // ---------------------------------------------------------------------------
@@ -1490,16 +1493,20 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     const uint64_t row0 = static_cast<uint64_t>(b0) * limit;
     // round 1: the per-wave totals, this wave's winners' state and first
     // synapses, and this thread's first item of the next tick
-    // the recording thread's loads go out in the same round; it runs on the
+    // the recording wave's loads go out in the same round; it runs on the
     // workgroup that selects nothing (the least work in this phase)
-    const bool recorder = c.part == c.P - 1 && threadIdx.x == 0;
+    const bool rec_wave = c.part == c.P - 1 && wave == 0;
+    const bool recorder = rec_wave && lane == 0;
     float pi_old = 0.0f;
     uint32_t supra = 0, rec_n = 0, in_n = 0, cells = 0, probes = 0, applied = 0;
     LateCounters late{};
+    if (rec_wave) {
+        if (fuse_post) supra = counter_total(c, kCSupra, c.tick);
+        if (step_index > 0) late = load_late_counters(c, c.tick - 1);
+    }
     if (recorder) {
         pi_old = ld(&c.ctl->population_inhibition);
         if (fuse_post) {
-            supra = ld(&c.ctl->tick_supra[c.tick & 1]);
             rec_n = ld(&c.ctl->rec_count[c.parity]);
             in_n = ld(&c.ctl->in_count[c.parity]);
             // the context of this step is resolved (phase 1 or 2); the next
@@ -1509,7 +1516,6 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
             probes = ld(&c.ctl->ctx_probes);
             applied = ld(&c.ctl->ctx_applied);
         }
-        if (step_index > 0) late = load_late_counters(c.ctl, c.tick - 1);
     }
     const DeliverPlan np = deliver_plan(c, sh, true);
     const bool deliver_next = ahead && np.delivers;
@@ -1564,11 +1570,10 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     }
     const float activity = static_cast<float>(all) / static_cast<float>(cfg.neuron_count);
     if (recorder) {
-        // tick-1's record is finished and its counters, which tick+1 reuses,
-        // are cleared (tick-1 is complete)
+        // tick-1's record is finished (tick-1 is complete); the recording
+        // wave then clears its counters, which tick+1 reuses
         LaneControl LEO_GLOBAL* ctl = c.ctl;
         if (step_index > 0) store_late_record(d, step_index - 1, late);
-        clear_counters(ctl, c.tick);
         ctl->active_count = all;
         ctl->block_selected = all;
         ctl->clipped = 0;
@@ -1596,6 +1601,7 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
             rec.error_code = 0;
         }
     }
+    if (rec_wave) clear_counters(c, c.tick);  // after its loads of tick-1's counters
     if (!fuse_post) return 0;
     // Post-fire updates of this wave's winners and their emission snapshots
     // (the post phase, runtime.rs:920-938, 1084-1106), folded in here when no
@@ -1652,7 +1658,7 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
         snapshot(r, j, act, ld(&d.p.rec_weight[slot]), c.a->m.rec_edge[slot]);
     }
     if (ahead) deliver_items(c, next, np, c.gtid + np.stride, delivered);
-    add_count(&c.ctl->tick_ainh[c.tick & 1], inhibitory);
+    count_wave(c, kCInhibitory, c.tick, inhibitory);
     if (threadIdx.x == 0) {  // the next deliveries read this tick's ring entry from LDS
         sh.ring_tick[rs] = c.tick;
         sh.ring_count[rs] = all;
@@ -1781,8 +1787,8 @@ __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, 
         if (c.part != 0) return;
     }
     __syncthreads();
+    if (threadIdx.x < kWaveSize) roll_counters(c, step_index);
     if (threadIdx.x == 0) {
-        roll_counters(c, step_index);
         LaneControl* ctl = c.ctl;
         ctl->active_count = active;
         ctl->block_selected = running;
@@ -2000,8 +2006,8 @@ __device__ __forceinline__ void phase_eligibility(const StepCtx& c, bool plastic
     const uint32_t p = c.parity, q = c.parity ^ 1;
     const uint32_t rec_n = ld(&c.ctl->rec_count[p]), in_n = ld(&c.ctl->in_count[p]);
     if (c.part == 0 && threadIdx.x == 0) {
-        c.ctl->tick_scan_rec[c.tick & 1] = rec_n;
-        c.ctl->tick_scan_in[c.tick & 1] = in_n;
+        *counter_word(c, 0, kCScanRec, c.tick) = rec_n;
+        *counter_word(c, 0, kCScanIn, c.tick) = in_n;
     }
     const float pop_cutoff = a.redundant_global ? 0.0f : ld(&c.ctl->pop_cutoff);
     LearnOut rec{d.rec_learn, &c.ctl->rec_learn_count, plastic, 0, 0};
@@ -2011,8 +2017,8 @@ __device__ __forceinline__ void phase_eligibility(const StepCtx& c, bool plastic
     eligibility_list(c, d.in_trace, NI, d.in_mark, d.in_list + p * NI, in_n, d.in_list + q * NI,
                      &c.ctl->in_count[q], a.m.in_target, a.m.in_branch, pop_cutoff, in);
     if (plastic) {
-        add_count(&c.ctl->tick_dest[c.tick & 1], in.claimed);
-        add_count(&c.ctl->tick_learn[c.tick & 1], in.listed);
+        count_wave(c, kCDest, c.tick, in.claimed);
+        count_wave(c, kCLearn, c.tick, in.listed);
     }
 }
 
@@ -2269,18 +2275,19 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
             d.ring_edge[rb * S + j] = a.m.rec_edge[slot];
         }
     }
-    add_count(&c.ctl->tick_ainh[c.tick & 1], inhibitory);
+    count_wave(c, kCInhibitory, c.tick, inhibitory);
     if (threadIdx.x == 0) {  // the next deliveries read this tick's ring entry from LDS
         sh.ring_tick[rs] = c.tick;
         sh.ring_count[rs] = A;
     }
     const uint32_t readout_wg = c.P - 1;
     if (c.part == readout_wg) {
+        const uint32_t supra = threadIdx.x < kWaveSize ? counter_total(c, kCSupra, c.tick) : 0u;
         if (threadIdx.x == 0) {
             LaneControl LEO_GLOBAL* ctl = c.ctl;
             // the loads go out together, before any store
             const float pi = ld(&ctl->population_inhibition);
-            const uint32_t supra = ld(&ctl->tick_supra[c.tick & 1]), selected = ld(&ctl->block_selected);
+            const uint32_t selected = ld(&ctl->block_selected);
             const uint32_t clipped = ld(&ctl->clipped), cells = ld(&ctl->ctx_count);
             const uint32_t probes = ld(&ctl->ctx_probes), applied = ld(&ctl->ctx_applied);
             const uint32_t rec_n = ld(&ctl->rec_count[c.parity]), in_n = ld(&ctl->in_count[c.parity]);
@@ -2750,9 +2757,9 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             if (c.part == c.P - 1) context_resolve(c, sp, sh);
             phase_deliver(c, sp, sh);
             if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 0))) break;
-        } else if (threadIdx.x == 0 && pending_events != 0) {
+        } else if (__lane_id() == 0 && pending_events != 0) {
             // the previous step's write_active has rolled this tick's counters
-            atomicAdd(&c.ctl->tick_events[c.tick & 1], pending_events);
+            atomicAdd(counter_word(c, c.part, kCEvents, c.tick), pending_events);
         }
         // this step's destination and learning-slot lists start empty (filled
         // by the eligibility phase) under a new claim epoch
@@ -2784,7 +2791,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             if (trace) phase_eligibility(c, plastic);
             if (pipeline) {
                 if (c.P == 1) context_resolve(c, next, sh);
-                pending_events = wg_total(delivered);
+                pending_events = wave_sum_u32(delivered);
             }
         } else {
             global_select(c, sh, s);
@@ -2810,8 +2817,8 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         delivered_ahead = pipeline;
         c.tick += 1;
     }
+    if (ok && c.part == 0 && threadIdx.x < kWaveSize && steps > 0) finalize_record(c, steps - 1, c.tick - 1);
     if (ok && c.part == 0 && threadIdx.x == 0) {
-        if (steps > 0) finalize_record(c.d, c.ctl, steps - 1, c.tick - 1);
         c.ctl->tick = c.tick;
         c.ctl->parity = c.parity;
         c.ctl->dest_epoch = c.dest_epoch;
@@ -2908,6 +2915,7 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
         d.wave_total[i] = 0;
         d.wave_touched[i] = 0;
     }
+    for (uint64_t i = t0; i < kMaxLaneWgs * kFlagWords; i += ts) d.wg_counts[i] = 0;
     if (part == 0 && threadIdx.x == 0) {
         LaneControl* ctl = d.ctl;
         ctl->tick = tick;
@@ -2932,12 +2940,6 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
         for (uint32_t k = 0; k < kRing; ++k) {
             ctl->ring_tick[k] = 0xffffffffu;
             ctl->ring_count[k] = 0;
-        }
-        for (int k = 0; k < 2; ++k) {
-            ctl->tick_touched[k] = ctl->tick_supra[k] = ctl->tick_events[k] = 0;
-            ctl->tick_dest[k] = ctl->tick_ainh[k] = ctl->tick_scan_rec[k] = ctl->tick_scan_in[k] = 0;
-            ctl->tick_learn[k] = 0;
-            ctl->tick_deep[k] = 0;
         }
     }
 }

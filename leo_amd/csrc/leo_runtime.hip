@@ -374,6 +374,7 @@ void copy_params(const LaneParams& dst, const LaneParams& src, const Sizes& z, h
 void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     Layout l;
     size_t o_ctl = l.add<LaneControl>(1), o_flag = l.add<uint32_t>(kMaxLaneWgs * kFlagWords);
+    size_t o_cnt = l.add<uint32_t>(kMaxLaneWgs * kFlagWords);
     size_t o_neu = l.add<uint32_t>(kNeuronWords * z.n), o_tl = l.add<uint32_t>(z.n);
     size_t o_ls = l.add<float>(z.n), o_dl = l.add<uint32_t>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
     size_t o_rl = l.add<uint32_t>(z.ns), o_il = l.add<uint32_t>(z.ni);
@@ -396,6 +397,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     LaneDesc& d = lane.desc;
     d.ctl = reinterpret_cast<LaneControl*>(b + o_ctl);
     d.barrier_flags = reinterpret_cast<uint32_t*>(b + o_flag);
+    d.wg_counts = reinterpret_cast<uint32_t*>(b + o_cnt);
     d.neuron = reinterpret_cast<uint32_t*>(b + o_neu);
     d.touched_list = reinterpret_cast<uint32_t*>(b + o_tl);
 
