@@ -1666,6 +1666,32 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     return delivered;
 }
 
+// First active-list position of each selecting wave's winners (block order,
+// runtime.rs:1010-1013) into starts[0..nwaves], starts[nwaves] = the total;
+// by the whole workgroup (the running scan uses sh.scan).
+__device__ __forceinline__ uint32_t wave_starts(const StepCtx& c, StepShared& sh, uint32_t* starts, uint32_t nwaves) {
+    uint32_t running = 0;
+    for (uint32_t base = 0; base < nwaves; base += kThreads) {
+        const uint32_t wv = base + threadIdx.x;
+        const uint32_t v = wv < nwaves ? ld(&c.d.wave_total[wv]) : 0;
+        sh.scan[threadIdx.x] = v;
+        __syncthreads();
+        for (uint32_t off = 1; off < kThreads; off <<= 1) {
+            const uint32_t add = threadIdx.x >= off ? sh.scan[threadIdx.x - off] : 0;
+            __syncthreads();
+            sh.scan[threadIdx.x] += add;
+            __syncthreads();
+        }
+        if (wv < nwaves) starts[wv] = running + sh.scan[threadIdx.x] - v;
+        const uint32_t chunk_total = sh.scan[kThreads - 1];
+        __syncthreads();
+        running += chunk_total;
+    }
+    if (threadIdx.x == 0) starts[nwaves] = running;
+    __syncthreads();
+    return running;
+}
+
 // Binding global cap: every block winner by selection key ascending
 // (activation desc, tie asc); the first max_active_global form the active list
 // (runtime.rs:1029-1057). Every workgroup lists the selecting waves' first
@@ -1703,25 +1729,7 @@ __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, 
     uint64_t* keys = reinterpret_cast<uint64_t*>(step_lds + kSelectStartsBytes);
     const uint32_t nwaves = selecting_waves(c);
     const uint32_t range = (cfg.block_count + nwaves - 1) / nwaves;
-    uint32_t running = 0;
-    for (uint32_t base = 0; base < nwaves; base += kThreads) {
-        const uint32_t wv = base + threadIdx.x;
-        const uint32_t v = wv < nwaves ? ld(&d.wave_total[wv]) : 0;
-        sh.scan[threadIdx.x] = v;
-        __syncthreads();
-        for (uint32_t off = 1; off < kThreads; off <<= 1) {
-            const uint32_t add = threadIdx.x >= off ? sh.scan[threadIdx.x - off] : 0;
-            __syncthreads();
-            sh.scan[threadIdx.x] += add;
-            __syncthreads();
-        }
-        if (wv < nwaves) starts[wv] = running + sh.scan[threadIdx.x] - v;
-        const uint32_t chunk_total = sh.scan[kThreads - 1];
-        __syncthreads();
-        running += chunk_total;
-    }
-    if (threadIdx.x == 0) starts[nwaves] = running;
-    __syncthreads();
+    const uint32_t running = wave_starts(c, sh, starts, nwaves);
     const uint32_t active = running < cap ? running : cap;
     uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
     float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
@@ -1946,12 +1954,12 @@ __device__ __forceinline__ void eligibility_list(const StepCtx& c, float LEO_GLO
                                                  const uint32_t LEO_GLOBAL* cur, uint32_t cur_n,
                                                  uint32_t LEO_GLOBAL* next, uint32_t LEO_GLOBAL* next_count,
                                                  const uint32_t* targets, const uint8_t* branches, float pop_cutoff,
-                                                 LearnOut& learn) {
+                                                 LearnOut& learn, uint32_t gstride) {
     const bool skip_zero = c.a->skip_zero_eligibility != 0;
     const uint32_t lane = __lane_id();
     const __amdgpu_buffer_rsrc_t rsrc = trace_rsrc(trace, slots);
-    for (uint32_t base = c.gtid - lane; base < cur_n; base += 2 * c.gstride) {
-        const uint32_t i0 = base + lane, i1 = base + c.gstride + lane;
+    for (uint32_t base = c.gtid - lane; base < cur_n; base += 2 * gstride) {
+        const uint32_t i0 = base + lane, i1 = base + gstride + lane;
         const bool v0 = i0 < cur_n, v1 = i1 < cur_n;
         const uint32_t s0 = v0 ? ld(&cur[i0]) : 0u;
         const uint32_t s1 = v1 ? ld(&cur[i1]) : 0u;
@@ -1997,7 +2005,9 @@ __device__ __forceinline__ void eligibility_list(const StepCtx& c, float LEO_GLO
     }
 }
 
-__device__ __forceinline__ void phase_eligibility(const StepCtx& c, bool plastic) {
+// The slots are dealt over the threads of the first gstride / kThreads
+// workgroups (all of them, or all but the readout workgroup).
+__device__ __forceinline__ void phase_eligibility(const StepCtx& c, bool plastic, uint32_t gstride) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -2012,10 +2022,10 @@ __device__ __forceinline__ void phase_eligibility(const StepCtx& c, bool plastic
     const float pop_cutoff = a.redundant_global ? 0.0f : ld(&c.ctl->pop_cutoff);
     LearnOut rec{d.rec_learn, &c.ctl->rec_learn_count, plastic, 0, 0};
     eligibility_list(c, d.rec_trace, NS, d.rec_mark, d.rec_list + p * NS, rec_n, d.rec_list + q * NS,
-                     &c.ctl->rec_count[q], a.m.rec_target, a.m.rec_branch, pop_cutoff, rec);
+                     &c.ctl->rec_count[q], a.m.rec_target, a.m.rec_branch, pop_cutoff, rec, gstride);
     LearnOut in{d.in_learn, &c.ctl->in_learn_count, plastic, rec.claimed, rec.listed};
     eligibility_list(c, d.in_trace, NI, d.in_mark, d.in_list + p * NI, in_n, d.in_list + q * NI,
-                     &c.ctl->in_count[q], a.m.in_target, a.m.in_branch, pop_cutoff, in);
+                     &c.ctl->in_count[q], a.m.in_target, a.m.in_branch, pop_cutoff, in, gstride);
     if (plastic) {
         count_wave(c, kCDest, c.tick, in.claimed);
         count_wave(c, kCLearn, c.tick, in.listed);
@@ -2044,6 +2054,12 @@ __device__ __forceinline__ float serial_sum_outputs(const float* v) {
 // (runtime.rs:1084-1106), and on the last workgroup the readout, softmax and
 // errors (runtime.rs:1108-1197, 1205-1206).
 // ---------------------------------------------------------------------------
+// The readout runs in phase 3, beside the eligibility update, on the last
+// workgroup (which selects no blocks); the post phase leaves its record
+// fields alone. With a non-binding global cap the active list is still being
+// written in that phase, so the readout takes it from the selecting waves'
+// winners (block order: the same list); otherwise the global selection has
+// written it before the phase's first barrier.
 __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, StepShared& sh, uint32_t step_index) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
@@ -2061,7 +2077,16 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
     // and scales, the bias and this thread's first 16 context-projection
     // weights; (2) the first 256 active ids and activations (into LDS) and
     // the context embeddings; (3) rows of 32 active neurons at a time.
-    const uint32_t A = ld(&ctl->active_count);
+    const bool from_waves = a.redundant_global != 0;
+    uint32_t* starts = reinterpret_cast<uint32_t*>(step_lds + 2 * kThreads * 4);
+    const uint32_t nwaves = selecting_waves(c);
+    const uint32_t range = (cfg.block_count + nwaves - 1) / nwaves;
+    const uint32_t N = cfg.neuron_count, rot = c.tick % N;
+    if (threadIdx.x == 0) {
+        d.records[step_index].p_target = 0.0f;
+        d.records[step_index].predicted = 0;
+    }
+    const uint32_t A = from_waves ? wave_starts(c, sh, starts, nwaves) : ld(&ctl->active_count);
     const uint32_t ctx_count = ld(&ctl->ctx_count);
     float l1 = ld(&d.p.bias[o1]), l2 = has2 ? ld(&d.p.bias[o2]) : 0.0f;
     constexpr uint32_t kDims = 16;
@@ -2104,8 +2129,18 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
     for (uint32_t b0 = 0; b0 < A; b0 += kThreads) {
         const uint32_t bn = min(kThreads, A - b0);
         __syncthreads();  // the previous block's ids are consumed (and the latent is written)
-        ids[threadIdx.x] = threadIdx.x < bn ? ld(&act_list[b0 + threadIdx.x]) : 0u;
-        if (threadIdx.x < bn) acts[threadIdx.x] = ld(&act_val[b0 + threadIdx.x]);
+        if (from_waves) {
+            uint32_t n = 0;
+            float act = 0.0f;
+            if (threadIdx.x < bn)
+                (void)winner_key(d, starts, nwaves, range, cfg.block_count, cfg.max_active_per_block,
+                                 b0 + threadIdx.x, N, rot, &n, &act);
+            ids[threadIdx.x] = n;
+            if (threadIdx.x < bn) acts[threadIdx.x] = act;
+        } else {
+            ids[threadIdx.x] = threadIdx.x < bn ? ld(&act_list[b0 + threadIdx.x]) : 0u;
+            if (threadIdx.x < bn) acts[threadIdx.x] = ld(&act_val[b0 + threadIdx.x]);
+        }
         __syncthreads();
         for (uint32_t r0 = 0; r0 < bn; r0 += kRows) {
             float w1[kRows], w2[kRows];
@@ -2292,8 +2327,10 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
             const uint32_t probes = ld(&ctl->ctx_probes), applied = ld(&ctl->ctx_applied);
             const uint32_t rec_n = ld(&ctl->rec_count[c.parity]), in_n = ld(&ctl->in_count[c.parity]);
             StepRecord LEO_GLOBAL& rec = d.records[step_index];
-            rec.p_target = 0.0f;
-            rec.predicted = 0;
+            if (!(sp.flags & kStepOutput)) {  // an output step's readout has set them
+                rec.p_target = 0.0f;
+                rec.predicted = 0;
+            }
             rec.population_inhibition = pi;
             rec.active = A;
             rec.suprathreshold = supra;
@@ -2305,10 +2342,6 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
             rec.eligible_rec = rec_n;
             rec.eligible_in = in_n;
             rec.error_code = 0;
-        }
-        if (sp.flags & kStepOutput) {
-            __syncthreads();
-            readout(c, sp, sh, step_index);
         }
     }
 }
@@ -2660,9 +2693,10 @@ __device__ __forceinline__ bool phase_barrier(const StepCtx& c, uint32_t& target
 }
 
 // Step loop. Phases (barriers): deliver (+context) | fold+select | active list +
-// eligibility | post + readout | signals | learning. Frozen steps stop after
-// the post phase; a binding global cap inserts the global sort before the
-// eligibility update.
+// eligibility + readout (on the last workgroup) | post (+ signals on a
+// plasticity step) | learning. Frozen steps stop after the post phase; a
+// binding global cap inserts the global sort before the eligibility update
+// and the readout.
 //
 // Workgroup b serves lane b % lane_stride (lane_stride is a multiple of the 8
 // XCDs, and workgroups are dealt to XCDs round-robin, so a lane's workgroups
@@ -2786,25 +2820,34 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             next = params();
             pipeline = (next.flags & kStepLearnTrace) == 0;
         }
+        // An output step's readout runs on the last workgroup beside the
+        // eligibility update, which the other workgroups share (a lane of one
+        // workgroup runs both), so a plasticity step computes its signals in
+        // the post phase (one barrier fewer). The post phase's state updates
+        // are read by neither the readout nor the signals.
+        const bool output = (sp.flags & kStepOutput) != 0;
+        const bool reader = output && c.part == c.P - 1;
+        const uint32_t elig_stride = output && c.P > 1 ? (c.P - 1) * kThreads : c.gstride;
         if (redundant) {
             const uint32_t delivered = write_active(c, sp, s, sh, fused, pipeline, next);
-            if (trace) phase_eligibility(c, plastic);
+            if (trace && !(reader && c.P > 1)) phase_eligibility(c, plastic, elig_stride);
             if (pipeline) {
                 if (c.P == 1) context_resolve(c, next, sh);
                 pending_events = wave_sum_u32(delivered);
             }
         } else {
             global_select(c, sh, s);
-            if (trace) {
+            if (trace || output) {  // the readout reads the global selection's list
                 if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 7))) break;
-                phase_eligibility(c, plastic);
+                if (trace && !(reader && c.P > 1)) phase_eligibility(c, plastic, elig_stride);
             }
         }
+        if (__builtin_expect(reader, 0)) readout(c, sp, sh, s);  // laid out off the frozen path
         if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 2))) break;
         if (!fused) {
             if (trace) c.parity ^= 1;
             phase_post(c, sp, s, sh);
-            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 3))) break;
+            if (!plastic && !(ok = phase_barrier<kProfile>(c, target, spin, clock, 3))) break;
         }
         if (plastic) {
             phase_signals(c, sh);
