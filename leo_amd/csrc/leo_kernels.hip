@@ -429,10 +429,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t trace_rsrc(const float LEO_GLO
 
 // Brings one trace slot to `tick` and adds `activation` to its branch
 // sensitivity (runtime.rs:710-766).
-__device__ __forceinline__ void activate_trace(float LEO_GLOBAL* trace, __amdgpu_buffer_rsrc_t rsrc, uint32_t slot,
-                                               uint32_t tick, float activation, const LeoConfig& cfg) {
+// With the slot's two record quarters already loaded (q0, q1).
+__device__ __forceinline__ void activate_loaded_trace(float LEO_GLOBAL* trace, uint32_t slot, uint32_t tick,
+                                                      float activation, const LeoConfig& cfg, f32x4 q0, f32x4 q1) {
     static_assert(kTBranch == 0 && kTAdapt0 == 3 && kTEligibility == 6 && kTLast == 7, "trace layout");
-    const f32x4 q0 = ld16_record(rsrc, slot, 0), q1 = ld16_record(rsrc, slot, 16);
     f32x4 LEO_GLOBAL* rec = reinterpret_cast<f32x4 LEO_GLOBAL*>(trace + static_cast<uint64_t>(slot) * kTraceWords);
     const uint32_t e = tick - __float_as_uint(q1.w);
     if (e == 0) {
@@ -600,6 +600,12 @@ struct DeliverItem {
     uint32_t edge;
     uint32_t cls;      // delay class of a ring item (0..3 for delay 8, 4, 2, 1)
     bool ring, inj;
+    // trace steps: a ring item's source and activation, an injection's trace
+    // record quarters and list mark, loaded with the item
+    uint32_t src;
+    float act;
+    f32x4 tq0, tq1;
+    uint32_t mark;
 };
 
 // The item's loads (no dependent load: the emission snapshot holds the
@@ -617,6 +623,11 @@ __device__ __forceinline__ DeliverItem deliver_fetch(const StepCtx& c, const Ste
     it.edge = 0;
     it.cls = 0;
     it.ring = it.inj = false;
+    it.src = 0;
+    it.act = 0.0f;
+    it.tq0 = it.tq1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    it.mark = 0;
+    const bool trace = (sp.flags & kStepLearnTrace) != 0;
     if (item < p.prev_count) {
         it.touch_n = ld(&d.ring_active[static_cast<uint64_t>(p.prev_slot) * cap + item]);
     } else if (item < p.off_in) {
@@ -635,6 +646,10 @@ __device__ __forceinline__ DeliverItem deliver_fetch(const StepCtx& c, const Ste
         it.slot = j;  // completed with the source at the trace activation
         it.key = (static_cast<uint64_t>(k) << 61) | (static_cast<uint64_t>(r) << 32) | (static_cast<uint64_t>(j) << 2);
         it.ring = true;
+        if (trace) {
+            it.src = ld(&d.ring_active[it.rbase]);
+            it.act = ld(&d.ring_act[it.rbase]);
+        }
     } else if (item < p.total) {
         const uint32_t i = item - p.off_in;
         it.slot = static_cast<uint64_t>(sp.symbol) * F + i;
@@ -642,6 +657,13 @@ __device__ __forceinline__ DeliverItem deliver_fetch(const StepCtx& c, const Ste
         it.key = (4ULL << 61) | (static_cast<uint64_t>(i) << 2) | a.m.in_branch[it.slot];
         it.value = ld(&d.p.in_weight[it.slot]);
         it.inj = true;
+        if (trace) {
+            const uint64_t NI = static_cast<uint64_t>(kSymbols) * F;
+            const __amdgpu_buffer_rsrc_t rsrc = trace_rsrc(d.in_trace, NI);
+            it.tq0 = ld16_record(rsrc, static_cast<uint32_t>(it.slot), 0);
+            it.tq1 = ld16_record(rsrc, static_cast<uint32_t>(it.slot), 16);
+            it.mark = ld(&d.in_mark[it.slot]);
+        }
     }
     return it;
 }
@@ -658,6 +680,7 @@ __device__ __forceinline__ void deliver_commit(const StepCtx& c, const StepParam
     const uint32_t S = cfg.synapses_per_neuron;
     const uint64_t NS = static_cast<uint64_t>(cfg.neuron_count) * S;
     const uint64_t NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
+    const bool trace = (sp.flags & kStepLearnTrace) != 0;
     bool scatter = it.inj;
     if (it.ring) {
         it.ring = edge_delay(it.edge) == (8u >> it.cls);
@@ -670,25 +693,33 @@ __device__ __forceinline__ void deliver_commit(const StepCtx& c, const StepParam
     } else if (it.touch_n != 0xffffffffu) {
         (*nf(d, it.touch_n, kNActivation)) = 0.0f;
     }
+    // a delivering recurrent slot's trace record and mark go out before the
+    // bucket claim (in the same round)
+    uint64_t rslot = 0;
+    if (trace && it.ring) {
+        rslot = it.slot + static_cast<uint64_t>(it.src) * S;
+        const __amdgpu_buffer_rsrc_t rsrc = trace_rsrc(d.rec_trace, NS);
+        it.tq0 = ld16_record(rsrc, static_cast<uint32_t>(rslot), 0);
+        it.tq1 = ld16_record(rsrc, static_cast<uint32_t>(rslot), 16);
+        it.mark = ld(&d.rec_mark[rslot]);
+    }
     if (scatter && scatter_event(c, it.target, it.key, it.value)) it.touch_n = it.target;
     if (it.touch_n != 0xffffffffu) touch_neuron(c, it.touch_n, p.tick);
     // frozen steps skip the appends below: their wave-uniform counter read
     // would wait for this item's stores before the next item's loads
-    if (!(sp.flags & kStepLearnTrace)) return;
+    if (!trace) return;
     bool new_rec = false, new_in = false;
     uint32_t eslot = 0;
     if (it.ring) {
-        const float act = ld(&d.ring_act[it.rbase]);
-        const uint64_t slot = it.slot + static_cast<uint64_t>(ld(&d.ring_active[it.rbase])) * S;
-        activate_trace(d.rec_trace, trace_rsrc(d.rec_trace, NS), static_cast<uint32_t>(slot), p.tick, act, cfg);
-        if (ld(&d.rec_mark[slot]) != kMarkListed) {
-            d.rec_mark[slot] = kMarkListed;
+        activate_loaded_trace(d.rec_trace, static_cast<uint32_t>(rslot), p.tick, it.act, cfg, it.tq0, it.tq1);
+        if (it.mark != kMarkListed) {
+            d.rec_mark[rslot] = kMarkListed;
             new_rec = true;
-            eslot = static_cast<uint32_t>(slot);
+            eslot = static_cast<uint32_t>(rslot);
         }
     } else if (it.inj) {
-        activate_trace(d.in_trace, trace_rsrc(d.in_trace, NI), static_cast<uint32_t>(it.slot), p.tick, 1.0f, cfg);
-        if (ld(&d.in_mark[it.slot]) != kMarkListed) {
+        activate_loaded_trace(d.in_trace, static_cast<uint32_t>(it.slot), p.tick, 1.0f, cfg, it.tq0, it.tq1);
+        if (it.mark != kMarkListed) {
             d.in_mark[it.slot] = kMarkListed;
             new_in = true;
             eslot = static_cast<uint32_t>(it.slot);
