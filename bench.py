@@ -123,7 +123,8 @@ def main() -> int:
         return copy_calibration()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box in this setup has one MI355X, so --gpus {args.gpus} "
-              "is not run (the lane-sharded multi-GPU design is described in DESIGN.md)", file=sys.stderr)
+              "is not run (stories would be sharded over devices by lane ranges, with the batch-end mean "
+              "chained over xGMI; that exchange is not built)", file=sys.stderr)
         return 2
 
     from leo_amd import native

@@ -5,7 +5,7 @@
  * The boundary mirrors the reference's execution-backend trait
  * `RuntimeBackend` (crates/leo-core/src/backend.rs:351-475) and its GPU
  * adapter `GpuRuntime` (backend.rs:547-794): a Rust `HipRuntime:
- * RuntimeBackend` binds these functions one-for-one (see INTEGRATION.md).
+ * RuntimeBackend` binds these functions one-for-one.
  * Plain pointers and sizes only; every call returns an int32 status (0 = ok)
  * and leo_hip_last_error() returns the message of the last failure on the
  * calling thread. A handle is single-threaded (RuntimeBackend is Send, not

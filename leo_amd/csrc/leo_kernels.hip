@@ -1522,7 +1522,7 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     const uint32_t rs = c.tick % kRing;
     const uint32_t b0 = min(cfg.block_count, wv * range);
     const uint64_t row0 = static_cast<uint64_t>(b0) * limit;
-    // round 1: the per-wave totals, this wave's winners' state and first
+    // first memory round: the per-wave totals, this wave's winners' state and first
     // synapses, and this thread's first item of the next tick
     // the recording wave's loads go out in the same round; it runs on the
     // workgroup that selects nothing (the least work in this phase)
@@ -1668,10 +1668,10 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
             delivered += 1;
         }
     };
-    // round 2: the bucket increment of this thread's first next-tick item
+    // second memory round: the bucket increment of this thread's first next-tick item
     // (the winners' state and first synapses are loaded with the totals)
     if (deliver_next) deliver_commit(c, next, np, item0, delivered);
-    // round 3: the delay-1 bucket increments
+    // third memory round: the delay-1 bucket increments
     if (pf) post_fire(first_n, first_act, fat, ad0, ad1, ad2, mem, thr, type);
     if (sn) snapshot(r0, j0, act0, weight0, edge0);
     // further rounds: more than 64 winners or synapses in this wave, more
