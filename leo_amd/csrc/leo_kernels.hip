@@ -1302,7 +1302,9 @@ __device__ __forceinline__ Window wave_window(uint32_t wave, uint32_t nb) {
 // 1010-1013), compacted from the range's first block row, so that phase 3
 // reads them in one round. A group with more touched neurons than the window
 // holds is taken in windows of whole blocks.
-__device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& sh) {
+// `keep_bits`: a trace step leaves the bitmap words set for its eligibility
+// update (the learning phase clears them from the touched list).
+__device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& sh, bool keep_bits) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -1353,7 +1355,7 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
 #pragma unroll
         for (uint32_t k = 0; k < kWordsPerLane; ++k) {
             const uint32_t at = k * kWaveSize + lane;
-            if (at < gw && word[k]) bits[at] = 0u;
+            if (!keep_bits && at < gw && word[k]) bits[at] = 0u;
         }
         // block starts: the list position of each block's first word
         wave_sync();
@@ -1869,23 +1871,28 @@ __device__ __forceinline__ void load_slot(SlotInputs& in, __amdgpu_buffer_rsrc_t
     in.last = __float_as_uint(q1.w);
 }
 
-// The destination's epochs: quarter 3 of its record.
-__device__ __forceinline__ void load_epochs(SlotInputs& in, const StepCtx& c, uint32_t dst) {
-    static_assert(kNTouched == 12 && kNSelected == 13, "record layout");
-    const f32x4 q3 = ld_quarter(neuron_rsrc(c.d, c.a->cfg.neuron_count), dst, 3);
-    in.touched_epoch = __float_as_uint(q3.x);
-    in.selected_epoch = __float_as_uint(q3.y);
+// Whether the destination was touched this tick: its bit in the touched
+// bitmap, which a trace step keeps until its learning phase (a 4-byte read
+// from a cache-resident array instead of a line of the destination's record).
+__device__ __forceinline__ void load_touched(SlotInputs& in, const StepCtx& c, uint32_t dst) {
+    const uint32_t nb = c.a->cfg.neurons_per_block;
+    const uint32_t blk = fast_div(dst, c.a->div_block), off = dst - blk * nb;
+    const uint32_t word = ld(&c.d.touched_bits[blk * block_words(nb) + off / 32]);
+    in.touched_epoch = (word >> (off & 31)) & 1u ? c.tick + 1 : 0u;
 }
 
-// The destination's state: quarters 0 and 2 of its record, its block's
-// selection and its threshold and excitability.
+// The destination's state: quarters 0, 2 and 3 of its record (membrane,
+// branches, refractory tick, selected epoch), its block's selection and its
+// threshold and excitability.
 __device__ __forceinline__ void load_destination(SlotInputs& in, const StepCtx& c, uint32_t dst) {
-    static_assert(kNMembrane == 0 && kNBranch0 + BR_TEMP == 8 && kNBranch0 + BR_GATE == 9 && kNRefractory == 11,
+    static_assert(kNMembrane == 0 && kNBranch0 + BR_TEMP == 8 && kNBranch0 + BR_GATE == 9 && kNRefractory == 11 &&
+                      kNSelected == 13,
                   "record layout");
     const LaneDesc& d = c.d;
     const uint32_t blk = fast_div(dst, c.a->div_block);
     const __amdgpu_buffer_rsrc_t rec = neuron_rsrc(d, c.a->cfg.neuron_count);
-    const f32x4 q0 = ld_quarter(rec, dst, 0), q2 = ld_quarter(rec, dst, 2);
+    const f32x4 q0 = ld_quarter(rec, dst, 0), q2 = ld_quarter(rec, dst, 2), q3 = ld_quarter(rec, dst, 3);
+    in.selected_epoch = __float_as_uint(q3.y);
     in.refractory_until = __float_as_uint(q2.w);
     in.temporal = q2.x;
     in.gate_acc = q2.y;
@@ -2007,8 +2014,8 @@ __device__ __forceinline__ void eligibility_list(const StepCtx& c, float LEO_GLO
             r1 = branches[s1];
             load_slot(a1, rsrc, s1);
         }
-        if (v0) load_epochs(a0, c, t0);
-        if (v1) load_epochs(a1, c, t1);
+        if (v0) load_touched(a0, c, t0);
+        if (v1) load_touched(a1, c, t1);
         if (v0 && a0.touched_epoch == c.tick + 1) load_destination(a0, c, t0);
         if (v1 && a1.touched_epoch == c.tick + 1) load_destination(a1, c, t1);
         float e0 = 0.0f, e1 = 0.0f;
@@ -2681,6 +2688,11 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
             const uint32_t first = min(cfg.block_count, w * range) * cfg.neurons_per_block;
             for (uint32_t i = lane; i < count; i += kWaveSize) {
                 const uint32_t n = ld(&d.touched_list[first + i]);
+                {  // the bitmap word this trace step kept for its eligibility update
+                    const uint32_t nb = cfg.neurons_per_block;
+                    const uint32_t blk = fast_div(n, a.div_block), off = n - blk * nb;
+                    d.touched_bits[blk * block_words(nb) + off / 32] = 0u;
+                }
                 const float local = ld(nf(d, n, kNActivation)) > 0.0f ? 1.0f : 0.0f;
                 const float local_err = local - cfg.target_activity;
                 const float delta = cfg.threshold_homeostasis_rate * (local_err + pop_err);
@@ -2840,7 +2852,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         // the context of a step delivered ahead: on the workgroup that owns no
         // selection blocks, beside the fold (first read by the readout)
         if (delivered_ahead && c.P > 1 && c.part == c.P - 1) context_resolve(c, sp, sh);
-        phase_fold_select(c, sh);
+        phase_fold_select(c, sh, trace);
         if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 1))) break;
         // a fused step followed by a frozen one starts the next tick in its
         // last phase: the next delivery runs before this step's closing
