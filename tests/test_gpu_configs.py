@@ -342,6 +342,19 @@ def test_binding_global_cap_beyond_1024_winners_matches_oracle(require_gpu, orac
             assert np.array_equal(g, c), f"story {i}: first differing step {np.nonzero(g != c)[0][:4]}"
         assert (grep.replay_steps, grep.replay_prefix_steps, grep.active_neurons_sum) == \
             (crep.replay_steps, crep.replay_prefix_steps, crep.active_neurons_sum)
+        # frozen steps with targets: a readout after the global selection
+        # with no eligibility update in the phase
+        cpu.begin_document()
+        gpu.begin_document()
+        text = stories[2]
+        frozen = [(256, text[0])] + [(text[i], text[i + 1]) for i in range(len(text) - 1)]
+        for i, (sym, tgt) in enumerate(frozen):
+            cm = cpu.step(sym, tgt, oracle.FROZEN)
+            gm = gpu.step(sym, tgt, native.FROZEN)
+            assert (gm.active_neurons, gm.global_cap_clipped_neurons, gm.predicted_symbol) == \
+                (cm.active_neurons, cm.global_cap_clipped_neurons, cm.predicted_symbol), i
+            assert gm.loss == cm.loss and gm.population_inhibition == cm.population_inhibition, i
+        assert np.array_equal(gpu.probabilities(), cpu.read_f32("probabilities"))
         got = gpu.model()
     finally:
         gpu.close()
