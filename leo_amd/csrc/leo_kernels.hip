@@ -956,11 +956,6 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
         ad0 *= k.fast;
         ad1 *= k.medium;
         ad2 *= k.slow;
-        (*nf(d, n, kNFatigue)) = fat;
-        (*nf(d, n, kNAdapt0)) = ad0;
-        (*nf(d, n, kNAdapt0 + 1)) = ad1;
-        (*nf(d, n, kNAdapt0 + 2)) = ad2;
-        (*nu(d, n, kNLastTick)) = tick;
     }
     if (cnt > 0) {
         // selects, not an indexed array (which would live in scratch)
@@ -1003,10 +998,6 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
         }
         (*nu(d, n, kNBucketCount)) = 0;
     }
-    (*nf(d, n, kNBranch0)) = b0;
-    (*nf(d, n, kNBranch0 + 1)) = b1;
-    (*nf(d, n, kNBranch0 + 2)) = b2;
-    (*nf(d, n, kNBranch0 + 3)) = b3;
     *refractory = refr;
     if (!refr) {
         const float gate = clampf(b3, 0.0f, 1.0f);
@@ -1015,7 +1006,12 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
         const float drive = excitability * net - fat - adaptation - pi;
         mem = mem + drive;
     }
-    if (e > 0 || !refr) (*nf(d, n, kNMembrane)) = mem;
+    // quarters 0-2 written whole (the wave owns the neuron during this
+    // phase; the activation and refractory tick are written back unchanged)
+    f32x4 LEO_GLOBAL* rq = reinterpret_cast<f32x4 LEO_GLOBAL*>(nf(d, n, 0));
+    rq[0] = f32x4{mem, q0.y, fat, ad0};
+    rq[1] = f32x4{ad1, ad2, b0, b1};
+    rq[2] = f32x4{b2, b3, __uint_as_float(e > 0 ? tick : last), q2.w};
     return mem - threshold;
 }
 
