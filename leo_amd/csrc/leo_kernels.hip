@@ -708,23 +708,15 @@ __device__ __forceinline__ void deliver_commit(const StepCtx& c, const StepParam
     // frozen steps skip the appends below: their wave-uniform counter read
     // would wait for this item's stores before the next item's loads
     if (!trace) return;
-    bool new_rec = false, new_in = false;
-    uint32_t eslot = 0;
-    if (it.ring) {
-        activate_loaded_trace(d.rec_trace, static_cast<uint32_t>(rslot), p.tick, it.act, cfg, it.tq0, it.tq1);
-        if (it.mark != kMarkListed) {
-            d.rec_mark[rslot] = kMarkListed;
-            new_rec = true;
-            eslot = static_cast<uint32_t>(rslot);
-        }
-    } else if (it.inj) {
-        activate_loaded_trace(d.in_trace, static_cast<uint32_t>(it.slot), p.tick, 1.0f, cfg, it.tq0, it.tq1);
-        if (it.mark != kMarkListed) {
-            d.in_mark[it.slot] = kMarkListed;
-            new_in = true;
-            eslot = static_cast<uint32_t>(it.slot);
-        }
-    }
+    // the slot's list mark through one selected pointer (two stores into
+    // different arrays would be merged through a private pointer table)
+    const bool fresh = (it.ring || it.inj) && it.mark != kMarkListed;
+    const uint32_t eslot = static_cast<uint32_t>(it.ring ? rslot : it.slot);
+    if (it.ring) activate_loaded_trace(d.rec_trace, eslot, p.tick, it.act, cfg, it.tq0, it.tq1);
+    else if (it.inj) activate_loaded_trace(d.in_trace, eslot, p.tick, 1.0f, cfg, it.tq0, it.tq1);
+    uint8_t LEO_GLOBAL* mark = it.ring ? d.rec_mark + rslot : d.in_mark + it.slot;
+    if (fresh) *mark = kMarkListed;
+    const bool new_rec = fresh && it.ring, new_in = fresh && !it.ring;
     uint32_t pos = wave_append(&ctl->rec_count[c.parity], new_rec);
     if (new_rec) d.rec_list[static_cast<uint64_t>(c.parity) * NS + pos] = eslot;
     pos = wave_append(&ctl->in_count[c.parity], new_in);
@@ -1315,6 +1307,7 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
     const uint32_t group = min(kGroupBlocks, kWaveSize * kWordsPerLane / wpb);
     const uint32_t cap = window_capacity(nb);
     const float pi = ld(&c.ctl->population_inhibition);
+    const FastDiv block_div = a.div_block_words;
     const Window w = wave_window(wave, nb);
     w.cands[lane] = 0;
     w.cut[lane] = ~0ULL;
@@ -1332,7 +1325,10 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
             const uint32_t at = k * kWaveSize + lane;
             word[k] = at < gw ? ld(&bits[at]) : 0u;
         }
-        // list positions in word order (row k holds words k*64 .. k*64+63)
+        // list positions in word order (row k holds words k*64 .. k*64+63);
+        // each row's neurons are listed as soon as its positions are known
+        // (the words are in registers), at positions below the window
+        // capacity: a group that fits the window is then fully listed
         uint32_t total = 0;
 #pragma unroll
         for (uint32_t k = 0; k < kWordsPerLane; ++k) {
@@ -1340,9 +1336,19 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
             if (k * kWaveSize < gw) {
                 const uint32_t cnt = __popc(word[k]);
                 const uint32_t incl = wave_incl_scan_u32(cnt);
-                const uint32_t p = total + incl - cnt;
+                uint32_t p = total + incl - cnt;
                 w.bits[at] = word[k];
                 w.pos[at] = p;
+                uint32_t v = word[k];
+                if (v != 0 && p < cap) {
+                    const uint32_t g = fast_div(at, block_div), base = (at - g * wpb) * 32;
+                    while (v) {
+                        const uint32_t bit = __ffs(v) - 1;
+                        v &= v - 1;
+                        if (p < cap) w.entry[p] = (g << 16) | (base + bit);
+                        ++p;
+                    }
+                }
                 total += __builtin_amdgcn_readlane(incl, kWaveSize - 1);
             }
         }
@@ -1369,12 +1375,12 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
                 }
                 hi = static_cast<uint32_t>(wave_max_u64(best));
             }
-            for (uint32_t k = 0; k < kWordsPerLane; ++k) {
+            for (uint32_t k = 0; total > cap && k < kWordsPerLane; ++k) {  // else listed in the scan
                 const uint32_t at = k * kWaveSize + lane;
                 if (at >= gw) break;
                 uint32_t v = w.bits[at], p = w.pos[at];
                 if (p >= hi || p + __popc(v) <= lo) continue;
-                const uint32_t g = fast_div(at, a.div_block_words), base = (at - g * wpb) * 32;
+                const uint32_t g = fast_div(at, block_div), base = (at - g * wpb) * 32;
                 while (v) {
                     const uint32_t bit = __ffs(v) - 1;
                     v &= v - 1;
