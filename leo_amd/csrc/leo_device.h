@@ -423,6 +423,7 @@ struct KernelArgs {
     // learning slot.
     uint32_t skip_zero_eligibility;
     uint32_t select_tile;            // select_tile_keys(neurons_per_block)
+    uint32_t profile_part;           // workgroup whose phases the profiling build times (of each lane)
     DeepSortPlan deep;
     FastDiv div_synapses;            // synapses_per_neuron
     FastDiv div_block;               // neurons_per_block

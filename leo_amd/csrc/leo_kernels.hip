@@ -1402,7 +1402,7 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
                 w.key[i] = deep ? kDeepPending : candidate ? selection_key(act, add_mod(n, N - rot, N)) : ~0ULL;
                 any_deep |= deep;
                 if (candidate) atomicAdd(&w.cands[g], 1u);
-                d.touched_list[listed + i] = n;
+                if (keep_bits) d.touched_list[listed + i] = n;  // read by a trace step's homeostasis only
             }
             wave_sync();
             if (__ballot(any_deep)) {
@@ -1554,7 +1554,12 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     }
     const DeliverPlan np = deliver_plan(c, sh, true);
     const bool deliver_next = ahead && np.delivers;
-    DeliverItem item0 = deliver_fetch(c, next, np, deliver_next ? c.gtid : np.total);
+    // the next tick's items are dealt 64 at a time to the workgroups in turn
+    // (chunk wave * P + part), so that every workgroup has a share of the
+    // delivery stores to drain before the closing barrier (dealt by thread
+    // id, the first workgroups took them all)
+    const uint32_t dealt = (wave_index() * c.P + c.part) * kWaveSize + __lane_id();
+    DeliverItem item0 = deliver_fetch(c, next, np, deliver_next ? dealt : np.total);
     if (ahead) reset_next_lists(c);
     // this wave's winners are in its LDS since phase 2: their state and
     // synapses are loaded in the same round as the totals
@@ -1692,7 +1697,7 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
         const uint64_t slot = static_cast<uint64_t>(n) * S + j;
         snapshot(r, j, act, ld(&d.p.rec_weight[slot]), c.a->m.rec_edge[slot]);
     }
-    if (ahead) deliver_items(c, next, np, c.gtid + np.stride, delivered);
+    if (ahead) deliver_items(c, next, np, dealt + np.stride, delivered);
     count_wave(c, kCInhibitory, c.tick, inhibitory);
     if (threadIdx.x == 0) {  // the next deliveries read this tick's ring entry from LDS
         sh.ring_tick[rs] = c.tick;
@@ -2730,7 +2735,7 @@ template <bool kProfile>
 __device__ __forceinline__ bool phase_barrier(const StepCtx& c, uint32_t& target, uint32_t spin_limit,
                                               PhaseClock& clock, uint32_t phase) {
     unsigned long long arrived = 0;
-    const bool timer = kProfile && c.part == 0 && threadIdx.x == 0;
+    const bool timer = kProfile && c.part == c.a->profile_part && threadIdx.x == 0;
     if (timer) clock.arrive(phase, arrived);
     const bool ok = lane_barrier(c.d, c.part, c.P, target, spin_limit, c.local);
     if (timer) clock.release(phase, arrived);
@@ -2798,7 +2803,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
     }
     __syncthreads();
     PhaseClock clock;
-    if (kProfile && c.part == 0 && threadIdx.x == 0) clock.start(c.d.phase_profile);
+    if (kProfile && c.part == args.profile_part && threadIdx.x == 0) clock.start(c.d.phase_profile);
     bool ok = true;
     // the next step's parameters are fetched one step ahead with vector loads
     // (a scalar load would be waited for at the next LDS access)

@@ -277,6 +277,7 @@ struct LeoHipRuntime {
     bool local_sync = true;
     LeoKernelStats telemetry{};
     bool phase_profile = false;
+    uint32_t profile_part = 0;  // LEO_HIP_PROFILE_PART: the workgroup of each lane the phase profile times
     double wall_clock_khz = 0.0;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     std::vector<hipEvent_t> launch_events;  // timing events of queued launches (pairs)
@@ -591,6 +592,7 @@ KernelArgs kernel_args(LeoHipRuntime* h, LaneDesc* lanes, uint32_t count, uint32
     a.div_block_words = make_fast_div(block_words(h->cfg.device.neurons_per_block));
     a.skip_zero_eligibility = h->negative_zero_weights ? 0u : 1u;
     a.select_tile = select_tile_keys(h->cfg.device.neurons_per_block);
+    a.profile_part = std::min(h->profile_part, P > 0 ? P - 1 : 0u);
     a.deep = deep_sort_plan(h->cfg.device.max_active_global, h->cfg.device.input_fanout,
                             h->cfg.device.synapses_per_neuron);
     return a;
@@ -2181,6 +2183,8 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         if (const char* env = std::getenv("LEO_HIP_MAX_STEPS_PER_LAUNCH"))
             h->max_steps_override = static_cast<uint32_t>(std::max(1, std::atoi(env)));
         if (const char* env = std::getenv("LEO_HIP_PHASE_PROFILE")) h->phase_profile = std::atoi(env) != 0;
+        if (const char* env = std::getenv("LEO_HIP_PROFILE_PART"))
+            h->profile_part = static_cast<uint32_t>(std::max(0, std::atoi(env)));
         int clock_khz = 0;
         LEO_HIP_CHECK(hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, device));
         h->wall_clock_khz = clock_khz > 0 ? clock_khz : 100000.0;
