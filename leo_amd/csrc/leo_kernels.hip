@@ -409,6 +409,15 @@ struct StepCtx {
     bool local;        // workgroups of the lane share one L2 (see lane_barrier)
 };
 
+// This thread's item index when a phase's items are dealt 64 at a time to the
+// first `parts` workgroups of the lane in turn (chunk wave * parts + part)
+// rather than by thread id: a list shorter than the threads then spreads its
+// memory traffic over every workgroup's CU instead of the first few, whose
+// stores would drain before their barrier arrivals.
+__device__ __forceinline__ uint32_t dealt_index(const StepCtx& c, uint32_t parts) {
+    return (wave_index() * parts + c.part) * kWaveSize + __lane_id();
+}
+
 // Waves that own selection blocks: with several workgroups per lane the last
 // one owns none (it resolves the context and takes deliveries instead).
 __device__ __forceinline__ uint32_t selecting_waves(const StepCtx& c) {
@@ -745,7 +754,7 @@ __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams
     reset_next_lists(c);
     const DeliverPlan p = deliver_plan(c, sh, false);
     uint32_t delivered = 0;
-    deliver_items(c, sp, p, c.gtid, delivered);
+    deliver_items(c, sp, p, dealt_index(c, p.stride / kThreads), delivered);
     count_wave(c, kCEvents, p.tick, delivered);
 }
 
@@ -1554,11 +1563,9 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     }
     const DeliverPlan np = deliver_plan(c, sh, true);
     const bool deliver_next = ahead && np.delivers;
-    // the next tick's items are dealt 64 at a time to the workgroups in turn
-    // (chunk wave * P + part), so that every workgroup has a share of the
-    // delivery stores to drain before the closing barrier (dealt by thread
-    // id, the first workgroups took them all)
-    const uint32_t dealt = (wave_index() * c.P + c.part) * kWaveSize + __lane_id();
+    // the next tick's items are dealt to the workgroups in turn (by thread
+    // id, the first 16 of 32 workgroups at D took them all)
+    const uint32_t dealt = dealt_index(c, c.P);
     DeliverItem item0 = deliver_fetch(c, next, np, deliver_next ? dealt : np.total);
     if (ahead) reset_next_lists(c);
     // this wave's winners are in its LDS since phase 2: their state and
@@ -2003,7 +2010,7 @@ __device__ __forceinline__ void eligibility_list(const StepCtx& c, float LEO_GLO
     const bool skip_zero = c.a->skip_zero_eligibility != 0;
     const uint32_t lane = __lane_id();
     const __amdgpu_buffer_rsrc_t rsrc = trace_rsrc(trace, slots);
-    for (uint32_t base = c.gtid - lane; base < cur_n; base += 2 * gstride) {
+    for (uint32_t base = dealt_index(c, gstride / kThreads) - lane; base < cur_n; base += 2 * gstride) {
         const uint32_t i0 = base + lane, i1 = base + gstride + lane;
         const bool v0 = i0 < cur_n, v1 = i1 < cur_n;
         const uint32_t s0 = v0 ? ld(&cur[i0]) : 0u;
@@ -2335,7 +2342,7 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
     const uint32_t total = A + A * S;
     const uint32_t refractory = c.tick + cfg.refractory_ticks + 1;
     uint32_t inhibitory = 0;
-    for (uint32_t item = c.gtid; item < total; item += c.gstride) {
+    for (uint32_t item = dealt_index(c, c.P); item < total; item += c.gstride) {
         if (item < A) {
             const uint32_t n = ld(&act_list[item]);
             const float act = ld(nf(d, n, kNActivation));
@@ -2472,7 +2479,8 @@ __device__ __forceinline__ void phase_signals(const StepCtx& c, StepShared& sh) 
     // batch of the list (read before the count is known; entries past it are
     // masked below)
     const uint32_t wave = wave_index(), lane = __lane_id();
-    const uint32_t waves = c.P * kWavesPerGroup, b0 = c.part * kWavesPerGroup + wave;
+    // batches of 64 destinations dealt to the workgroups in turn
+    const uint32_t waves = c.P * kWavesPerGroup, b0 = wave * c.P + c.part;
     const uint32_t N = cfg.neuron_count;
     const uint32_t count = ld(&c.ctl->dest_count);
     const uint32_t first_at = b0 * kWaveSize + lane;
@@ -2585,7 +2593,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
         // the readout workgroup updates the bias and the context projection;
         // the other workgroups share the output rows and the synapse slots
         const uint32_t sharers = c.P > 1 ? c.P - 1 : 1;
-        const uint32_t first = c.part < sharers ? c.gtid : ~0u, stride = sharers * kThreads;
+        const uint32_t first = c.part < sharers ? dealt_index(c, sharers) : ~0u, stride = sharers * kThreads;
         // the learning-slot list lengths and this thread's first learning
         // slots go out with the errors (slots read before the lengths are
         // known are masked by the loops below)
