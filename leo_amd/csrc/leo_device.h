@@ -341,6 +341,7 @@ struct SharedModel {
     const uint64_t LEO_GLOBAL* bucket_offset;   // N+1
     const uint64_t LEO_GLOBAL* shadow_offset;   // N+1: each deep-capable target's shadow range (entries)
     const uint32_t LEO_GLOBAL* rec_edge;        // N*S: pack_edge(target, delay, branch) of each recurrent slot
+    const uint32_t LEO_GLOBAL* in_edge;         // 258*F: pack_edge(target, 1, branch) of each input slot
 };
 
 // A recurrent synapse packed into one word: target (28 bits), log2 of the

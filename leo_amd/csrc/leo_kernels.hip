@@ -18,6 +18,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "glibc_expf.h"
 #define LEO_KERNEL_TRANSLATION_UNIT  // global-address-space descriptor pointers
 #include "leo_device.h"
@@ -662,8 +664,9 @@ __device__ __forceinline__ DeliverItem deliver_fetch(const StepCtx& c, const Ste
     } else if (item < p.total) {
         const uint32_t i = item - p.off_in;
         it.slot = static_cast<uint64_t>(sp.symbol) * F + i;
-        it.target = a.m.in_target[it.slot];
-        it.key = (4ULL << 61) | (static_cast<uint64_t>(i) << 2) | a.m.in_branch[it.slot];
+        const uint32_t edge = a.m.in_edge[it.slot];  // target and branch in one load
+        it.target = edge_target(edge);
+        it.key = (4ULL << 61) | (static_cast<uint64_t>(i) << 2) | edge_branch(edge);
         it.value = ld(&d.p.in_weight[it.slot]);
         it.inj = true;
         if (trace) {
@@ -1966,22 +1969,6 @@ __device__ __forceinline__ bool finish_slot(const StepCtx& c, const SlotInputs& 
     return mag > cfg.eligibility_epsilon;
 }
 
-// Wave-aggregated append of two predicates per lane (every lane active): one
-// atomic for the wave; lane order within each predicate, the first's before
-// the second's.
-__device__ __forceinline__ void wave_append2(uint32_t LEO_GLOBAL* counter, bool p0, bool p1, uint32_t& pos0,
-                                             uint32_t& pos1) {
-    const unsigned long long m0 = __ballot(p0), m1 = __ballot(p1);
-    const uint32_t n0 = static_cast<uint32_t>(__popcll(m0));
-    const uint32_t total = n0 + static_cast<uint32_t>(__popcll(m1));
-    uint32_t base = 0;
-    if (total != 0 && __lane_id() == 0) base = atomicAdd(counter, total);
-    base = __builtin_amdgcn_readfirstlane(base);
-    const unsigned long long below = (1ULL << __lane_id()) - 1ULL;
-    pos0 = base + static_cast<uint32_t>(__popcll(m0 & below));
-    pos1 = base + n0 + static_cast<uint32_t>(__popcll(m1 & below));
-}
-
 // Where a plasticity step lists its learning slots and claims their
 // destinations (runtime.rs:1214-1243).
 struct LearnOut {
@@ -1992,8 +1979,33 @@ struct LearnOut {
     uint32_t listed;             // this thread's learning slots listed
 };
 
-// Eligible slots of one list, two per lane per iteration (their loads in
-// flight together); kept slots are compacted into the next list. On a
+// Wave-aggregated append of K predicates per lane (every lane active): one
+// atomic for the wave; lane order within each predicate, predicate k's
+// entries before predicate k+1's.
+template <uint32_t K>
+__device__ __forceinline__ void wave_append_k(uint32_t LEO_GLOBAL* counter, const bool (&p)[K], uint32_t (&pos)[K]) {
+    unsigned long long m[K];
+    uint32_t total = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) {
+        m[k] = __ballot(p[k]);
+        total += static_cast<uint32_t>(__popcll(m[k]));
+    }
+    uint32_t base = 0;
+    if (total != 0 && __lane_id() == 0) base = atomicAdd(counter, total);
+    base = __builtin_amdgcn_readfirstlane(base);
+    const unsigned long long below = (1ULL << __lane_id()) - 1ULL;
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) {
+        pos[k] = base + static_cast<uint32_t>(__popcll(m[k] & below));
+        base += static_cast<uint32_t>(__popcll(m[k]));
+    }
+}
+
+// Eligible slots of one list, K per lane per iteration (their loads in
+// flight together: 2 when the list gives each thread a few slots, more when
+// it gives each many, as on story lanes with few workgroups); kept slots are
+// compacted into the next list. On a
 // plasticity step the kept slots whose update can change their weight
 // (nonzero eligibility; every kept slot when skip_zero_eligibility is off) are
 // listed as learning slots, and their destinations are claimed once each
@@ -2001,60 +2013,93 @@ struct LearnOut {
 // The reference also computes signals for the other destinations (the
 // targets of zero-eligibility slots and the active neurons); no update reads
 // them.
+// Each slot's packed synapse (`edges`) gives its destination and branch in
+// one load.
+template <uint32_t K>
 __device__ __forceinline__ void eligibility_list(const StepCtx& c, float LEO_GLOBAL* trace, uint64_t slots,
                                                  uint8_t LEO_GLOBAL* marks,
                                                  const uint32_t LEO_GLOBAL* cur, uint32_t cur_n,
                                                  uint32_t LEO_GLOBAL* next, uint32_t LEO_GLOBAL* next_count,
-                                                 const uint32_t* targets, const uint8_t* branches, float pop_cutoff,
-                                                 LearnOut& learn, uint32_t gstride) {
+                                                 const uint32_t* edges, float pop_cutoff, LearnOut& learn,
+                                                 uint32_t gstride) {
     const bool skip_zero = c.a->skip_zero_eligibility != 0;
     const uint32_t lane = __lane_id();
     const __amdgpu_buffer_rsrc_t rsrc = trace_rsrc(trace, slots);
-    for (uint32_t base = dealt_index(c, gstride / kThreads) - lane; base < cur_n; base += 2 * gstride) {
-        const uint32_t i0 = base + lane, i1 = base + gstride + lane;
-        const bool v0 = i0 < cur_n, v1 = i1 < cur_n;
-        const uint32_t s0 = v0 ? ld(&cur[i0]) : 0u;
-        const uint32_t s1 = v1 ? ld(&cur[i1]) : 0u;
-        uint32_t t0 = 0, t1 = 0;
-        uint8_t r0 = 0, r1 = 0;
-        SlotInputs a0{}, a1{};
-        if (v0) {
-            t0 = targets[s0];
-            r0 = branches[s0];
-            load_slot(a0, rsrc, s0);
+    for (uint32_t base = dealt_index(c, gstride / kThreads) - lane; base < cur_n; base += K * gstride) {
+        bool v[K];
+        uint32_t sl[K], t[K];
+        uint8_t r[K];
+        SlotInputs in[K];
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k) {
+            const uint32_t i = base + k * gstride + lane;
+            v[k] = i < cur_n;
+            sl[k] = v[k] ? ld(&cur[i]) : 0u;
+            t[k] = 0;
+            r[k] = 0;
+            in[k] = SlotInputs{};
         }
-        if (v1) {
-            t1 = targets[s1];
-            r1 = branches[s1];
-            load_slot(a1, rsrc, s1);
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k) {
+            if (v[k]) {
+                const uint32_t edge = edges[sl[k]];
+                t[k] = edge_target(edge);
+                r[k] = static_cast<uint8_t>(edge_branch(edge));
+                load_slot(in[k], rsrc, sl[k]);
+            }
         }
-        if (v0) load_touched(a0, c, t0);
-        if (v1) load_touched(a1, c, t1);
-        if (v0 && a0.touched_epoch == c.tick + 1) load_destination(a0, c, t0);
-        if (v1 && a1.touched_epoch == c.tick + 1) load_destination(a1, c, t1);
-        float e0 = 0.0f, e1 = 0.0f;
-        const bool k0 = v0 && finish_slot(c, a0, trace, s0, r0, pop_cutoff, e0);
-        const bool k1 = v1 && finish_slot(c, a1, trace, s1, r1, pop_cutoff, e1);
-        if (v0 && !k0) marks[s0] = kMarkDropped;
-        if (v1 && !k1) marks[s1] = kMarkDropped;
-        uint32_t p0, p1;
-        wave_append2(next_count, k0, k1, p0, p1);
-        if (k0) next[p0] = s0;
-        if (k1) next[p1] = s1;
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k)
+            if (v[k]) load_touched(in[k], c, t[k]);
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k)
+            if (v[k] && in[k].touched_epoch == c.tick + 1) load_destination(in[k], c, t[k]);
+        float e[K];
+        bool kept[K];
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k) {
+            e[k] = 0.0f;
+            kept[k] = v[k] && finish_slot(c, in[k], trace, sl[k], r[k], pop_cutoff, e[k]);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k)
+            if (v[k] && !kept[k]) marks[sl[k]] = kMarkDropped;
+        uint32_t pos[K];
+        wave_append_k<K>(next_count, kept, pos);
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k)
+            if (kept[k]) next[pos[k]] = sl[k];
         if (learn.plastic) {  // wave-uniform
-            const bool l0 = k0 && (e0 != 0.0f || !skip_zero), l1 = k1 && (e1 != 0.0f || !skip_zero);
-            wave_append2(learn.count, l0, l1, p0, p1);
-            if (l0) learn.list[p0] = s0;
-            if (l1) learn.list[p1] = s1;
-            const bool w0 = l0 && atomicExch(nu(c.d, t0, kNDestEpoch), c.dest_epoch) != c.dest_epoch;
-            const bool w1 = l1 && atomicExch(nu(c.d, t1, kNDestEpoch), c.dest_epoch) != c.dest_epoch;
-            wave_append2(&c.ctl->dest_count, w0, w1, p0, p1);
-            if (w0) c.d.dest_list[p0] = t0;
-            if (w1) c.d.dest_list[p1] = t1;
-            learn.listed += (l0 ? 1u : 0u) + (l1 ? 1u : 0u);
-            learn.claimed += (w0 ? 1u : 0u) + (w1 ? 1u : 0u);
+            bool l[K];
+#pragma unroll
+            for (uint32_t k = 0; k < K; ++k) l[k] = kept[k] && (e[k] != 0.0f || !skip_zero);
+            wave_append_k<K>(learn.count, l, pos);
+#pragma unroll
+            for (uint32_t k = 0; k < K; ++k)
+                if (l[k]) learn.list[pos[k]] = sl[k];
+            bool w[K];
+#pragma unroll
+            for (uint32_t k = 0; k < K; ++k)
+                w[k] = l[k] && atomicExch(nu(c.d, t[k], kNDestEpoch), c.dest_epoch) != c.dest_epoch;
+            wave_append_k<K>(&c.ctl->dest_count, w, pos);
+#pragma unroll
+            for (uint32_t k = 0; k < K; ++k) {
+                if (w[k]) c.d.dest_list[pos[k]] = t[k];
+                learn.listed += l[k] ? 1u : 0u;
+                learn.claimed += w[k] ? 1u : 0u;
+            }
         }
     }
+}
+
+// Slots per lane and iteration for a list of n slots over gstride threads:
+// four once every thread has at least eight slots (two iterations of four
+// instead of four of two), else two (wider iterations cost a lane with only a
+// few slots more than they save: +0.5 us per supervised canonical step).
+template <class F>
+__device__ __forceinline__ void eligibility_width(uint32_t n, uint32_t gstride, F&& walk) {
+    if (n >= 8u * gstride) walk(std::integral_constant<uint32_t, 4>{});
+    else walk(std::integral_constant<uint32_t, 2>{});
 }
 
 // The slots are dealt over the threads of the first gstride / kThreads
@@ -2073,11 +2118,17 @@ __device__ __forceinline__ void phase_eligibility(const StepCtx& c, bool plastic
     }
     const float pop_cutoff = a.redundant_global ? 0.0f : ld(&c.ctl->pop_cutoff);
     LearnOut rec{d.rec_learn, &c.ctl->rec_learn_count, plastic, 0, 0};
-    eligibility_list(c, d.rec_trace, NS, d.rec_mark, d.rec_list + p * NS, rec_n, d.rec_list + q * NS,
-                     &c.ctl->rec_count[q], a.m.rec_target, a.m.rec_branch, pop_cutoff, rec, gstride);
+    eligibility_width(rec_n, gstride, [&](auto width) {
+        eligibility_list<decltype(width)::value>(c, d.rec_trace, NS, d.rec_mark, d.rec_list + p * NS, rec_n,
+                                                 d.rec_list + q * NS, &c.ctl->rec_count[q], a.m.rec_edge,
+                                                 pop_cutoff, rec, gstride);
+    });
     LearnOut in{d.in_learn, &c.ctl->in_learn_count, plastic, rec.claimed, rec.listed};
-    eligibility_list(c, d.in_trace, NI, d.in_mark, d.in_list + p * NI, in_n, d.in_list + q * NI,
-                     &c.ctl->in_count[q], a.m.in_target, a.m.in_branch, pop_cutoff, in, gstride);
+    eligibility_width(in_n, gstride, [&](auto width) {
+        eligibility_list<decltype(width)::value>(c, d.in_trace, NI, d.in_mark, d.in_list + p * NI, in_n,
+                                                 d.in_list + q * NI, &c.ctl->in_count[q], a.m.in_edge,
+                                                 pop_cutoff, in, gstride);
+    });
     if (plastic) {
         count_wave(c, kCDest, c.tick, in.claimed);
         count_wave(c, kCLearn, c.tick, in.listed);

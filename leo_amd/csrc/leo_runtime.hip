@@ -1241,7 +1241,7 @@ void upload_topology(LeoHipRuntime* h, const LeoModelView& m) {
     size_t o_ex = l.add<float>(z.n), o_ty = l.add<uint8_t>(z.n), o_rt = l.add<uint32_t>(z.ns);
     size_t o_rb = l.add<uint8_t>(z.ns), o_rd = l.add<uint8_t>(z.ns), o_it = l.add<uint32_t>(z.ni);
     size_t o_ib = l.add<uint8_t>(z.ni), o_off = l.add<uint64_t>(z.n + 1), o_edge = l.add<uint32_t>(z.ns);
-    size_t o_sho = l.add<uint64_t>(z.n + 1);
+    size_t o_sho = l.add<uint64_t>(z.n + 1), o_iedge = l.add<uint32_t>(z.ni);
     h->shared.allocate(l.cursor);
     char* b = h->shared.base;
     h->sm.excitability = reinterpret_cast<const float*>(b + o_ex);
@@ -1254,8 +1254,11 @@ void upload_topology(LeoHipRuntime* h, const LeoModelView& m) {
     h->sm.bucket_offset = reinterpret_cast<const uint64_t*>(b + o_off);
     h->sm.rec_edge = reinterpret_cast<const uint32_t*>(b + o_edge);
     h->sm.shadow_offset = reinterpret_cast<const uint64_t*>(b + o_sho);
+    h->sm.in_edge = reinterpret_cast<const uint32_t*>(b + o_iedge);
     std::vector<uint32_t> edges(z.ns);
     for (uint64_t i = 0; i < z.ns; ++i) edges[i] = pack_edge(m.rec_target[i], m.rec_delay[i], m.rec_branch[i]);
+    std::vector<uint32_t> in_edges(z.ni);  // the delay field is unused (log2 delay 0)
+    for (uint64_t i = 0; i < z.ni; ++i) in_edges[i] = pack_edge(m.in_target[i], 1, m.in_branch[i]);
     hipStream_t s = h->stream;
     upload(b + o_ex, m.excitability, z.n * 4, s);
     upload(b + o_ty, m.neuron_type, z.n, s);
@@ -1267,6 +1270,7 @@ void upload_topology(LeoHipRuntime* h, const LeoModelView& m) {
     upload(b + o_off, offsets.data(), offsets.size() * 8, s);
     upload(b + o_sho, shadow.data(), shadow.size() * 8, s);
     upload(b + o_edge, edges.data(), z.ns * 4, s);
+    upload(b + o_iedge, in_edges.data(), z.ni * 4, s);
     sync(s);
 }
 
