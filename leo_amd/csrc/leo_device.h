@@ -462,6 +462,22 @@ struct MergeArgs {
     // with stale_flag, one word set when any element of the tensor merges.
     uint32_t LEO_GLOBAL* stale;
     uint32_t stale_flag;
+    // Candidate list (leo_merge_candidates): when set, only the listed
+    // positions are visited (elements, or rows of `row` elements), `*list_count`
+    // of them; the others are unchanged in every lane.
+    const uint32_t LEO_GLOBAL* list;
+    const unsigned long long LEO_GLOBAL* list_count;
+};
+
+// Positions changed in any lane of a group: the OR of the lanes' change
+// bitmaps (one bit per element, or per output row), listed in `list`.
+struct MergeCandidates {
+    const uint32_t* const* bits;  // per-lane bitmap of the tensor
+    uint32_t lane_count;
+    uint64_t words;
+    uint64_t positions;
+    uint32_t LEO_GLOBAL* list;
+    unsigned long long LEO_GLOBAL* count;
 };
 
 // Sparse moves between a canonical tensor and a packed buffer: element

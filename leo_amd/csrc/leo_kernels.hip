@@ -3129,10 +3129,44 @@ __device__ __forceinline__ void mark_stale(const MergeArgs& m, uint64_t i) {
     atomicOr(&m.stale[bit >> 5], 1u << (bit & 31));
 }
 
+// One bitmap word per thread: the OR over the group's lanes, its set
+// positions appended to the list (one atomic per wave; the list's order does
+// not matter, every element is merged on its own).
+__global__ void __launch_bounds__(kThreads) leo_merge_candidates(MergeCandidates mc) {
+    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * kThreads; base < mc.words;
+         base += static_cast<uint64_t>(gridDim.x) * kThreads) {
+        const uint64_t w = base + threadIdx.x;
+        uint32_t word = 0;
+        if (w < mc.words) {
+            for (uint32_t l = 0; l < mc.lane_count; ++l) word |= mc.bits[l][w];
+            const uint64_t tail = mc.positions - w * 32;  // positions in this word
+            if (tail < 32) word &= (1u << tail) - 1u;
+        }
+        const uint32_t n = static_cast<uint32_t>(__popc(word));
+        const uint32_t incl = wave_incl_scan_u32(n);
+        const uint32_t total = __builtin_amdgcn_readlane(incl, kWaveSize - 1);
+        unsigned long long at = 0;
+        if (__lane_id() == kWaveSize - 1 && total) at = atomicAdd(mc.count, static_cast<unsigned long long>(total));
+        at = static_cast<unsigned long long>(__builtin_amdgcn_readlane(static_cast<uint32_t>(at), kWaveSize - 1)) |
+             (static_cast<unsigned long long>(__builtin_amdgcn_readlane(static_cast<uint32_t>(at >> 32), kWaveSize - 1))
+              << 32);
+        at += incl - n;
+        while (word) {
+            const uint32_t bit = __ffs(word) - 1;
+            word &= word - 1;
+            mc.list[at++] = static_cast<uint32_t>(w * 32 + bit);
+        }
+    }
+}
+
 __global__ void __launch_bounds__(kThreads) leo_merge_fixed(MergeArgs m) {
     unsigned long long local = 0, changes = 0;
-    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < m.count;
-         i += static_cast<uint64_t>(gridDim.x) * kThreads) {
+    // visited elements: all of them, or the listed positions' elements
+    const uint64_t per = m.row ? m.row : 1u;
+    const uint64_t visits = m.list ? *m.list_count * per : m.count;
+    for (uint64_t k = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; k < visits;
+         k += static_cast<uint64_t>(gridDim.x) * kThreads) {
+        const uint64_t i = m.list ? static_cast<uint64_t>(m.list[k / per]) * per + k % per : k;
         uint64_t at = m.row ? (i / m.row) * m.stride + (i % m.row) : i;
         const float base = m.canonical[at];
         if (m.mode == kMergeFinalize) {
@@ -3148,9 +3182,11 @@ __global__ void __launch_bounds__(kThreads) leo_merge_fixed(MergeArgs m) {
         }
         double sum = 0.0;
         bool any = false;
-        if (m.mode == kMergeAccumulate && !m.first) {
-            sum = m.acc[i];
+        if (m.mode == kMergeAccumulate && (m.list || !m.first)) {
+            // with a list the flags were cleared before the first group, so an
+            // element first listed in a later group starts from zero
             any = m.any[i] != 0;
+            sum = any || !m.list ? m.acc[i] : 0.0;
         }
         for (uint32_t l = 0; l < m.lane_count; ++l) {
             float delta = m.lanes[l][at] - base;

@@ -37,6 +37,7 @@ __global__ void leo_lane_steps_profiled(const KernelArgs* args);
 __global__ void leo_reset_lanes(KernelArgs args, uint32_t set_tick, uint32_t new_tick);
 
 __global__ void leo_merge_fixed(MergeArgs m);
+__global__ void leo_merge_candidates(MergeCandidates mc);
 __global__ void leo_sparse_move(SparseMove mv);
 __global__ void leo_fold_changes(FoldArgs f);
 
@@ -247,6 +248,7 @@ struct LeoHipRuntime {
     leo::Arena lane_descs;     // LaneDesc[max(1,max_lanes)]
     leo::Arena kernel_args_buf;  // KernelArgs of the step kernel
     leo::Arena merge_acc;        // f64 sums + changed flags of the lane-group merge
+    leo::Arena merge_list;       // candidate positions of one tensor's merge
     uint32_t resident_lanes = 0; // story lanes that fit on the device at once
     uint32_t max_steps_override = 0;
     float last_launch_ms = 0.0f;  // duration of the latest lane-steps launch (HIP events)
@@ -1516,7 +1518,9 @@ size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<HostContext>
 // f64 sums + changed flags for every fixed-parameter element (lane groups).
 size_t merge_accumulator_bytes(const Sizes& z) {
     const uint64_t elements = z.n + z.ns + z.ni + z.n * kOutputs + kOutputs + kOutputs * z.e;
-    return static_cast<size_t>(elements) * 9;
+    // f64 sums and flags of the lane groups, and the candidate list (at most
+    // one position per element of the largest bitmap-tracked tensor)
+    return static_cast<size_t>(elements) * 9 + static_cast<size_t>(std::max({z.n, z.ns, z.ni})) * 4 + 256;
 }
 
 // Device mean of every fixed-parameter tensor (parallel.rs:746-782). kMergeDirect
@@ -1527,8 +1531,8 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes, uint32_t
                      bool first = true, uint32_t total_lanes = 0) {
     const Sizes& z = h->z;
     const uint32_t L = static_cast<uint32_t>(lanes.size());
-    // scratch: 6 pointer tables of L entries + 1 counter + error word
-    size_t need = 6 * L * sizeof(float*) + 256;  // + counters
+    // scratch: 6 pointer tables of L entries, 4 bitmap tables, counters, error word
+    size_t need = 10 * L * sizeof(float*) + 256;  // + counters
     if (h->merge_scratch.bytes < need) {
         h->merge_scratch.allocate(need);
     }
@@ -1542,12 +1546,23 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes, uint32_t
         tables[4 * L + l] = p.bias;
         tables[5 * L + l] = p.ctx_out;
     }
+    // the lanes' change bitmaps of the four tensors they track per element
+    // (output weights per neuron row)
+    std::vector<const uint32_t*> bit_tables(4 * L);
+    for (uint32_t l = 0; l < L; ++l) {
+        const LaneDesc& d = lanes[l]->desc;
+        bit_tables[0 * L + l] = d.ch_threshold;
+        bit_tables[1 * L + l] = d.ch_rec;
+        bit_tables[2 * L + l] = d.ch_in;
+        bit_tables[3 * L + l] = d.ch_out;
+    }
     char* base = h->merge_scratch.base;
     upload(base, tables.data(), tables.size() * sizeof(float*), h->stream);
-    // counters: merged elements, changed lane values, then the error word
-    auto* counter = reinterpret_cast<unsigned long long*>(base + 6 * L * sizeof(float*));
-    auto* error = reinterpret_cast<uint32_t*>(counter + 2);
-    LEO_HIP_CHECK(hipMemsetAsync(counter, 0, 24, h->stream));
+    upload(base + 6 * L * sizeof(float*), bit_tables.data(), bit_tables.size() * sizeof(uint32_t*), h->stream);
+    // counters: merged elements, changed lane values, the candidate count, then the error word
+    auto* counter = reinterpret_cast<unsigned long long*>(base + 10 * L * sizeof(float*));
+    auto* error = reinterpret_cast<uint32_t*>(counter + 3);
+    LEO_HIP_CHECK(hipMemsetAsync(counter, 0, 32, h->stream));
     LEO_HIP_CHECK(hipEventRecord(h->ev_start, h->stream));
     struct Job {
         float* canonical;
@@ -1566,6 +1581,12 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes, uint32_t
     uint64_t elements = 0;
     for (int j = 0; j < 6; ++j) elements += jobs[j].count;
     if (mode != kMergeDirect && h->merge_acc.bytes < elements * 9) h->merge_acc.allocate(elements * 9);
+    // lane groups: every element's group flag starts clear (an element listed
+    // first in a later group starts its sum from zero)
+    if (mode == kMergeAccumulate && first)
+        LEO_HIP_CHECK(hipMemsetAsync(h->merge_acc.base + elements * 8, 0, elements, h->stream));
+    const uint64_t max_positions = std::max({z.n, z.ns, z.ni});
+    if (mode != kMergeFinalize && h->merge_list.bytes < max_positions * 4) h->merge_list.allocate(max_positions * 4);
     uint64_t acc_at = 0;
     for (int j = 0; j < 6; ++j) {
         MergeArgs m{};
@@ -1596,6 +1617,25 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes, uint32_t
                   : jobs[j].kind == kMergeContextOut ? h->stale_flags + 1
                   : h->stale_bits[jobs[j].kind];
         m.stale_flag = (jobs[j].kind == kMergeBias || jobs[j].kind == kMergeContextOut) ? 1u : 0u;
+        if (mode != kMergeFinalize && j < 4) {
+            // positions changed in any lane (every merged element is among them)
+            const uint64_t positions = j == 3 ? z.n : jobs[j].count;
+            MergeCandidates mc{};
+            mc.bits = reinterpret_cast<const uint32_t* const*>(base + 6 * L * sizeof(float*) +
+                                                               static_cast<size_t>(j) * L * sizeof(uint32_t*));
+            mc.lane_count = L;
+            mc.words = z.words(positions);
+            mc.positions = positions;
+            mc.list = reinterpret_cast<uint32_t*>(h->merge_list.base);
+            mc.count = counter + 2;
+            LEO_HIP_CHECK(hipMemsetAsync(counter + 2, 0, 8, h->stream));
+            const uint64_t cblocks = std::min<uint64_t>((mc.words + kThreads - 1) / kThreads, 4096);
+            hipLaunchKernelGGL(leo_merge_candidates, dim3(static_cast<uint32_t>(std::max<uint64_t>(cblocks, 1))),
+                               dim3(kThreads), 0, h->stream, mc);
+            LEO_HIP_CHECK(hipGetLastError());
+            m.list = mc.list;
+            m.list_count = mc.count;
+        }
         uint64_t blocks = std::min<uint64_t>((m.count + kThreads - 1) / kThreads, 4096);
         hipLaunchKernelGGL(leo_merge_fixed, dim3(static_cast<uint32_t>(std::max<uint64_t>(blocks, 1))), dim3(kThreads), 0,
                            h->stream, m);
