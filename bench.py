@@ -175,7 +175,7 @@ def main() -> int:
                          ks["section_bytes"][0], ks["section_lane_steps"][0]),
         "replay": section("leo_lane_steps (canonical runtime)", ks["section_launches"][1],
                           ks["section_kernel_ms"][1], ks["section_bytes"][1], ks["section_lane_steps"][1]),
-        "merge": section("leo_merge_fixed", ks["merge_launches"], ks["merge_ms"], ks["merge_bytes"], 0),
+        "merge": section("leo_merge_candidates + leo_merge_fixed", ks["merge_launches"], ks["merge_ms"], ks["merge_bytes"], 0),
     }
     line = {
         "metric": "trained bytes/sec (FP32, 1 MI355X)",

@@ -1588,6 +1588,8 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes, uint32_t
     const uint64_t max_positions = std::max({z.n, z.ns, z.ni});
     if (mode != kMergeFinalize && h->merge_list.bytes < max_positions * 4) h->merge_list.allocate(max_positions * 4);
     uint64_t acc_at = 0;
+    uint32_t candidate_launches = 0;
+    double bitmap_bytes = 0.0;
     for (int j = 0; j < 6; ++j) {
         MergeArgs m{};
         m.mode = mode;
@@ -1635,6 +1637,8 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes, uint32_t
             LEO_HIP_CHECK(hipGetLastError());
             m.list = mc.list;
             m.list_count = mc.count;
+            candidate_launches += 1;
+            bitmap_bytes += 4.0 * static_cast<double>(mc.words) * L;
         }
         uint64_t blocks = std::min<uint64_t>((m.count + kThreads - 1) / kThreads, 4096);
         hipLaunchKernelGGL(leo_merge_fixed, dim3(static_cast<uint32_t>(std::max<uint64_t>(blocks, 1))), dim3(kThreads), 0,
@@ -1651,12 +1655,12 @@ uint64_t merge_fixed(LeoHipRuntime* h, const std::vector<Lane*>& lanes, uint32_t
     float ms = 0.0f;
     LEO_HIP_CHECK(hipEventElapsedTime(&ms, h->ev_start, h->ev_stop));
     LeoKernelStats& t = h->telemetry;
-    t.merge_launches += 6;
+    t.merge_launches += 6 + candidate_launches;
     t.merge_ms += ms;
-    // algorithmic bytes of the mean: 24 per changed lane value, 4 (L+1) per
-    // merged element (canonical write and the lane scatters)
+    // algorithmic bytes of the mean: the lanes' change bitmaps the candidate
+    // pass ORs, 24 per changed lane value, 4 (L+1) per merged element
     t.merge_lane_changes += counts[1];
-    t.merge_bytes += 24.0 * static_cast<double>(counts[1]);
+    t.merge_bytes += bitmap_bytes + 24.0 * static_cast<double>(counts[1]);
     if (mode != kMergeAccumulate) {
         const double lanes_total = mode == kMergeFinalize ? total_lanes : L;
         t.merge_elements += updates;
