@@ -252,6 +252,7 @@ struct LeoHipRuntime {
     uint32_t resident_lanes = 0; // story lanes that fit on the device at once
     uint32_t max_steps_override = 0;
     float last_launch_ms = 0.0f;  // duration of the latest lane-steps launch (HIP events)
+    double canonical_step_ms = 0.0;  // slowest per-step average of a timed canonical replay launch
     leo::Arena merge_scratch;  // lane pointer table + counters
     // Host-stale marks of the canonical image: elements changed since the
     // caller's host mirror was last synchronised that the change bitmaps no
@@ -934,6 +935,16 @@ size_t max_steps_per_launch(const LeoHipRuntime* h, size_t lanes) {
     return static_cast<size_t>(std::min(4096.0, std::max(8.0, steps)));
 }
 
+// The first launch of a canonical replay segment: the worst-case bound until
+// a replay launch has been timed, then as many steps as the slowest timed
+// replay launch's per-step average fits in a quarter of a second.
+size_t first_canonical_chunk(const LeoHipRuntime* h) {
+    const size_t bound = max_steps_per_launch(h, 1);
+    if (h->max_steps_override || h->canonical_step_ms <= 0.0) return bound;
+    const double fit = 250.0 / h->canonical_step_ms;
+    return static_cast<size_t>(std::min(4096.0, std::max(static_cast<double>(bound), fit)));
+}
+
 // Later launches of a long schedule are sized from the last one's measured
 // duration toward a quarter of a second (at most 4x growth per launch), so
 // the step cost actually seen, not the worst case, sets the launch count.
@@ -1091,7 +1102,7 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
     size_t staged = 0, largest = 0, launches = 0;
     for (size_t k = 0; k < segments.size(); ++k) {
         if (segments[k].reset_before) staged += PinnedStaging::rounded(sizeof(LaneDesc));
-        size_t chunk = max_steps_per_launch(h, 1);
+        size_t chunk = first_canonical_chunk(h);
         for (size_t at = 0; at < segments[k].steps.size();) {
             const size_t n = std::min(chunk, segments[k].steps.size() - at);
             cuts[k].push_back(n);
@@ -1142,6 +1153,8 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
     try {
         for (QueuedLaunch& q : queued) {
             complete_launch(h, q);
+            if (const size_t n = q.runs[0].steps.size())
+                h->canonical_step_ms = std::max(h->canonical_step_ms, static_cast<double>(h->last_launch_ms) / n);
             absorb_canonical(h, q.runs[0], out);
         }
     } catch (...) {
