@@ -38,6 +38,12 @@ __device__ __forceinline__ float maxnum(float a, float b) {  // Rust f32::max
     if (b != b) return a;
     return a > b ? a : b;
 }
+// Rust's w.max(0.0) / w.min(0.0), the sign projections of runtime.rs:1475-1479
+// and parallel.rs:1202-1206, as rustc lowers them on x86_64 (maxss/minss with
+// the constant second operand, which wins on equal values and on NaN): -0.0
+// and NaN project to +0.0.
+__device__ __forceinline__ float max_zero(float v) { return v > 0.0f ? v : 0.0f; }
+__device__ __forceinline__ float min_zero(float v) { return v < 0.0f ? v : 0.0f; }
 // (a + b) mod n for a, b < n
 __device__ __forceinline__ uint32_t add_mod(uint32_t a, uint32_t b, uint32_t n) {
     const uint32_t v = a + b;
@@ -2693,7 +2699,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
                 const float old_w = ld(&d.p.rec_weight[slot]);
                 float nw = clampf(old_w + delta, wmin, wmax);
                 const bool excitatory = a.m.neuron_type[src] == 0;
-                nw = excitatory ? maxnum(nw, 0.0f) : fminf(nw, 0.0f);
+                nw = excitatory ? max_zero(nw) : min_zero(nw);
                 if (!finitef(nw)) set_error(ctl, kErrRecurrent);
                 bool changed = nw != old_w;
                 if (!excitatory && ld(nu(d, src, kNSelected)) == tick + 1) {
@@ -3109,7 +3115,7 @@ __device__ __forceinline__ float merge_project(const MergeArgs& m, uint64_t i, f
         case kMergeThreshold: return clampf(v, 0.05f, 2.0f);
         case kMergeRecurrent:
             v = clampf(v, m.weight_min, m.weight_max);
-            return m.neuron_type[i / m.synapses_per_neuron] == 0 ? maxnum(v, 0.0f) : fminf(v, 0.0f);
+            return m.neuron_type[i / m.synapses_per_neuron] == 0 ? max_zero(v) : min_zero(v);
         case kMergeInput: return clampf(v, 0.0f, m.weight_max);
         case kMergeOutput:
         case kMergeContextOut: return clampf(v, m.weight_min, m.weight_max);

@@ -63,6 +63,12 @@ inline float clampf(float v, float lo, float hi) {  // Rust f32::clamp
     if (v > hi) v = hi;
     return v;
 }
+// Rust's w.max(0.0) / w.min(0.0) (the sign projections, runtime.rs:1475-1479,
+// parallel.rs:1202-1206) as rustc lowers them on x86_64: maxss/minss with the
+// constant as the second operand, and that operand wins when the values
+// compare equal or one is NaN. So -0.0 and NaN both project to +0.0.
+inline float max_zero(float v) { return v > 0.0f ? v : 0.0f; }
+inline float min_zero(float v) { return v < 0.0f ? v : 0.0f; }
 inline float maxf(float a, float b) {  // Rust f32::max (maxNum)
     if (std::isnan(a)) return b;
     if (std::isnan(b)) return a;
@@ -1139,7 +1145,7 @@ struct Runtime {
             float delta = bounded_delta(-lr * strength * g, mu);
             float old_w = model.rec_weight[slot];
             float nw = clampf(old_w + delta, wmin, wmax);
-            nw = model.neuron_type[slot / S] == 0 ? maxf(nw, 0.0f) : std::min(nw, 0.0f);
+            nw = model.neuron_type[slot / S] == 0 ? max_zero(nw) : min_zero(nw);
             if (!std::isfinite(nw)) {
                 model.stats.numerical_rejections = sat_add(model.stats.numerical_rejections, 1);
                 numerical("non-finite recurrent update rejected");
@@ -1574,7 +1580,7 @@ std::pair<size_t, size_t> apply_deltas_with_divisor(Model& master, const std::ve
     uint64_t inc = 0;
     for (auto* d : deltas) inc = sat_add(inc, d->revision_increment);
     master.parameter_revision = sat_add(master.parameter_revision, inc);
-    // project_parameter_constraints_sparse
+    // project_parameter_constraints_sparse (parallel.rs:1169-1246)
     const float wmin = master.cfg.c.weight_min, wmax = master.cfg.c.weight_max;
     const size_t S = master.S(), E = master.E();
     for (auto* d : deltas) {
@@ -1582,7 +1588,7 @@ std::pair<size_t, size_t> apply_deltas_with_divisor(Model& master, const std::ve
         for (auto& u : d->excitability) master.excitability[u.index] = clampf(master.excitability[u.index], 0.1f, 4.0f);
         for (auto& u : d->recurrent_weight) {
             float w = clampf(master.rec_weight[u.index], wmin, wmax);
-            w = master.neuron_type[u.index / S] == 0 ? maxf(w, 0.0f) : std::min(w, 0.0f);
+            w = master.neuron_type[u.index / S] == 0 ? max_zero(w) : min_zero(w);
             master.rec_weight[u.index] = w;
         }
         for (auto& u : d->input_weight) master.in_weight[u.index] = clampf(master.in_weight[u.index], 0.0f, wmax);
@@ -1598,12 +1604,17 @@ std::pair<size_t, size_t> apply_deltas_with_divisor(Model& master, const std::ve
         }
         for (auto& u : d->context_output_weight) master.ctx_out[u.index] = clampf(master.ctx_out[u.index], wmin, wmax);
     }
-    // validate_sparse_merge
+    // validate_sparse_merge (parallel.rs:1248-1345)
     if (!std::isfinite(master.stats.training_loss_sum)) internal("merged model statistics contain a non-finite loss");
     for (auto* d : deltas) {
         for (auto& u : d->threshold) {
             float v = master.threshold[u.index];
             if (!std::isfinite(v) || v < 0.05f || v > 2.0f) internal("merged threshold violates canonical parameter bounds");
+        }
+        for (auto& u : d->excitability) {
+            float v = master.excitability[u.index];
+            if (!std::isfinite(v) || v < 0.1f || v > 4.0f)
+                internal("merged excitability violates canonical parameter bounds");
         }
         for (auto& u : d->recurrent_weight) {
             float w = master.rec_weight[u.index];
@@ -1620,6 +1631,19 @@ std::pair<size_t, size_t> apply_deltas_with_divisor(Model& master, const std::ve
         }
         for (auto& u : d->output_bias)
             if (!std::isfinite(master.bias[u.index])) internal("merged output bias is non-finite");
+        for (auto& u : d->context) {
+            auto [slot, probes] = master.resolve_context_slot(u.order, u.key, false);
+            (void)probes;
+            if (slot < 0) continue;
+            const size_t s = static_cast<size_t>(slot);
+            if (master.ctx_keys[s] == 0 && master.ctx_obs[s] != 0)
+                internal("merged context slot has observations without a key");
+            for (size_t dd = 0; dd < E; ++dd) {
+                float w = master.ctx_emb[s * E + dd];
+                if (!std::isfinite(w) || w < wmin || w > wmax)
+                    internal("merged context embedding violates canonical parameter bounds");
+            }
+        }
         for (auto& u : d->context_output_weight) {
             float w = master.ctx_out[u.index];
             if (!std::isfinite(w) || w < wmin || w > wmax) internal("merged context output weight violates canonical parameter bounds");
