@@ -108,6 +108,58 @@ def measured_traffic(workload: str):
     return None
 
 
+def canonical_steps(workload: str, frozen: int, supervised: int) -> int:
+    """Per-step kernel time of the canonical runtime, the lane that runs the
+    serial replay: `frozen` FROZEN steps of one document (a replay prefix,
+    advance_frozen_batch, backend.rs:428-431) and `supervised` TRAINING steps
+    (replay targets, training_step_batch, backend.rs:413-422), timed with HIP
+    events over the step-kernel launches. With LEO_HIP_PHASE_PROFILE=1 the line
+    also carries the per-phase work and barrier-wait time of one workgroup of
+    the lane (LEO_HIP_PROFILE_PART picks which) in microseconds per step."""
+    from leo_amd import native
+    from leo_amd.runtime import HipRuntime
+    from leo_amd.workload import WORKLOADS, synthetic_stories, workload_model
+
+    w = WORKLOADS[workload]
+    model = workload_model(w)
+    data, offsets = synthetic_stories(w, 64)
+    text = bytes(data)
+    need = max(frozen, supervised) + 201
+    while len(text) < need:
+        text += text
+    runtime = HipRuntime(model, device=0, max_lanes=1)
+    profiled = os.environ.get("LEO_HIP_PHASE_PROFILE", "0") not in ("", "0")
+
+    def timed(label, run, steps):
+        runtime.kernel_stats(reset=True)
+        started = time.perf_counter()
+        run()
+        wall = time.perf_counter() - started
+        ks = runtime.kernel_stats()
+        out = {"metric": f"canonical {label} step", "workload": w.name, "steps": steps,
+               "kernel_us_per_step": ks["kernel_ms"] * 1e3 / steps, "wall_us_per_step": wall * 1e6 / steps,
+               "launches": ks["launches"], "active_per_step": ks["active"] / steps,
+               "events_per_step": ks["events"] / steps, "touched_per_step": ks["touched"] / steps}
+        if profiled:
+            out["phase_work_us"] = [round(x / steps, 3) for x in ks["phase_work_us"]]
+            out["phase_wait_us"] = [round(x / steps, 3) for x in ks["phase_wait_us"]]
+        print(json.dumps(out), flush=True)
+
+    try:
+        runtime.begin_document()  # warm-up: the kernels' first launches
+        runtime.advance_frozen_batch([(b, None) for b in text[:200]])
+        if frozen:
+            runtime.begin_document()
+            timed("frozen", lambda: runtime.advance_frozen_batch([(b, None) for b in text[:frozen]]), frozen)
+        if supervised:
+            runtime.begin_document()
+            steps = [(text[i], text[i + 1]) for i in range(supervised)]
+            timed("supervised", lambda: runtime.training_step_batch(steps, native.TRAINING), supervised)
+    finally:
+        runtime.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -118,9 +170,14 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of known size (PMC counter calibration)")
+    ap.add_argument("--canonical-steps", nargs=2, type=int, metavar=("FROZEN", "SUPERVISED"),
+                    help="time FROZEN prefix steps and SUPERVISED replay-target steps of the canonical runtime "
+                         "(kernel time per step) instead of the training benchmark")
     args = ap.parse_args()
     if args.copy_calibration:
         return copy_calibration()
+    if args.canonical_steps:
+        return canonical_steps(args.workload, *args.canonical_steps)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box in this setup has one MI355X, so --gpus {args.gpus} "
               "is not run (stories would be sharded over devices by lane ranges, with the batch-end mean "

@@ -407,7 +407,8 @@ int32_t leo_hip_commit_packed_host_model(LeoHipRuntime* runtime, const LeoPacked
  * tensors needs more than 8 MiB of staging (indices and values, e.g. more
  * than about 8,100 output rows or 1M recurrent elements) is refused with
  * LEO_ERR_INVALID_ARGUMENT before anything is written. All runtimes on a GPU
- * share its scratch: calls that overlap on one GPU race. */
+ * share its scratch, so overlapping calls on one GPU are serialised by a
+ * per-device lock held until the commit's copies and kernels are done. */
 int32_t leo_hip_commit_packed_host_model_no_alloc(LeoHipRuntime* runtime, const LeoPackedUpdate* update);
 /* RuntimeBackend::model_mut (backend.rs:357): replace the canonical model. */
 int32_t leo_hip_upload_model(LeoHipRuntime* runtime, const LeoModelView* model);

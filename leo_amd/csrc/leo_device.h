@@ -163,6 +163,7 @@ enum : uint32_t {
     kErrOutput = 1, kErrBias = 2, kErrContextProjection = 3, kErrContextEmbedding = 4,
     kErrRecurrent = 5, kErrInput = 6, kErrInhibitory = 7, kErrCapacity = 8, kErrBarrier = 9,
 };
+constexpr uint32_t kNoFail = 0xffffffffu;
 
 // Device-resident scalars of a lane that persist across launches.
 struct LaneControl {
@@ -188,7 +189,12 @@ struct LaneControl {
     uint32_t active_count;
     uint32_t bias_dirty;
     uint32_t ctx_out_dirty;
+    // Sticky device guard: the first guard a step trips (kErr* code). A lane
+    // whose word is set runs no further steps, in this launch or in later
+    // ones, until the host has read the code and clears it.
     uint32_t error_code;
+    uint32_t error_step;             // schedule index (within its launch) of the step that tripped it
+    uint32_t bias_fail;              // first output whose bias this learning step makes non-finite, or kNoFail
     uint32_t ring_tick[kRing];       // tick whose active set ring slot holds (UINT32_MAX = empty)
     uint32_t ring_count[kRing];      // active count of that tick
     // The barrier counter has a 128-byte L2 line of its own: its polls and

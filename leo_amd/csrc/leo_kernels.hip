@@ -121,6 +121,11 @@ __device__ uint64_t context_key(const uint32_t* history, uint32_t len, uint32_t 
 }
 
 __device__ __forceinline__ void set_error(LaneControl* ctl, uint32_t code) { atomicCAS(&ctl->error_code, 0u, code); }
+// A numerical guard of schedule step `step`: the first code set wins and
+// records its step (the lane stops after that step).
+__device__ __forceinline__ void set_step_error(LaneControl* ctl, uint32_t code, uint32_t step) {
+    if (atomicCAS(&ctl->error_code, 0u, code) == 0u) ctl->error_step = step;
+}
 __device__ __forceinline__ void mark_bit(uint32_t* bits, uint32_t index) { atomicOr(&bits[index >> 5], 1u << (index & 31)); }
 
 // Wave-aggregated append: one atomic per wave instead of one per lane. Must be
@@ -2198,6 +2203,7 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
     const uint32_t A = from_waves ? wave_starts(c, sh, starts, nwaves) : ld(&ctl->active_count);
     const uint32_t ctx_count = ld(&ctl->ctx_count);
     float l1 = ld(&d.p.bias[o1]), l2 = has2 ? ld(&d.p.bias[o2]) : 0.0f;
+    const float bias1 = l1, bias2 = l2;
     constexpr uint32_t kDims = 16;
     float x1[kDims], x2[kDims];
 #pragma unroll
@@ -2384,6 +2390,27 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
     if (sp.target_index >= 0 && (threadIdx.x == static_cast<uint32_t>(sp.target_index) ||
                                  (has2 && o2 == static_cast<uint32_t>(sp.target_index))))
         d.records[step_index].p_target = threadIdx.x == static_cast<uint32_t>(sp.target_index) ? p1 : p2;
+    __syncthreads();  // thread 0 has read the argmax partials in sh.red
+    if (sp.flags & kStepLearn) {
+        // The learning phase's bias update (runtime.rs:1290-1298), checked
+        // ahead: the reference adds the outputs' deltas in order and stops at
+        // the first bias that becomes non-finite (after writing it), before
+        // the context, synapse and homeostasis updates. The learning phase
+        // reads the first such output from the control word.
+        const float olr = cfg.output_learning_rate, ss = sp.supervised_strength, mu = cfg.max_update;
+        const float e1 = static_cast<int32_t>(o1) == sp.target_index ? p1 - 1.0f : p1;
+        const float e2 = static_cast<int32_t>(o2) == sp.target_index ? p2 - 1.0f : p2;
+        uint32_t fail = kNoFail;
+        if (!finitef(bias1 + bounded(-olr * ss * e1, mu))) fail = o1;
+        else if (has2 && !finitef(bias2 + bounded(-olr * ss * e2, mu))) fail = o2;
+        for (int off = 32; off > 0; off >>= 1) fail = min(fail, static_cast<uint32_t>(__shfl_xor(static_cast<int>(fail), off)));
+        if (lane == 0) sh.red[wave] = fail;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (uint32_t w = 1; w < kWavesPerGroup; ++w) fail = min(fail, static_cast<uint32_t>(sh.red[w]));
+            ctl->bias_fail = fail;
+        }
+    }
     __syncthreads();
 }
 
@@ -2567,7 +2594,8 @@ __device__ __forceinline__ float inhibitory_step(const LeoConfig& cfg, float w, 
     return clampf(w + delta, cfg.weight_min, 0.0f);
 }
 
-__device__ __forceinline__ void context_update(const StepCtx& c, const StepParams& sp, StepShared& sh) {
+__device__ __forceinline__ void context_update(const StepCtx& c, const StepParams& sp, StepShared& sh,
+                                               uint32_t step_index) {
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = c.d;
     LaneControl* ctl = c.ctl;
@@ -2608,7 +2636,7 @@ __device__ __forceinline__ void context_update(const StepCtx& c, const StepParam
             const float gradient = sh.err[i / E] * latent[k];
             const float delta = bounded(-lr * strength * gradient, mu);
             const float updated = clampf(old[k] + delta, wmin, wmax);
-            if (!finitef(updated)) set_error(ctl, kErrContextProjection);
+            if (!finitef(updated)) set_step_error(ctl, kErrContextProjection, step_index);
             d.p.ctx_out[i] = updated;
         }
     }
@@ -2618,7 +2646,7 @@ __device__ __forceinline__ void context_update(const StepCtx& c, const StepParam
         const float gradient = ld(&ctl->ctx_scales[k]) * grad[e];
         const float delta = bounded(-lr * strength * gradient, mu);
         const float updated = clampf(ld(&d.p.ctx_emb[slot * E + e]) + delta, wmin, wmax);
-        if (!finitef(updated)) set_error(ctl, kErrContextEmbedding);
+        if (!finitef(updated)) set_step_error(ctl, kErrContextEmbedding, step_index);
         d.p.ctx_emb[slot * E + e] = updated;
     }
     for (uint32_t k = threadIdx.x; k < count; k += kThreads) {
@@ -2630,7 +2658,8 @@ __device__ __forceinline__ void context_update(const StepCtx& c, const StepParam
     __syncthreads();
 }
 
-__device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& sp, StepShared& sh) {
+__device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& sp, StepShared& sh,
+                                            uint32_t step_index) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -2646,6 +2675,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
     const uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap;
     const float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap;
     const float mu = cfg.max_update, wmin = cfg.weight_min, wmax = cfg.weight_max;
+    uint32_t bias_fail = kNoFail;
     if (learn) {
         // the readout workgroup updates the bias and the context projection;
         // the other workgroups share the output rows and the synapse slots
@@ -2661,6 +2691,9 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
         const uint32_t rec_first = plastic && first < NS ? ld(&rec_cur[first]) : 0u;
         const uint32_t in_first = plastic && first < NI ? ld(&in_cur[first]) : 0u;
         for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) sh.err[o] = ld(&d.errors[o]);
+        // an output whose bias becomes non-finite ends the step's learning
+        // after the output rows and the bias up to it (runtime.rs:1296-1300)
+        bias_fail = ld(&ctl->bias_fail);
         __syncthreads();
         const float ss = sp.supervised_strength;
         const float olr = cfg.output_learning_rate;
@@ -2677,16 +2710,19 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
         }
         // bias and context projection on the readout workgroup
         if (c.part == c.P - 1) {
-            for (uint32_t o = threadIdx.x; o < kOutputs; o += kThreads) {
+            for (uint32_t o = threadIdx.x; o <= min(bias_fail, kOutputs - 1); o += kThreads) {
                 const float raw = -olr * ss * sh.err[o];
                 const float b = ld(&d.p.bias[o]) + bounded(raw, mu);
-                if (!finitef(b)) set_error(ctl, kErrBias);
                 d.p.bias[o] = b;
             }
-            if (threadIdx.x == 0) ctl->bias_dirty = 1;
-            if (ld(&ctl->ctx_applied) && ld(&ctl->ctx_count) > 0) context_update(c, sp, sh);
+            if (threadIdx.x == 0) {
+                ctl->bias_dirty = 1;
+                if (bias_fail != kNoFail) set_step_error(ctl, kErrBias, step_index);
+            }
+            if (bias_fail == kNoFail && ld(&ctl->ctx_applied) && ld(&ctl->ctx_count) > 0)
+                context_update(c, sp, sh, step_index);
         }
-        if (plastic) {
+        if (plastic && bias_fail == kNoFail) {
             const float cs = ss * sp.plasticity_scale;
             const float lr = cfg.recurrent_learning_rate;
             for (uint32_t i = first; i < rec_n; i += stride) {
@@ -2700,12 +2736,12 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
                 float nw = clampf(old_w + delta, wmin, wmax);
                 const bool excitatory = a.m.neuron_type[src] == 0;
                 nw = excitatory ? max_zero(nw) : min_zero(nw);
-                if (!finitef(nw)) set_error(ctl, kErrRecurrent);
+                if (!finitef(nw)) set_step_error(ctl, kErrRecurrent, step_index);
                 bool changed = nw != old_w;
                 if (!excitatory && ld(nu(d, src, kNSelected)) == tick + 1) {
                     const float tgt_act = ld(nf(d, dst, kNActivation)) > 0.0f ? 1.0f : 0.0f;
                     const float nw2 = inhibitory_step(cfg, nw, ld(nf(d, src, kNActivation)), tgt_act, sp.strength);
-                    if (!finitef(nw2)) set_error(ctl, kErrInhibitory);
+                    if (!finitef(nw2)) set_step_error(ctl, kErrInhibitory, step_index);
                     changed = changed || nw2 != nw;
                     nw = nw2;
                 }
@@ -2720,7 +2756,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
                 const float delta = bounded(-lr * cs * gradient, mu);
                 const float old_w = ld(&d.p.in_weight[slot]);
                 const float nw = clampf(old_w + delta, 0.0f, wmax);
-                if (!finitef(nw)) set_error(ctl, kErrInput);
+                if (!finitef(nw)) set_step_error(ctl, kErrInput, step_index);
                 if (nw != old_w) mark_bit(d.ch_in, slot);
                 d.p.in_weight[slot] = nw;
             }
@@ -2729,7 +2765,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
         // already handled with their learning slot above (a kept eligible
         // slot with nonzero eligibility, or any kept slot without the zero
         // skip)
-        const uint32_t inh_items = A * S;
+        const uint32_t inh_items = bias_fail == kNoFail ? A * S : 0u;
         const bool skip_zero = a.skip_zero_eligibility != 0;
         for (uint32_t item = first; item < inh_items; item += stride) {
             const uint32_t r = fast_div(item, a.div_synapses), j = item - r * S;
@@ -2743,7 +2779,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
             const float tgt_act = ld(nf(d, dst, kNActivation)) > 0.0f ? 1.0f : 0.0f;
             const float old_w = ld(&d.p.rec_weight[slot]);
             const float nw = inhibitory_step(cfg, old_w, ld(nf(d, src, kNActivation)), tgt_act, sp.strength);
-            if (!finitef(nw)) set_error(ctl, kErrInhibitory);
+            if (!finitef(nw)) set_step_error(ctl, kErrInhibitory, step_index);
             if (nw != old_w) mark_bit(d.ch_rec, static_cast<uint32_t>(slot));
             d.p.rec_weight[slot] = nw;
         }
@@ -2765,6 +2801,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
                     const uint32_t blk = fast_div(n, a.div_block), off = n - blk * nb;
                     d.touched_bits[blk * block_words(nb) + off / 32] = 0u;
                 }
+                if (bias_fail != kNoFail) continue;  // the failed step ends before homeostasis
                 const float local = ld(nf(d, n, kNActivation)) > 0.0f ? 1.0f : 0.0f;
                 const float local_err = local - cfg.target_activity;
                 const float delta = cfg.threshold_homeostasis_rate * (local_err + pop_err);
@@ -2844,6 +2881,10 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
     c.P = P;
     c.gtid = c.part * kThreads + threadIdx.x;
     c.gstride = P * kThreads;
+    // a lane whose guard tripped in an earlier launch runs nothing until the
+    // host has read the code (every workgroup reads it before its first
+    // barrier, and no step of this launch can set it before then)
+    if (ld(&c.ctl->error_code) != 0) return;
     c.tick = ld(&c.ctl->tick);
     c.parity = ld(&c.ctl->parity);
     c.dest_epoch = ld(&c.ctl->dest_epoch);
@@ -2891,7 +2932,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
     if (steps > 0) fetch(0);
     // a step whose delivery ran in the previous step's last phase, and the
     // event count of that delivery (thread 0 of each workgroup)
-    bool delivered_ahead = false;
+    bool delivered_ahead = false, stopped = false;
     uint32_t pending_events = 0;
     for (uint32_t s = 0; s < steps && ok; ++s) {
         const StepParams sp = params();
@@ -2969,13 +3010,22 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 4))) break;
         }
         if (learn || !(sp.flags & kStepFrozen)) {
-            phase_learn(c, sp, sh);
+            phase_learn(c, sp, sh, s);
             if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 5))) break;
+            // a numerical guard of this step ends the lane here, as the
+            // reference's step returns its error (every workgroup reads the
+            // word after the barrier that follows the guards)
+            if (learn && ld(&c.ctl->error_code) != 0) {
+                stopped = true;
+                c.tick += 1;
+                break;
+            }
         }
         delivered_ahead = pipeline;
         c.tick += 1;
     }
-    if (ok && c.part == 0 && threadIdx.x < kWaveSize && steps > 0) finalize_record(c, steps - 1, c.tick - 1);
+    if (ok && !stopped && c.part == 0 && threadIdx.x < kWaveSize && steps > 0)
+        finalize_record(c, steps - 1, c.tick - 1);
     if (ok && c.part == 0 && threadIdx.x == 0) {
         c.ctl->tick = c.tick;
         c.ctl->parity = c.parity;
@@ -3038,6 +3088,10 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
     const uint32_t lane = blockIdx.x % L;
     const uint32_t part = blockIdx.x / L, parts = gridDim.x / L;
     const LaneDesc& d = args.lanes[lane];
+    // a lane stopped by a guard keeps the state the guard left until the
+    // host has read the code and cleared it (a reset queued behind the
+    // failing launch does nothing)
+    if (d.ctl->error_code != 0) return;
     const uint32_t tick = set_tick ? new_tick : d.ctl->tick;
     const uint64_t N = cfg.neuron_count, S = cfg.synapses_per_neuron;
     const uint64_t NS = N * S, NI = static_cast<uint64_t>(kSymbols) * cfg.input_fanout;
@@ -3092,7 +3146,6 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
         ctl->dest_count = 0;
         ctl->rec_learn_count = 0;
         ctl->in_learn_count = 0;
-        ctl->error_code = 0;
         ctl->barrier = 0;
         ctl->abort = 0;
         for (uint32_t k = 0; k < kRing; ++k) {

@@ -218,6 +218,9 @@ struct Lane {
     uint32_t tick = 0;
     uint32_t plasticity_phase = 0;
     bool persistent_activity = false;
+    // the host has reported this lane's device guard: its sticky error word
+    // is cleared before the next work queued on the lane
+    bool error_seen = false;
 };
 
 struct ContextDelta {
@@ -507,13 +510,16 @@ void fold_changes(LeoHipRuntime* h) {
 // (leo_hip_commit_packed_host_model_no_alloc): a file-scope device array, one
 // copy per GPU, held until the process ends. Host code uses its per-device
 // address from hipGetSymbolAddress, never the array's name. Every call on a
-// GPU shares that GPU's copy: calls that overlap on one GPU race.
+// GPU shares that GPU's copy, so calls on one GPU (from any runtime) take
+// that GPU's lock for the whole commit, through its final synchronisation,
+// and run one after another.
 constexpr size_t kStaticScratchBytes = size_t(8) << 20;
 static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 
 constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mutex;
 char* g_scratch_ptr[kMaxScratchDevices] = {};
+std::mutex g_scratch_user[kMaxScratchDevices];  // held by the commit that stages through the device's copy
 
 // The device address of `scratch` on `device` (which must be current),
 // looked up once per device.
@@ -624,7 +630,16 @@ void stage_descs(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
     h->staging.publish(h->stream);
 }
 
+// Clears the sticky error word of a lane whose guard the host has already
+// reported, on `stream`, ahead of the next work queued there.
+void clear_reported_error(Lane& lane, hipStream_t stream) {
+    if (!lane.error_seen) return;
+    LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->error_code, 0, 4, stream));
+    lane.error_seen = false;
+}
+
 void reset_lane_objects(LeoHipRuntime* h, const std::vector<Lane*>& lanes, bool set_tick, uint32_t new_tick) {
+    for (Lane* l : lanes) clear_reported_error(*l, h->stream);
     stage_descs(h, lanes);
     reset_lanes(h, static_cast<uint32_t>(lanes.size()), set_tick, new_tick);
     for (Lane* l : lanes) {
@@ -692,10 +707,18 @@ StepParams make_step(const LeoHostConfig& c, Lane& lane, uint32_t symbol, int32_
     return sp;
 }
 
+constexpr size_t kAllSteps = ~size_t(0);
+
 struct LaneRun {
     Lane* lane;
     std::vector<StepParams> steps;
     std::vector<StepRecord> records;
+    // steps that ran to the end: all of them, or those before the step whose
+    // numerical guard stopped the lane
+    size_t completed = kAllSteps;
+    // the lane's plasticity phase before each step (canonical schedules), to
+    // put the host mirror back where a stopped step left it
+    std::vector<uint32_t> phase;
 };
 
 // Algorithmic HBM bytes of one lane-step: each DRAM-resident element a phase
@@ -825,10 +848,12 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
         lane.desc.step_count = static_cast<uint32_t>(r.steps.size());
         h->staging.h2d(const_cast<StepParams*>(lane.desc.steps), r.steps.data(), r.steps.size() * sizeof(StepParams));
         // cleared on the transfer stream, after the previous launch's
-        // control words have been downloaded there
+        // control words have been downloaded there; the error word only once
+        // the host has reported its code (a launch queued behind a failed
+        // one finds it set and runs nothing)
         static_assert(offsetof(LaneControl, xcc_mask) == offsetof(LaneControl, barrier) + 8, "cleared together");
         LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->barrier, 0, 12, h->staging.xfer));  // barrier, abort, xcc_mask
-        LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->error_code, 0, 4, h->staging.xfer));
+        clear_reported_error(lane, h->staging.xfer);
         h->staging.pending_uploads = true;
     }
     std::vector<Lane*> lanes;
@@ -866,6 +891,20 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
     return q;
 }
 
+// The reference's error text for a device guard code (runtime.rs:1297, :1352,
+// :1373, :1483, :1515, :1556).
+std::string guard_message(uint32_t code, uint32_t bias_index) {
+    switch (code) {
+        case kErrBias: return "output bias " + std::to_string(bias_index) + " became non-finite";
+        case kErrContextProjection: return "non-finite context output update rejected";
+        case kErrContextEmbedding: return "non-finite context embedding update rejected";
+        case kErrRecurrent: return "non-finite recurrent update rejected";
+        case kErrInput: return "non-finite input update rejected";
+        case kErrInhibitory: return "non-finite inhibitory update rejected";
+        default: return "non-finite output update rejected";
+    }
+}
+
 // Completes a queued launch once the transfer stream has drained past it:
 // records, timing, telemetry, and the device's error and tick checks.
 void complete_launch(LeoHipRuntime* h, QueuedLaunch& q) {
@@ -892,11 +931,20 @@ void complete_launch(LeoHipRuntime* h, QueuedLaunch& q) {
     }
     for (uint32_t i = 0; i < count; ++i) {
         if (ctl[i].error_code != 0) {
-            uint32_t code = ctl[i].error_code;
+            const uint32_t code = ctl[i].error_code;
+            LaneRun& run = q.runs[i];
+            run.lane->error_seen = true;
             if (code == kErrBarrier) throw Error(LEO_ERR_DEVICE, "device lane barrier timed out");
             if (code == kErrCapacity)
                 throw Error(LEO_ERR_UNSUPPORTED, "global selection exceeds the device sort capacity");
-            throw Error(LEO_ERR_NUMERICAL, "device numerical guard tripped (code " + std::to_string(code) + ")");
+            // a numerical guard stopped the lane after the learning phase of
+            // step error_step (runtime.rs: the step returns its error there):
+            // the steps before it ran to the end, and the kernel left the tick
+            // after the stopped step
+            run.completed = std::min<size_t>(ctl[i].error_step, run.steps.size());
+            run.lane->tick = ctl[i].tick;
+            throw Error(LEO_ERR_NUMERICAL, guard_message(code, ctl[i].bias_fail) + " (device guard " +
+                                               std::to_string(code) + ")");
         }
         if (ctl[i].tick != q.end_tick[i]) throw Error(LEO_ERR_INTERNAL, "device lane tick diverged from the host mirror");
     }
@@ -978,9 +1026,19 @@ void run_lanes(LeoHipRuntime* h, std::vector<LaneRun>& runs) {
                                                                          runs[i].steps.begin() + end), {}});
             index.push_back(i);
         }
-        run_lanes_once(h, part);
-        for (size_t k = 0; k < part.size(); ++k)
-            std::copy(part[k].records.begin(), part[k].records.end(), runs[index[k]].records.begin() + at);
+        auto keep = [&] {
+            for (size_t k = 0; k < part.size(); ++k) {
+                std::copy(part[k].records.begin(), part[k].records.end(), runs[index[k]].records.begin() + at);
+                if (part[k].completed != kAllSteps) runs[index[k]].completed = at + part[k].completed;
+            }
+        };
+        try {
+            run_lanes_once(h, part);
+        } catch (...) {
+            keep();
+            throw;
+        }
+        keep();
         at += step;
         chunk = next_chunk(h, step);
     }
@@ -1040,6 +1098,19 @@ void absorb_canonical(LeoHipRuntime* h, const LaneRun& r, std::vector<LeoStepMet
     }
 }
 
+// After a numerical guard stopped the canonical lane: the steps before the
+// stopped one count as the reference counts them (the stopped step's error
+// returns before its revision, homeostasis and statistics), and the
+// plasticity phase is the one the stopped step started from.
+void absorb_stopped(LeoHipRuntime* h, LaneRun& r, std::vector<LeoStepMetrics>& out) {
+    if (r.completed == kAllSteps) return;
+    const size_t n = std::min(r.completed, r.records.size());
+    if (r.completed < r.phase.size()) r.lane->plasticity_phase = r.phase[r.completed];
+    r.steps.resize(n);
+    r.records.resize(n);
+    absorb_canonical(h, r, out);
+}
+
 // Execute steps on the canonical runtime; stats and revision update the
 // canonical mirrors exactly as Runtime::step does.
 // `outputs[i]` asks for the readout of step i even when it does not learn.
@@ -1049,13 +1120,20 @@ std::vector<LeoStepMetrics> canonical_steps(LeoHipRuntime* h, const std::vector<
     LaneRun run{&lane, {}, {}};
     run.steps.reserve(steps.size());
     uint32_t tick = lane.tick;
-    for (size_t i = 0; i < steps.size(); ++i)
+    for (size_t i = 0; i < steps.size(); ++i) {
+        run.phase.push_back(lane.plasticity_phase);
         run.steps.push_back(
             make_step(h->cfg, lane, steps[i].symbol, steps[i].target, permissions[i], tick++, outputs[i]));
+    }
     std::vector<LaneRun> runs;
     runs.push_back(std::move(run));
-    run_lanes(h, runs);
     std::vector<LeoStepMetrics> out;
+    try {
+        run_lanes(h, runs);
+    } catch (...) {
+        absorb_stopped(h, runs[0], out);
+        throw;
+    }
     out.reserve(steps.size());
     absorb_canonical(h, runs[0], out);
     return out;
@@ -1139,9 +1217,11 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
             LaneRun run{&lane, {}, {}};
             run.steps.reserve(n);
             uint32_t tick = lane.tick;
-            for (size_t i = at; i < at + n; ++i)
+            for (size_t i = at; i < at + n; ++i) {
+                run.phase.push_back(lane.plasticity_phase);
                 run.steps.push_back(make_step(h->cfg, lane, seg.steps[i].symbol, seg.steps[i].target,
                                               seg.permissions[i], tick++, false));
+            }
             std::vector<LaneRun> runs;
             runs.push_back(std::move(run));
             const size_t e = 2 * queued.size();
@@ -1152,7 +1232,14 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
     LEO_HIP_CHECK(hipStreamSynchronize(h->staging.xfer));  // every queued kernel and download is complete
     try {
         for (QueuedLaunch& q : queued) {
-            complete_launch(h, q);
+            try {
+                complete_launch(h, q);
+            } catch (...) {
+                // the launches queued behind a stopped one found the sticky
+                // error word set and ran nothing
+                absorb_stopped(h, q.runs[0], out);
+                throw;
+            }
             if (const size_t n = q.runs[0].steps.size())
                 h->canonical_step_ms = std::max(h->canonical_step_ms, static_cast<double>(h->last_launch_ms) / n);
             absorb_canonical(h, q.runs[0], out);
@@ -2528,6 +2615,9 @@ int32_t leo_hip_commit_packed_host_model_no_alloc(LeoHipRuntime* h, const LeoPac
         leo::Staging staging;
         staging.fixed = leo::static_scratch(h->device);
         staging.capacity = leo::kStaticScratchBytes;
+        // apply_packed synchronises its stream before returning, so the
+        // device's copy is free again when the lock is released
+        std::lock_guard<std::mutex> lock(leo::g_scratch_user[h->device]);
         leo::apply_packed(h, *update, false, staging);
     });
 }

@@ -17,6 +17,7 @@ HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "liboracle.so"
 
 FROZEN, PROVISIONAL, TRAINING, VERIFIED = 0, 1, 2, 3
+ERR_INTERNAL, ERR_NUMERICAL, ERR_ARGUMENT = 1, 2, 3  # ORACLE_ERR_* (leo_oracle.h)
 F_NAMES = ["membrane", "activation", "fatigue", "branches", "adapt0", "adapt1", "adapt2", "surrogate",
            "rec_bs", "rec_ms", "rec_fs", "rec_as0", "rec_as1", "rec_as2", "rec_e",
            "in_bs", "in_ms", "in_fs", "in_as0", "in_as1", "in_as2", "in_e",

@@ -1082,7 +1082,7 @@ struct Runtime {
         for (size_t o = 0; o < OUTPUT_CLASSES; ++o) {
             float raw = -olr * ss * errors[o];
             model.bias[o] += bounded_delta(raw, mu);
-            if (!std::isfinite(model.bias[o])) numerical("output bias became non-finite");
+            if (!std::isfinite(model.bias[o])) numerical("output bias " + std::to_string(o) + " became non-finite");
         }
         if (context_applied) update_context_projection(ss);
         LearnMetrics lm;
