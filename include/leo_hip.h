@@ -422,6 +422,14 @@ int32_t leo_hip_parameter_changes(LeoHipRuntime* runtime, int32_t which, uint64_
 int32_t leo_hip_probabilities(LeoHipRuntime* runtime, float* out257);
 int32_t leo_hip_read_list(LeoHipRuntime* runtime, int32_t which, uint64_t* out,
                           uint64_t capacity, uint64_t* count);
+/* RuntimeBackend::active_neurons + activation (backend.rs:388-390, which the
+ * GPU adapter serves from its host mirror, cuda.rs:3086-3092, refreshed with
+ * the device's active list and values after each step, cuda.rs:5213-5229):
+ * the last step's active neurons in selection order with their activations
+ * (every other neuron's activation is 0). Returns the count in *count; writes
+ * up to `capacity` entries of each array that is non-null. */
+int32_t leo_hip_read_active(LeoHipRuntime* runtime, uint64_t* neurons, float* activations,
+                            uint64_t capacity, uint64_t* count);
 /* Transient state of the canonical runtime for parity checks; `count` must
  * equal the state's element count. */
 int32_t leo_hip_read_state(LeoHipRuntime* runtime, int32_t which, float* out, uint64_t count);

@@ -2713,6 +2713,32 @@ int32_t leo_hip_read_list(LeoHipRuntime* h, int32_t which, uint64_t* out, uint64
     });
 }
 
+int32_t leo_hip_read_active(LeoHipRuntime* h, uint64_t* neurons, float* activations, uint64_t capacity,
+                            uint64_t* count) {
+    return guarded([&] {
+        leo::BusyGuard g(h);
+        const leo::LaneDesc& d = h->canonical->desc;
+        leo::LaneControl ctl{};
+        leo::download(&ctl, d.ctl, sizeof(ctl), h->stream);
+        leo::sync(h->stream);
+        // the ring entry of the last tick (a reset empties the ring)
+        const uint32_t last = ctl.tick - 1, rs = last % leo::kRing;
+        const uint32_t n = (ctl.tick > 0 && ctl.ring_tick[rs] == last) ? ctl.ring_count[rs] : 0;
+        std::vector<uint32_t> ids(n);
+        std::vector<float> values(n);
+        const uint64_t at = static_cast<uint64_t>(rs) * h->z.cap;
+        leo::download(ids.data(), d.ring_active + at, n * 4, h->stream);
+        leo::download(values.data(), d.ring_act + at, n * 4, h->stream);
+        leo::sync(h->stream);
+        if (count) *count = n;
+        const uint64_t k = std::min<uint64_t>(capacity, n);
+        for (uint64_t i = 0; i < k; ++i) {
+            if (neurons) neurons[i] = ids[i];
+            if (activations) activations[i] = values[i];
+        }
+    });
+}
+
 int32_t leo_hip_read_state(LeoHipRuntime* h, int32_t which, float* out, uint64_t count) {
     return guarded([&] {
         leo::BusyGuard g(h);

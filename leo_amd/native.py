@@ -197,6 +197,7 @@ SIGNATURES = {
     "leo_hip_parameter_changes": (_I32, [_P, _I32, _P, _U64, _P, _P, _P]),
     "leo_hip_probabilities": (_I32, [_P, _P]),
     "leo_hip_read_list": (_I32, [_P, _I32, _P, _U64, _P]),
+    "leo_hip_read_active": (_I32, [_P, _P, _P, _U64, _P]),
     "leo_hip_read_state": (_I32, [_P, _I32, _P, _U64]),
     "leo_hip_current_tick": (_U64, [_P]),
     "leo_hip_kernel_stats": (_I32, [_P, _P, _I32]),

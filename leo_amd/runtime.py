@@ -158,6 +158,14 @@ class HipRuntime:
         native.check(self._lib, self._lib.leo_hip_create(ctypes.byref(self._hc), ctypes.byref(view), device,
                                                           max_lanes, ctypes.byref(self._handle)))
         self._template = model
+        self.device = device
+
+    def fork(self, model: Model) -> "HipRuntime":
+        """RuntimeBackend::fork (backend.rs:623-633 -> cuda.rs:2347-2356): a
+        runtime for `model` on this runtime's device, with the whole model
+        uploaded and its transient state reset (one story lane: a fork trains
+        one worker story)."""
+        return HipRuntime(model, device=self.device, max_lanes=1)
 
     def close(self) -> None:
         if self._handle:
@@ -324,8 +332,26 @@ class HipRuntime:
         self._call("leo_hip_read_list", which, buf.ctypes.data, buf.size, ctypes.byref(count))
         return buf[: int(count.value)].astype(np.int64)
 
+    def _read_active(self) -> Tuple[np.ndarray, np.ndarray]:
+        count = ctypes.c_uint64()
+        self._call("leo_hip_read_active", None, None, 0, ctypes.byref(count))
+        n = int(count.value)
+        ids = np.zeros(max(n, 1), dtype=np.uint64)
+        values = np.zeros(max(n, 1), dtype=np.float32)
+        self._call("leo_hip_read_active", ids.ctypes.data, values.ctypes.data, ids.size, ctypes.byref(count))
+        return ids[:n].astype(np.int64), values[:n]
+
     def active_neurons(self) -> np.ndarray:
-        return self.read_list(native.LIST_ACTIVE)
+        """RuntimeBackend::active_neurons (backend.rs:389): the last step's
+        active neurons in selection order."""
+        return self._read_active()[0]
+
+    def activation(self, neuron: int) -> float:
+        """RuntimeBackend::activation (backend.rs:390): the neuron's activation
+        after the last step (0 unless it is active)."""
+        ids, values = self._read_active()
+        hit = np.nonzero(ids == neuron)[0]
+        return float(values[hit[0]]) if hit.size else 0.0
 
     def read_state(self, name: str) -> np.ndarray:
         n = self.config.model.neuron_count

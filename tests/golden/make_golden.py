@@ -4,6 +4,7 @@ stories:
 
     python tests/golden/make_golden.py          # workloadA_batches.npz / .json
     python tests/golden/make_golden.py --long   # workloadA_1M.json
+    python tests/golden/make_golden.py --long-b # workloadB_1M.json (~35 minutes of oracle time)
 
 workloadA_batches holds two logical batches: the inputs (story bytes,
 offsets), every per-step loss, the replay schedule counts, the full threshold
@@ -18,9 +19,15 @@ how many slots of each context order are taken. Context orders 4 to 6
 (4,096 slots each) are full by the second checkpoint, so from there on every
 allocation at those orders evicts the weakest slot of its probe window.
 
+workloadB_1M holds workload B (16,384 units, 8 story lanes per logical
+batch, 30% replay) trained batch by batch until more than 2^20 bytes are
+trained: the same checkpoint records (after 2^14, 2^17, 2^19 and 2^20 bytes)
+plus that batch's merge and replay report. Every batch runs the lane-ordered
+batch-end mean and the keyed context merge.
+
 tests/test_golden.py checks that the oracle still reproduces them (CPU; the
-long run up to its first checkpoint) and that the HIP path matches them bit
-for bit (GPU).
+long runs up to their first checkpoint) and that the HIP path matches them
+bit for bit (GPU).
 """
 from __future__ import annotations
 
@@ -134,8 +141,74 @@ def main_long() -> None:
     print("wrote", HERE / "workloadA_1M.json")
 
 
+LONG_B_CHECKPOINTS = (1 << 14, 1 << 17, 1 << 19, 1 << 20)
+LONG_B_STORIES = 1600  # N(800,250)-byte stories: ~1,310 of them pass 2^20 bytes
+
+
+def long_run_batches(runtime, train_batch, stories, lanes, checkpoints=LONG_B_CHECKPOINTS, on_checkpoint=None):
+    """Trains logical batches of `lanes` consecutive stories (story lanes, the
+    lane-ordered batch-end mean and the keyed context merge, then replay:
+    training.rs:1585-1727) until the last checkpoint is passed. Returns the
+    checkpoint records, taken at the first batch boundary at or past each, with
+    that batch's merge and replay report."""
+    records, trained, pending = [], 0, list(checkpoints)
+    for start in range(0, len(stories) - lanes + 1, lanes):
+        report = train_batch(runtime, stories[start:start + lanes])
+        trained += sum(len(s) for s in stories[start:start + lanes])
+        if pending and trained >= pending[0]:
+            pending.pop(0)
+            model = runtime.model()
+            spo = model.config.context.slots_per_order
+            rec = model_record(model)
+            rec.update(stories=start + lanes, trained_bytes=trained, bits_per_byte=float(model.bits_per_byte()),
+                       context_slots_taken=[int((model.ctx_keys[o * spo:(o + 1) * spo] != 0).sum())
+                                            for o in range(model.config.context.max_order)],
+                       batch_report={"replay_segments": int(report.replay_segments),
+                                     "replay_steps": int(report.replay_steps),
+                                     "replay_prefix_steps": int(report.replay_prefix_steps),
+                                     "merge_fixed_parameter_updates": int(report.merge_fixed_parameter_updates),
+                                     "merge_context_keys": int(report.merge_context_keys),
+                                     "mean_loss": float(report.mean_loss)})
+            records.append(rec)
+            if on_checkpoint:
+                on_checkpoint(rec)
+            if not pending:
+                break
+    return records
+
+
+def long_b_stories():
+    w = WORKLOADS["B"]
+    data, offsets = synthetic_stories(w, LONG_B_STORIES)
+    return w, [data[int(offsets[i]):int(offsets[i + 1])].tobytes() for i in range(LONG_B_STORIES)]
+
+
+def main_long_b() -> None:
+    """workloadB_1M.json: workload B (16,384 units, 8 story lanes per logical
+    batch, 30% replay) past 2^20 trained bytes."""
+    from oracle import binding
+
+    w, stories = long_b_stories()
+    model = workload_model(w)
+    rt = binding.OracleRuntime(model)
+
+    def train(r, batch):
+        report, _ = r.train_story_batch(batch, binding.TRAINING, replay=True)
+        return report
+
+    records = long_run_batches(rt, train, stories, w.lanes,
+                               on_checkpoint=lambda rec: print("checkpoint", rec["trained_bytes"],
+                                                               rec["bits_per_byte"], flush=True))
+    out = {"workload": "B", "lanes": w.lanes, "checkpoints": list(LONG_B_CHECKPOINTS),
+           "initial": model_record(model), "records": records}
+    (HERE / "workloadB_1M.json").write_text(json.dumps(out, indent=1, sort_keys=True) + "\n")
+    print("wrote", HERE / "workloadB_1M.json")
+
+
 if __name__ == "__main__":
-    if "--long" in sys.argv[1:]:
+    if "--long-b" in sys.argv[1:]:
+        main_long_b()
+    elif "--long" in sys.argv[1:]:
         main_long()
     else:
         main()

@@ -162,3 +162,75 @@ def test_hip_path_matches_long_fixture(require_gpu):
     assert len(got) == len(record["records"])
     for g, want in zip(got, record["records"]):
         _check_long_record(g, want, f"hip at {want['trained_bytes']} bytes")
+
+
+# --- workload B past 2^20 trained bytes (tests/golden/make_golden.py --long-b) -----------
+# 8 story lanes per logical batch: the lane-ordered batch-end mean
+# (parallel.rs:694-798) and the keyed context merge (parallel.rs:1024-1113)
+# run every batch, then 30% replay on the merged model (training.rs:1585-1727).
+def _long_b_fixture():
+    return json.loads((GOLDEN / "workloadB_1M.json").read_text())
+
+
+def _check_long_b_record(got, want, label):
+    _check_long_record(got, want, label)
+    assert got["batch_report"] == want["batch_report"], f"{label}: batch report"
+
+
+def test_long_b_fixture_passes_a_mebibyte():
+    record = _long_b_fixture()
+    assert record["lanes"] == 8 and record["records"][-1]["trained_bytes"] >= 1 << 20
+    # the mean merges changes of many lanes and keys every batch
+    assert all(r["batch_report"]["merge_context_keys"] > 0 for r in record["records"])
+
+
+def test_oracle_reproduces_long_b_fixture_first_checkpoint(oracle):
+    import sys
+
+    sys.path.insert(0, str(GOLDEN))
+    import make_golden
+
+    record = _long_b_fixture()
+    w, stories = make_golden.long_b_stories()
+    rt = oracle.OracleRuntime(workload_model(w))
+
+    def train(r, batch):
+        report, _ = r.train_story_batch(batch, oracle.TRAINING, replay=True)
+        return report
+
+    got = make_golden.long_run_batches(rt, train, stories, record["lanes"], checkpoints=record["checkpoints"][:1])
+    _check_long_b_record(got[0], record["records"][0], "oracle, first checkpoint")
+
+
+@pytest.mark.gpu
+def test_hip_path_matches_long_b_fixture(require_gpu):
+    import sys
+
+    from leo_amd.runtime import HipRuntime
+
+    sys.path.insert(0, str(GOLDEN))
+    import make_golden
+
+    record = _long_b_fixture()
+    w, stories = make_golden.long_b_stories()
+    say = lambda *a: print(*a, file=sys.__stderr__, flush=True)  # noqa: E731
+    done = [0]
+
+    def train(r, batch):
+        report, _ = r.train_batch(batch, native.TRAINING, replay=True)
+        done[0] += 1
+        if done[0] % 20 == 0:
+            say(f"golden B long run: {done[0]} batches trained")
+        return report
+
+    rt = HipRuntime(workload_model(w), device=0, max_lanes=record["lanes"])
+    try:
+        say("golden: workload B, 8 story lanes per batch with replay, past 2^20 trained bytes")
+        got = make_golden.long_run_batches(rt, train, stories, record["lanes"], checkpoints=record["checkpoints"],
+                                           on_checkpoint=lambda rec: say("checkpoint", rec["trained_bytes"],
+                                                                         rec["bits_per_byte"]))
+    finally:
+        rt.close()
+    assert len(got) == len(record["records"])
+    for g, want in zip(got, record["records"]):
+        _check_long_b_record(g, want, f"hip at {want['trained_bytes']} bytes")

@@ -237,14 +237,19 @@ def test_workload_e_shaped_batch_matches_oracle(require_gpu, oracle, model_e_red
     assert_models_equal(got, cpu.model(), "E-shaped reduced batch")
 
 
-def test_workload_e_full_size_batch_is_deterministic_and_valid(require_gpu):
+@pytest.fixture(scope="module")
+def model_e():
+    print("building the workload E model (4,194,304 units)", flush=True)
+    return drive_to_e_regime(workload_model(WORKLOADS["E"]))
+
+
+def test_workload_e_full_size_batch_is_deterministic_and_valid(require_gpu, model_e):
     """Workload E at full size (4,194,304 units, 2^27 recurrent synapses,
     heavy-tailed in-degree capped at 4096) driven into its regime: an 8-story
     batch cut to 48 bytes with replay (about 400 lane steps and 120 replay
     steps), run twice from the same model."""
     w = WORKLOADS["E"]
-    print("building the workload E model (4,194,304 units)", flush=True)
-    model = drive_to_e_regime(workload_model(w))
+    model = model_e
     data, offsets = synthetic_stories(w, 8)
     stories = [s[:48] for s in story_list(data, offsets)]
     trained = sum(map(len, stories))
@@ -275,6 +280,55 @@ def test_workload_e_full_size_batch_is_deterministic_and_valid(require_gpu):
     assert a.targets == trained + 8 and a.replay_steps > 0
     assert stats[0]["deep_radix_folds"] > 0
     assert a.active_neurons_sum > 0.02 * w.neurons * a.activity_steps
+    finals[0].validate()
+
+
+def test_workload_e_lane_groups_and_multi_launch_story(require_gpu, model_e, monkeypatch):
+    """E's batch shape at full size: more stories than resident lanes (two
+    lane groups of two, joined by the grouped batch-end mean) and a story of
+    160 bytes whose schedule is cut into launches of 32 steps (the reference
+    carries long stories across chunks, cuda.rs:8555-8581). The same batch
+    with all four lanes resident and the launches sized by the runtime must
+    give the identical model, replay schedule and counters; the model stays
+    valid."""
+    w = WORKLOADS["E"]
+    data, offsets = synthetic_stories(w, 4, 16)
+    stories = [s[:160] if i == 0 else s[:48] for i, s in enumerate(story_list(data, offsets))]
+    assert len(stories[0]) == 160
+    trained = sum(map(len, stories))
+    finals, reports, stats = [], [], []
+    for resident, launch_steps in ((2, 32), (4, None)):
+        monkeypatch.setenv("LEO_HIP_RESIDENT_LANES", str(resident))
+        if launch_steps:
+            monkeypatch.setenv("LEO_HIP_MAX_STEPS_PER_LAUNCH", str(launch_steps))
+        else:
+            monkeypatch.delenv("LEO_HIP_MAX_STEPS_PER_LAUNCH", raising=False)
+        print(f"workload E: 4 stories ({trained} bytes, the first 160) with replay, {resident} resident lanes, "
+              f"launches of {launch_steps or 'any'} steps", flush=True)
+        rt = _runtime(model_e, 4)
+        try:
+            assert rt.resident_lanes == resident
+            rt.kernel_stats(reset=True)
+            rep, losses = rt.train_batch(stories, native.TRAINING, replay=True)
+            stats.append(rt.kernel_stats())
+            finals.append(rt.model())
+            reports.append(rep)
+        finally:
+            rt.close()
+        print(f"  story {rep.story_seconds:.2f} s, replay {rep.replay_seconds:.2f} s, "
+              f"{stats[-1]['launches']} launches, {rep.replay_steps} replay steps", flush=True)
+        assert all(len(l) == len(s) + 1 and np.isfinite(l).all() for l, s in zip(losses, stories))
+    assert_models_equal(finals[0], finals[1], "two lane groups with cut launches vs one group")
+    for field in ("mean_loss", "targets", "replay_steps", "replay_prefix_steps", "merge_fixed_parameter_updates",
+                  "merge_context_keys", "active_neurons_sum", "emitted_events"):
+        assert getattr(reports[0], field) == getattr(reports[1], field), field
+    for key in ("lane_steps", "events", "touched", "active", "learning_slots", "deep_radix_folds"):
+        assert stats[0][key] == stats[1][key], key
+    # the long story spans several launches in both runs, cut differently
+    # (161 steps in launches of 32 take six; the runtime's own sizing differs)
+    assert stats[0]["launches"] >= 6 and stats[1]["launches"] >= 6
+    assert stats[0]["launches"] != stats[1]["launches"]
+    assert reports[0].targets == trained + 4 and reports[0].replay_steps > 0
     finals[0].validate()
 
 
