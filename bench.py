@@ -48,20 +48,43 @@ def _device_sync() -> None:
         raise RuntimeError("hipDeviceSynchronize failed")
 
 
-# Bounded CPU sample: at a million units the oracle trains ~25 bytes/s per
-# thread (with replay), so large workloads time the first stories of the batch
-# truncated to a prefix (about half a minute of CPU work).
-CPU_SAMPLE = {"D": (8, 128), "E": (8, 64)}
+# Bounded CPU sample: at a million units the oracle trains ~12 bytes/s per
+# thread (with replay), so large workloads time the first min(lanes, cores)
+# stories of the batch truncated to a prefix (about half a minute of CPU work).
+CPU_PREFIX = {"D": 128, "E": 64}
+# host threads a GPU box grants one GPU's job, whatever the machine reports
+HOST_SHARE = 16
+
+
+def host_cpu():
+    """(cores this process may use, capped at the box's per-GPU share; nproc; CPU model)."""
+    nproc = os.cpu_count() or 1
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = nproc
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return min(usable, HOST_SHARE), nproc, model
 
 
 def cpu_baseline(workload, model, data, offsets, replay: bool):
-    """Time the CPU oracle on one batch of the same workload (bounded sample)."""
+    """Time the CPU oracle on one batch of the same workload (bounded sample):
+    one thread per story as training.rs:1669-1683 runs them, min(lanes, cores)
+    stories."""
     from oracle import binding
 
+    cores, nproc, cpu_model = host_cpu()
     stories = [data[int(offsets[i]):int(offsets[i + 1])].tobytes() for i in range(len(offsets) - 1)]
     sample = "1 batch"
-    if workload.name in CPU_SAMPLE:
-        count, prefix = CPU_SAMPLE[workload.name]
+    if workload.name in CPU_PREFIX:
+        count, prefix = min(len(stories), cores), CPU_PREFIX[workload.name]
         stories = [s[:prefix] for s in stories[:count]]
         sample = f"the batch's first {count} stories truncated to {prefix} bytes"
     rt = binding.OracleRuntime(model)
@@ -72,7 +95,9 @@ def cpu_baseline(workload, model, data, offsets, replay: bool):
     return {
         "value": nbytes / seconds,
         "unit": "bytes/s",
-        "cores": min(len(stories), os.cpu_count() or 1),
+        "cores": min(len(stories), cores),
+        "nproc": nproc,
+        "cpu_model": cpu_model,
         "kind": "port",
         "sample": f"{sample} of workload {workload.name}: {len(stories)} stories, {nbytes} bytes, "
                   f"replay {'on' if replay else 'off'}, {seconds:.1f} s",
@@ -207,12 +232,15 @@ def main() -> int:
     runtime.kernel_stats(reset=True)
     trained = 0
     replay_steps = prefix_steps = 0
+    wall = {"story": 0.0, "merge": 0.0, "replay": 0.0}  # host wall clock of each part, summed over the batches
     t0 = time.perf_counter()
     for b in range(args.warmup, total_batches):
         rep = runtime.train_batch_packed(*batches[b], native.TRAINING, replay=replay)
         trained += int(batches[b][1][-1])
         replay_steps += rep.replay_steps
         prefix_steps += rep.replay_prefix_steps
+        for k in wall:
+            wall[k] += getattr(rep, k + "_seconds")
     _device_sync()
     elapsed = time.perf_counter() - t0
     ks = runtime.kernel_stats()
@@ -254,6 +282,7 @@ def main() -> int:
             "trained_bytes": trained,
             "replay_steps": replay_steps,
             "replay_prefix_steps": prefix_steps,
+            "wall_ms_per_step": {k: v * 1e3 / args.steps for k, v in wall.items()},
             "bits_per_byte": bpb,
         },
         "roofline": {

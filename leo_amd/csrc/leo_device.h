@@ -486,6 +486,23 @@ struct MergeCandidates {
     unsigned long long LEO_GLOBAL* count;
 };
 
+// Changed context slots of story lanes for the batch-end keyed merge: each
+// slot set in a lane's change bitmap as one packed record (slot, key low and
+// high word, observations, E embedding words) in the lane's region of `out`
+// (`stride` words), appended at the lane's counter.
+struct ContextChanges {
+    const uint32_t* const* bits;     // per lane: changed-slot bitmap (ch_ctx)
+    const uint64_t* const* keys;     // per lane: ctx_keys
+    const uint32_t* const* obs;      // per lane: ctx_obs
+    const float* const* emb;         // per lane: ctx_emb
+    uint64_t slots;
+    uint64_t words;                  // bitmap words per lane
+    uint64_t stride;                 // words of `out` per lane
+    uint32_t E;
+    uint32_t LEO_GLOBAL* out;
+    unsigned long long LEO_GLOBAL* counts;  // per lane
+};
+
 // Sparse moves between a canonical tensor and a packed buffer: element
 // index[k] (row index[k], `row` elements from index*stride, when row > 0)
 // of `tensor` to or from packed[k] (packed[k*row .. k*row+row)).

@@ -3218,6 +3218,51 @@ __global__ void __launch_bounds__(kThreads) leo_merge_candidates(MergeCandidates
     }
 }
 
+// One lane per blockIdx.y: the lane's changed context slots (one bitmap word
+// per thread) packed into its region, appended with one atomic per wave (the
+// host orders the records by key).
+__global__ void __launch_bounds__(kThreads) leo_context_changes(ContextChanges g) {
+    const uint32_t l = blockIdx.y;
+    const uint32_t rec_words = 4 + g.E;
+    const uint32_t* bits = g.bits[l];
+    const uint64_t* keys = g.keys[l];
+    const uint32_t* obs = g.obs[l];
+    const float* emb = g.emb[l];
+    uint32_t LEO_GLOBAL* out = g.out + static_cast<uint64_t>(l) * g.stride;
+    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * kThreads; base < g.words;
+         base += static_cast<uint64_t>(gridDim.x) * kThreads) {
+        const uint64_t w = base + threadIdx.x;
+        uint32_t word = 0;
+        if (w < g.words) {
+            word = bits[w];
+            const uint64_t tail = g.slots - w * 32;  // slots in this word
+            if (tail < 32) word &= (1u << tail) - 1u;
+        }
+        const uint32_t n = static_cast<uint32_t>(__popc(word));
+        const uint32_t incl = wave_incl_scan_u32(n);
+        const uint32_t total = __builtin_amdgcn_readlane(incl, kWaveSize - 1);
+        unsigned long long at = 0;
+        if (__lane_id() == kWaveSize - 1 && total) at = atomicAdd(&g.counts[l], static_cast<unsigned long long>(total));
+        at = static_cast<unsigned long long>(__builtin_amdgcn_readlane(static_cast<uint32_t>(at), kWaveSize - 1)) |
+             (static_cast<unsigned long long>(__builtin_amdgcn_readlane(static_cast<uint32_t>(at >> 32), kWaveSize - 1))
+              << 32);
+        at += incl - n;
+        while (word) {
+            const uint32_t bit = __ffs(word) - 1;
+            word &= word - 1;
+            const uint64_t slot = w * 32 + bit;
+            uint32_t LEO_GLOBAL* rec = out + at * rec_words;
+            const uint64_t key = keys[slot];
+            rec[0] = static_cast<uint32_t>(slot);
+            rec[1] = static_cast<uint32_t>(key);
+            rec[2] = static_cast<uint32_t>(key >> 32);
+            rec[3] = obs[slot];
+            for (uint32_t e = 0; e < g.E; ++e) rec[4 + e] = __float_as_uint(emb[slot * g.E + e]);
+            at += 1;
+        }
+    }
+}
+
 __global__ void __launch_bounds__(kThreads) leo_merge_fixed(MergeArgs m) {
     unsigned long long local = 0, changes = 0;
     // visited elements: all of them, or the listed positions' elements

@@ -38,6 +38,7 @@ __global__ void leo_reset_lanes(KernelArgs args, uint32_t set_tick, uint32_t new
 
 __global__ void leo_merge_fixed(MergeArgs m);
 __global__ void leo_merge_candidates(MergeCandidates mc);
+__global__ void leo_context_changes(ContextChanges g);
 __global__ void leo_sparse_move(SparseMove mv);
 __global__ void leo_fold_changes(FoldArgs f);
 
@@ -89,8 +90,12 @@ struct PinnedStaging {
     char* base = nullptr;
     size_t capacity = 0, used = 0;
     hipStream_t xfer = nullptr;
+    // when set, copies go to this stream (the step stream) instead of the
+    // transfer stream: its work is ordered already and no event joins the two
+    hipStream_t route = nullptr;
     hipEvent_t uploaded = nullptr, computed = nullptr;
     bool pending_uploads = false;
+    hipStream_t active() const { return route ? route : xfer; }
     PinnedStaging() = default;
     PinnedStaging(const PinnedStaging&) = delete;
     PinnedStaging& operator=(const PinnedStaging&) = delete;
@@ -129,29 +134,35 @@ struct PinnedStaging {
         if (!bytes) return;
         char* p = take(bytes);
         std::memcpy(p, src, bytes);
-        LEO_HIP_CHECK(hipMemcpyAsync(dst, p, bytes, hipMemcpyHostToDevice, xfer));
-        pending_uploads = true;
+        LEO_HIP_CHECK(hipMemcpyAsync(dst, p, bytes, hipMemcpyHostToDevice, active()));
+        pending_uploads = route == nullptr;
     }
     // the stream `s` waits for every upload issued so far
     void publish(hipStream_t s) {
-        if (!pending_uploads) return;
+        if (!pending_uploads || route == s) return;
         LEO_HIP_CHECK(hipEventRecord(uploaded, xfer));
         LEO_HIP_CHECK(hipStreamWaitEvent(s, uploaded, 0));
         pending_uploads = false;
     }
     // later transfers start after the work queued on `s` so far
     void follow(hipStream_t s) {
+        if (route == s) return;
         LEO_HIP_CHECK(hipEventRecord(computed, s));
         LEO_HIP_CHECK(hipStreamWaitEvent(xfer, computed, 0));
     }
     // a download into staging space; valid after drain()
     const char* d2h(const void* src, size_t bytes) {
         char* p = take(bytes);
-        if (bytes) LEO_HIP_CHECK(hipMemcpyAsync(p, src, bytes, hipMemcpyDeviceToHost, xfer));
+        if (bytes) LEO_HIP_CHECK(hipMemcpyAsync(p, src, bytes, hipMemcpyDeviceToHost, active()));
         return p;
     }
-    void drain() {
+    // every copy issued so far is complete
+    void wait() {
         if (xfer) LEO_HIP_CHECK(hipStreamSynchronize(xfer));
+        if (route) LEO_HIP_CHECK(hipStreamSynchronize(route));
+    }
+    void drain() {
+        wait();
         used = 0;
     }
 };
@@ -257,6 +268,7 @@ struct LeoHipRuntime {
     float last_launch_ms = 0.0f;  // duration of the latest lane-steps launch (HIP events)
     double canonical_step_ms = 0.0;  // slowest per-step average of a timed canonical replay launch
     leo::Arena merge_scratch;  // lane pointer table + counters
+    leo::Arena ctx_scratch;    // the story lanes' changed context slots (download_lane_contexts)
     // Host-stale marks of the canonical image: elements changed since the
     // caller's host mirror was last synchronised that the change bitmaps no
     // longer hold (tracking restarts fold them in here; the batch-end mean and
@@ -852,8 +864,8 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
         // the host has reported its code (a launch queued behind a failed
         // one finds it set and runs nothing)
         static_assert(offsetof(LaneControl, xcc_mask) == offsetof(LaneControl, barrier) + 8, "cleared together");
-        LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->barrier, 0, 12, h->staging.xfer));  // barrier, abort, xcc_mask
-        clear_reported_error(lane, h->staging.xfer);
+        LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->barrier, 0, 12, h->staging.active()));  // barrier, abort, xcc_mask
+        clear_reported_error(lane, h->staging.active());
         h->staging.pending_uploads = true;
     }
     std::vector<Lane*> lanes;
@@ -1483,29 +1495,91 @@ std::vector<uint64_t> bits_to_indices(const std::vector<uint32_t>& bits, uint64_
     return out;
 }
 
-// Context tables and changed-slot bits of story lanes, queued for download on
-// the runtime stream (valid after the next synchronisation).
-void download_lane_contexts(LeoHipRuntime* h, const std::vector<Lane*>& lanes, std::vector<HostContext>& lane_ctx,
-                            std::vector<std::vector<uint32_t>>& lane_bits) {
-    for (Lane* l : lanes) {
-        lane_ctx.push_back(download_context(h, l->desc.p));
-        lane_bits.push_back(download_bits(h, l->desc.ch_ctx, h->z.slots));
+// A story lane's changed context slots (the slots of its change bitmap):
+// slot, key, observations and embedding row of each, in no particular order.
+struct LaneContext {
+    std::vector<uint32_t> slot;
+    std::vector<uint64_t> key;
+    std::vector<uint32_t> obs;
+    std::vector<float> emb;
+};
+
+// The changed context slots of story lanes, gathered on the device
+// (leo_context_changes) and downloaded: one record per changed slot instead
+// of every lane's whole tables.
+void download_lane_contexts(LeoHipRuntime* h, const std::vector<Lane*>& lanes, std::vector<LaneContext>& lane_ctx) {
+    const Sizes& z = h->z;
+    const uint32_t L = static_cast<uint32_t>(lanes.size());
+    if (L == 0) return;
+    const uint64_t rec_words = 4 + z.e, stride = z.slots * rec_words;
+    const size_t tables = 4 * static_cast<size_t>(L) * sizeof(void*);
+    const size_t counts_at = (tables + 255) & ~size_t(255);
+    const size_t out_at = (counts_at + L * 8 + 255) & ~size_t(255);
+    const size_t need = out_at + static_cast<size_t>(L) * stride * 4;
+    if (h->ctx_scratch.bytes < need) h->ctx_scratch.allocate(need);
+    std::vector<const void*> ptrs(4 * L);
+    for (uint32_t l = 0; l < L; ++l) {
+        const LaneDesc& d = lanes[l]->desc;
+        ptrs[0 * L + l] = d.ch_ctx;
+        ptrs[1 * L + l] = d.p.ctx_keys;
+        ptrs[2 * L + l] = d.p.ctx_obs;
+        ptrs[3 * L + l] = d.p.ctx_emb;
+    }
+    char* base = h->ctx_scratch.base;
+    upload(base, ptrs.data(), tables, h->stream);
+    auto* counts = reinterpret_cast<unsigned long long*>(base + counts_at);
+    LEO_HIP_CHECK(hipMemsetAsync(counts, 0, L * 8, h->stream));
+    ContextChanges g{};
+    g.bits = reinterpret_cast<const uint32_t* const*>(base);
+    g.keys = reinterpret_cast<const uint64_t* const*>(base + 1 * L * sizeof(void*));
+    g.obs = reinterpret_cast<const uint32_t* const*>(base + 2 * L * sizeof(void*));
+    g.emb = reinterpret_cast<const float* const*>(base + 3 * L * sizeof(void*));
+    g.slots = z.slots;
+    g.words = z.words(z.slots);
+    g.stride = stride;
+    g.E = static_cast<uint32_t>(z.e);
+    g.out = reinterpret_cast<uint32_t*>(base + out_at);
+    g.counts = counts;
+    const uint64_t blocks = std::min<uint64_t>((g.words + kThreads - 1) / kThreads, 64);
+    hipLaunchKernelGGL(leo_context_changes, dim3(static_cast<uint32_t>(std::max<uint64_t>(blocks, 1)), L),
+                       dim3(kThreads), 0, h->stream, g);
+    LEO_HIP_CHECK(hipGetLastError());
+    std::vector<unsigned long long> n(L);
+    download(n.data(), counts, L * 8, h->stream);
+    sync(h->stream);
+    std::vector<uint32_t> packed;
+    for (uint32_t l = 0; l < L; ++l) {
+        if (n[l] > z.slots) throw Error(LEO_ERR_INTERNAL, "more changed context slots than slots");
+        packed.resize(n[l] * rec_words);
+        if (n[l]) download(packed.data(), g.out + l * stride, packed.size() * 4, h->stream);
+        sync(h->stream);
+        LaneContext c;
+        c.slot.resize(n[l]);
+        c.key.resize(n[l]);
+        c.obs.resize(n[l]);
+        c.emb.resize(n[l] * z.e);
+        for (uint64_t k = 0; k < n[l]; ++k) {
+            const uint32_t* r = packed.data() + k * rec_words;
+            c.slot[k] = r[0];
+            c.key[k] = static_cast<uint64_t>(r[1]) | (static_cast<uint64_t>(r[2]) << 32);
+            c.obs[k] = r[3];
+            std::memcpy(c.emb.data() + k * z.e, r + 4, z.e * 4);
+        }
+        lane_ctx.push_back(std::move(c));
     }
 }
 
-size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<HostContext>& lane_ctx,
-                                const std::vector<std::vector<uint32_t>>& lane_bits);
+size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<LaneContext>& lane_ctx);
 
 size_t merge_context(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
-    std::vector<HostContext> lane_ctx;
-    std::vector<std::vector<uint32_t>> lane_bits;
-    download_lane_contexts(h, lanes, lane_ctx, lane_bits);
-    return merge_context_downloaded(h, lane_ctx, lane_bits);
+    std::vector<LaneContext> lane_ctx;
+    download_lane_contexts(h, lanes, lane_ctx);
+    return merge_context_downloaded(h, lane_ctx);
 }
 
-// Keyed context merge (parallel.rs:1169-1345) over every lane's downloaded tables.
-size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<HostContext>& lane_ctx,
-                                const std::vector<std::vector<uint32_t>>& lane_bits) {
+// Keyed context merge (parallel.rs:1024-1113, projection and validation
+// :1169-1345) over every lane's changed context slots.
+size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<LaneContext>& lane_ctx) {
     const Sizes& z = h->z;
     const size_t E = z.e;
     const uint64_t spo = h->cfg.device.context_slots_per_order;
@@ -1516,9 +1590,9 @@ size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<HostContext>
     // per-lane deltas against the pre-merge canonical (context_deltas_for_slots)
     std::vector<std::vector<ContextDelta>> deltas(lanes);
     for (size_t li = 0; li < lanes; ++li) {
-        const HostContext& t = lane_ctx[li];
-        for (uint64_t slot : bits_to_indices(lane_bits[li], z.slots)) {
-            uint64_t key = t.keys[slot];
+        const LaneContext& t = lane_ctx[li];
+        for (size_t k = 0; k < t.slot.size(); ++k) {
+            const uint64_t slot = t.slot[k], key = t.key[k];
             if (key == 0) continue;
             size_t order = static_cast<size_t>(slot / spo + 1);
             int64_t bslot = find_context_slot(master, h->cfg, order, key);
@@ -1527,10 +1601,10 @@ size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<HostContext>
             bool changed = false;
             for (size_t e = 0; e < E; ++e) {
                 float before = bslot >= 0 ? master.emb[static_cast<size_t>(bslot) * E + e] : 0.0f;
-                d.emb[e] = t.emb[slot * E + e] - before;
+                d.emb[e] = t.emb[k * E + e] - before;
                 changed |= d.emb[e] != 0.0f;
             }
-            d.obs_inc = t.obs[slot] > bobs ? t.obs[slot] - bobs : 0;
+            d.obs_inc = t.obs[k] > bobs ? t.obs[k] - bobs : 0;
             if (changed || d.obs_inc > 0) deltas[li].push_back(std::move(d));
         }
         std::sort(deltas[li].begin(), deltas[li].end(), [](const ContextDelta& a, const ContextDelta& b) {
@@ -1796,8 +1870,7 @@ void story_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets
     uint64_t targets = 0;
     size_t cursor = 0;
     double run_seconds = 0.0, merge_seconds = 0.0;
-    std::vector<HostContext> group_ctx;
-    std::vector<std::vector<uint32_t>> group_bits;
+    std::vector<LaneContext> group_ctx;
     std::vector<Lane*> lanes;
     for (uint32_t g = 0; g < groups; ++g) {
         auto t0 = std::chrono::steady_clock::now();
@@ -1859,7 +1932,7 @@ void story_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets
         }
         if (groups > 1) {
             merge_fixed(h, lanes, kMergeAccumulate, g == 0, count);
-            download_lane_contexts(h, lanes, group_ctx, group_bits);
+            download_lane_contexts(h, lanes, group_ctx);
             sync(h->stream);
             merge_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
         }
@@ -1872,7 +1945,7 @@ void story_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets
         ctx = merge_context(h, lanes);
     } else {
         fixed = merge_fixed(h, {}, kMergeFinalize, false, count);
-        ctx = merge_context_downloaded(h, group_ctx, group_bits);
+        ctx = merge_context_downloaded(h, group_ctx);
     }
     h->stats = merged;
     h->revision += revision_increment;
