@@ -237,6 +237,15 @@ struct LaneParams {
     float LEO_GLOBAL* ctx_out;          // 257 * E, output-major
 };
 
+// One tensor copied to several lanes (leo_broadcast): the source is read once.
+constexpr uint32_t kMaxBroadcast = 64;
+struct Broadcast {
+    const uint4 LEO_GLOBAL* src;
+    uint64_t vectors;                    // 16-byte vectors
+    uint32_t count;                      // destinations
+    uint4 LEO_GLOBAL* dst[kMaxBroadcast];
+};
+
 // Words of a neuron's state record.
 enum NeuronField : uint32_t {
     kNMembrane = 0,

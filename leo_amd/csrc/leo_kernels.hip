@@ -3042,6 +3042,18 @@ __global__ void __launch_bounds__(kThreads) leo_lane_steps_profiled(const Kernel
     lane_steps<true>(*args);
 }
 
+// A story group's fork of the canonical parameters (parallel.rs: each worker
+// starts from base.clone()): every 16-byte vector of one canonical tensor is
+// read once and stored to each lane's copy.
+__global__ void __launch_bounds__(kThreads) leo_broadcast(Broadcast b) {
+    const uint64_t t0 = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const uint64_t ts = static_cast<uint64_t>(gridDim.x) * kThreads;
+    for (uint64_t i = t0; i < b.vectors; i += ts) {
+        const uint4 v = b.src[i];
+        for (uint32_t l = 0; l < b.count; ++l) b.dst[l][i] = v;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // reset_transient_state (runtime.rs:365-425) for every lane in args.
 //
@@ -3050,8 +3062,13 @@ __global__ void __launch_bounds__(kThreads) leo_lane_steps_profiled(const Kernel
 // zero (1 = listed as eligible, 2 = dropped from the list with its values
 // kept). Every group of 16 slots with a nonzero mark has its 16 trace
 // records (512 contiguous bytes) rewritten; a clean slot keeps its last tick,
-// which only scales zeros, unless the tick is set (a new tick may lie below
-// it, so every record is rewritten).
+// also when the reset sets a new tick below it. Its values are zero, so its
+// next activation at tick t leaves (activation, 0, ..., 0, t) whatever the
+// old tick was: the elapsed ticks t - last wrap to a large count when last
+// > t, and the decays of a large count are finite (every decay lies in
+// [0, 1), config.rs:318-334), so they scale the zeros to zeros; with last == t
+// only the branch sensitivity is added to. Lane state starts zero-filled
+// (tick 0), so the first reset finds every slot clean.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void fill_u32(uint32_t LEO_GLOBAL* p, uint64_t n, uint32_t v, uint64_t t0, uint64_t ts) {
     // p is 256-byte aligned (lane-state layout)
@@ -3066,11 +3083,12 @@ __device__ __forceinline__ void fill_f32(float LEO_GLOBAL* p, uint64_t n, uint64
     fill_u32(reinterpret_cast<uint32_t LEO_GLOBAL*>(p), n, 0u, t0, ts);
 }
 
-__device__ __forceinline__ void clear_trace_group(const LaneDesc& d, uint64_t g, uint32_t tick, bool set_tick) {
+// Group g of 16 slots, whose marks `m` the caller has loaded (a launch of its
+// own: plain loads see the previous kernels' stores).
+__device__ __forceinline__ void clear_trace_group(const LaneDesc& d, uint64_t g, uint4 m, uint32_t tick) {
     uint4 LEO_GLOBAL* marks = reinterpret_cast<uint4 LEO_GLOBAL*>(d.rec_mark);
-    const uint4 m = marks[g];  // a launch of its own: plain loads see the previous kernels' stores
     const bool dirty = (m.x | m.y | m.z | m.w) != 0u;
-    if (!dirty && !set_tick) return;
+    if (!dirty) return;
     // 16 records of 32 bytes: zero sensitivities, last tick = tick
     uint4 LEO_GLOBAL* rec = reinterpret_cast<uint4 LEO_GLOBAL*>(d.rec_trace + 16 * g * kTraceWords);
     const uint4 zero = make_uint4(0u, 0u, 0u, 0u), with_tick = make_uint4(0u, 0u, 0u, tick);
@@ -3079,7 +3097,7 @@ __device__ __forceinline__ void clear_trace_group(const LaneDesc& d, uint64_t g,
         rec[2 * k] = zero;
         rec[2 * k + 1] = with_tick;
     }
-    if (dirty) marks[g] = zero;
+    marks[g] = zero;
 }
 
 __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uint32_t set_tick, uint32_t new_tick) {
@@ -3106,14 +3124,30 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
         for (uint64_t i = t0; i < 4 * N; i += ts) rec[i] = make_uint4(0u, 0u, (i & 3) == 2 ? tick : 0u, 0u);
     }
     const uint64_t groups = NS / 16;
-    for (uint64_t g = t0; g < groups; g += ts) clear_trace_group(d, g, tick, set_tick != 0);
+    {
+        // four groups' marks in flight per thread before any is cleared
+        const uint4 LEO_GLOBAL* marks = reinterpret_cast<const uint4 LEO_GLOBAL*>(d.rec_mark);
+        constexpr uint32_t kAhead = 4;
+        for (uint64_t g = t0; g < groups; g += kAhead * ts) {
+            uint4 m[kAhead];
+#pragma unroll
+            for (uint32_t k = 0; k < kAhead; ++k) {
+                const uint64_t gk = g + k * ts;
+                m[k] = make_uint4(0u, 0u, 0u, 0u);
+                if (gk < groups) m[k] = marks[gk];
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < kAhead; ++k)
+                if (g + k * ts < groups) clear_trace_group(d, g + k * ts, m[k], tick);
+        }
+    }
     auto clear_record = [&](float LEO_GLOBAL* trace, uint64_t i) {
         uint4 LEO_GLOBAL* rec = reinterpret_cast<uint4 LEO_GLOBAL*>(trace + i * kTraceWords);
         rec[0] = make_uint4(0u, 0u, 0u, 0u);
         rec[1] = make_uint4(0u, 0u, 0u, tick);
     };
     for (uint64_t i = 16 * groups + t0; i < NS; i += ts) {
-        if (d.rec_mark[i] != 0 || set_tick) {
+        if (d.rec_mark[i] != 0) {
             clear_record(d.rec_trace, i);
             d.rec_mark[i] = 0;
         }

@@ -39,6 +39,7 @@ __global__ void leo_reset_lanes(KernelArgs args, uint32_t set_tick, uint32_t new
 __global__ void leo_merge_fixed(MergeArgs m);
 __global__ void leo_merge_candidates(MergeCandidates mc);
 __global__ void leo_context_changes(ContextChanges g);
+__global__ void leo_broadcast(Broadcast b);
 __global__ void leo_sparse_move(SparseMove mv);
 __global__ void leo_fold_changes(FoldArgs f);
 
@@ -135,7 +136,7 @@ struct PinnedStaging {
         char* p = take(bytes);
         std::memcpy(p, src, bytes);
         LEO_HIP_CHECK(hipMemcpyAsync(dst, p, bytes, hipMemcpyHostToDevice, active()));
-        pending_uploads = route == nullptr;
+        if (!route) pending_uploads = true;
     }
     // the stream `s` waits for every upload issued so far
     void publish(hipStream_t s) {
@@ -165,6 +166,21 @@ struct PinnedStaging {
         wait();
         used = 0;
     }
+};
+
+// Routes the staging's copies onto `s` while in scope, after everything
+// already queued on the transfer stream (uploads and downloads alike). The
+// copies issued outside the scope keep their own event handoffs.
+struct StagingRoute {
+    PinnedStaging& staging;
+    StagingRoute(PinnedStaging& st, hipStream_t s) : staging(st) {
+        staging.pending_uploads = true;
+        staging.publish(s);
+        staging.route = s;
+    }
+    ~StagingRoute() { staging.route = nullptr; }
+    StagingRoute(const StagingRoute&) = delete;
+    StagingRoute& operator=(const StagingRoute&) = delete;
 };
 
 struct Layout {
@@ -232,13 +248,6 @@ struct Lane {
     // the host has reported this lane's device guard: its sticky error word
     // is cleared before the next work queued on the lane
     bool error_seen = false;
-};
-
-struct ContextDelta {
-    size_t order;
-    uint64_t key;
-    std::vector<float> emb;
-    uint32_t obs_inc;
 };
 
 }  // namespace
@@ -375,19 +384,49 @@ LaneParams allocate_params(Arena& arena, const Sizes& z, hipStream_t stream) {
     return p;
 }
 
-void copy_params(const LaneParams& dst, const LaneParams& src, const Sizes& z, hipStream_t s) {
-    auto cp = [&](void* d, const void* from, size_t bytes) {
-        LEO_HIP_CHECK(hipMemcpyAsync(d, from, bytes, hipMemcpyDeviceToDevice, s));
+// The canonical parameters into every lane of `lanes` (fork(base.clone())
+// for a story group): one leo_broadcast per tensor reads the canonical copy
+// once for up to kMaxBroadcast lanes; a tensor whose size or addresses are
+// not in 16-byte units is copied lane by lane.
+void broadcast_params(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
+    const Sizes& z = h->z;
+    struct Tensor {
+        void* (*field)(const LaneParams&);
+        size_t bytes;
     };
-    cp(dst.threshold, src.threshold, z.n * 4);
-    cp(dst.rec_weight, src.rec_weight, z.ns * 4);
-    cp(dst.in_weight, src.in_weight, z.ni * 4);
-    cp(dst.out_w, src.out_w, z.n * kOutStride * 4);
-    cp(dst.bias, src.bias, kOutStride * 4);
-    cp(dst.ctx_keys, src.ctx_keys, z.slots * 8);
-    cp(dst.ctx_emb, src.ctx_emb, z.slots * z.e * 4);
-    cp(dst.ctx_obs, src.ctx_obs, z.slots * 4);
-    cp(dst.ctx_out, src.ctx_out, kOutputs * z.e * 4);
+    const Tensor tensors[] = {
+        {[](const LaneParams& p) -> void* { return p.threshold; }, z.n * 4},
+        {[](const LaneParams& p) -> void* { return p.rec_weight; }, z.ns * 4},
+        {[](const LaneParams& p) -> void* { return p.in_weight; }, z.ni * 4},
+        {[](const LaneParams& p) -> void* { return p.out_w; }, z.n * kOutStride * 4},
+        {[](const LaneParams& p) -> void* { return p.bias; }, kOutStride * 4},
+        {[](const LaneParams& p) -> void* { return p.ctx_keys; }, z.slots * 8},
+        {[](const LaneParams& p) -> void* { return p.ctx_emb; }, z.slots * z.e * 4},
+        {[](const LaneParams& p) -> void* { return p.ctx_obs; }, z.slots * 4},
+        {[](const LaneParams& p) -> void* { return p.ctx_out; }, kOutputs * z.e * 4},
+    };
+    auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    for (const Tensor& t : tensors) {
+        if (t.bytes == 0) continue;
+        const void* src = t.field(h->canon);
+        bool vectors = t.bytes % 16 == 0 && aligned(src);
+        for (Lane* l : lanes) vectors = vectors && aligned(t.field(l->desc.p));
+        if (!vectors) {
+            for (Lane* l : lanes)
+                LEO_HIP_CHECK(hipMemcpyAsync(t.field(l->desc.p), src, t.bytes, hipMemcpyDeviceToDevice, h->stream));
+            continue;
+        }
+        for (size_t at = 0; at < lanes.size(); at += kMaxBroadcast) {
+            Broadcast b{};
+            b.src = static_cast<const uint4*>(src);
+            b.vectors = t.bytes / 16;
+            b.count = static_cast<uint32_t>(std::min<size_t>(kMaxBroadcast, lanes.size() - at));
+            for (uint32_t i = 0; i < b.count; ++i) b.dst[i] = static_cast<uint4*>(t.field(lanes[at + i]->desc.p));
+            const uint64_t grid = std::min<uint64_t>((b.vectors + kThreads - 1) / kThreads, 8 * static_cast<uint64_t>(h->cus));
+            hipLaunchKernelGGL(leo_broadcast, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, h->stream, b);
+            LEO_HIP_CHECK(hipGetLastError());
+        }
+    }
 }
 
 void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
@@ -866,7 +905,7 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
         static_assert(offsetof(LaneControl, xcc_mask) == offsetof(LaneControl, barrier) + 8, "cleared together");
         LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->barrier, 0, 12, h->staging.active()));  // barrier, abort, xcc_mask
         clear_reported_error(lane, h->staging.active());
-        h->staging.pending_uploads = true;
+        if (!h->staging.route) h->staging.pending_uploads = true;
     }
     std::vector<Lane*> lanes;
     for (auto& r : runs) lanes.push_back(r.lane);
@@ -1218,6 +1257,9 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
     }
     std::vector<QueuedLaunch> queued;
     queued.reserve(launches);
+    // one lane and one stream: resets, uploads, launches and downloads run in
+    // queue order on the step stream, with no event handoff between streams
+    StagingRoute on_step_stream(h->staging, h->stream);
     for (size_t k = 0; k < segments.size(); ++k) {
         const CanonicalSegment& seg = segments[k];
         if (seg.reset_before) {
@@ -1241,7 +1283,7 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
             at += n;
         }
     }
-    LEO_HIP_CHECK(hipStreamSynchronize(h->staging.xfer));  // every queued kernel and download is complete
+    h->staging.wait();  // every queued kernel and download is complete
     try {
         for (QueuedLaunch& q : queued) {
             try {
@@ -1578,7 +1620,11 @@ size_t merge_context(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
 }
 
 // Keyed context merge (parallel.rs:1024-1113, projection and validation
-// :1169-1345) over every lane's changed context slots.
+// :1169-1345) over every lane's changed context slots. Each (order, key)
+// gets one f64 sum per embedding column, accumulated lane by lane in lane
+// order (a key appears at most once in a lane's table), so the sums are those
+// of the reference's per-key walk over the workers; an open-addressing table
+// finds a key's sum in one probe run instead of a scan over every lane.
 size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<LaneContext>& lane_ctx) {
     const Sizes& z = h->z;
     const size_t E = z.e;
@@ -1587,63 +1633,60 @@ size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<LaneContext>
     sync(h->stream);
     const HostContext before = master;
     const size_t lanes = lane_ctx.size();
+    struct Merged {
+        size_t order;
+        uint64_t key;
+        uint64_t obs;
+        size_t sum_at;  // first of E f64 sums in `sums`
+    };
+    std::vector<Merged> merged;
+    std::vector<double> sums;
+    size_t changed_slots = 0;
+    for (const LaneContext& t : lane_ctx) changed_slots += t.slot.size();
+    size_t cap = 64;
+    while (cap < 2 * changed_slots) cap <<= 1;
+    std::vector<int64_t> table(cap, -1);
+    auto bucket_of = [&](size_t order, uint64_t key) {
+        uint64_t x = key ^ (static_cast<uint64_t>(order) * 0x9E3779B97F4A7C15ULL);
+        x ^= x >> 29;
+        x *= 0xBF58476D1CE4E5B9ULL;
+        x ^= x >> 32;
+        return static_cast<size_t>(x) & (cap - 1);
+    };
+    std::vector<float> delta(E);
     // per-lane deltas against the pre-merge canonical (context_deltas_for_slots)
-    std::vector<std::vector<ContextDelta>> deltas(lanes);
     for (size_t li = 0; li < lanes; ++li) {
         const LaneContext& t = lane_ctx[li];
         for (size_t k = 0; k < t.slot.size(); ++k) {
             const uint64_t slot = t.slot[k], key = t.key[k];
             if (key == 0) continue;
-            size_t order = static_cast<size_t>(slot / spo + 1);
-            int64_t bslot = find_context_slot(master, h->cfg, order, key);
-            uint32_t bobs = bslot >= 0 ? master.obs[static_cast<size_t>(bslot)] : 0;
-            ContextDelta d{order, key, std::vector<float>(E), 0};
+            const size_t order = static_cast<size_t>(slot / spo + 1);
+            const int64_t bslot = find_context_slot(master, h->cfg, order, key);
+            const uint32_t bobs = bslot >= 0 ? master.obs[static_cast<size_t>(bslot)] : 0;
             bool changed = false;
             for (size_t e = 0; e < E; ++e) {
-                float before = bslot >= 0 ? master.emb[static_cast<size_t>(bslot) * E + e] : 0.0f;
-                d.emb[e] = t.emb[k * E + e] - before;
-                changed |= d.emb[e] != 0.0f;
+                const float b = bslot >= 0 ? master.emb[static_cast<size_t>(bslot) * E + e] : 0.0f;
+                delta[e] = t.emb[k * E + e] - b;
+                changed |= delta[e] != 0.0f;
             }
-            d.obs_inc = t.obs[k] > bobs ? t.obs[k] - bobs : 0;
-            if (changed || d.obs_inc > 0) deltas[li].push_back(std::move(d));
+            const uint32_t obs_inc = t.obs[k] > bobs ? t.obs[k] - bobs : 0;
+            if (!changed && obs_inc == 0) continue;
+            size_t at = bucket_of(order, key);
+            while (table[at] >= 0 && (merged[static_cast<size_t>(table[at])].order != order ||
+                                      merged[static_cast<size_t>(table[at])].key != key))
+                at = (at + 1) & (cap - 1);
+            if (table[at] < 0) {
+                table[at] = static_cast<int64_t>(merged.size());
+                merged.push_back(Merged{order, key, 0, sums.size()});
+                sums.resize(sums.size() + E, 0.0);
+            }
+            Merged& m = merged[static_cast<size_t>(table[at])];
+            for (size_t e = 0; e < E; ++e) {
+                if (!std::isfinite(delta[e])) throw Error(LEO_ERR_INTERNAL, "invalid keyed context worker delta");
+                sums[m.sum_at + e] += static_cast<double>(delta[e]);
+            }
+            m.obs += obs_inc;
         }
-        std::sort(deltas[li].begin(), deltas[li].end(), [](const ContextDelta& a, const ContextDelta& b) {
-            return std::make_pair(a.order, a.key) < std::make_pair(b.order, b.key);
-        });
-    }
-    struct Merged {
-        size_t order;
-        uint64_t key;
-        std::vector<double> sum;
-        uint64_t obs;
-    };
-    std::vector<Merged> merged;
-    std::vector<size_t> pos(lanes, 0);
-    while (true) {
-        bool found = false;
-        std::pair<size_t, uint64_t> next{0, 0};
-        for (size_t li = 0; li < lanes; ++li)
-            if (pos[li] < deltas[li].size()) {
-                auto k = std::make_pair(deltas[li][pos[li]].order, deltas[li][pos[li]].key);
-                if (!found || k < next) {
-                    next = k;
-                    found = true;
-                }
-            }
-        if (!found) break;
-        Merged m{next.first, next.second, std::vector<double>(E, 0.0), 0};
-        for (size_t li = 0; li < lanes; ++li) {
-            if (pos[li] < deltas[li].size() && deltas[li][pos[li]].order == next.first && deltas[li][pos[li]].key == next.second) {
-                const ContextDelta& d = deltas[li][pos[li]];
-                for (size_t e = 0; e < E; ++e) {
-                    if (!std::isfinite(d.emb[e])) throw Error(LEO_ERR_INTERNAL, "invalid keyed context worker delta");
-                    m.sum[e] += static_cast<double>(d.emb[e]);
-                }
-                m.obs = m.obs + d.obs_inc;
-                pos[li] += 1;
-            }
-        }
-        merged.push_back(std::move(m));
     }
     std::sort(merged.begin(), merged.end(), [](const Merged& a, const Merged& b) {
         if (a.obs != b.obs) return a.obs > b.obs;
@@ -1653,23 +1696,24 @@ size_t merge_context_downloaded(LeoHipRuntime* h, const std::vector<LaneContext>
     for (const Merged& m : merged) {
         int64_t slot = resolve_context_slot(master, h->cfg, m.order, m.key, true, E);
         for (size_t e = 0; e < E; ++e)
-            master.emb[static_cast<size_t>(slot) * E + e] += static_cast<float>(m.sum[e] / divisor);
+            master.emb[static_cast<size_t>(slot) * E + e] += static_cast<float>(sums[m.sum_at + e] / divisor);
         uint32_t inc = static_cast<uint32_t>(std::min<uint64_t>(m.obs, UINT32_MAX));
         uint32_t& o = master.obs[static_cast<size_t>(slot)];
         o = (o > UINT32_MAX - inc) ? UINT32_MAX : o + inc;
     }
-    // projection + validation of the merged embeddings (parallel.rs:1226-1233, 1317-1333)
+    // projection + validation of the merged embeddings (parallel.rs:1226-1233,
+    // 1317-1333): the slot of every key a worker changed, each once (the
+    // clamp is idempotent, so a key changed by several workers is projected
+    // the same)
     const float wmin = h->cfg.device.weight_min, wmax = h->cfg.device.weight_max;
-    for (auto& lane_deltas : deltas) {
-        for (const ContextDelta& d : lane_deltas) {
-            int64_t slot = resolve_context_slot(master, h->cfg, d.order, d.key, false, E);
-            if (slot < 0) continue;
-            for (size_t e = 0; e < E; ++e) {
-                float& w = master.emb[static_cast<size_t>(slot) * E + e];
-                if (w < wmin) w = wmin;
-                if (w > wmax) w = wmax;
-                if (!std::isfinite(w)) throw Error(LEO_ERR_INTERNAL, "merged context embedding violates canonical parameter bounds");
-            }
+    for (const Merged& m : merged) {
+        int64_t slot = resolve_context_slot(master, h->cfg, m.order, m.key, false, E);
+        if (slot < 0) continue;
+        for (size_t e = 0; e < E; ++e) {
+            float& w = master.emb[static_cast<size_t>(slot) * E + e];
+            if (w < wmin) w = wmin;
+            if (w > wmax) w = wmax;
+            if (!std::isfinite(w)) throw Error(LEO_ERR_INTERNAL, "merged context embedding violates canonical parameter bounds");
         }
     }
     upload(h->canon.ctx_keys, master.keys.data(), z.slots * 8, h->stream);
@@ -1878,10 +1922,10 @@ void story_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets
         lanes.clear();
         for (uint32_t i = lo; i < hi; ++i) {
             Lane& l = story_lane(h, i - lo);
-            copy_params(l.desc.p, h->canon, h->z, h->stream);  // fork(base.clone())
-            clear_changes(l, h->z, h->stream);                  // enable_parameter_tracking
+            clear_changes(l, h->z, h->stream);  // enable_parameter_tracking
             lanes.push_back(&l);
         }
+        broadcast_params(h, lanes);  // fork(base.clone())
         reset_lane_objects(h, lanes, true, 0);  // Runtime::new (tick 0) + begin_document
         std::vector<LaneRun> runs;
         for (uint32_t i = lo; i < hi; ++i) {
