@@ -31,6 +31,7 @@ constexpr uint32_t kOutputs = 257;
 constexpr uint32_t kOutStride = 288;
 constexpr uint32_t kEndIndex = 256;
 constexpr uint32_t kRing = 9;             // delay ring: max delay 8 + 1 (runtime.rs:200-208)
+constexpr uint32_t kBucketSets = kRing;   // delivery bucket sets of a lane with one-barrier frozen runs
 constexpr uint32_t kMaxOrder = 16;        // config.rs:452-456
 constexpr uint32_t kThreads = 256;        // threads per workgroup
 constexpr uint32_t kMaxBlockNeurons = 1024;
@@ -110,6 +111,12 @@ enum : uint32_t {
     kStepLearn = 1u << 4,         // target present and strength > 0
     kStepOutput = 1u << 5,        // compute logits/probabilities
     kStepNeuralLoss = 1u << 6,    // also record the neural-only loss terms (runtime.rs:1119, 1151-1167)
+    // Delays whose events this step's tick may deliver when it emits them (a
+    // one-barrier frozen step): bit kStepEarlyShift + log2(delay) is set when
+    // the arrival step lies in the same launch and runs no learning trace
+    // (the delivery of a trace step activates the delivering slots' traces).
+    kStepEarlyShift = 8,
+    kStepEarlyMask = 0xfu << 8,
 };
 
 // One scheduled step, prepared by the host from the story bytes
@@ -197,6 +204,7 @@ struct LaneControl {
     uint32_t bias_fail;              // first output whose bias this learning step makes non-finite, or kNoFail
     uint32_t ring_tick[kRing];       // tick whose active set ring slot holds (UINT32_MAX = empty)
     uint32_t ring_count[kRing];      // active count of that tick
+    uint32_t ring_early[kRing];      // delays (bit = delay) of that tick's events already delivered at emission
     // The barrier counter has a 128-byte L2 line of its own: its polls and
     // arrivals would otherwise queue behind the per-step counter atomics and
     // the step record's stores to the same line.
@@ -255,9 +263,9 @@ enum NeuronField : uint32_t {
     kNBranch0 = 6,      // branch accumulators 0..3 (excitatory, inhibitory, temporal, gate)
     kNLastTick = 10,
     kNRefractory = 11,  // refractory_until
-    kNTouched = 12,     // touched epoch: tick+1 when touched this tick
+    kNTouched = 12,     // touched epoch: tick+1 when folded (touched) at tick
     kNSelected = 13,    // selected epoch: tick+1 when selected this tick
-    kNBucketCount = 14, // deliveries in the neuron's bucket this tick
+    kNSpare = 14,       // unused (bucket counts live in LaneDesc::bucket_count)
     kNDestEpoch = 15,   // learning-destination claim epoch
 };
 constexpr uint32_t kNeuronWords = 16;
@@ -295,8 +303,14 @@ struct LaneDesc {
     // change the weight (nonzero eligibility), listed by the eligibility phase
     uint32_t LEO_GLOBAL* rec_learn;     // NS (LaneControl rec_learn_count)
     uint32_t LEO_GLOBAL* in_learn;      // NI (LaneControl in_learn_count)
-    uint64_t LEO_GLOBAL* bucket;        // 2 words per entry: delivery-order key, value bits; kFixedEntries
-                                        // per target first, then the overflow ranges
+    // Delivery buckets in bucket_sets sets (1, or kBucketSets on a lane that
+    // takes frozen runs with one barrier per step): the deliveries of tick t
+    // go to set t % bucket_sets, so events emitted up to 8 ticks ahead wait
+    // in their own set while the current tick's set is folded.
+    uint64_t LEO_GLOBAL* bucket;        // per set: 2 words per entry: delivery-order key, value bits;
+                                        // kFixedEntries per target first, then the overflow ranges
+    uint32_t LEO_GLOBAL* bucket_count;  // per set: N entry counts (nonzero only with the target's touched bit set)
+    uint64_t bucket_stride;             // words of `bucket` per set
     uint64_t LEO_GLOBAL* shadow;        // 2 words per entry: the radix sort's second buffer (shadow_offset)
     // block selection
     uint32_t LEO_GLOBAL* range_winners; // blocks * max_active_per_block: winners of each selecting wave's block
@@ -304,8 +318,12 @@ struct LaneDesc {
     float LEO_GLOBAL* range_winner_act; // same layout: activation of each winner
     float LEO_GLOBAL* block_cutoff;     // blocks
     uint32_t LEO_GLOBAL* block_epoch;   // blocks: tick+1 when the block's selection above is current
-    uint32_t LEO_GLOBAL* touched_bits;  // blocks * block_words: neurons touched this tick, cleared by phase 2
-    uint32_t LEO_GLOBAL* wave_total;    // kMaxWaves: block winners of each selecting wave's block range
+    uint32_t LEO_GLOBAL* touched_bits;  // per set, blocks * block_words: neurons with deliveries at the set's
+                                        // tick, cleared by phase 2
+    uint32_t touched_stride;            // words of `touched_bits` per set
+    uint32_t bucket_sets;               // 1 or kBucketSets
+    uint32_t LEO_GLOBAL* wave_total;    // 2 * kMaxWaves, by tick parity: block winners of each selecting
+                                        // wave's block range
     uint32_t LEO_GLOBAL* wave_touched;  // kMaxWaves: touched neurons of each selecting wave's range, listed in
                                         // touched_list from the range's first neuron on
     // ring: per slot, up to max_active_global active neurons, activation, and S snapshot values each

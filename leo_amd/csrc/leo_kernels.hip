@@ -398,6 +398,7 @@ struct alignas(16) StepShared {
     // this workgroup's copy of the emission ring bookkeeping (LaneControl ring_*)
     uint32_t ring_tick[kRing];
     uint32_t ring_count[kRing];
+    uint32_t ring_early[kRing];
     // each selecting wave's winner count and first 64 winners (phase 2 to 3)
     uint32_t win_count[kWavesPerGroup];
     uint32_t win_n[kWavesPerGroup][kWaveSize];
@@ -501,7 +502,9 @@ __device__ __forceinline__ LateCounters load_late_counters(const StepCtx& c, uin
         for (uint32_t k = 0; k < kCounterKinds; ++k) v[k] += ld(counter_word(c, w, k, tick));
     }
     LateCounters out;
-    out.events = wave_sum_u32(v[kCEvents]);
+    // the fold counted every entry it folded, the tick's F injections too
+    const uint32_t folded = wave_sum_u32(v[kCEvents]), F = c.a->cfg.input_fanout;
+    out.events = folded > F ? folded - F : 0u;
     out.touched = wave_sum_u32(v[kCTouched]);
     out.scanned_rec = wave_sum_u32(v[kCScanRec]);
     out.scanned_in = wave_sum_u32(v[kCScanIn]);
@@ -545,33 +548,53 @@ __device__ __forceinline__ void roll_counters(const StepCtx& c, uint32_t step_in
     clear_counters(c, c.tick);
 }
 
+// The bucket set of the deliveries of `tick` (LaneDesc::bucket_sets).
+__device__ __forceinline__ uint32_t set_of(const LaneDesc& d, uint32_t tick) {
+    return d.bucket_sets == 1 ? 0u : tick % kBucketSets;
+}
+__device__ __forceinline__ uint64_t LEO_GLOBAL* set_bucket(const LaneDesc& d, uint32_t set) {
+    return d.bucket + set * d.bucket_stride;
+}
+__device__ __forceinline__ uint32_t LEO_GLOBAL* set_counts(const LaneDesc& d, uint32_t set, uint32_t N) {
+    return d.bucket_count + static_cast<uint64_t>(set) * N;
+}
+__device__ __forceinline__ uint32_t LEO_GLOBAL* set_touched(const LaneDesc& d, uint32_t set) {
+    return d.touched_bits + static_cast<uint64_t>(set) * d.touched_stride;
+}
+// This tick's per-wave winner totals (two buffers by tick parity).
+__device__ __forceinline__ uint32_t LEO_GLOBAL* wave_totals(const LaneDesc& d, uint32_t tick) {
+    return d.wave_total + (tick & 1u) * kMaxWaves;
+}
+
 // Entry p of target n's delivery bucket: the first kFixedEntries at fixed
 // places (kFixedEntries*n + p), the rest in the target's overflow range.
 __device__ __forceinline__ uint64_t bucket_entry(uint64_t overflow, uint32_t n, uint32_t p) {
     return p < kFixedEntries ? static_cast<uint64_t>(kFixedEntries) * n + p : overflow + (p - kFixedEntries);
 }
 
-// One delivery into target's bucket (the fold of phase 2 orders the bucket
-// by key); true when it is the target's first delivery of the tick.
-__device__ __forceinline__ bool scatter_event(const StepCtx& c, uint32_t target, uint64_t key, float value) {
+// One delivery into target's bucket of `set` (the fold of phase 2 orders the
+// bucket by key); true when it is the target's first delivery of the tick.
+__device__ __forceinline__ bool scatter_event(const StepCtx& c, uint32_t set, uint32_t target, uint64_t key,
+                                              float value) {
     // the overflow offset is loaded with the counter increment (one round trip)
     const uint64_t overflow = c.a->m.bucket_offset[target];
-    const uint32_t p = atomicAdd(nu(c.d, target, kNBucketCount), 1u);
+    const uint32_t p = atomicAdd(set_counts(c.d, set, c.a->cfg.neuron_count) + target, 1u);
     const uint64_t at = bucket_entry(overflow, target, p);
-    c.d.bucket[2 * at] = key;
-    c.d.bucket[2 * at + 1] = __float_as_uint(value);
+    uint64_t LEO_GLOBAL* bucket = set_bucket(c.d, set);
+    bucket[2 * at] = key;
+    bucket[2 * at + 1] = __float_as_uint(value);
     return p == 0;
 }
 
-// Touched marks of neuron n at `tick`: the epoch for phase 3, and the block's
-// bitmap bit for phase 2. A delivery marks its target only when it is the
-// target's first of the tick (bucket count 0); setting a bit is idempotent,
-// so a neuron also marked as previously active is marked twice harmlessly.
+// Touched mark of neuron n at `tick`: the block's bitmap bit in the tick's
+// set, read by phase 2 (which writes the touched epoch when it folds n). A
+// delivery marks its target only when it is the target's first of the tick
+// (bucket count 0); setting a bit is idempotent, so a neuron also marked as
+// previously active is marked twice harmlessly.
 __device__ __forceinline__ void touch_neuron(const StepCtx& c, uint32_t n, uint32_t tick) {
     const uint32_t nb = c.a->cfg.neurons_per_block;
     const uint32_t blk = fast_div(n, c.a->div_block), off = n - blk * nb;
-    (*nu(c.d, n, kNTouched)) = tick + 1;
-    atomicOr(&c.d.touched_bits[blk * block_words(nb) + off / 32], 1u << (off & 31));
+    atomicOr(&set_touched(c.d, set_of(c.d, tick))[blk * block_words(nb) + off / 32], 1u << (off & 31));
 }
 
 // The items of one tick's delivery: the previous active set, the ring
@@ -596,9 +619,10 @@ __device__ __forceinline__ DeliverPlan deliver_plan(const StepCtx& c, const Step
     p.prev_slot = (tick + kRing - 1) % kRing;
     p.prev_count = (!ahead && tick > 0 && sh.ring_tick[p.prev_slot] == tick - 1) ? sh.ring_count[p.prev_slot] : 0;
     // delivery classes: delay 8, 4, 2, 1 in that order (chronological by emission tick)
+    // (a class whose events the emitting tick delivered itself has none left)
     auto class_items = [&](uint32_t delay, uint32_t& rs) {
         rs = (tick + kRing - delay) % kRing;
-        const bool valid = tick >= delay && sh.ring_tick[rs] == tick - delay;
+        const bool valid = tick >= delay && sh.ring_tick[rs] == tick - delay && (sh.ring_early[rs] & delay) == 0;
         return (valid ? sh.ring_count[rs] : 0) * S;
     };
     p.rs1 = 0;
@@ -726,7 +750,7 @@ __device__ __forceinline__ void deliver_commit(const StepCtx& c, const StepParam
         it.tq1 = ld16_record(rsrc, static_cast<uint32_t>(rslot), 16);
         it.mark = ld(&d.rec_mark[rslot]);
     }
-    if (scatter && scatter_event(c, it.target, it.key, it.value)) it.touch_n = it.target;
+    if (scatter && scatter_event(c, set_of(d, p.tick), it.target, it.key, it.value)) it.touch_n = it.target;
     if (it.touch_n != 0xffffffffu) touch_neuron(c, it.touch_n, p.tick);
     // frozen steps skip the appends below: their wave-uniform counter read
     // would wait for this item's stores before the next item's loads
@@ -767,9 +791,8 @@ __device__ __forceinline__ void reset_next_lists(const StepCtx& c) {
 __device__ __forceinline__ void phase_deliver(const StepCtx& c, const StepParams& sp, const StepShared& sh) {
     reset_next_lists(c);
     const DeliverPlan p = deliver_plan(c, sh, false);
-    uint32_t delivered = 0;
+    uint32_t delivered = 0;  // counted by the fold instead (it folds every delivered entry)
     deliver_items(c, sp, p, dealt_index(c, p.stride / kThreads), delivered);
-    count_wave(c, kCEvents, p.tick, delivered);
 }
 
 // ---------------------------------------------------------------------------
@@ -924,28 +947,53 @@ __device__ __forceinline__ void sort8(uint64_t (&k)[8], uint32_t (&v)[8]) {
 // unless refractory, applies the drive (runtime.rs:940-975). Returns the
 // margin membrane - threshold; *refractory tells whether the neuron skipped.
 // A neuron with more than 8 deliveries this tick is left untouched and
-// *deferred set: the wave folds it with deep_fold.
-__device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float pi, bool* refractory, bool* deferred) {
+// *deferred set: the wave folds it with deep_fold. *entries is the bucket's
+// entry count (its deliveries of the tick, folded here or by deep_fold).
+//
+// `post_pending`: the previous tick was a one-barrier frozen step, which
+// left its winners' post-fire updates (runtime.rs:920-938, 1084-1106) and
+// activation reset (runtime.rs:544-555) to this fold: a record whose
+// activation is nonzero belongs to such a winner (an activation is nonzero
+// only from a neuron's selection to the next tick's reset), and every
+// winner is touched at the next tick. They are applied here before the
+// decay, in the order and with the values the post phase would have used
+// (the threshold does not change in a frozen step).
+__device__ __forceinline__ void apply_post_fire(const LeoConfig& cfg, uint32_t fired_tick, float threshold,
+                                                float& act, float& mem, float& fat, float& ad0, float& ad1,
+                                                float& ad2, uint32_t& refractory_until) {
+    fat = fat + cfg.fatigue_gain * act;
+    ad0 = ad0 + cfg.adaptation_fast_gain * act;
+    ad1 = ad1 + cfg.adaptation_medium_gain * act;
+    ad2 = ad2 + cfg.adaptation_slow_gain * act;
+    mem = mem - threshold * cfg.membrane_reset_fraction;
+    refractory_until = fired_tick + cfg.refractory_ticks + 1;
+    act = 0.0f;
+}
+
+__device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float pi, uint32_t set, bool post_pending,
+                                            bool* refractory, bool* deferred, uint32_t* entries) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
     const uint32_t N = cfg.neuron_count, tick = c.tick;
-    // the record in three 16-byte loads (membrane .. bucket count)
+    // the record in three 16-byte loads (membrane .. refractory tick)
     static_assert(kNMembrane == 0 && kNFatigue == 2 && kNAdapt0 == 3 && kNBranch0 == 6 && kNLastTick == 10 &&
-                      kNRefractory == 11 && kNBucketCount == 14,
+                      kNRefractory == 11 && kNTouched == 12,
                   "record layout");
     const __amdgpu_buffer_rsrc_t rec = neuron_rsrc(d, N);
     const f32x4 q0 = ld_quarter(rec, n, 0), q1 = ld_quarter(rec, n, 1), q2 = ld_quarter(rec, n, 2);
-    const f32x4 q3 = ld_quarter(rec, n, 3);
+    uint32_t LEO_GLOBAL* counts = set_counts(d, set, N);
+    const uint64_t LEO_GLOBAL* bucket = set_bucket(d, set);
     float mem = q0.x, fat = q0.z, ad0 = q0.w, ad1 = q1.x, ad2 = q1.y;
     float b0 = q1.z, b1 = q1.w, b2 = q2.x, b3 = q2.y;
     const uint32_t last = __float_as_uint(q2.z);
-    const uint32_t cnt = __float_as_uint(q3.z);
+    const uint32_t cnt = ld(&counts[n]);
+    *entries = cnt;
     const uint64_t overflow = a.m.bucket_offset[n];  // loaded with the state (used when cnt > kFixedEntries)
     // the fixed bucket entries (one 64-byte run, 16 bytes each: key, value)
     // are read with the state; N * 64 bytes fits a buffer like the records
     static_assert(kFixedEntries == 4, "the fold reads four fixed entries");
-    const __amdgpu_buffer_rsrc_t fixed = coherent_rsrc(d.bucket, N * kFixedEntries * 16);
+    const __amdgpu_buffer_rsrc_t fixed = coherent_rsrc(bucket, N * kFixedEntries * 16);
     f32x4 fe[kFixedEntries];
 #pragma unroll
     for (uint32_t x = 0; x < kFixedEntries; ++x) fe[x] = ld16(fixed, (n * kFixedEntries + x) * 16);
@@ -954,11 +1002,15 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
     };
     const uint64_t k0 = entry_key(fe[0]), k1 = entry_key(fe[1]);
     const uint32_t v0 = __float_as_uint(fe[0].z), v1 = __float_as_uint(fe[1].z);
-    const bool refr = __float_as_uint(q2.w) > tick;
     const float threshold = ld(&d.p.threshold[n]);
     const float excitability = a.m.excitability[n];  // in the same round, though a refractory neuron skips it
     *deferred = cnt > 8;
     if (cnt > 8) return 0.0f;  // every load above is in flight together; nothing written yet
+    float act = q0.y;
+    uint32_t refractory_until = __float_as_uint(q2.w);
+    if (post_pending && act > 0.0f)
+        apply_post_fire(cfg, tick - 1, threshold, act, mem, fat, ad0, ad1, ad2, refractory_until);
+    const bool refr = refractory_until > tick;
     const uint32_t e = tick - last;
     if (e > 0) {
         const StateDecays k = state_decays(cfg, e);
@@ -1000,7 +1052,7 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
                 k[x] = x < cnt ? entry_key(fe[x]) : ~0ULL;
                 v[x] = x < cnt ? __float_as_uint(fe[x].z) : 0u;
             }
-            const uint64_t LEO_GLOBAL* over = d.bucket + 2 * overflow;
+            const uint64_t LEO_GLOBAL* over = bucket + 2 * overflow;
 #pragma unroll
             for (uint32_t x = kFixedEntries; x < 8; ++x) {
                 k[x] = x < cnt ? ld(&over[2 * (x - kFixedEntries)]) : ~0ULL;
@@ -1011,7 +1063,7 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
             for (uint32_t x = 0; x < 8; ++x)
                 if (x < cnt) add(k[x], v[x]);
         }
-        (*nu(d, n, kNBucketCount)) = 0;
+        counts[n] = 0;
     }
     *refractory = refr;
     if (!refr) {
@@ -1024,9 +1076,10 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
     // quarters 0-2 written whole (the wave owns the neuron during this
     // phase; the activation and refractory tick are written back unchanged)
     f32x4 LEO_GLOBAL* rq = reinterpret_cast<f32x4 LEO_GLOBAL*>(nf(d, n, 0));
-    rq[0] = f32x4{mem, q0.y, fat, ad0};
+    rq[0] = f32x4{mem, act, fat, ad0};
     rq[1] = f32x4{ad1, ad2, b0, b1};
-    rq[2] = f32x4{b2, b3, __uint_as_float(e > 0 ? tick : last), q2.w};
+    rq[2] = f32x4{b2, b3, __uint_as_float(e > 0 ? tick : last), __uint_as_float(refractory_until)};
+    (*nu(d, n, kNTouched)) = tick + 1;
     return mem - threshold;
 }
 
@@ -1057,21 +1110,27 @@ constexpr uint32_t kDeepTiles = 8;  // 64-entry tiles a lane has in flight
 // `hist` (256 words of LDS) -- and every lane adds the entries in that order
 // (uniform values, so every lane holds the same sums). Lane 0 writes the
 // state.
-__device__ float deep_fold(const StepCtx& c, uint32_t n, float pi, bool* refractory, uint32_t* hist) {
+__device__ float deep_fold(const StepCtx& c, uint32_t n, float pi, uint32_t set, bool post_pending, bool* refractory,
+                           uint32_t* hist) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
     const uint32_t N = cfg.neuron_count, tick = c.tick, lane = __lane_id();
     const __amdgpu_buffer_rsrc_t rec = neuron_rsrc(d, N);
     const f32x4 q0 = ld_quarter(rec, n, 0), q1 = ld_quarter(rec, n, 1), q2 = ld_quarter(rec, n, 2);
-    const f32x4 q3 = ld_quarter(rec, n, 3);
+    uint32_t LEO_GLOBAL* counts = set_counts(d, set, N);
+    uint64_t LEO_GLOBAL* const set_base = set_bucket(d, set);
     const uint64_t overflow = a.m.bucket_offset[n];
     const float threshold = ld(&d.p.threshold[n]);
     float mem = q0.x, fat = q0.z, ad0 = q0.w, ad1 = q1.x, ad2 = q1.y;
     float b0 = q1.z, b1 = q1.w, b2 = q2.x, b3 = q2.y;
-    // every lane read the same record: the count is uniform
-    const uint32_t last = __float_as_uint(q2.z), cnt = __builtin_amdgcn_readfirstlane(__float_as_uint(q3.z));
-    const bool refr = __float_as_uint(q2.w) > tick;
+    // every lane read the same count: it is uniform
+    const uint32_t last = __float_as_uint(q2.z), cnt = __builtin_amdgcn_readfirstlane(ld(&counts[n]));
+    float act = q0.y;
+    uint32_t refractory_until = __float_as_uint(q2.w);
+    const bool fired = post_pending && act > 0.0f;
+    if (fired) apply_post_fire(cfg, tick - 1, threshold, act, mem, fat, ad0, ad1, ad2, refractory_until);
+    const bool refr = refractory_until > tick;
     const uint32_t e = tick - last;
     if (e > 0) {
         const StateDecays k = state_decays(cfg, e);
@@ -1093,20 +1152,20 @@ __device__ float deep_fold(const StepCtx& c, uint32_t n, float pi, bool* refract
         b2 = br == 2 ? b2 + v : b2;
         b3 = br == 3 ? b3 + v : b3;
     };
-    DeepArray bucket{d.bucket, overflow, n, true};
+    DeepArray bucket{set_base, overflow, n, true};
     if (cnt <= kDeepRegisterEntries) {
         // two entries per lane; rank = number of smaller keys (keys unique)
         uint64_t k0 = ~0ULL, k1 = ~0ULL;
         uint32_t v0 = 0, v1 = 0;
         if (lane < cnt) {
             const uint64_t at = bucket.at(lane);
-            k0 = ld(&d.bucket[2 * at]);
-            v0 = static_cast<uint32_t>(ld(&d.bucket[2 * at + 1]));
+            k0 = ld(&set_base[2 * at]);
+            v0 = static_cast<uint32_t>(ld(&set_base[2 * at + 1]));
         }
         if (lane + kWaveSize < cnt) {
             const uint64_t at = bucket.at(lane + kWaveSize);
-            k1 = ld(&d.bucket[2 * at]);
-            v1 = static_cast<uint32_t>(ld(&d.bucket[2 * at + 1]));
+            k1 = ld(&set_base[2 * at]);
+            v1 = static_cast<uint32_t>(ld(&set_base[2 * at + 1]));
         }
         uint32_t r0 = 0, r1 = 0;
         for (uint32_t q = 0; q < cnt; ++q) {
@@ -1158,7 +1217,7 @@ __device__ float deep_fold(const StepCtx& c, uint32_t n, float pi, bool* refract
 #pragma unroll
             for (uint32_t k = 0; k < kDeepTiles; ++k) {
                 const uint32_t p = t0 + k * kWaveSize + lane;
-                keys[k] = p < cnt ? ld(&d.bucket[2 * bucket.at(p)]) : 0ULL;
+                keys[k] = p < cnt ? ld(&set_base[2 * bucket.at(p)]) : 0ULL;
             }
 #pragma unroll
             for (uint32_t k = 0; k < kDeepTiles; ++k)
@@ -1252,7 +1311,12 @@ __device__ float deep_fold(const StepCtx& c, uint32_t n, float pi, bool* refract
             (*nf(d, n, kNAdapt0 + 2)) = ad2;
             (*nu(d, n, kNLastTick)) = tick;
         }
-        (*nu(d, n, kNBucketCount)) = 0;
+        counts[n] = 0;
+        (*nu(d, n, kNTouched)) = tick + 1;
+        if (fired) {
+            (*nf(d, n, kNActivation)) = 0.0f;
+            (*nu(d, n, kNRefractory)) = refractory_until;
+        }
         (*nf(d, n, kNBranch0)) = b0;
         (*nf(d, n, kNBranch0 + 1)) = b1;
         (*nf(d, n, kNBranch0 + 2)) = b2;
@@ -1314,8 +1378,13 @@ __device__ __forceinline__ Window wave_window(uint32_t wave, uint32_t nb) {
 // reads them in one round. A group with more touched neurons than the window
 // holds is taken in windows of whole blocks.
 // `keep_bits`: a trace step leaves the bitmap words set for its eligibility
-// update (the learning phase clears them from the touched list).
-__device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& sh, bool keep_bits) {
+// update (the learning phase clears them from the touched list). `pi` is the
+// population inhibition the previous tick left; `post_pending` that the
+// previous tick's winners still await their post-fire updates (fold_drive).
+// The fold counts the tick's delivered entries (kCEvents: the F injections
+// included, which the record takes off).
+__device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& sh, bool keep_bits, float pi,
+                                                  bool post_pending) {
     const KernelArgs& a = *c.a;
     const LaneDesc& d = c.d;
     const LeoConfig& cfg = a.cfg;
@@ -1329,7 +1398,7 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
     const uint32_t wpb = block_words(nb);
     const uint32_t group = min(kGroupBlocks, kWaveSize * kWordsPerLane / wpb);
     const uint32_t cap = window_capacity(nb);
-    const float pi = ld(&c.ctl->population_inhibition);
+    const uint32_t set = set_of(d, tick);
     const FastDiv block_div = a.div_block_words;
     const Window w = wave_window(wave, nb);
     w.cands[lane] = 0;
@@ -1338,10 +1407,10 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
     // this wave's touched neurons are listed from its range's first neuron on
     // (no shared counter to wait for)
     const uint32_t first_listed = b0 * nb;
-    uint32_t supra = 0, staged = 0, listed_before = 0;
+    uint32_t supra = 0, staged = 0, listed_before = 0, entries = 0;
     for (uint32_t gb = b0; gb < b1; gb += group) {
         const uint32_t gn = min(group, b1 - gb), gw = gn * wpb;
-        uint32_t* bits = d.touched_bits + static_cast<uint64_t>(gb) * wpb;
+        uint32_t* bits = set_touched(d, set) + static_cast<uint64_t>(gb) * wpb;
         uint32_t word[kWordsPerLane];
 #pragma unroll
         for (uint32_t k = 0; k < kWordsPerLane; ++k) {
@@ -1420,7 +1489,9 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
                 const uint32_t g = e >> 16;
                 const uint32_t n = (gb + g) * nb + (e & 0xffffu);
                 bool refractory = false, deep = false;
-                const float act = clampf(fold_drive(c, n, pi, &refractory, &deep), 0.0f, 1.0f);
+                uint32_t folded = 0;
+                const float act = clampf(fold_drive(c, n, pi, set, post_pending, &refractory, &deep, &folded), 0.0f, 1.0f);
+                entries += folded;
                 const bool candidate = !deep && !refractory && act > 0.0f;
                 w.key[i] = deep ? kDeepPending : candidate ? selection_key(act, add_mod(n, N - rot, N)) : ~0ULL;
                 any_deep |= deep;
@@ -1441,7 +1512,7 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
                         const uint32_t g = e >> 16;
                         const uint32_t n = (gb + g) * nb + (e & 0xffffu);
                         bool refractory = false;
-                        const float act = clampf(deep_fold(c, n, pi, &refractory, hist), 0.0f, 1.0f);
+                        const float act = clampf(deep_fold(c, n, pi, set, post_pending, &refractory, hist), 0.0f, 1.0f);
                         const bool candidate = !refractory && act > 0.0f;
                         if (lane == 0) {
                             w.key[i] = candidate ? selection_key(act, add_mod(n, N - rot, N)) : ~0ULL;
@@ -1513,10 +1584,12 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
         wave_sync();
     }
     supra = wave_sum_u32(supra);
+    entries = wave_sum_u32(entries);
     if (lane == 0) {
         if (supra) atomicAdd(counter_word(c, c.part, kCSupra, tick), supra);
+        if (entries) atomicAdd(counter_word(c, c.part, kCEvents, tick), entries);
         sh.win_count[wave] = staged;
-        d.wave_total[wv] = staged;
+        wave_totals(d, tick)[wv] = staged;
         d.wave_touched[wv] = listed_before;
         if (listed_before) atomicAdd(counter_word(c, c.part, kCTouched, tick), listed_before);
     }
@@ -1534,11 +1607,10 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
 // from the ring), and the delivering workgroups take the remaining items.
 // The memory operations are grouped into three rounds: the winners with the
 // first next-tick item; the winners' state and synapses with that item's
-// bucket increment; the delay-1 bucket increments. Returns this thread's
-// count of delivered events.
-__device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepParams& sp, uint32_t step_index,
-                                                 StepShared& sh, bool fuse_post, bool ahead,
-                                                 const StepParams& next) {
+// bucket increment; the delay-1 bucket increments.
+__device__ __forceinline__ void write_active(const StepCtx& c, const StepParams& sp, uint32_t step_index,
+                                             StepShared& sh, bool fuse_post, bool ahead, const StepParams& next,
+                                             bool late_done) {
     const LeoConfig& cfg = c.a->cfg;
     const LaneDesc& d = c.d;
     const uint32_t cap = cfg.max_active_global, limit = cfg.max_active_per_block;
@@ -1560,7 +1632,7 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     LateCounters late{};
     if (rec_wave) {
         if (fuse_post) supra = counter_total(c, kCSupra, c.tick);
-        if (step_index > 0) late = load_late_counters(c, c.tick - 1);
+        if (step_index > 0 && !late_done) late = load_late_counters(c, c.tick - 1);
     }
     if (recorder) {
         pi_old = ld(&c.ctl->population_inhibition);
@@ -1618,7 +1690,7 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     uint32_t before = 0, all = 0;
     for (uint32_t base = 0; base < nwaves; base += kWaveSize) {
         const uint32_t w = base + lane;
-        const uint32_t v = w < nwaves ? ld(&d.wave_total[w]) : 0;
+        const uint32_t v = w < nwaves ? ld(&wave_totals(d, c.tick)[w]) : 0;
         before += wave_sum_u32(w < wv ? v : 0);
         all += wave_sum_u32(v);
     }
@@ -1634,13 +1706,14 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
         // tick-1's record is finished (tick-1 is complete); the recording
         // wave then clears its counters, which tick+1 reuses
         LaneControl LEO_GLOBAL* ctl = c.ctl;
-        if (step_index > 0) store_late_record(d, step_index - 1, late);
+        if (step_index > 0 && !late_done) store_late_record(d, step_index - 1, late);
         ctl->active_count = all;
         ctl->block_selected = all;
         ctl->clipped = 0;
         ctl->pop_cutoff = 0.0f;
         ctl->ring_tick[rs] = c.tick;
         ctl->ring_count[rs] = all;
+        ctl->ring_early[rs] = 0;
         const float pi = clampf(pi_old + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
                                 cfg.population_inhibition_max);
         ctl->population_inhibition = pi;
@@ -1663,12 +1736,13 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
         }
     }
     if (rec_wave) clear_counters(c, c.tick);  // after its loads of tick-1's counters
-    if (!fuse_post) return 0;
+    if (!fuse_post) return;
     // Post-fire updates of this wave's winners and their emission snapshots
     // (the post phase, runtime.rs:920-938, 1084-1106), folded in here when no
     // eligibility update or readout of this step reads the state in between.
     // The wave's first 64 winners are in its LDS since phase 2.
     const uint32_t refractory = c.tick + cfg.refractory_ticks + 1;
+    const uint32_t next_set = set_of(d, c.tick + 1);
     uint32_t inhibitory = 0, delivered = 0;
     auto post_fire = [&](uint32_t n, float act, float fat, float ad0, float ad1, float ad2, float mem, float thr,
                          uint8_t type) {
@@ -1694,7 +1768,7 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
             // delivery from the ring would be
             const uint64_t key = (3ull << 61) | (static_cast<uint64_t>(before + r) << 32) |
                                  (static_cast<uint64_t>(j) << 2) | edge_branch(edge);
-            if (scatter_event(c, edge_target(edge), key, value)) touch_neuron(c, edge_target(edge), c.tick + 1);
+            if (scatter_event(c, next_set, edge_target(edge), key, value)) touch_neuron(c, edge_target(edge), c.tick + 1);
             delivered += 1;
         }
     };
@@ -1723,8 +1797,197 @@ __device__ __forceinline__ uint32_t write_active(const StepCtx& c, const StepPar
     if (threadIdx.x == 0) {  // the next deliveries read this tick's ring entry from LDS
         sh.ring_tick[rs] = c.tick;
         sh.ring_count[rs] = all;
+        sh.ring_early[rs] = 0;
     }
-    return delivered;
+}
+
+// ---------------------------------------------------------------------------
+// One-barrier frozen steps. On a lane with kBucketSets bucket sets, a frozen
+// step whose next step is frozen too (neither reads eligibilities or the
+// readout) runs as a single phase: the fold and selection of its tick t,
+// then, with no barrier between, every event its winners emit, each into the
+// bucket set of its arrival tick t + delay (up to 8 ticks ahead, a set no
+// other wave folds in this phase), and tick t+1's other deliveries (the
+// input injection, the ring classes of earlier two-phase ticks). No wave
+// waits for another: an event is keyed by its winner's staged position in
+// its wave's block range (row0 + k) instead of its active-list rank. The
+// active list is the waves' staged winners in wave order, so both keys order
+// a tick's events alike and the fold sums them in the reference's order
+// (runtime.rs:605-639). What needs every wave's winners waits for the next
+// phase: the winners' post-fire updates and activation reset for their fold
+// at t+1 (fold_drive), the population inhibition and the step record for
+// frozen_prologue. The ring keeps no entries for tick t (its readers find a
+// stale tick there and deliver nothing from it: every event of t is
+// already in its bucket).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void frozen_emit(const StepCtx& c, StepShared& sh, uint32_t early, const StepParams& next) {
+    const LeoConfig& cfg = c.a->cfg;
+    const LaneDesc& d = c.d;
+    const uint32_t wave = wave_index(), lane = __lane_id();
+    const uint32_t nwaves = selecting_waves(c);
+    const uint32_t wv = c.part * kWavesPerGroup + wave;
+    const uint32_t range = (cfg.block_count + nwaves - 1) / nwaves;
+    const uint32_t b0 = min(cfg.block_count, wv * range);
+    const uint64_t row0 = static_cast<uint64_t>(b0) * cfg.max_active_per_block;
+    const uint32_t S = cfg.synapses_per_neuron;
+    // tick t+1's other deliveries, dealt over every workgroup: this thread's
+    // first item's loads go out before the winners' work
+    const DeliverPlan np = deliver_plan(c, sh, true);
+    const uint32_t dealt = dealt_index(c, c.P);
+    DeliverItem item0 = deliver_fetch(c, next, np, np.delivers ? dealt : np.total);
+    reset_next_lists(c);
+    const uint32_t mine = sh.win_count[wave];
+    // staged winners past the wave's LDS copy are read back from memory the
+    // wave has just written
+    if (mine > kWaveSize) __builtin_amdgcn_s_waitcnt(0);
+    auto winner = [&](uint32_t r, uint32_t& n, float& act) {
+        if (r < kWaveSize) {
+            n = sh.win_n[wave][r];
+            act = sh.win_act[wave][r];
+        } else {
+            n = ld(&d.range_winners[row0 + r]);
+            act = ld(&d.range_winner_act[row0 + r]);
+        }
+    };
+    // the winners are touched at t+1, whose fold applies their post-fire
+    // updates; the inhibitory ones count for this tick's record
+    uint32_t inhibitory = 0;
+    for (uint32_t r = lane; r < mine; r += kWaveSize) {
+        uint32_t n;
+        float act;
+        winner(r, n, act);
+        inhibitory += c.a->m.neuron_type[n] != 0 ? 1u : 0u;
+        touch_neuron(c, n, c.tick + 1);
+    }
+    // every synapse of every winner whose delay is early (runtime.rs:1084-1106
+    // emits them into the ring; the value is the snapshot the ring would
+    // hold); the other delays' events stay for the ring, which the next
+    // phase's prologue fills
+    const uint32_t items = early ? mine * S : 0u;
+    for (uint32_t item = lane; item < items; item += kWaveSize) {
+        const uint32_t r = fast_div(item, c.a->div_synapses), j = item - r * S;
+        uint32_t n;
+        float act;
+        winner(r, n, act);
+        const uint64_t slot = static_cast<uint64_t>(n) * S + j;
+        const float value = act * ld(&d.p.rec_weight[slot]);
+        const uint32_t edge = c.a->m.rec_edge[slot];
+        const uint32_t dl = (edge >> kEdgeTargetBits) & 3u;  // delay 1 << dl, delivery class 3 - dl
+        if ((early & (1u << dl)) == 0) continue;
+        const uint32_t arrival = c.tick + (1u << dl);
+        const uint64_t key = (static_cast<uint64_t>(3u - dl) << 61) | ((row0 + r) << 32) |
+                             (static_cast<uint64_t>(j) << 2) | edge_branch(edge);
+        if (scatter_event(c, set_of(d, arrival), edge_target(edge), key, value))
+            touch_neuron(c, edge_target(edge), arrival);
+    }
+    uint32_t delivered = 0;  // counted by the fold
+    if (np.delivers) deliver_commit(c, next, np, item0, delivered);
+    deliver_items(c, next, np, dealt + np.stride, delivered);
+    count_wave(c, kCInhibitory, c.tick, inhibitory);
+}
+
+// The start of the phase after a one-barrier frozen step (tick t-1, step
+// step_index-1): every wave sums that tick's winners from the waves' totals
+// and takes the population inhibition forward from the value the previous
+// fold read (runtime.rs:1076-1082; every wave computes the same value);
+// the recording wave writes the step's record and clears the counters that
+// tick t+1 reuses. Returns tick t-1's population inhibition, which the fold
+// of t reads.
+__device__ __forceinline__ float frozen_prologue(const StepCtx& c, StepShared& sh, uint32_t step_index,
+                                                float pi_before, uint32_t early) {
+    const LeoConfig& cfg = c.a->cfg;
+    const LaneDesc& d = c.d;
+    const uint32_t prev = c.tick - 1, nwaves = selecting_waves(c), lane = __lane_id(), wave = wave_index();
+    const uint32_t wv = c.part * kWavesPerGroup + wave;
+    const uint32_t LEO_GLOBAL* totals = wave_totals(d, prev);
+    uint32_t all = 0, before = 0;
+    for (uint32_t base = 0; base < nwaves; base += kWaveSize) {
+        const uint32_t w = base + lane;
+        const uint32_t v = w < nwaves ? ld(&totals[w]) : 0u;
+        all += wave_sum_u32(v);
+        before += wave_sum_u32(w < wv ? v : 0u);
+    }
+    const uint32_t rs = prev % kRing;
+    if (early != 0xfu && wv < nwaves) {
+        // some delays' events go through the ring: the tick's active list
+        // (runtime.rs:1010-1013) and emission snapshots, at active-list
+        // positions (the wave's winners of tick t-1 are still in its LDS:
+        // this tick's fold has not run yet)
+        const uint32_t cap = cfg.max_active_global, S = cfg.synapses_per_neuron;
+        const uint32_t range = (cfg.block_count + nwaves - 1) / nwaves;
+        const uint64_t row0 = static_cast<uint64_t>(min(cfg.block_count, wv * range)) * cfg.max_active_per_block;
+        const uint32_t mine = sh.win_count[wave];
+        auto winner = [&](uint32_t r, uint32_t& n, float& act) {
+            if (r < kWaveSize) {
+                n = sh.win_n[wave][r];
+                act = sh.win_act[wave][r];
+            } else {
+                n = ld(&d.range_winners[row0 + r]);
+                act = ld(&d.range_winner_act[row0 + r]);
+            }
+        };
+        const uint64_t first = static_cast<uint64_t>(rs) * cap + before;
+        for (uint32_t r = lane; r < mine; r += kWaveSize) {
+            uint32_t n;
+            float act;
+            winner(r, n, act);
+            d.ring_active[first + r] = n;
+            d.ring_act[first + r] = act;
+        }
+        for (uint32_t item = lane; item < mine * S; item += kWaveSize) {
+            const uint32_t r = fast_div(item, c.a->div_synapses), j = item - r * S;
+            uint32_t n;
+            float act;
+            winner(r, n, act);
+            const uint64_t slot = static_cast<uint64_t>(n) * S + j;
+            const uint64_t at = (first + r) * S + j;
+            d.ring_value[at] = act * ld(&d.p.rec_weight[slot]);
+            d.ring_edge[at] = c.a->m.rec_edge[slot];
+        }
+    }
+    if (threadIdx.x == 0) {  // this workgroup's deliveries read the slot from LDS
+        sh.ring_tick[rs] = prev;
+        sh.ring_count[rs] = all;
+        sh.ring_early[rs] = early;
+    }
+    const float activity = static_cast<float>(all) / static_cast<float>(cfg.neuron_count);
+    const float pi = clampf(pi_before + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
+                            cfg.population_inhibition_max);
+    if (c.part == c.P - 1 && wave_index() == 0) {
+        const LateCounters late = load_late_counters(c, prev);
+        const uint32_t supra = counter_total(c, kCSupra, prev);
+        if (lane == 0) {
+            LaneControl LEO_GLOBAL* ctl = c.ctl;
+            const uint32_t rec_n = ld(&ctl->rec_count[c.parity]), in_n = ld(&ctl->in_count[c.parity]);
+            const uint32_t cells = ld(&ctl->ctx_count), probes = ld(&ctl->ctx_probes);
+            const uint32_t applied = ld(&ctl->ctx_applied);
+            StepRecord LEO_GLOBAL& rec = d.records[step_index - 1];
+            rec.p_target = 0.0f;
+            rec.predicted = 0;
+            rec.population_inhibition = pi;
+            rec.active = all;
+            rec.suprathreshold = supra;
+            rec.block_selected = all;
+            rec.clipped = 0;
+            rec.context_cells = cells;
+            rec.context_probes = probes;
+            rec.context_applied = applied;
+            rec.eligible_rec = rec_n;
+            rec.eligible_in = in_n;
+            rec.error_code = 0;
+            store_late_record(d, step_index - 1, late);
+            ctl->active_count = all;
+            ctl->block_selected = all;
+            ctl->clipped = 0;
+            ctl->pop_cutoff = 0.0f;
+            ctl->population_inhibition = pi;
+            ctl->ring_tick[rs] = prev;
+            ctl->ring_count[rs] = all;
+            ctl->ring_early[rs] = early;
+        }
+        clear_counters(c, c.tick);  // after the loads of tick t-1's counters, whose words t+1 reuses
+    }
+    return pi;
 }
 
 // First active-list position of each selecting wave's winners (block order,
@@ -1734,7 +1997,7 @@ __device__ __forceinline__ uint32_t wave_starts(const StepCtx& c, StepShared& sh
     uint32_t running = 0;
     for (uint32_t base = 0; base < nwaves; base += kThreads) {
         const uint32_t wv = base + threadIdx.x;
-        const uint32_t v = wv < nwaves ? ld(&c.d.wave_total[wv]) : 0;
+        const uint32_t v = wv < nwaves ? ld(&wave_totals(c.d, c.tick)[wv]) : 0;
         sh.scan[threadIdx.x] = v;
         __syncthreads();
         for (uint32_t off = 1; off < kThreads; off <<= 1) {
@@ -1867,6 +2130,7 @@ __device__ __forceinline__ void global_select(const StepCtx& c, StepShared& sh, 
         if (running <= kMaxBlockNeurons || running <= cap) ctl->pop_cutoff = pop_cutoff;
         ctl->ring_tick[rs] = tick;
         ctl->ring_count[rs] = active;
+        ctl->ring_early[rs] = 0;
         const float activity = static_cast<float>(active) / static_cast<float>(N);
         ctl->population_inhibition = clampf(
             ld(&ctl->population_inhibition) + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
@@ -1905,7 +2169,7 @@ __device__ __forceinline__ void load_slot(SlotInputs& in, __amdgpu_buffer_rsrc_t
 __device__ __forceinline__ void load_touched(SlotInputs& in, const StepCtx& c, uint32_t dst) {
     const uint32_t nb = c.a->cfg.neurons_per_block;
     const uint32_t blk = fast_div(dst, c.a->div_block), off = dst - blk * nb;
-    const uint32_t word = ld(&c.d.touched_bits[blk * block_words(nb) + off / 32]);
+    const uint32_t word = ld(&set_touched(c.d, set_of(c.d, c.tick))[blk * block_words(nb) + off / 32]);
     in.touched_epoch = (word >> (off & 31)) & 1u ? c.tick + 1 : 0u;
 }
 
@@ -2450,6 +2714,7 @@ __device__ __forceinline__ void phase_post(const StepCtx& c, const StepParams& s
     if (threadIdx.x == 0) {  // the next deliveries read this tick's ring entry from LDS
         sh.ring_tick[rs] = c.tick;
         sh.ring_count[rs] = A;
+        sh.ring_early[rs] = 0;
     }
     const uint32_t readout_wg = c.P - 1;
     if (c.part == readout_wg) {
@@ -2799,7 +3064,7 @@ __device__ __forceinline__ void phase_learn(const StepCtx& c, const StepParams& 
                 {  // the bitmap word this trace step kept for its eligibility update
                     const uint32_t nb = cfg.neurons_per_block;
                     const uint32_t blk = fast_div(n, a.div_block), off = n - blk * nb;
-                    d.touched_bits[blk * block_words(nb) + off / 32] = 0u;
+                    set_touched(d, set_of(d, c.tick))[blk * block_words(nb) + off / 32] = 0u;
                 }
                 if (bias_fail != kNoFail) continue;  // the failed step ends before homeostasis
                 const float local = ld(nf(d, n, kNActivation)) > 0.0f ? 1.0f : 0.0f;
@@ -2906,6 +3171,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
     if (threadIdx.x < kRing) {
         sh.ring_tick[threadIdx.x] = ld(&c.ctl->ring_tick[threadIdx.x]);
         sh.ring_count[threadIdx.x] = ld(&c.ctl->ring_count[threadIdx.x]);
+        sh.ring_early[threadIdx.x] = ld(&c.ctl->ring_early[threadIdx.x]);
     }
     __syncthreads();
     PhaseClock clock;
@@ -2930,10 +3196,13 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         return p;
     };
     if (steps > 0) fetch(0);
-    // a step whose delivery ran in the previous step's last phase, and the
-    // event count of that delivery (thread 0 of each workgroup)
-    bool delivered_ahead = false, stopped = false;
-    uint32_t pending_events = 0;
+    // a step whose delivery ran in the previous step's last phase; a step
+    // after a one-barrier frozen step (frozen_emit), and the population
+    // inhibition the last fold read
+    bool delivered_ahead = false, stopped = false, after_one_barrier = false;
+    float pi_read = 0.0f;
+    uint32_t early_prev = 0;  // kStepEarly delays of the one-barrier step before
+    const bool one_barrier_lane = c.d.bucket_sets != 1 && c.P > 1 && redundant;
     for (uint32_t s = 0; s < steps && ok; ++s) {
         const StepParams sp = params();
         if (s + 1 < steps) fetch(s + 1);
@@ -2947,9 +3216,6 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             if (c.part == c.P - 1) context_resolve(c, sp, sh);
             phase_deliver(c, sp, sh);
             if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 0))) break;
-        } else if (__lane_id() == 0 && pending_events != 0) {
-            // the previous step's write_active has rolled this tick's counters
-            atomicAdd(counter_word(c, c.part, kCEvents, c.tick), pending_events);
         }
         // this step's destination and learning-slot lists start empty (filled
         // by the eligibility phase) under a new claim epoch
@@ -2962,11 +3228,16 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
                 c.ctl->in_learn_count = 0;
             }
         }
+        // the previous tick's record and population inhibition after a
+        // one-barrier frozen step (before this step's context replaces the
+        // context fields that record reads)
+        const float pi =
+            after_one_barrier ? frozen_prologue(c, sh, s, pi_read, early_prev) : ld(&c.ctl->population_inhibition);
+        pi_read = pi;
         // the context of a step delivered ahead: on the workgroup that owns no
         // selection blocks, beside the fold (first read by the readout)
         if (delivered_ahead && c.P > 1 && c.part == c.P - 1) context_resolve(c, sp, sh);
-        phase_fold_select(c, sh, trace);
-        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 1))) break;
+        phase_fold_select(c, sh, trace, pi, after_one_barrier);
         // a fused step followed by a frozen one starts the next tick in its
         // last phase: the next delivery runs before this step's closing
         // barrier (one barrier fewer again)
@@ -2976,6 +3247,24 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             next = params();
             pipeline = (next.flags & kStepLearnTrace) == 0;
         }
+        // and with the bucket sets, a frozen step followed by a fused frozen
+        // one takes a single phase (its delay-1 events are early: the host
+        // marks the delays of every launched step)
+        if (one_barrier_lane && pipeline && !(next.flags & kStepOutput) && (sp.flags & (1u << kStepEarlyShift))) {
+            early_prev = (sp.flags & kStepEarlyMask) >> kStepEarlyShift;
+            frozen_emit(c, sh, early_prev, next);
+            // after a two-phase step, the roll its successor's active-list
+            // phase would make: that step's record is finished and the
+            // counters tick+1 reuses are cleared (a one-barrier step's
+            // prologue did both)
+            if (!after_one_barrier && c.part == c.P - 1 && wave_index() == 0) roll_counters(c, s);
+            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 6))) break;
+            delivered_ahead = true;
+            after_one_barrier = true;
+            c.tick += 1;
+            continue;
+        }
+        if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 1))) break;
         // An output step's readout runs on the last workgroup beside the
         // eligibility update, which the other workgroups share (a lane of one
         // workgroup runs both), so a plasticity step computes its signals in
@@ -2985,12 +3274,9 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         const bool reader = output && c.part == c.P - 1;
         const uint32_t elig_stride = output && c.P > 1 ? (c.P - 1) * kThreads : c.gstride;
         if (redundant) {
-            const uint32_t delivered = write_active(c, sp, s, sh, fused, pipeline, next);
+            write_active(c, sp, s, sh, fused, pipeline, next, after_one_barrier);
             if (trace && !(reader && c.P > 1)) phase_eligibility(c, plastic, elig_stride);
-            if (pipeline) {
-                if (c.P == 1) context_resolve(c, next, sh);
-                pending_events = wave_sum_u32(delivered);
-            }
+            if (pipeline && c.P == 1) context_resolve(c, next, sh);
         } else {
             global_select(c, sh, s);
             if (trace || output) {  // the readout reads the global selection's list
@@ -3022,6 +3308,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             }
         }
         delivered_ahead = pipeline;
+        after_one_barrier = false;
         c.tick += 1;
     }
     if (ok && !stopped && c.part == 0 && threadIdx.x < kWaveSize && steps > 0)
@@ -3156,9 +3443,32 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
     for (uint64_t i = t0; i < NI; i += ts) d.in_mark[i] = 0;
     for (uint64_t i = t0; i < cfg.context_embedding_dim; i += ts) d.ctx_latent[i] = 0.0f;
     fill_u32(d.block_epoch, cfg.block_count, 0u, t0, ts);
-    fill_u32(d.touched_bits, static_cast<uint64_t>(cfg.block_count) * block_words(cfg.neurons_per_block), 0u, t0, ts);
+    {
+        // bucket counts and touched bits of every set (deliveries pending for
+        // later ticks are dropped): a nonzero count always has its target's
+        // bit set, as a tick's first delivery to a target touches it, so the
+        // set bits name every count to clear
+        const uint32_t nb = cfg.neurons_per_block, wpb = block_words(nb);
+        const uint64_t words = static_cast<uint64_t>(cfg.block_count) * wpb;
+        for (uint32_t set = 0; set < d.bucket_sets; ++set) {
+            uint32_t LEO_GLOBAL* bits = set_touched(d, set);
+            uint32_t LEO_GLOBAL* counts = set_counts(d, set, cfg.neuron_count);
+            for (uint64_t w = t0; w < words; w += ts) {
+                uint32_t v = bits[w];
+                if (v == 0) continue;
+                const uint64_t blk = w / wpb, base = blk * nb + (w - blk * wpb) * 32;
+                while (v) {
+                    const uint32_t b = __ffs(v) - 1;
+                    v &= v - 1;
+                    counts[base + b] = 0u;
+                }
+                bits[w] = 0u;
+            }
+        }
+    }
     for (uint64_t i = t0; i < kMaxWaves; i += ts) {
         d.wave_total[i] = 0;
+        d.wave_total[kMaxWaves + i] = 0;
         d.wave_touched[i] = 0;
     }
     for (uint64_t i = t0; i < kMaxLaneWgs * kFlagWords; i += ts) d.wg_counts[i] = 0;
@@ -3185,6 +3495,7 @@ __global__ void __launch_bounds__(kThreads) leo_reset_lanes(KernelArgs args, uin
         for (uint32_t k = 0; k < kRing; ++k) {
             ctl->ring_tick[k] = 0xffffffffu;
             ctl->ring_count[k] = 0;
+            ctl->ring_early[k] = 0;
         }
     }
 }

@@ -304,6 +304,10 @@ struct LeoHipRuntime {
     bool local_sync = true;
     LeoKernelStats telemetry{};
     bool phase_profile = false;
+    // delivery bucket sets of the canonical lane: kBucketSets lets its frozen
+    // runs take one barrier per step; 1 (LEO_HIP_BUCKET_SETS=1, or too little
+    // device memory) keeps two
+    uint32_t canonical_sets = leo::kBucketSets;
     uint32_t profile_part = 0;  // LEO_HIP_PROFILE_PART: the workgroup of each lane the phase profile times
     double wall_clock_khz = 0.0;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
@@ -429,18 +433,36 @@ void broadcast_params(LeoHipRuntime* h, const std::vector<Lane*>& lanes) {
     }
 }
 
-void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
+// Bytes of one delivery bucket set (entries, counts, touched bitmap).
+size_t bucket_set_bytes(const Sizes& z) {
+    return static_cast<size_t>(2 * z.bucket_total) * 8 + static_cast<size_t>(z.n) * 4 +
+           static_cast<size_t>(z.blocks * z.block_words) * 4;
+}
+
+// Bucket sets of the canonical lane: the extra sets take at most a quarter
+// of the free device memory.
+uint32_t canonical_bucket_sets(const LeoHipRuntime* h) {
+    if (h->canonical_sets == 1) return 1;
+    size_t free_bytes = 0, total_bytes = 0;
+    LEO_HIP_CHECK(hipMemGetInfo(&free_bytes, &total_bytes));
+    return (kBucketSets - 1) * bucket_set_bytes(h->z) <= free_bytes / 4 ? kBucketSets : 1u;
+}
+
+// Lane state with `sets` delivery bucket sets (1, or kBucketSets for a lane
+// that takes frozen runs with one barrier per step).
+void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream, uint32_t sets = 1) {
     Layout l;
     size_t o_ctl = l.add<LaneControl>(1), o_flag = l.add<uint32_t>(kMaxLaneWgs * kFlagWords);
     size_t o_cnt = l.add<uint32_t>(kMaxLaneWgs * kFlagWords);
     size_t o_neu = l.add<uint32_t>(kNeuronWords * z.n), o_tl = l.add<uint32_t>(z.n);
-    size_t o_ls = l.add<float>(z.n), o_dl = l.add<uint32_t>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total);
+    size_t o_ls = l.add<float>(z.n), o_dl = l.add<uint32_t>(z.n), o_bk = l.add<uint64_t>(2 * z.bucket_total * sets);
+    size_t o_bc = l.add<uint32_t>(z.n * sets);
     size_t o_rl = l.add<uint32_t>(z.ns), o_il = l.add<uint32_t>(z.ni);
     size_t o_sh = l.add<uint64_t>(2 * std::max<uint64_t>(z.shadow_total, 1));
     size_t o_bw = l.add<uint32_t>(z.blocks * z.limit), o_bcut = l.add<float>(z.blocks);
     size_t o_bwa = l.add<float>(z.blocks * z.limit);
-    size_t o_wt = l.add<uint32_t>(kMaxWaves), o_wtt = l.add<uint32_t>(kMaxWaves);
-    size_t o_bep = l.add<uint32_t>(z.blocks), o_tb = l.add<uint32_t>(z.blocks * z.block_words);
+    size_t o_wt = l.add<uint32_t>(2 * kMaxWaves), o_wtt = l.add<uint32_t>(kMaxWaves);
+    size_t o_bep = l.add<uint32_t>(z.blocks), o_tb = l.add<uint32_t>(z.blocks * z.block_words * sets);
     size_t o_ra = l.add<uint32_t>(kRing * z.cap), o_rv = l.add<float>(kRing * z.cap), o_rval = l.add<float>(kRing * z.cap * z.s);
     size_t o_redge = l.add<uint32_t>(kRing * z.cap * z.s);
     size_t o_rt = l.add<float>(kTraceWords * z.ns), o_rm = l.add<uint8_t>(z.ns), o_rlist = l.add<uint32_t>(2 * z.ns);
@@ -465,6 +487,10 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream) {
     d.rec_learn = reinterpret_cast<uint32_t*>(b + o_rl);
     d.in_learn = reinterpret_cast<uint32_t*>(b + o_il);
     d.bucket = reinterpret_cast<uint64_t*>(b + o_bk);
+    d.bucket_count = reinterpret_cast<uint32_t*>(b + o_bc);
+    d.bucket_stride = 2 * z.bucket_total;
+    d.bucket_sets = sets;
+    d.touched_stride = static_cast<uint32_t>(z.blocks * z.block_words);
     d.range_winners = reinterpret_cast<uint32_t*>(b + o_bw);
     d.range_winner_act = reinterpret_cast<float*>(b + o_bwa);
     d.block_cutoff = reinterpret_cast<float*>(b + o_bcut);
@@ -897,6 +923,16 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
         lane.desc.records = reinterpret_cast<StepRecord*>(
             lane.schedule.base + ((static_cast<size_t>(lane.schedule_capacity) * sizeof(StepParams) + 255) & ~size_t(255)));
         lane.desc.step_count = static_cast<uint32_t>(r.steps.size());
+        // the delays whose events a step's tick may deliver at emission: the
+        // arrival step is in this launch and runs no learning trace
+        for (size_t i = 0; i < r.steps.size(); ++i) {
+            uint32_t early = 0;
+            for (uint32_t dl = 0; dl < 4; ++dl) {
+                const size_t at = i + (size_t(1) << dl);
+                if (at < r.steps.size() && !(r.steps[at].flags & kStepLearnTrace)) early |= 1u << dl;
+            }
+            r.steps[i].flags = (r.steps[i].flags & ~static_cast<uint32_t>(kStepEarlyMask)) | (early << kStepEarlyShift);
+        }
         h->staging.h2d(const_cast<StepParams*>(lane.desc.steps), r.steps.data(), r.steps.size() * sizeof(StepParams));
         // cleared on the transfer stream, after the previous launch's
         // control words have been downloaded there; the error word only once
@@ -2448,6 +2484,8 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         if (const char* env = std::getenv("LEO_HIP_MAX_STEPS_PER_LAUNCH"))
             h->max_steps_override = static_cast<uint32_t>(std::max(1, std::atoi(env)));
         if (const char* env = std::getenv("LEO_HIP_PHASE_PROFILE")) h->phase_profile = std::atoi(env) != 0;
+        if (const char* env = std::getenv("LEO_HIP_BUCKET_SETS"))
+            h->canonical_sets = std::atoi(env) == 1 ? 1u : leo::kBucketSets;
         if (const char* env = std::getenv("LEO_HIP_PROFILE_PART"))
             h->profile_part = static_cast<uint32_t>(std::max(0, std::atoi(env)));
         int clock_khz = 0;
@@ -2457,7 +2495,7 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         h->canon = leo::allocate_params(h->canon_params, h->z, h->stream);
         leo::upload_model(h.get(), *model);
         h->canonical = std::make_unique<leo::Lane>();
-        leo::allocate_lane_state(*h->canonical, h->z, h->stream);
+        leo::allocate_lane_state(*h->canonical, h->z, h->stream, leo::canonical_bucket_sets(h.get()));
         h->canonical->desc.p = h->canon;
         leo::allocate_stale(h.get());
         (void)leo::static_scratch(device);  // set-up of the allocation-free entry point on this device
@@ -2690,7 +2728,7 @@ int32_t leo_hip_upload_model(LeoHipRuntime* h, const LeoModelView* model) {
         h->lanes.clear();
         leo::LaneParams p = h->canon;
         uint32_t tick = h->canonical->tick;
-        leo::allocate_lane_state(*h->canonical, h->z, h->stream);
+        leo::allocate_lane_state(*h->canonical, h->z, h->stream, leo::canonical_bucket_sets(h));
         h->canonical->desc.p = p;
         std::vector<leo::Lane*> lanes{h->canonical.get()};
         leo::reset_lane_objects(h, lanes, true, tick);

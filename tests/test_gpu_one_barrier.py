@@ -1,0 +1,86 @@
+"""One-barrier frozen runs on the canonical lane.
+
+With its kBucketSets delivery bucket sets, the canonical lane runs a frozen
+step that is followed by a fused frozen step as a single phase: the winners'
+events go into the bucket set of their arrival tick when they are emitted
+(up to 8 ticks ahead), keyed by staged position instead of active-list rank,
+their post-fire updates wait for the next fold, and the step record is
+written by the next phase. Events whose arrival step runs a learning trace, or
+lies past the launch, go through the ring as before.
+
+Timelines of frozen runs of every length around the 1/2/4/8 delays, with
+supervised steps between them and launches cut at several lengths, must give
+the oracle's metrics, touched counts and model (runtime.rs:537-1106), and the
+same work counters as the two-phase step loop (LEO_HIP_BUCKET_SETS=1)."""
+from __future__ import annotations
+
+import pytest
+
+from leo_amd import native
+from leo_amd.model import BEGIN_DOCUMENT, END_DOCUMENT, Model
+from tests.helpers import assert_models_equal, small_redundant_config, story
+
+pytestmark = pytest.mark.gpu
+
+# frozen run lengths between supervised pairs: each side of the 1, 2, 4 and 8
+# tick delays, a lone frozen step, none, and a long run
+FROZEN_RUNS = [1, 2, 3, 4, 5, 7, 8, 9, 16, 0, 1, 30]
+COUNTERS = ("lane_steps", "events", "touched", "active", "scanned_rec", "scanned_in", "kept_rec", "kept_in",
+            "destinations", "active_inhibitory", "learning_slots", "deep_register_folds", "deep_radix_folds")
+
+
+def _timeline(text: bytes):
+    steps = [(BEGIN_DOCUMENT, text[0])] + [(text[i], text[i + 1]) for i in range(len(text) - 1)]
+    steps.append((text[-1], END_DOCUMENT))
+    timeline, at = [], 0
+    for run in FROZEN_RUNS:
+        for _ in range(run):
+            if at < len(steps):
+                timeline.append((steps[at][0], None))
+                at += 1
+        for _ in range(2):
+            if at < len(steps):
+                timeline.append(steps[at])
+                at += 1
+    timeline += [(s, None) for s, _ in steps[at:]]  # a frozen tail to the launch's end
+    return timeline
+
+
+@pytest.mark.parametrize("launch_steps", [None, 6, 13])
+def test_one_barrier_frozen_runs_match_oracle_and_two_phase(require_gpu, oracle, monkeypatch, launch_steps):
+    from leo_amd.runtime import HipRuntime
+
+    model = Model.initialize(small_redundant_config())
+    timeline = _timeline(story(5, 140))
+    assert sum(1 for _, t in timeline if t is None) > 100
+    cpu = oracle.OracleRuntime(model)
+    cpu.begin_document()
+    want, touched = [], 0
+    for s, t in timeline:
+        m = cpu.step(s, t, oracle.TRAINING if t is not None else oracle.FROZEN)
+        touched += len(cpu.read_list("touched"))
+        if t is not None:
+            want.append(m)
+    if launch_steps:
+        monkeypatch.setenv("LEO_HIP_MAX_STEPS_PER_LAUNCH", str(launch_steps))
+    stats = {}
+    for sets in ("9", "1"):
+        monkeypatch.setenv("LEO_HIP_BUCKET_SETS", sets)
+        print(f"{len(timeline)} steps, bucket sets {sets}, launches of {launch_steps or 'any'} steps", flush=True)
+        gpu = HipRuntime(model, device=0, max_lanes=1)
+        try:
+            gpu.begin_document()
+            gpu.kernel_stats(reset=True)
+            got = gpu.replay_streaming_batch(timeline, native.TRAINING)
+            assert len(got) == len(want)
+            for i, (g, c) in enumerate(zip(got, want)):
+                assert g.loss == c.loss and g.active_neurons == c.active_neurons, (sets, i)
+                assert g.predicted_symbol == c.predicted_symbol, (sets, i)
+                assert g.population_inhibition == c.population_inhibition, (sets, i)
+            assert_models_equal(gpu.model(), cpu.model(), f"bucket sets {sets}")
+            stats[sets] = gpu.kernel_stats()
+        finally:
+            gpu.close()
+        assert stats[sets]["touched"] == touched, sets
+    for key in COUNTERS:
+        assert stats["9"][key] == stats["1"][key], key
