@@ -3096,6 +3096,8 @@ struct PhaseClock {
         last = wall_clock64();
         out[kPhases + phase] += last - arrived;
     }
+    // a section inside a phase, [from, to), added to slot `slot`
+    __device__ void section(uint32_t slot, unsigned long long from, unsigned long long to) { out[slot] += to - from; }
 };
 
 template <bool kProfile>
@@ -3231,13 +3233,20 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         // the previous tick's record and population inhibition after a
         // one-barrier frozen step (before this step's context replaces the
         // context fields that record reads)
+        // the profiling build times a one-barrier step's prologue, context
+        // and fold in the slots of the phases such a step does not run
+        const bool timer = kProfile && c.part == args.profile_part && threadIdx.x == 0;
+        const unsigned long long t_start = timer ? wall_clock64() : 0;
         const float pi =
             after_one_barrier ? frozen_prologue(c, sh, s, pi_read, early_prev) : ld(&c.ctl->population_inhibition);
         pi_read = pi;
+        const unsigned long long t_prologue = timer ? wall_clock64() : 0;
         // the context of a step delivered ahead: on the workgroup that owns no
         // selection blocks, beside the fold (first read by the readout)
         if (delivered_ahead && c.P > 1 && c.part == c.P - 1) context_resolve(c, sp, sh);
+        const unsigned long long t_context = timer ? wall_clock64() : 0;
         phase_fold_select(c, sh, trace, pi, after_one_barrier);
+        const unsigned long long t_fold = timer ? wall_clock64() : 0;
         // a fused step followed by a frozen one starts the next tick in its
         // last phase: the next delivery runs before this step's closing
         // barrier (one barrier fewer again)
@@ -3252,6 +3261,11 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         // marks the delays of every launched step)
         if (one_barrier_lane && pipeline && !(next.flags & kStepOutput) && (sp.flags & (1u << kStepEarlyShift))) {
             early_prev = (sp.flags & kStepEarlyMask) >> kStepEarlyShift;
+            if (timer) {
+                clock.section(3, t_start, t_prologue);
+                clock.section(4, t_prologue, t_context);
+                clock.section(5, t_context, t_fold);
+            }
             frozen_emit(c, sh, early_prev, next);
             // after a two-phase step, the roll its successor's active-list
             // phase would make: that step's record is finished and the
