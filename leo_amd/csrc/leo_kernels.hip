@@ -548,6 +548,32 @@ __device__ __forceinline__ void roll_counters(const StepCtx& c, uint32_t step_in
     clear_counters(c, c.tick);
 }
 
+// The selecting waves' winner totals of one tick: `all`, and `before` those of
+// the waves below wv, by a whole wave (uniform). Up to 256 waves' totals are
+// loaded in one round, and each lane's partial sums are reduced once.
+__device__ __forceinline__ void sum_totals(const uint32_t LEO_GLOBAL* totals, uint32_t nwaves, uint32_t wv,
+                                           uint32_t& all, uint32_t& before) {
+    constexpr uint32_t kAtOnce = 4;
+    const uint32_t lane = __lane_id();
+    all = before = 0;
+    for (uint32_t base = 0; base < nwaves; base += kAtOnce * kWaveSize) {
+        uint32_t v[kAtOnce];
+#pragma unroll
+        for (uint32_t k = 0; k < kAtOnce; ++k) {
+            const uint32_t w = base + k * kWaveSize + lane;
+            v[k] = w < nwaves ? ld(&totals[w]) : 0u;
+        }
+        uint32_t a = 0, b = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < kAtOnce; ++k) {
+            a += v[k];
+            b += base + k * kWaveSize + lane < wv ? v[k] : 0u;
+        }
+        all += wave_sum_u32(a);
+        before += wave_sum_u32(b);
+    }
+}
+
 // The bucket set of the deliveries of `tick` (LaneDesc::bucket_sets).
 __device__ __forceinline__ uint32_t set_of(const LaneDesc& d, uint32_t tick) {
     return d.bucket_sets == 1 ? 0u : tick % kBucketSets;
@@ -1688,12 +1714,7 @@ __device__ __forceinline__ void write_active(const StepCtx& c, const StepParams&
         edge0 = c.a->m.rec_edge[slot];
     }
     uint32_t before = 0, all = 0;
-    for (uint32_t base = 0; base < nwaves; base += kWaveSize) {
-        const uint32_t w = base + lane;
-        const uint32_t v = w < nwaves ? ld(&wave_totals(d, c.tick)[w]) : 0;
-        before += wave_sum_u32(w < wv ? v : 0);
-        all += wave_sum_u32(v);
-    }
+    sum_totals(wave_totals(d, c.tick), nwaves, wv, all, before);
     uint32_t* act_list = d.ring_active + static_cast<uint64_t>(rs) * cap + before;
     float* act_val = d.ring_act + static_cast<uint64_t>(rs) * cap + before;
     for (uint32_t i = lane; i < mine; i += kWaveSize) {
@@ -1901,12 +1922,7 @@ __device__ __forceinline__ float frozen_prologue(const StepCtx& c, StepShared& s
     const uint32_t wv = c.part * kWavesPerGroup + wave;
     const uint32_t LEO_GLOBAL* totals = wave_totals(d, prev);
     uint32_t all = 0, before = 0;
-    for (uint32_t base = 0; base < nwaves; base += kWaveSize) {
-        const uint32_t w = base + lane;
-        const uint32_t v = w < nwaves ? ld(&totals[w]) : 0u;
-        all += wave_sum_u32(v);
-        before += wave_sum_u32(w < wv ? v : 0u);
-    }
+    sum_totals(totals, nwaves, wv, all, before);
     const uint32_t rs = prev % kRing;
     if (early != 0xfu && wv < nwaves) {
         // some delays' events go through the ring: the tick's active list
