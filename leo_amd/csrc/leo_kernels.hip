@@ -258,13 +258,25 @@ __device__ __forceinline__ uint32_t xcc_id() {
 
 // Barrier of the P workgroups of one lane; false when the lane aborted
 // (another workgroup's wait timed out or the host's spin limit ran out).
-// Workgroups on one XCD (`local`) share its L2: each stores its arrival epoch
-// to a flag of its own 128-byte line, and the first wave polls the P flags,
-// one lane per flag, so that arrivals and polls spread over the L2 channels
-// (a shared counter queues every arrival atomic and every poll on one
-// channel: measured, a frozen step at 32 workgroups took 10% longer). A lane
-// spread over several XCDs counts arrivals with a device-scope atomic counter
+// Workgroups on one XCD (`local`) share its L2: each stores its arrival word
+// to its own 128-byte line, and the first wave polls the P lines, one lane
+// per line, so that arrivals and polls spread over the L2 channels (a shared
+// counter queues every arrival atomic and every poll on one channel:
+// measured, a frozen step at 32 workgroups took 10% longer). A lane spread
+// over several XCDs counts arrivals with a device-scope atomic counter
 // between release and acquire fences.
+//
+// An arrival word is (epoch << 16) | carry, where epoch is the barrier's
+// number modulo 2^16 and carry the sum of `carries` (LDS, one value per wave,
+// 16 bits in all). Each workgroup has two words, used by the epoch's parity:
+// a workgroup can be at most one barrier ahead of a poller (it passes a
+// barrier only once every workgroup has arrived), so the word of the polled
+// parity holds the polled epoch or the one two before it, and the carry read
+// with the epoch is that barrier's. With `sums` (LDS, 1 + kWavesPerGroup
+// words, read after the barrier), the polling wave writes the sum of every
+// workgroup's carry to sums[0] and, for wave k of this workgroup, the sum of
+// the carries before it in lane order (the workgroups before this one, then
+// this one's waves before k) to sums[1 + k].
 //
 // Visibility. With `local` (all workgroups of the lane verified to run on one
 // XCD, and every cross-workgroup read done with ld()), waiting until this
@@ -273,7 +285,8 @@ __device__ __forceinline__ uint32_t xcc_id() {
 // the L2 so other XCDs see the data. The wait is bounded: on timeout the lane
 // is aborted, so every workgroup leaves the step loop and the grid drains.
 __device__ __forceinline__ bool lane_barrier(const LaneDesc& d, uint32_t part, uint32_t P, uint32_t& target,
-                                             uint32_t spin_limit, bool local) {
+                                             uint32_t spin_limit, bool local, const uint32_t* carries = nullptr,
+                                             uint32_t* sums = nullptr) {
     __shared__ uint32_t s_abort;
     LaneControl* ctl = d.ctl;
     if (P == 1) {
@@ -284,17 +297,43 @@ __device__ __forceinline__ bool lane_barrier(const LaneDesc& d, uint32_t part, u
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         target += P;  // every thread keeps the count (the polling wave compares against it)
-        const uint32_t epoch = __builtin_amdgcn_readfirstlane(target / P);
+        const uint32_t epoch = __builtin_amdgcn_readfirstlane(target / P) & 0xffffu, parity = epoch & 1u;
         if (threadIdx.x < kWaveSize) {
             const uint32_t lane = threadIdx.x;
             uint32_t LEO_GLOBAL* flags = d.barrier_flags;
+            uint32_t carry = 0;
+            if (carries) {
+#pragma unroll
+                for (uint32_t k = 0; k < kWavesPerGroup; ++k) carry += carries[k];
+            }
             if (lane == 0)
-                __hip_atomic_store(&flags[part * kFlagWords], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&flags[part * kFlagWords + parity], (epoch << 16) | (carry & 0xffffu),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             uint32_t spins = 0, aborted = 0;
             for (;;) {
                 bool arrived = true;
-                for (uint32_t w = lane; w < P; w += kWaveSize) arrived &= ld(&flags[w * kFlagWords]) >= epoch;
-                if (__all(arrived)) break;
+                uint32_t all = 0, before = 0;
+                for (uint32_t w = lane; w < P; w += kWaveSize) {
+                    const uint32_t v = ld(&flags[w * kFlagWords + parity]);
+                    arrived &= (v >> 16) == epoch;
+                    all += v & 0xffffu;
+                    before += w < part ? v & 0xffffu : 0u;
+                }
+                if (__all(arrived)) {
+                    if (sums) {
+                        all = wave_sum_u32(all);
+                        before = wave_sum_u32(before);
+                        if (lane == 0) {
+                            sums[0] = all;
+#pragma unroll
+                            for (uint32_t k = 0; k < kWavesPerGroup; ++k) {
+                                sums[1 + k] = before;
+                                before += carries[k];
+                            }
+                        }
+                    }
+                    break;
+                }
                 if ((spins & 15) == 15 && ld(&ctl->abort) != 0) {
                     aborted = 1;
                     break;
@@ -381,6 +420,9 @@ __device__ __forceinline__ uint64_t selection_key(float act, uint32_t tie) {
 }
 __device__ __forceinline__ float key_activation(uint64_t key) { return __uint_as_float(~static_cast<uint32_t>(key >> 32)); }
 
+// Steps whose parameters one load round brings into LDS.
+constexpr uint32_t kStepChunk = 64;
+
 // Shared memory of the step kernel, reused phase by phase.
 struct alignas(16) StepShared {
     float err[kOutStride];                                      // errors / logits
@@ -403,6 +445,12 @@ struct alignas(16) StepShared {
     uint32_t win_count[kWavesPerGroup];
     uint32_t win_n[kWavesPerGroup][kWaveSize];
     float win_act[kWavesPerGroup][kWaveSize];
+    // the winner totals a one-barrier step's barrier carries: every wave's,
+    // and those of the workgroups before this one (lane_barrier)
+    uint32_t lane_sums[1 + kWavesPerGroup];
+    // the step parameters of kStepChunk + 1 steps from a multiple of
+    // kStepChunk on (the last one is the next chunk's first)
+    uint32_t step_chunk[(kStepChunk + 1) * (sizeof(StepParams) / 4)];
 };
 
 // Dynamic LDS (step_lds_bytes): one phase-2 window per wave (Window below);
@@ -421,6 +469,7 @@ struct StepCtx {
     uint32_t parity;   // current eligible list
     uint32_t dest_epoch;
     bool local;        // workgroups of the lane share one L2 (see lane_barrier)
+    bool carried;      // a one-barrier step's barrier carries the waves' winner totals
 };
 
 // This thread's item index when a phase's items are dealt 64 at a time to the
@@ -599,17 +648,31 @@ __device__ __forceinline__ uint64_t bucket_entry(uint64_t overflow, uint32_t n, 
 }
 
 // One delivery into target's bucket of `set` (the fold of phase 2 orders the
-// bucket by key); true when it is the target's first delivery of the tick.
-__device__ __forceinline__ bool scatter_event(const StepCtx& c, uint32_t set, uint32_t target, uint64_t key,
-                                              float value) {
-    // the overflow offset is loaded with the counter increment (one round trip)
-    const uint64_t overflow = c.a->m.bucket_offset[target];
-    const uint32_t p = atomicAdd(set_counts(c.d, set, c.a->cfg.neuron_count) + target, 1u);
-    const uint64_t at = bucket_entry(overflow, target, p);
+// bucket by key), in two parts so that a thread can claim several entries in
+// one round: the claim of an entry (the target's overflow offset, loaded with
+// the counter increment) and its write. The write tells whether it is the
+// target's first delivery of the tick.
+struct EntryClaim {
+    uint64_t overflow;
+    uint32_t p;
+};
+__device__ __forceinline__ EntryClaim claim_entry(const StepCtx& c, uint32_t set, uint32_t target) {
+    EntryClaim k;
+    k.overflow = c.a->m.bucket_offset[target];
+    k.p = atomicAdd(set_counts(c.d, set, c.a->cfg.neuron_count) + target, 1u);
+    return k;
+}
+__device__ __forceinline__ bool write_entry(const StepCtx& c, uint32_t set, uint32_t target, const EntryClaim& k,
+                                            uint64_t key, float value) {
+    const uint64_t at = bucket_entry(k.overflow, target, k.p);
     uint64_t LEO_GLOBAL* bucket = set_bucket(c.d, set);
     bucket[2 * at] = key;
     bucket[2 * at + 1] = __float_as_uint(value);
-    return p == 0;
+    return k.p == 0;
+}
+__device__ __forceinline__ bool scatter_event(const StepCtx& c, uint32_t set, uint32_t target, uint64_t key,
+                                              float value) {
+    return write_entry(c, set, target, claim_entry(c, set, target), key, value);
 }
 
 // Touched mark of neuron n at `tick`: the block's bitmap bit in the tick's
@@ -1883,25 +1946,65 @@ __device__ __forceinline__ void frozen_emit(const StepCtx& c, StepShared& sh, ui
     // every synapse of every winner whose delay is early (runtime.rs:1084-1106
     // emits them into the ring; the value is the snapshot the ring would
     // hold); the other delays' events stay for the ring, which the next
-    // phase's prologue fills
+    // phase's prologue fills. A lane takes up to kEmitBatch events per round
+    // of memory operations (their synapse loads, then their bucket claims,
+    // then their entry writes), and the first round also claims the bucket
+    // entry of its next-tick injection, whose loads went out above.
+    constexpr uint32_t kEmitBatch = 4;
     const uint32_t items = early ? mine * S : 0u;
-    for (uint32_t item = lane; item < items; item += kWaveSize) {
-        const uint32_t r = fast_div(item, c.a->div_synapses), j = item - r * S;
-        uint32_t n;
-        float act;
-        winner(r, n, act);
-        const uint64_t slot = static_cast<uint64_t>(n) * S + j;
-        const float value = act * ld(&d.p.rec_weight[slot]);
-        const uint32_t edge = c.a->m.rec_edge[slot];
-        const uint32_t dl = (edge >> kEdgeTargetBits) & 3u;  // delay 1 << dl, delivery class 3 - dl
-        if ((early & (1u << dl)) == 0) continue;
-        const uint32_t arrival = c.tick + (1u << dl);
-        const uint64_t key = (static_cast<uint64_t>(3u - dl) << 61) | ((row0 + r) << 32) |
-                             (static_cast<uint64_t>(j) << 2) | edge_branch(edge);
-        if (scatter_event(c, set_of(d, arrival), edge_target(edge), key, value))
-            touch_neuron(c, edge_target(edge), arrival);
+    const bool inj0 = np.delivers && item0.inj;
+    const uint32_t inj_set = set_of(d, c.tick + 1);
+    const uint32_t rounds = items > 0 ? (items + kEmitBatch * kWaveSize - 1) / (kEmitBatch * kWaveSize) : 1u;
+    for (uint32_t round = 0; round < rounds; ++round) {
+        const uint32_t base = round * kEmitBatch * kWaveSize;
+        uint32_t edge[kEmitBatch], rj[kEmitBatch];
+        float value[kEmitBatch];
+        bool live[kEmitBatch];
+#pragma unroll
+        for (uint32_t k = 0; k < kEmitBatch; ++k) {
+            const uint32_t item = base + k * kWaveSize + lane;
+            live[k] = item < items;
+            edge[k] = 0;
+            value[k] = 0.0f;
+            rj[k] = 0;
+            if (live[k]) {
+                const uint32_t r = fast_div(item, c.a->div_synapses), j = item - r * S;
+                uint32_t n;
+                float act;
+                winner(r, n, act);
+                const uint64_t slot = static_cast<uint64_t>(n) * S + j;
+                value[k] = act * ld(&d.p.rec_weight[slot]);
+                edge[k] = c.a->m.rec_edge[slot];
+                rj[k] = item;
+            }
+        }
+        EntryClaim claim[kEmitBatch];
+        uint32_t set[kEmitBatch];
+#pragma unroll
+        for (uint32_t k = 0; k < kEmitBatch; ++k) {
+            const uint32_t dl = (edge[k] >> kEdgeTargetBits) & 3u;  // delay 1 << dl, delivery class 3 - dl
+            live[k] = live[k] && (early & (1u << dl)) != 0;
+            set[k] = set_of(d, c.tick + (1u << dl));
+            if (live[k]) claim[k] = claim_entry(c, set[k], edge_target(edge[k]));
+        }
+        EntryClaim inj{};
+        const bool inj_here = round == 0 && inj0;
+        if (inj_here) inj = claim_entry(c, inj_set, item0.target);
+#pragma unroll
+        for (uint32_t k = 0; k < kEmitBatch; ++k) {
+            if (!live[k]) continue;
+            const uint32_t dl = (edge[k] >> kEdgeTargetBits) & 3u;
+            const uint32_t r = fast_div(rj[k], c.a->div_synapses), j = rj[k] - r * S;
+            const uint64_t key = (static_cast<uint64_t>(3u - dl) << 61) | ((row0 + r) << 32) |
+                                 (static_cast<uint64_t>(j) << 2) | edge_branch(edge[k]);
+            if (write_entry(c, set[k], edge_target(edge[k]), claim[k], key, value[k]))
+                touch_neuron(c, edge_target(edge[k]), c.tick + (1u << dl));
+        }
+        if (inj_here && write_entry(c, inj_set, item0.target, inj, item0.key, item0.value))
+            touch_neuron(c, item0.target, c.tick + 1);
     }
     uint32_t delivered = 0;  // counted by the fold
+    item0.inj = item0.inj && !inj0;  // an injection claimed above is done
     if (np.delivers) deliver_commit(c, next, np, item0, delivered);
     deliver_items(c, next, np, dealt + np.stride, delivered);
     count_wave(c, kCInhibitory, c.tick, inhibitory);
@@ -1920,9 +2023,14 @@ __device__ __forceinline__ float frozen_prologue(const StepCtx& c, StepShared& s
     const LaneDesc& d = c.d;
     const uint32_t prev = c.tick - 1, nwaves = selecting_waves(c), lane = __lane_id(), wave = wave_index();
     const uint32_t wv = c.part * kWavesPerGroup + wave;
-    const uint32_t LEO_GLOBAL* totals = wave_totals(d, prev);
     uint32_t all = 0, before = 0;
-    sum_totals(totals, nwaves, wv, all, before);
+    if (c.carried) {
+        // from the barrier: the lane's total and the waves before this one
+        all = sh.lane_sums[0];
+        before = sh.lane_sums[1 + wave];
+    } else {
+        sum_totals(wave_totals(d, prev), nwaves, wv, all, before);
+    }
     const uint32_t rs = prev % kRing;
     if (early != 0xfu && wv < nwaves) {
         // some delays' events go through the ring: the tick's active list
@@ -3118,11 +3226,12 @@ struct PhaseClock {
 
 template <bool kProfile>
 __device__ __forceinline__ bool phase_barrier(const StepCtx& c, uint32_t& target, uint32_t spin_limit,
-                                              PhaseClock& clock, uint32_t phase) {
+                                              PhaseClock& clock, uint32_t phase, const uint32_t* carries = nullptr,
+                                              uint32_t* sums = nullptr) {
     unsigned long long arrived = 0;
     const bool timer = kProfile && c.part == c.a->profile_part && threadIdx.x == 0;
     if (timer) clock.arrive(phase, arrived);
-    const bool ok = lane_barrier(c.d, c.part, c.P, target, spin_limit, c.local);
+    const bool ok = lane_barrier(c.d, c.part, c.P, target, spin_limit, c.local, carries, sums);
     if (timer) clock.release(phase, arrived);
     return ok;
 }
@@ -3150,7 +3259,12 @@ __device__ __forceinline__ LaneDesc load_uniform(const LaneDesc* p) {
     return out;
 }
 
-template <bool kProfile>
+// kFrozenOnly: every step of the launch is a frozen step without output and
+// the global cap cannot bind (the host checks both); the steps' flags say so
+// at compile time, so the kernel carries none of the learning, readout,
+// eligibility and global-selection code (a smaller program and register set
+// for the serial replay prefix).
+template <bool kProfile, bool kFrozenOnly>
 __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
     __shared__ StepShared sh;
     const uint32_t stride = args.lane_stride, P = args.wgs_per_lane;
@@ -3174,17 +3288,21 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
     c.local = false;
     uint32_t target = 0;
     const uint32_t steps = c.d.step_count;
-    const bool redundant = args.redundant_global != 0;
+    const bool redundant = kFrozenOnly || args.redundant_global != 0;
     const uint32_t spin = args.spin_limit;
     if (P > 1 && args.local_sync) {
-        // each workgroup clears its barrier flag (last launch's epochs)
+        // each workgroup clears its arrival words (last launch's epochs)
         // before the launch's first barrier, which counts arrivals instead
-        if (threadIdx.x == 0) {
-            atomicOr(&c.ctl->xcc_mask, 1u << xcc_id());
-            c.d.barrier_flags[c.part * kFlagWords] = 0u;
-        }
+        if (threadIdx.x == 0) atomicOr(&c.ctl->xcc_mask, 1u << xcc_id());
+        if (threadIdx.x < 2) c.d.barrier_flags[c.part * kFlagWords + threadIdx.x] = 0u;
         if (!lane_barrier(c.d, c.part, P, target, spin, false)) return;
         c.local = __popc(ld(&c.ctl->xcc_mask)) == 1;
+    }
+    {
+        // a workgroup's winners fit the 16 bits its arrival word carries
+        const uint32_t range = (args.cfg.block_count + selecting_waves(c) - 1) / selecting_waves(c);
+        c.carried = c.local && P > 1 &&
+                    static_cast<uint64_t>(range) * args.cfg.max_active_per_block * kWavesPerGroup <= 0xffffu;
     }
     if (threadIdx.x < kRing) {
         sh.ring_tick[threadIdx.x] = ld(&c.ctl->ring_tick[threadIdx.x]);
@@ -3195,25 +3313,34 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
     PhaseClock clock;
     if (kProfile && c.part == args.profile_part && threadIdx.x == 0) clock.start(c.d.phase_profile);
     bool ok = true;
-    // the next step's parameters are fetched one step ahead with vector loads
-    // (a scalar load would be waited for at the next LDS access)
+    // the step parameters come kStepChunk steps at a time, with one round
+    // of coalesced loads into LDS: a load per step, even issued a step
+    // ahead, would be waited for by the step's first wait on its own loads
+    // (the vector memory counter drains in order)
     constexpr uint32_t kStepWords = sizeof(StepParams) / 4;
     static_assert(sizeof(StepParams) % 4 == 0, "step parameters are 32-bit words");
-    uint32_t ahead[kStepWords];
-    auto fetch = [&](uint32_t index) {
-        const uint32_t LEO_GLOBAL* src = reinterpret_cast<const uint32_t LEO_GLOBAL*>(c.d.steps + index);
-#pragma unroll
-        for (uint32_t i = 0; i < kStepWords; ++i) ahead[i] = ld(&src[i]);
+    uint32_t chunk_base = 0;
+    auto load_chunk = [&](uint32_t first) {
+        chunk_base = first;
+        const uint32_t LEO_GLOBAL* src = reinterpret_cast<const uint32_t LEO_GLOBAL*>(c.d.steps + first);
+        const uint32_t words = min(kStepChunk + 1, steps - first) * kStepWords;
+        for (uint32_t i = threadIdx.x; i < words; i += kThreads) sh.step_chunk[i] = ld(&src[i]);
+        __syncthreads();
     };
-    auto params = [&]() {
+    auto params = [&](uint32_t index) {  // a step of the current chunk (or the next chunk's first)
         StepParams p;
         uint32_t w[kStepWords];
+        const uint32_t at = (index - chunk_base) * kStepWords;
 #pragma unroll
-        for (uint32_t i = 0; i < kStepWords; ++i) w[i] = __builtin_amdgcn_readfirstlane(ahead[i]);
+        for (uint32_t i = 0; i < kStepWords; ++i) w[i] = __builtin_amdgcn_readfirstlane(sh.step_chunk[at + i]);
         __builtin_memcpy(&p, w, sizeof(StepParams));
+        if (kFrozenOnly) {
+            p.flags = (p.flags & ~static_cast<uint32_t>(kStepLearnTrace | kStepAllocate | kStepLearn | kStepOutput)) |
+                      kStepFrozen;
+            p.plasticity_scale = 0.0f;
+        }
         return p;
     };
-    if (steps > 0) fetch(0);
     // a step whose delivery ran in the previous step's last phase; a step
     // after a one-barrier frozen step (frozen_emit), and the population
     // inhibition the last fold read
@@ -3222,8 +3349,8 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
     uint32_t early_prev = 0;  // kStepEarly delays of the one-barrier step before
     const bool one_barrier_lane = c.d.bucket_sets != 1 && c.P > 1 && redundant;
     for (uint32_t s = 0; s < steps && ok; ++s) {
-        const StepParams sp = params();
-        if (s + 1 < steps) fetch(s + 1);
+        if (s % kStepChunk == 0) load_chunk(s);
+        const StepParams sp = params(s);
         const bool trace = (sp.flags & kStepLearnTrace) != 0;
         const bool learn = (sp.flags & kStepLearn) != 0;
         // steps without eligibility updates or readout fold the post phase
@@ -3269,7 +3396,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         StepParams next{};
         bool pipeline = false;
         if (fused && !learn && s + 1 < steps) {
-            next = params();
+            next = params(s + 1);
             pipeline = (next.flags & kStepLearnTrace) == 0;
         }
         // and with the bucket sets, a frozen step followed by a fused frozen
@@ -3288,7 +3415,9 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             // counters tick+1 reuses are cleared (a one-barrier step's
             // prologue did both)
             if (!after_one_barrier && c.part == c.P - 1 && wave_index() == 0) roll_counters(c, s);
-            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 6))) break;
+            if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 6, c.carried ? sh.win_count : nullptr,
+                                               c.carried ? sh.lane_sums : nullptr)))
+                break;
             delivered_ahead = true;
             after_one_barrier = true;
             c.tick += 1;
@@ -3353,10 +3482,13 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
 // The arguments live in device memory (read with scalar loads): a by-value
 // argument whose address is taken is copied to scratch.
 __global__ void __launch_bounds__(kThreads) leo_lane_steps(const KernelArgs* __restrict__ args) {
-    lane_steps<false>(*args);
+    lane_steps<false, false>(*args);
 }
 __global__ void __launch_bounds__(kThreads) leo_lane_steps_profiled(const KernelArgs* __restrict__ args) {
-    lane_steps<true>(*args);
+    lane_steps<true, false>(*args);
+}
+__global__ void __launch_bounds__(kThreads) leo_lane_steps_frozen(const KernelArgs* __restrict__ args) {
+    lane_steps<false, true>(*args);
 }
 
 // A story group's fork of the canonical parameters (parallel.rs: each worker

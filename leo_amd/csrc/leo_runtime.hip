@@ -34,6 +34,7 @@ namespace leo {
 
 __global__ void leo_lane_steps(const KernelArgs* args);
 __global__ void leo_lane_steps_profiled(const KernelArgs* args);
+__global__ void leo_lane_steps_frozen(const KernelArgs* args);
 __global__ void leo_reset_lanes(KernelArgs args, uint32_t set_tick, uint32_t new_tick);
 
 __global__ void leo_merge_fixed(MergeArgs m);
@@ -309,6 +310,9 @@ struct LeoHipRuntime {
     // device memory) keeps two
     uint32_t canonical_sets = leo::kBucketSets;
     uint32_t profile_part = 0;  // LEO_HIP_PROFILE_PART: the workgroup of each lane the phase profile times
+    // launches whose steps are all frozen without output run the step kernel
+    // built for them (LEO_HIP_FROZEN_KERNEL=0: never)
+    bool frozen_kernel = true;
     double wall_clock_khz = 0.0;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     std::vector<hipEvent_t> launch_events;  // timing events of queued launches (pairs)
@@ -786,6 +790,12 @@ StepParams make_step(const LeoHostConfig& c, Lane& lane, uint32_t symbol, int32_
 
 constexpr size_t kAllSteps = ~size_t(0);
 
+// A step the frozen-only step kernel runs: frozen, with neither learning nor
+// output (the replay's prefix steps, advance_frozen_batch).
+inline bool frozen_only_step(const StepParams& sp) {
+    return (sp.flags & kStepFrozen) && !(sp.flags & (kStepLearnTrace | kStepAllocate | kStepLearn | kStepOutput));
+}
+
 struct LaneRun {
     Lane* lane;
     std::vector<StepParams> steps;
@@ -955,7 +965,11 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
     h->staging.publish(h->stream);
     const KernelArgs* device_args = reinterpret_cast<const KernelArgs*>(h->kernel_args_buf.base);
     void* params[] = {&device_args};
+    bool frozen_only = h->frozen_kernel && a.redundant_global != 0;
+    for (const LaneRun& r : runs)
+        for (const StepParams& sp : r.steps) frozen_only = frozen_only && frozen_only_step(sp);
     const void* kernel = h->phase_profile ? reinterpret_cast<const void*>(&leo_lane_steps_profiled)
+                         : frozen_only    ? reinterpret_cast<const void*>(&leo_lane_steps_frozen)
                                           : reinterpret_cast<const void*>(&leo_lane_steps);
     if (h->phase_profile)
         for (auto& r : runs) LEO_HIP_CHECK(hipMemsetAsync(r.lane->desc.phase_profile, 0, 2 * kPhases * 8, h->stream));
@@ -1251,6 +1265,16 @@ struct CanonicalSegment {
 // count, then four times the previous one (at most 4096); the results do not
 // depend on how the steps are cut into launches. Metrics of the steps are
 // appended to `out` in order.
+// Frozen prefix steps at the start of a replay segment (the permission alone
+// makes a canonical step frozen without output: make_step).
+size_t leading_frozen_steps(const CanonicalSegment& seg) {
+    size_t n = 0;
+    while (n < seg.permissions.size() && seg.permissions[n] == LEO_FROZEN) ++n;
+    return n;
+}
+// The shortest leading frozen run that is launched on its own.
+constexpr size_t kFrozenLaunchMin = 64;
+
 void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment>& segments,
                             std::vector<LeoStepMetrics>& out) {
     Lane& lane = *h->canonical;
@@ -1268,8 +1292,13 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
     for (size_t k = 0; k < segments.size(); ++k) {
         if (segments[k].reset_before) staged += PinnedStaging::rounded(sizeof(LaneDesc));
         size_t chunk = first_canonical_chunk(h);
+        // a long leading run of frozen prefix steps gets launches of its own
+        // (the frozen-only kernel's), the rest of the segment the others
+        const size_t frozen_run = h->frozen_kernel ? leading_frozen_steps(segments[k]) : 0;
+        const size_t split = frozen_run >= kFrozenLaunchMin ? frozen_run : 0;
         for (size_t at = 0; at < segments[k].steps.size();) {
-            const size_t n = std::min(chunk, segments[k].steps.size() - at);
+            const size_t end = at < split ? split : segments[k].steps.size();
+            const size_t n = std::min(chunk, end - at);
             cuts[k].push_back(n);
             staged += launch_staging_bytes(1, {n});
             largest = std::max(largest, n);
@@ -2469,13 +2498,14 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         h->cus = prop.multiProcessorCount;
         // cooperative capacity: the smaller occupancy of the step kernel and
         // its phase-profiling build (either may be launched on the same grid)
-        int occupancy[2] = {0, 0};
-        const void* step_kernels[2] = {reinterpret_cast<const void*>(&leo::leo_lane_steps),
-                                       reinterpret_cast<const void*>(&leo::leo_lane_steps_profiled)};
-        for (int k = 0; k < 2; ++k)
+        int occupancy[3] = {0, 0, 0};
+        const void* step_kernels[3] = {reinterpret_cast<const void*>(&leo::leo_lane_steps),
+                                       reinterpret_cast<const void*>(&leo::leo_lane_steps_profiled),
+                                       reinterpret_cast<const void*>(&leo::leo_lane_steps_frozen)};
+        for (int k = 0; k < 3; ++k)
             LEO_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(
                 &occupancy[k], step_kernels[k], leo::kThreads, leo::step_lds_bytes(config->device.neurons_per_block)));
-        h->coop_blocks_per_cu = std::min(occupancy[0], occupancy[1]);
+        h->coop_blocks_per_cu = std::min({occupancy[0], occupancy[1], occupancy[2]});
         if (h->coop_blocks_per_cu <= 0) throw Error(LEO_ERR_DEVICE, "step kernel cannot be resident");
         if (const char* env = std::getenv("LEO_HIP_WGS_PER_LANE")) h->wgs_override = static_cast<uint32_t>(std::atoi(env));
         if (const char* env = std::getenv("LEO_HIP_CANONICAL_WGS"))
@@ -2488,6 +2518,7 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
             h->canonical_sets = std::atoi(env) == 1 ? 1u : leo::kBucketSets;
         if (const char* env = std::getenv("LEO_HIP_PROFILE_PART"))
             h->profile_part = static_cast<uint32_t>(std::max(0, std::atoi(env)));
+        if (const char* env = std::getenv("LEO_HIP_FROZEN_KERNEL")) h->frozen_kernel = std::atoi(env) != 0;
         int clock_khz = 0;
         LEO_HIP_CHECK(hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, device));
         h->wall_clock_khz = clock_khz > 0 ? clock_khz : 100000.0;

@@ -84,3 +84,51 @@ def test_one_barrier_frozen_runs_match_oracle_and_two_phase(require_gpu, oracle,
         assert stats[sets]["touched"] == touched, sets
     for key in COUNTERS:
         assert stats["9"][key] == stats["1"][key], key
+
+
+@pytest.mark.parametrize("launch_steps", [None, 100])
+def test_frozen_only_kernel_matches_oracle_and_general_kernel(require_gpu, oracle, monkeypatch, launch_steps):
+    """A launch of frozen steps without output runs the step kernel built for
+    them (no learning, readout or eligibility code; LEO_HIP_FROZEN_KERNEL=0
+    keeps the general one). A long frozen prefix (advance_frozen_batch,
+    backend.rs:428-431) followed by a mixed timeline must give the oracle's
+    metrics, touched counts and model, and the same work counters as the
+    general kernel."""
+    from leo_amd.runtime import HipRuntime
+
+    model = Model.initialize(small_redundant_config())
+    text = story(9, 420)
+    prefix = [(BEGIN_DOCUMENT, None)] + [(b, None) for b in text[:259]]
+    rest = _timeline(text[259:])
+    cpu = oracle.OracleRuntime(model)
+    cpu.begin_document()
+    want, touched = [], 0
+    for s, t in prefix + rest:
+        m = cpu.step(s, t, oracle.TRAINING if t is not None else oracle.FROZEN)
+        touched += len(cpu.read_list("touched"))
+        if t is not None:
+            want.append(m)
+    if launch_steps:
+        monkeypatch.setenv("LEO_HIP_MAX_STEPS_PER_LAUNCH", str(launch_steps))
+    stats = {}
+    for kernel in ("1", "0"):
+        monkeypatch.setenv("LEO_HIP_FROZEN_KERNEL", kernel)
+        print(f"frozen-only kernel {kernel}, launches of {launch_steps or 'any'} steps", flush=True)
+        gpu = HipRuntime(model, device=0, max_lanes=1)
+        try:
+            gpu.begin_document()
+            gpu.kernel_stats(reset=True)
+            gpu.advance_frozen_batch(prefix)
+            got = gpu.replay_streaming_batch(rest, native.TRAINING)
+            assert len(got) == len(want)
+            for i, (g, c) in enumerate(zip(got, want)):
+                assert g.loss == c.loss and g.active_neurons == c.active_neurons, (kernel, i)
+                assert g.predicted_symbol == c.predicted_symbol, (kernel, i)
+                assert g.population_inhibition == c.population_inhibition, (kernel, i)
+            assert_models_equal(gpu.model(), cpu.model(), f"frozen-only kernel {kernel}")
+            stats[kernel] = gpu.kernel_stats()
+        finally:
+            gpu.close()
+        assert stats[kernel]["touched"] == touched, kernel
+    for key in COUNTERS:
+        assert stats["1"][key] == stats["0"][key], key
