@@ -258,7 +258,7 @@ def main() -> int:
     sections = {
         "story": section("leo_lane_steps (story lanes)", ks["section_launches"][0], ks["section_kernel_ms"][0],
                          ks["section_bytes"][0], ks["section_lane_steps"][0]),
-        "replay": section("leo_lane_steps (canonical runtime)", ks["section_launches"][1],
+        "replay": section("leo_lane_steps + leo_lane_steps_frozen (canonical runtime)", ks["section_launches"][1],
                           ks["section_kernel_ms"][1], ks["section_bytes"][1], ks["section_lane_steps"][1]),
         "merge": section("leo_merge_candidates + leo_merge_fixed", ks["merge_launches"], ks["merge_ms"], ks["merge_bytes"], 0),
     }
@@ -292,7 +292,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": measured_traffic(w.name),
-            "kernel": "leo_lane_steps",
+            "kernel": "leo_lane_steps + leo_lane_steps_frozen",
             "launches": ks["launches"],
             "kernel_ms_total": ks["kernel_ms"],
             "avg_launch_us": ks["kernel_ms"] * 1e3 / max(ks["launches"], 1),
