@@ -86,6 +86,30 @@ __device__ __forceinline__ StateDecays state_decays(const LeoConfig& cfg, uint32
     }
     return {r0, r1, r2, r3, r4, r5};
 }
+// The decays of elapsed counts below kDecayTable, computed by state_decays
+// at each step-kernel launch into LDS (the same function, so the same
+// values): a touched neuron's decay is then one table read instead of a loop
+// over the count's bits. Larger counts take the loop.
+constexpr uint32_t kDecayTable = 512;
+__shared__ float decay_table[kDecayTable * 6];
+__device__ __forceinline__ void fill_decay_table(const LeoConfig& cfg) {
+    for (uint32_t e = threadIdx.x; e < kDecayTable; e += blockDim.x) {
+        const StateDecays k = state_decays(cfg, e);
+        float* t = &decay_table[e * 6];
+        t[0] = k.branch;
+        t[1] = k.membrane;
+        t[2] = k.fatigue;
+        t[3] = k.fast;
+        t[4] = k.medium;
+        t[5] = k.slow;
+    }
+}
+__device__ __forceinline__ StateDecays decays_at(const LeoConfig& cfg, uint32_t elapsed) {
+    if (elapsed >= kDecayTable) return state_decays(cfg, elapsed);
+    const float* t = &decay_table[elapsed * 6];
+    return {t[0], t[1], t[2], t[3], t[4], t[5]};
+}
+
 // learning.rs:7-24
 __device__ __forceinline__ float analog_rank_surrogate(float margin, float cutoff, bool selected, float width,
                                                        float gain) {
@@ -511,7 +535,7 @@ __device__ __forceinline__ void activate_loaded_trace(float LEO_GLOBAL* trace, u
         trace[static_cast<uint64_t>(slot) * kTraceWords + kTBranch] = q0.x + activation;
         return;
     }
-    const StateDecays k = state_decays(cfg, e);
+    const StateDecays k = decays_at(cfg, e);
     const float bs = q0.x * k.branch;
     rec[0] = f32x4{bs + activation, q0.y * k.membrane, q0.z * k.fatigue, q0.w * k.fast};
     rec[1] = f32x4{q1.x * k.medium, q1.y * k.slow, q1.z, __uint_as_float(tick)};
@@ -1102,7 +1126,7 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
     const bool refr = refractory_until > tick;
     const uint32_t e = tick - last;
     if (e > 0) {
-        const StateDecays k = state_decays(cfg, e);
+        const StateDecays k = decays_at(cfg, e);
         b0 *= k.branch;
         b1 *= k.branch;
         b2 *= k.branch;
@@ -1222,7 +1246,7 @@ __device__ float deep_fold(const StepCtx& c, uint32_t n, float pi, uint32_t set,
     const bool refr = refractory_until > tick;
     const uint32_t e = tick - last;
     if (e > 0) {
-        const StateDecays k = state_decays(cfg, e);
+        const StateDecays k = decays_at(cfg, e);
         b0 *= k.branch;
         b1 *= k.branch;
         b2 *= k.branch;
@@ -3309,6 +3333,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         sh.ring_count[threadIdx.x] = ld(&c.ctl->ring_count[threadIdx.x]);
         sh.ring_early[threadIdx.x] = ld(&c.ctl->ring_early[threadIdx.x]);
     }
+    fill_decay_table(args.cfg);
     __syncthreads();
     PhaseClock clock;
     if (kProfile && c.part == args.profile_part && threadIdx.x == 0) clock.start(c.d.phase_profile);
