@@ -2350,7 +2350,7 @@ __device__ __forceinline__ bool finish_slot(const StepCtx& c, const SlotInputs& 
     float bs = in.bs, ms = in.ms, fs = in.fs, as0 = in.as0, as1 = in.as1, as2 = in.as2;
     const uint32_t el = tick - in.last;
     if (el > 0) {
-        const StateDecays k = state_decays(cfg, el);
+        const StateDecays k = decays_at(cfg, el);
         bs *= k.branch;
         ms *= k.membrane;
         fs *= k.fatigue;
