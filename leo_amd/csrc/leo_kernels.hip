@@ -673,22 +673,22 @@ __device__ __forceinline__ uint64_t bucket_entry(uint64_t overflow, uint32_t n, 
 
 // One delivery into target's bucket of `set` (the fold of phase 2 orders the
 // bucket by key), in two parts so that a thread can claim several entries in
-// one round: the claim of an entry (the target's overflow offset, loaded with
-// the counter increment) and its write. The write tells whether it is the
-// target's first delivery of the tick.
+// one round: the claim of an entry (the counter increment) and its write.
+// An entry past the target's fixed ones reads the target's overflow offset
+// first (rare: the fixed entries hold nearly every target of a sparse tick).
+// The write tells whether it is the target's first delivery of the tick.
 struct EntryClaim {
-    uint64_t overflow;
     uint32_t p;
 };
 __device__ __forceinline__ EntryClaim claim_entry(const StepCtx& c, uint32_t set, uint32_t target) {
     EntryClaim k;
-    k.overflow = c.a->m.bucket_offset[target];
     k.p = atomicAdd(set_counts(c.d, set, c.a->cfg.neuron_count) + target, 1u);
     return k;
 }
 __device__ __forceinline__ bool write_entry(const StepCtx& c, uint32_t set, uint32_t target, const EntryClaim& k,
                                             uint64_t key, float value) {
-    const uint64_t at = bucket_entry(k.overflow, target, k.p);
+    const uint64_t overflow = k.p < kFixedEntries ? 0 : c.a->m.bucket_offset[target];
+    const uint64_t at = bucket_entry(overflow, target, k.p);
     uint64_t LEO_GLOBAL* bucket = set_bucket(c.d, set);
     bucket[2 * at] = key;
     bucket[2 * at + 1] = __float_as_uint(value);
@@ -1102,7 +1102,7 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
     const uint32_t last = __float_as_uint(q2.z);
     const uint32_t cnt = ld(&counts[n]);
     *entries = cnt;
-    const uint64_t overflow = a.m.bucket_offset[n];  // loaded with the state (used when cnt > kFixedEntries)
+
     // the fixed bucket entries (one 64-byte run, 16 bytes each: key, value)
     // are read with the state; N * 64 bytes fits a buffer like the records
     static_assert(kFixedEntries == 4, "the fold reads four fixed entries");
@@ -1165,7 +1165,7 @@ __device__ __forceinline__ float fold_drive(const StepCtx& c, uint32_t n, float 
                 k[x] = x < cnt ? entry_key(fe[x]) : ~0ULL;
                 v[x] = x < cnt ? __float_as_uint(fe[x].z) : 0u;
             }
-            const uint64_t LEO_GLOBAL* over = bucket + 2 * overflow;
+            const uint64_t LEO_GLOBAL* over = bucket + 2 * a.m.bucket_offset[n];
 #pragma unroll
             for (uint32_t x = kFixedEntries; x < 8; ++x) {
                 k[x] = x < cnt ? ld(&over[2 * (x - kFixedEntries)]) : ~0ULL;
