@@ -1683,12 +1683,15 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
             wave_sync();
             lo = hi;
         }
-        // block results; a block without touched neurons keeps a stale epoch
-        // (no winners, cutoff 0)
+        // block results, read only by a trace step's eligibility update (as
+        // this tick's, by epoch); a block without touched neurons keeps a
+        // stale epoch (no winners, cutoff 0)
         if (lane < gn && w.start[lane + 1] > w.start[lane]) {
             const uint32_t b = gb + lane;
-            d.block_cutoff[b] = w.cut[lane] != ~0ULL ? key_activation(w.cut[lane]) : 0.0f;
-            d.block_epoch[b] = tick + 1;
+            if (keep_bits) {
+                d.block_cutoff[b] = w.cut[lane] != ~0ULL ? key_activation(w.cut[lane]) : 0.0f;
+                d.block_epoch[b] = tick + 1;
+            }
             supra += w.cands[lane];
         }
         w.cands[lane] = 0;
