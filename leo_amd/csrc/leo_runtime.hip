@@ -1968,10 +1968,15 @@ void story_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets
     if (count == 0) throw Error(LEO_ERR_INVALID_ARGUMENT, "training batch cannot be empty");
     for (uint32_t i = 0; i < count; ++i)
         if (offsets[i + 1] <= offsets[i]) throw Error(LEO_ERR_UNSUPPORTED, "empty stories are not supported in a device batch");
-    // stories run in groups of the lanes that fit on the device; the groups'
-    // lanes join the batch-end mean in story order
+    // stories run in groups of the lanes that fit on the device, as few
+    // groups as that allows, with the stories split evenly over them (a
+    // group's launch then gives each lane the same share of the workgroups:
+    // at D, 32 + 32 lanes of 16 workgroups ran the story pass 14% faster than
+    // 54 + 10 lanes of 9 and 32); the groups' lanes join the batch-end mean
+    // in story order
     const uint32_t resident = std::max<uint32_t>(1, std::min(h->resident_lanes, h->max_lanes));
     const uint32_t groups = (count + resident - 1) / resident;
+    const uint32_t per_group = (count + groups - 1) / groups;
     const uint32_t S = h->cfg.device.synapses_per_neuron;
     LeoStatistics merged = h->stats;
     uint64_t revision_increment = 0;
@@ -1983,7 +1988,7 @@ void story_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets
     std::vector<Lane*> lanes;
     for (uint32_t g = 0; g < groups; ++g) {
         auto t0 = std::chrono::steady_clock::now();
-        const uint32_t lo = g * resident, hi = std::min(count, lo + resident);
+        const uint32_t lo = g * per_group, hi = std::min(count, lo + per_group);
         lanes.clear();
         for (uint32_t i = lo; i < hi; ++i) {
             Lane& l = story_lane(h, i - lo);
@@ -2090,14 +2095,16 @@ void evaluate_stories(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* of
     }
     const uint32_t S = h->cfg.device.synapses_per_neuron, E = h->cfg.device.context_embedding_dim;
     const uint32_t resident = std::max<uint32_t>(1, std::min(h->resident_lanes, h->max_lanes));
+    const size_t groups = (stories.size() + resident - 1) / resident;
+    const size_t per_group = groups > 0 ? (stories.size() + groups - 1) / groups : 1;  // even groups, as above
     const float uniform_loss = std::log(static_cast<float>(kOutputs));  // loss_from_logits fallback
     uint32_t tick = h->canonical->tick;
     double loss_sum = 0.0;
     uint64_t correct = 0;
     size_t cursor = 0;
     rep.neuron_count = h->z.n;
-    for (size_t lo = 0; lo < stories.size(); lo += resident) {
-        const size_t hi = std::min(stories.size(), lo + resident);
+    for (size_t lo = 0; lo < stories.size(); lo += per_group) {
+        const size_t hi = std::min(stories.size(), lo + per_group);
         BorrowedParams borrowed;
         std::vector<LaneRun> runs;
         std::vector<std::vector<HostStep>> host_steps;

@@ -175,17 +175,18 @@ def test_train_batch_with_replay_parity(require_gpu, oracle, make):
     gpu.close()
 
 
-@pytest.mark.parametrize("make", ["test_toml", "small_redundant"])
-def test_story_batch_in_lane_groups_parity(require_gpu, oracle, make, monkeypatch):
+@pytest.mark.parametrize("make,resident", [("test_toml", 2), ("small_redundant", 2), ("small_redundant", 4)])
+def test_story_batch_in_lane_groups_parity(require_gpu, oracle, make, resident, monkeypatch):
     # 5 stories with 2 resident lanes: groups 2+2+1 accumulate the lane-ordered
-    # f64 mean and the keyed context merge across groups
-    monkeypatch.setenv("LEO_HIP_RESIDENT_LANES", "2")
+    # f64 mean and the keyed context merge across groups; with 4, the two
+    # groups the capacity needs take 3+2 stories (split evenly, not 4+1)
+    monkeypatch.setenv("LEO_HIP_RESIDENT_LANES", str(resident))
     cfg = toml_test_config() if make == "test_toml" else small_redundant_config()
     model = Model.initialize(cfg)
     stories = [story(500 + k, 40 + 13 * k) for k in range(5)]
     cpu = oracle.OracleRuntime(model)
     gpu = _runtime(model)
-    assert gpu.resident_lanes == 2
+    assert gpu.resident_lanes == resident
     for replay in (False, True):
         crep, closs = cpu.train_story_batch(stories, oracle.TRAINING, replay=replay)
         grep, gloss = gpu.train_batch(stories, native.TRAINING, replay=replay)
