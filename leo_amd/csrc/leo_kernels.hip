@@ -690,8 +690,9 @@ __device__ __forceinline__ bool write_entry(const StepCtx& c, uint32_t set, uint
     const uint64_t overflow = k.p < kFixedEntries ? 0 : c.a->m.bucket_offset[target];
     const uint64_t at = bucket_entry(overflow, target, k.p);
     uint64_t LEO_GLOBAL* bucket = set_bucket(c.d, set);
-    bucket[2 * at] = key;
-    bucket[2 * at + 1] = __float_as_uint(value);
+    // the 16-byte entry (key, value) in one store
+    *reinterpret_cast<uint4 LEO_GLOBAL*>(bucket + 2 * at) =
+        make_uint4(static_cast<uint32_t>(key), static_cast<uint32_t>(key >> 32), __float_as_uint(value), 0u);
     return k.p == 0;
 }
 __device__ __forceinline__ bool scatter_event(const StepCtx& c, uint32_t set, uint32_t target, uint64_t key,
