@@ -2603,10 +2603,12 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
     const uint32_t o1 = threadIdx.x, o2 = threadIdx.x + kThreads;
     const bool has2 = o2 < kOutputs;
     float* lat = sh.aux;
-    // Memory rounds: (1) the active and context counts, the context slots
-    // and scales, the bias and this thread's first 16 context-projection
-    // weights; (2) the first 256 active ids and activations (into LDS) and
-    // the context embeddings; (3) rows of 32 active neurons at a time.
+    // Memory rounds: (1) the context count, slots and scales, the bias and
+    // the waves' winner totals; (2) the context embeddings; (3) the first 256
+    // active ids and activations (into LDS) with this thread's first 16
+    // context-projection weights; (4) rows of 32 active neurons at a time.
+    // (A load's wait also waits for every load issued before it, so the
+    // projection weights, needed last, go out after the embeddings.)
     const bool from_waves = a.redundant_global != 0;
     uint32_t* starts = reinterpret_cast<uint32_t*>(step_lds + 2 * kThreads * 4);
     const uint32_t nwaves = selecting_waves(c);
@@ -2616,27 +2618,23 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
         d.records[step_index].p_target = 0.0f;
         d.records[step_index].predicted = 0;
     }
-    const uint32_t A = from_waves ? wave_starts(c, sh, starts, nwaves) : ld(&ctl->active_count);
+    // the slots past the count are loaded too (and not used), so that the
+    // slots do not wait for the count
     const uint32_t ctx_count = ld(&ctl->ctx_count);
+    uint32_t slot[kMaxOrder];
+    float scale[kMaxOrder];
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxOrder; ++i) {
+        slot[i] = threadIdx.x < E ? ld(&ctl->ctx_slots[i]) : 0u;
+        scale[i] = threadIdx.x < E ? ld(&ctl->ctx_scales[i]) : 0.0f;
+    }
     float l1 = ld(&d.p.bias[o1]), l2 = has2 ? ld(&d.p.bias[o2]) : 0.0f;
     const float bias1 = l1, bias2 = l2;
-    constexpr uint32_t kDims = 16;
-    float x1[kDims], x2[kDims];
-#pragma unroll
-    for (uint32_t k = 0; k < kDims; ++k) {
-        x1[k] = k < E ? ld(&d.p.ctx_out[o1 * E + k]) : 0.0f;
-        x2[k] = k < E && has2 ? ld(&d.p.ctx_out[o2 * E + k]) : 0.0f;
-    }
+    const uint32_t A = from_waves ? wave_starts(c, sh, starts, nwaves) : ld(&ctl->active_count);
     // context latent (runtime.rs:1120-1136): serial over active slots per
     // dimension
     for (uint32_t e = threadIdx.x; e < E; e += kThreads) {
-        uint32_t slot[kMaxOrder];
-        float scale[kMaxOrder], emb[kMaxOrder];
-#pragma unroll
-        for (uint32_t i = 0; i < kMaxOrder; ++i) {
-            slot[i] = i < ctx_count ? ld(&ctl->ctx_slots[i]) : 0u;
-            scale[i] = i < ctx_count ? ld(&ctl->ctx_scales[i]) : 0.0f;
-        }
+        float emb[kMaxOrder];
 #pragma unroll
         for (uint32_t i = 0; i < kMaxOrder; ++i)
             emb[i] = i < ctx_count && scale[i] > 0.0f ? ld(&d.p.ctx_emb[static_cast<uint64_t>(slot[i]) * E + e]) : 0.0f;
@@ -2646,6 +2644,13 @@ __device__ __forceinline__ void readout(const StepCtx& c, const StepParams& sp, 
             if (i < ctx_count && scale[i] > 0.0f) v += emb[i] * scale[i];
         lat[e] = v;
         d.ctx_latent[e] = v;
+    }
+    constexpr uint32_t kDims = 16;
+    float x1[kDims], x2[kDims];
+#pragma unroll
+    for (uint32_t k = 0; k < kDims; ++k) {
+        x1[k] = k < E ? ld(&d.p.ctx_out[o1 * E + k]) : 0.0f;
+        x2[k] = k < E && has2 ? ld(&d.p.ctx_out[o2 * E + k]) : 0.0f;
     }
     // logits[o] = bias[o] + sum over active in order of W[n][o]*a_n (+ context
     // once): thread t owns outputs t and t+256; the active ids and
