@@ -18,6 +18,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -139,6 +140,21 @@ struct PinnedStaging {
         LEO_HIP_CHECK(hipMemcpyAsync(dst, p, bytes, hipMemcpyHostToDevice, active()));
         if (!route) pending_uploads = true;
     }
+    // one upload of pieces placed at byte offsets of `dst` (the bytes between
+    // pieces are left undefined)
+    struct Piece {
+        const void* src;
+        size_t bytes, at;
+    };
+    void h2d_gather(void* dst, std::initializer_list<Piece> pieces) {
+        size_t bytes = 0;
+        for (const Piece& piece : pieces) bytes = std::max(bytes, piece.at + piece.bytes);
+        char* p = take(bytes);
+        for (const Piece& piece : pieces)
+            if (piece.bytes) std::memcpy(p + piece.at, piece.src, piece.bytes);
+        LEO_HIP_CHECK(hipMemcpyAsync(dst, p, bytes, hipMemcpyHostToDevice, active()));
+        if (!route) pending_uploads = true;
+    }
     // the stream `s` waits for every upload issued so far
     void publish(hipStream_t s) {
         if (!pending_uploads || route == s) return;
@@ -240,7 +256,7 @@ struct Lane {
     Arena state;
     Arena params;
     LaneDesc desc{};
-    Arena schedule;  // steps + records
+    Arena schedule;  // header (single-lane launches), steps, records
     uint32_t schedule_capacity = 0;
     // host mirrors of per-runtime scalars (deterministic from the schedule)
     uint32_t tick = 0;
@@ -896,13 +912,21 @@ size_t launch_staging_bytes(size_t lanes, const std::vector<size_t>& steps) {
     return staged;
 }
 
+// A lane's schedule buffer: a header, then the step parameters, then the
+// step records. A launch of one lane keeps its kernel arguments and lane
+// descriptor in the header, so that they go up with the schedule in one copy.
+constexpr size_t kHeaderArgs = 0, kHeaderDesc = 512, kScheduleHeader = 1024;
+static_assert(sizeof(KernelArgs) <= kHeaderDesc && sizeof(LaneDesc) <= kScheduleHeader - kHeaderDesc,
+              "schedule header");
+
 // Every lane's schedule buffer holds `steps` steps (allocated while nothing
 // queued can be reading the old one).
 void ensure_schedule(Lane& lane, size_t steps) {
     const uint32_t need = static_cast<uint32_t>(std::max<size_t>(steps, 1));
     if (need <= lane.schedule_capacity) return;
     const uint32_t cap = std::max<uint32_t>(need, 256);
-    lane.schedule.allocate(static_cast<size_t>(cap) * (sizeof(StepParams) + sizeof(StepRecord)) + 512);
+    lane.schedule.allocate(kScheduleHeader + static_cast<size_t>(cap) * (sizeof(StepParams) + sizeof(StepRecord)) +
+                           512);
     lane.schedule_capacity = cap;
 }
 
@@ -926,12 +950,15 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
     const uint32_t P = plan.P, stride = plan.stride;
     if (P > kMaxLaneWgs) throw Error(LEO_ERR_INTERNAL, "more workgroups per lane than barrier flags");
     h->staging.follow(h->stream);  // the uploads replace what queued work may still read
+    // a single lane's kernel arguments and descriptor go up with its schedule
+    const bool single = count == 1;
     for (auto& r : runs) {
         Lane& lane = *r.lane;
         if (r.steps.size() > lane.schedule_capacity) throw Error(LEO_ERR_INTERNAL, "schedule buffer not sized");
-        lane.desc.steps = reinterpret_cast<const StepParams*>(lane.schedule.base);
+        lane.desc.steps = reinterpret_cast<const StepParams*>(lane.schedule.base + kScheduleHeader);
         lane.desc.records = reinterpret_cast<StepRecord*>(
-            lane.schedule.base + ((static_cast<size_t>(lane.schedule_capacity) * sizeof(StepParams) + 255) & ~size_t(255)));
+            lane.schedule.base + kScheduleHeader +
+            ((static_cast<size_t>(lane.schedule_capacity) * sizeof(StepParams) + 255) & ~size_t(255)));
         lane.desc.step_count = static_cast<uint32_t>(r.steps.size());
         // the delays whose events a step's tick may deliver at emission: the
         // arrival step is in this launch and runs no learning trace
@@ -943,7 +970,8 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
             }
             r.steps[i].flags = (r.steps[i].flags & ~static_cast<uint32_t>(kStepEarlyMask)) | (early << kStepEarlyShift);
         }
-        h->staging.h2d(const_cast<StepParams*>(lane.desc.steps), r.steps.data(), r.steps.size() * sizeof(StepParams));
+        if (!single)
+            h->staging.h2d(const_cast<StepParams*>(lane.desc.steps), r.steps.data(), r.steps.size() * sizeof(StepParams));
         // cleared on the transfer stream, after the previous launch's
         // control words have been downloaded there; the error word only once
         // the host has reported its code (a launch queued behind a failed
@@ -953,17 +981,30 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
         clear_reported_error(lane, h->staging.active());
         if (!h->staging.route) h->staging.pending_uploads = true;
     }
-    std::vector<Lane*> lanes;
-    for (auto& r : runs) lanes.push_back(r.lane);
-    stage_descs(h, lanes);
     if (static_cast<uint64_t>(plan.grid) > cooperative_capacity(h->cus, h->coop_blocks_per_cu))
         throw Error(LEO_ERR_INTERNAL, "cooperative launch exceeds the resident workgroup capacity");
-    KernelArgs a = kernel_args(h, reinterpret_cast<LaneDesc*>(h->lane_descs.base), count, P);
-    a.lane_stride = stride;
-    if (!h->kernel_args_buf.base) h->kernel_args_buf.allocate(sizeof(KernelArgs));
-    h->staging.h2d(h->kernel_args_buf.base, &a, sizeof(KernelArgs));
+    KernelArgs a;
+    const KernelArgs* device_args = nullptr;
+    if (single) {
+        const LaneRun& r = runs[0];
+        char* header = r.lane->schedule.base;
+        a = kernel_args(h, reinterpret_cast<LaneDesc*>(header + kHeaderDesc), 1, P);
+        a.lane_stride = stride;
+        h->staging.h2d_gather(header, {{&a, sizeof(KernelArgs), kHeaderArgs},
+                                       {&r.lane->desc, sizeof(LaneDesc), kHeaderDesc},
+                                       {r.steps.data(), r.steps.size() * sizeof(StepParams), kScheduleHeader}});
+        device_args = reinterpret_cast<const KernelArgs*>(header + kHeaderArgs);
+    } else {
+        std::vector<Lane*> lanes;
+        for (auto& r : runs) lanes.push_back(r.lane);
+        stage_descs(h, lanes);
+        a = kernel_args(h, reinterpret_cast<LaneDesc*>(h->lane_descs.base), count, P);
+        a.lane_stride = stride;
+        if (!h->kernel_args_buf.base) h->kernel_args_buf.allocate(sizeof(KernelArgs));
+        h->staging.h2d(h->kernel_args_buf.base, &a, sizeof(KernelArgs));
+        device_args = reinterpret_cast<const KernelArgs*>(h->kernel_args_buf.base);
+    }
     h->staging.publish(h->stream);
-    const KernelArgs* device_args = reinterpret_cast<const KernelArgs*>(h->kernel_args_buf.base);
     void* params[] = {&device_args};
     bool frozen_only = h->frozen_kernel && a.redundant_global != 0;
     for (const LaneRun& r : runs)
@@ -2330,12 +2371,22 @@ std::vector<std::pair<size_t, size_t>> select_replay_ranges(const std::vector<fl
     return selected;
 }
 
-// Replay on the canonical runtime (training.rs:162-255, 394-470, 1848-1954).
-void replay_story(LeoHipRuntime* h, const uint8_t* story, size_t len, const std::vector<float>& losses, int32_t permission,
-                  LeoBatchReport& rep) {
+// One story's replay on the canonical runtime: its segments, and whether the
+// replay ends with a reset of the runtime.
+struct StoryReplay {
+    std::vector<CanonicalSegment> segments;
+    bool cleanup = false;
+};
+
+// Plans one story's replay (training.rs:162-255, 394-470, 1848-1954): the
+// selected ranges as canonical segments; the prefix and target step counts go
+// into the report.
+StoryReplay plan_replay(LeoHipRuntime* h, const uint8_t* story, size_t len, const std::vector<float>& losses,
+                        int32_t permission, LeoBatchReport& rep) {
+    StoryReplay plan;
     auto ranges = select_replay_ranges(losses, h->cfg.replay_fraction, h->cfg.replay_segment_bytes);
     rep.replay_segments += ranges.size();
-    if (ranges.empty() || len == 0) return;
+    if (ranges.empty() || len == 0) return plan;
     auto position_step = [&](size_t p, bool supervised) {
         HostStep s{p == 0 ? kBegin : story[p - 1], -1};
         if (supervised) s.target = p < len ? static_cast<int32_t>(story[p]) : static_cast<int32_t>(kEnd);
@@ -2397,8 +2448,30 @@ void replay_story(LeoHipRuntime* h, const uint8_t* story, size_t len, const std:
             }
             segments.push_back(std::move(seg));
         }
-        if (segments.empty()) return;
+        if (segments.empty()) return plan;
     }
+    plan.segments = std::move(segments);
+    plan.cleanup = cleanup;
+    return plan;
+}
+
+// Replays the stories of a batch one after another on the canonical runtime,
+// queued as one run of segments with one wait at the end. Every story's first
+// segment starts with a reset, so the reset that ends a story's replay is
+// queued only when no later story's segment follows it (a second reset with
+// no step between changes nothing).
+void replay_stories(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets, uint32_t count,
+                    const std::vector<std::vector<float>>& losses, int32_t permission, LeoBatchReport& rep) {
+    std::vector<CanonicalSegment> segments;
+    bool cleanup = false;
+    for (uint32_t i = 0; i < count; ++i) {
+        StoryReplay plan = plan_replay(h, bytes + offsets[i], static_cast<size_t>(offsets[i + 1] - offsets[i]),
+                                       losses[i], permission, rep);
+        if (plan.segments.empty()) continue;
+        for (CanonicalSegment& seg : plan.segments) segments.push_back(std::move(seg));
+        cleanup = plan.cleanup;
+    }
+    if (segments.empty()) return;
     std::vector<LeoStepMetrics> metrics;
     run_canonical_segments(h, segments, metrics);
     size_t at = 0;
@@ -2725,10 +2798,7 @@ int32_t leo_hip_train_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64
             }
         }
         auto t1 = std::chrono::steady_clock::now();
-        if (replay_enabled)
-            for (uint32_t i = 0; i < count; ++i)
-                leo::replay_story(h, bytes + offsets[i], static_cast<size_t>(offsets[i + 1] - offsets[i]), losses[i],
-                                  permission, rep);
+        if (replay_enabled) leo::replay_stories(h, bytes, offsets, count, losses, permission, rep);
         rep.replay_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
         if (report) *report = rep;
     });
