@@ -355,6 +355,11 @@ struct LaneDesc {
     StepRecord LEO_GLOBAL* records;
     uint32_t step_count;
     uint32_t pad;
+    // where the launch's first thread stores the lane's outcome of the
+    // previous launch (error code, error step, bias fail, tick) before this
+    // launch can change it, for a host that reads the outcomes of a queue of
+    // launches at once; null: nowhere
+    uint32_t LEO_GLOBAL* outcome;
     // phase profile (profiling kernel only): per phase, summed wall-clock ticks of
     // workgroup 0's own work [0..kPhases) and of its barrier wait [kPhases..2*kPhases)
     unsigned long long LEO_GLOBAL* phase_profile;

@@ -3311,6 +3311,14 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
     c.P = P;
     c.gtid = c.part * kThreads + threadIdx.x;
     c.gstride = P * kThreads;
+    // the previous launch's outcome: no workgroup passes this launch's first
+    // barrier before this one has arrived there, so no step has changed it
+    if (c.d.outcome && c.part == 0 && threadIdx.x == 0) {
+        c.d.outcome[0] = ld(&c.ctl->error_code);
+        c.d.outcome[1] = ld(&c.ctl->error_step);
+        c.d.outcome[2] = ld(&c.ctl->bias_fail);
+        c.d.outcome[3] = ld(&c.ctl->tick);
+    }
     // a lane whose guard tripped in an earlier launch runs nothing until the
     // host has read the code (every workgroup reads it before its first
     // barrier, and no step of this launch can set it before then)

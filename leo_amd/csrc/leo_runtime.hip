@@ -287,6 +287,7 @@ struct LeoHipRuntime {
     uint32_t max_lanes = 0;
     leo::Arena lane_descs;     // LaneDesc[max(1,max_lanes)]
     leo::Arena kernel_args_buf;  // KernelArgs of the step kernel
+    leo::Arena replay_results;   // a canonical run's launch outcomes and step records
     leo::Arena merge_acc;        // f64 sums + changed flags of the lane-group merge
     leo::Arena merge_list;       // candidate positions of one tensor's merge
     uint32_t resident_lanes = 0; // story lanes that fit on the device at once
@@ -935,8 +936,11 @@ void ensure_schedule(Lane& lane, size_t steps) {
 // buffers they replace), the control words' clears and the kernel, then the
 // downloads on the transfer stream. The caller has reserved the staging
 // space of everything it queues before the next drain, and sized the
-// schedule buffers. The lanes' host tick mirrors advance at once.
-QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent_t start, hipEvent_t stop) {
+// schedule buffers. The lanes' host tick mirrors advance at once. With
+// `deferred_records` (one lane only), the step records go there and nothing
+// is downloaded: the caller downloads the records and fills in the outcome.
+QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent_t start, hipEvent_t stop,
+                           StepRecord* deferred_records = nullptr) {
     QueuedLaunch q;
     const uint32_t count = static_cast<uint32_t>(runs.size());
     uint64_t max_tick = 0;
@@ -952,6 +956,7 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
     h->staging.follow(h->stream);  // the uploads replace what queued work may still read
     // a single lane's kernel arguments and descriptor go up with its schedule
     const bool single = count == 1;
+    if (deferred_records && !single) throw Error(LEO_ERR_INTERNAL, "deferred records of more than one lane");
     for (auto& r : runs) {
         Lane& lane = *r.lane;
         if (r.steps.size() > lane.schedule_capacity) throw Error(LEO_ERR_INTERNAL, "schedule buffer not sized");
@@ -959,6 +964,7 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
         lane.desc.records = reinterpret_cast<StepRecord*>(
             lane.schedule.base + kScheduleHeader +
             ((static_cast<size_t>(lane.schedule_capacity) * sizeof(StepParams) + 255) & ~size_t(255)));
+        if (deferred_records) lane.desc.records = deferred_records;
         lane.desc.step_count = static_cast<uint32_t>(r.steps.size());
         // the delays whose events a step's tick may deliver at emission: the
         // arrival step is in this launch and runs no learning trace
@@ -1024,8 +1030,10 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
     q.records.resize(count);
     q.ctl.resize(count);
     for (uint32_t i = 0; i < count; ++i) {
-        q.records[i] = h->staging.d2h(runs[i].lane->desc.records, runs[i].steps.size() * sizeof(StepRecord));
-        q.ctl[i] = h->staging.d2h(runs[i].lane->desc.ctl, sizeof(LaneControl));
+        if (!deferred_records) {
+            q.records[i] = h->staging.d2h(runs[i].lane->desc.records, runs[i].steps.size() * sizeof(StepRecord));
+            q.ctl[i] = h->staging.d2h(runs[i].lane->desc.ctl, sizeof(LaneControl));
+        }
         runs[i].lane->tick += static_cast<uint32_t>(runs[i].steps.size());
         q.end_tick.push_back(runs[i].lane->tick);
     }
@@ -1353,7 +1361,21 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
             if (seg.reset_before) canonical_reset(h);
         return;
     }
+    // The launches' step records and outcomes stay on the device until the
+    // run's end (each launch stores its predecessor's outcome as it starts):
+    // one download of them all and of the lane's control words after the
+    // last launch, instead of two downloads behind every launch.
+    std::vector<size_t> record_at;
+    size_t results_bytes = PinnedStaging::rounded(launches * 4 * sizeof(uint32_t));
+    for (const auto& c : cuts)
+        for (size_t n : c) {
+            record_at.push_back(results_bytes);
+            results_bytes += PinnedStaging::rounded(n * sizeof(StepRecord));
+        }
+    staged += PinnedStaging::rounded(results_bytes) + PinnedStaging::rounded(sizeof(LaneControl));
     sync(h->stream);
+    if (h->replay_results.bytes < results_bytes) h->replay_results.allocate(results_bytes);
+    uint32_t* outcomes = reinterpret_cast<uint32_t*>(h->replay_results.base);
     ensure_schedule(lane, largest);
     h->staging.reserve(staged);
     while (h->launch_events.size() < 2 * launches) {
@@ -1366,6 +1388,10 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
     // one lane and one stream: resets, uploads, launches and downloads run in
     // queue order on the step stream, with no event handoff between streams
     StagingRoute on_step_stream(h->staging, h->stream);
+    struct OutcomeScope {  // later launches of the lane store no outcome
+        Lane& lane;
+        ~OutcomeScope() { lane.desc.outcome = nullptr; }
+    } outcome_scope{lane};
     for (size_t k = 0; k < segments.size(); ++k) {
         const CanonicalSegment& seg = segments[k];
         if (seg.reset_before) {
@@ -1384,12 +1410,32 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
             }
             std::vector<LaneRun> runs;
             runs.push_back(std::move(run));
-            const size_t e = 2 * queued.size();
-            queued.push_back(enqueue_lanes(h, std::move(runs), h->launch_events[e], h->launch_events[e + 1]));
+            const size_t i = queued.size();
+            lane.desc.outcome = i > 0 ? outcomes + 4 * (i - 1) : nullptr;
+            queued.push_back(enqueue_lanes(h, std::move(runs), h->launch_events[2 * i], h->launch_events[2 * i + 1],
+                                           reinterpret_cast<StepRecord*>(h->replay_results.base + record_at[i])));
             at += n;
         }
     }
+    const char* last_ctl = h->staging.d2h(lane.desc.ctl, sizeof(LaneControl));
+    const char* results = h->staging.d2h(h->replay_results.base, results_bytes);
     h->staging.wait();  // every queued kernel and download is complete
+    // the outcome of every launch but the last, as its successor found it
+    std::vector<LaneControl> outcome(queued.size());
+    for (size_t i = 0; i < queued.size(); ++i) {
+        if (i + 1 < queued.size()) {
+            uint32_t w[4];
+            std::memcpy(w, results + 4 * sizeof(uint32_t) * i, sizeof(w));
+            outcome[i].error_code = w[0];
+            outcome[i].error_step = w[1];
+            outcome[i].bias_fail = w[2];
+            outcome[i].tick = w[3];
+        } else {
+            std::memcpy(&outcome[i], last_ctl, sizeof(LaneControl));
+        }
+        queued[i].records[0] = results + record_at[i];
+        queued[i].ctl[0] = reinterpret_cast<const char*>(&outcome[i]);
+    }
     try {
         for (QueuedLaunch& q : queued) {
             try {
