@@ -288,6 +288,7 @@ struct LeoHipRuntime {
     leo::Arena lane_descs;     // LaneDesc[max(1,max_lanes)]
     leo::Arena kernel_args_buf;  // KernelArgs of the step kernel
     leo::Arena replay_results;   // a canonical run's launch outcomes and step records
+    std::vector<hipEvent_t> chunk_events;  // a canonical run's result chunks downloaded
     leo::Arena merge_acc;        // f64 sums + changed flags of the lane-group merge
     leo::Arena merge_list;       // candidate positions of one tensor's merge
     uint32_t resident_lanes = 0; // story lanes that fit on the device at once
@@ -337,6 +338,7 @@ struct LeoHipRuntime {
     ~LeoHipRuntime() {
         if (staging.xfer) (void)hipStreamSynchronize(staging.xfer);
         for (hipEvent_t e : launch_events) (void)hipEventDestroy(e);
+        for (hipEvent_t e : chunk_events) (void)hipEventDestroy(e);
     }
 };
 
@@ -1323,6 +1325,8 @@ size_t leading_frozen_steps(const CanonicalSegment& seg) {
 }
 // The shortest leading frozen run that is launched on its own.
 constexpr size_t kFrozenLaunchMin = 64;
+// Launches whose results come down in one copy.
+constexpr size_t kResultChunk = 32;
 
 void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment>& segments,
                             std::vector<LeoStepMetrics>& out) {
@@ -1361,21 +1365,31 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
             if (seg.reset_before) canonical_reset(h);
         return;
     }
-    // The launches' step records and outcomes stay on the device until the
-    // run's end (each launch stores its predecessor's outcome as it starts):
-    // one download of them all and of the lane's control words after the
-    // last launch, instead of two downloads behind every launch.
+    // The launches' step records and outcomes stay on the device: each launch
+    // stores its predecessor's outcome as it starts, in the slot in front of
+    // its own records. They come down in chunks of launches, one copy behind
+    // a chunk's last launch, and the host takes a chunk in while the later
+    // launches run (a launch's outcome arrives with its successor's chunk;
+    // the last launch's, with the lane's control words).
+    constexpr size_t kSlot = 256;
     std::vector<size_t> record_at;
-    size_t results_bytes = PinnedStaging::rounded(launches * 4 * sizeof(uint32_t));
+    size_t results_bytes = 0;
     for (const auto& c : cuts)
         for (size_t n : c) {
+            results_bytes += kSlot;
             record_at.push_back(results_bytes);
             results_bytes += PinnedStaging::rounded(n * sizeof(StepRecord));
         }
-    staged += PinnedStaging::rounded(results_bytes) + PinnedStaging::rounded(sizeof(LaneControl));
+    auto records_end = [&](size_t i) { return i + 1 < launches ? record_at[i + 1] - kSlot : results_bytes; };
+    staged += results_bytes + PinnedStaging::rounded(sizeof(LaneControl));
     sync(h->stream);
     if (h->replay_results.bytes < results_bytes) h->replay_results.allocate(results_bytes);
-    uint32_t* outcomes = reinterpret_cast<uint32_t*>(h->replay_results.base);
+    const size_t chunks = (launches + kResultChunk - 1) / kResultChunk;
+    while (h->chunk_events.size() < chunks) {
+        hipEvent_t e;
+        LEO_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        h->chunk_events.push_back(e);
+    }
     ensure_schedule(lane, largest);
     h->staging.reserve(staged);
     while (h->launch_events.size() < 2 * launches) {
@@ -1385,6 +1399,9 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
     }
     std::vector<QueuedLaunch> queued;
     queued.reserve(launches);
+    std::vector<size_t> chunk_from;
+    std::vector<const char*> chunk_host;
+    const char* last_ctl = nullptr;
     // one lane and one stream: resets, uploads, launches and downloads run in
     // queue order on the step stream, with no event handoff between streams
     StagingRoute on_step_stream(h->staging, h->stream);
@@ -1411,33 +1428,45 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
             std::vector<LaneRun> runs;
             runs.push_back(std::move(run));
             const size_t i = queued.size();
-            lane.desc.outcome = i > 0 ? outcomes + 4 * (i - 1) : nullptr;
+            char* results = h->replay_results.base;
+            lane.desc.outcome = i > 0 ? reinterpret_cast<uint32_t*>(results + record_at[i] - kSlot) : nullptr;
             queued.push_back(enqueue_lanes(h, std::move(runs), h->launch_events[2 * i], h->launch_events[2 * i + 1],
-                                           reinterpret_cast<StepRecord*>(h->replay_results.base + record_at[i])));
+                                           reinterpret_cast<StepRecord*>(results + record_at[i])));
+            if ((i + 1) % kResultChunk == 0 || i + 1 == launches) {
+                if (i + 1 == launches) last_ctl = h->staging.d2h(lane.desc.ctl, sizeof(LaneControl));
+                const size_t c = i / kResultChunk, from = record_at[c * kResultChunk] - kSlot;
+                chunk_from.push_back(from);
+                chunk_host.push_back(h->staging.d2h(results + from, records_end(i) - from));
+                LEO_HIP_CHECK(hipEventRecord(h->chunk_events[c], h->stream));
+            }
             at += n;
         }
     }
-    const char* last_ctl = h->staging.d2h(lane.desc.ctl, sizeof(LaneControl));
-    const char* results = h->staging.d2h(h->replay_results.base, results_bytes);
-    h->staging.wait();  // every queued kernel and download is complete
-    // the outcome of every launch but the last, as its successor found it
-    std::vector<LaneControl> outcome(queued.size());
-    for (size_t i = 0; i < queued.size(); ++i) {
-        if (i + 1 < queued.size()) {
-            uint32_t w[4];
-            std::memcpy(w, results + 4 * sizeof(uint32_t) * i, sizeof(w));
-            outcome[i].error_code = w[0];
-            outcome[i].error_step = w[1];
-            outcome[i].bias_fail = w[2];
-            outcome[i].tick = w[3];
-        } else {
-            std::memcpy(&outcome[i], last_ctl, sizeof(LaneControl));
-        }
-        queued[i].records[0] = results + record_at[i];
-        queued[i].ctl[0] = reinterpret_cast<const char*>(&outcome[i]);
-    }
+    // where a device offset of the results arrived, once its chunk is in
+    size_t chunks_in = 0;
+    auto arrived = [&](size_t i, size_t offset) {
+        const size_t c = i / kResultChunk;
+        for (; chunks_in <= c; ++chunks_in) LEO_HIP_CHECK(hipEventSynchronize(h->chunk_events[chunks_in]));
+        return chunk_host[c] + (offset - chunk_from[c]);
+    };
     try {
-        for (QueuedLaunch& q : queued) {
+        for (size_t i = 0; i < queued.size(); ++i) {
+            QueuedLaunch& q = queued[i];
+            // the outcome as the successor found it, or the control words
+            LaneControl outcome{};
+            if (i + 1 < queued.size()) {
+                uint32_t w[4];
+                std::memcpy(w, arrived(i + 1, record_at[i + 1] - kSlot), sizeof(w));
+                outcome.error_code = w[0];
+                outcome.error_step = w[1];
+                outcome.bias_fail = w[2];
+                outcome.tick = w[3];
+            } else {
+                arrived(i, record_at[i]);
+                std::memcpy(&outcome, last_ctl, sizeof(LaneControl));
+            }
+            q.records[0] = arrived(i, record_at[i]);
+            q.ctl[0] = reinterpret_cast<const char*>(&outcome);
             try {
                 complete_launch(h, q);
             } catch (...) {
