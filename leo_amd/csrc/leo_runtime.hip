@@ -1309,13 +1309,6 @@ struct CanonicalSegment {
     std::vector<int32_t> permissions;
 };
 
-// Runs the segments on the canonical runtime as the sequential executor
-// would (reset, then the steps, segment by segment), with every reset,
-// schedule upload, launch and download queued back to back and one wait at
-// the end instead of one per launch. Launches take the first launch's step
-// count, then four times the previous one (at most 4096); the results do not
-// depend on how the steps are cut into launches. Metrics of the steps are
-// appended to `out` in order.
 // Frozen prefix steps at the start of a replay segment (the permission alone
 // makes a canonical step frozen without output: make_step).
 size_t leading_frozen_steps(const CanonicalSegment& seg) {
@@ -1328,6 +1321,13 @@ constexpr size_t kFrozenLaunchMin = 64;
 // Launches whose results come down in one copy.
 constexpr size_t kResultChunk = 32;
 
+// Runs the segments on the canonical runtime as the sequential executor
+// would (reset, then the steps, segment by segment), with every reset,
+// upload, launch and results download queued back to back before the host
+// waits for the first results. Launches take the first launch's step count,
+// then four times the previous one (at most 4096); the results do not depend
+// on how the steps are cut into launches. Metrics of the steps are appended
+// to `out` in order.
 void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment>& segments,
                             std::vector<LeoStepMetrics>& out) {
     Lane& lane = *h->canonical;
