@@ -213,6 +213,18 @@ struct LaneControl {
     uint32_t xcc_mask;               // XCDs the lane's workgroups run on (bit per XCD)
 };
 
+// The words a launch's workgroups synchronise through, zero when the launch
+// starts: a lane's own (LaneControl::barrier, abort, xcc_mask, cleared before
+// each launch), or a planned launch's own zeroed copy.
+struct LaunchWords {
+    uint32_t barrier;
+    uint32_t abort;
+    uint32_t xcc_mask;
+};
+static_assert(offsetof(LaneControl, abort) == offsetof(LaneControl, barrier) + offsetof(LaunchWords, abort) &&
+                  offsetof(LaneControl, xcc_mask) == offsetof(LaneControl, barrier) + offsetof(LaunchWords, xcc_mask),
+              "a lane's launch words are LaneControl::barrier, abort, xcc_mask");
+
 // Per-tick work counters of the step records, kept per workgroup: workgroup p
 // adds to the words of its own 128-byte line (p * kFlagWords + 2 * kind +
 // tick parity), and a recording wave sums the P lines. (One shared line
@@ -360,6 +372,7 @@ struct LaneDesc {
     // launch can change it, for a host that reads the outcomes of a queue of
     // launches at once; null: nowhere
     uint32_t LEO_GLOBAL* outcome;
+    LaunchWords LEO_GLOBAL* launch;  // this launch's barrier words
     // phase profile (profiling kernel only): per phase, summed wall-clock ticks of
     // workgroup 0's own work [0..kPhases) and of its barrier wait [kPhases..2*kPhases)
     unsigned long long LEO_GLOBAL* phase_profile;

@@ -313,6 +313,7 @@ __device__ __forceinline__ bool lane_barrier(const LaneDesc& d, uint32_t part, u
                                              uint32_t* sums = nullptr) {
     __shared__ uint32_t s_abort;
     LaneControl* ctl = d.ctl;
+    LaunchWords LEO_GLOBAL* words = d.launch;
     if (P == 1) {
         __syncthreads();
         return true;
@@ -358,14 +359,14 @@ __device__ __forceinline__ bool lane_barrier(const LaneDesc& d, uint32_t part, u
                     }
                     break;
                 }
-                if ((spins & 15) == 15 && ld(&ctl->abort) != 0) {
+                if ((spins & 15) == 15 && ld(&words->abort) != 0) {
                     aborted = 1;
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
                 if (++spins > spin_limit) {
                     if (lane == 0) {
-                        __hip_atomic_store(&ctl->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(&words->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         set_error(ctl, kErrBarrier);
                     }
                     aborted = 1;
@@ -381,20 +382,20 @@ __device__ __forceinline__ bool lane_barrier(const LaneDesc& d, uint32_t part, u
     __syncthreads();
     target += P;
     if (threadIdx.x == 0) {
-        __hip_atomic_fetch_add(&ctl->barrier, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(&words->barrier, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         uint32_t spins = 0;
         uint32_t aborted = 0;
         for (;;) {
             // one poll in flight per workgroup; the abort flag every 16th
-            const uint32_t arrived = __hip_atomic_load(&ctl->barrier, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t arrived = __hip_atomic_load(&words->barrier, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
             if (arrived >= target) break;
-            if ((spins & 15) == 15 && ld(&ctl->abort) != 0) {
+            if ((spins & 15) == 15 && ld(&words->abort) != 0) {
                 aborted = 1;
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
             if (++spins > spin_limit) {
-                __hip_atomic_store(&ctl->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&words->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 set_error(ctl, kErrBarrier);
                 aborted = 1;
                 break;
@@ -3334,10 +3335,10 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
     if (P > 1 && args.local_sync) {
         // each workgroup clears its arrival words (last launch's epochs)
         // before the launch's first barrier, which counts arrivals instead
-        if (threadIdx.x == 0) atomicOr(&c.ctl->xcc_mask, 1u << xcc_id());
+        if (threadIdx.x == 0) atomicOr(&c.d.launch->xcc_mask, 1u << xcc_id());
         if (threadIdx.x < 2) c.d.barrier_flags[c.part * kFlagWords + threadIdx.x] = 0u;
         if (!lane_barrier(c.d, c.part, P, target, spin, false)) return;
-        c.local = __popc(ld(&c.ctl->xcc_mask)) == 1;
+        c.local = __popc(ld(&c.d.launch->xcc_mask)) == 1;
     }
     {
         // a workgroup's winners fit the 16 bits its arrival word carries

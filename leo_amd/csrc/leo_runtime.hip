@@ -288,6 +288,7 @@ struct LeoHipRuntime {
     leo::Arena lane_descs;     // LaneDesc[max(1,max_lanes)]
     leo::Arena kernel_args_buf;  // KernelArgs of the step kernel
     leo::Arena replay_results;   // a canonical run's launch outcomes and step records
+    leo::Arena replay_plan;      // a canonical run's launch headers and step parameters
     std::vector<hipEvent_t> chunk_events;  // a canonical run's result chunks downloaded
     leo::Arena merge_acc;        // f64 sums + changed flags of the lane-group merge
     leo::Arena merge_list;       // candidate positions of one tensor's merge
@@ -499,6 +500,7 @@ void allocate_lane_state(Lane& lane, const Sizes& z, hipStream_t stream, uint32_
     char* b = lane.state.base;
     LaneDesc& d = lane.desc;
     d.ctl = reinterpret_cast<LaneControl*>(b + o_ctl);
+    d.launch = reinterpret_cast<LaunchWords*>(&d.ctl->barrier);
     d.barrier_flags = reinterpret_cast<uint32_t*>(b + o_flag);
     d.wg_counts = reinterpret_cast<uint32_t*>(b + o_cnt);
     d.neuron = reinterpret_cast<uint32_t*>(b + o_neu);
@@ -738,15 +740,23 @@ void clear_reported_error(Lane& lane, hipStream_t stream) {
     lane.error_seen = false;
 }
 
-void reset_lane_objects(LeoHipRuntime* h, const std::vector<Lane*>& lanes, bool set_tick, uint32_t new_tick) {
+// A reset's device part (the lanes' descriptors up, then leo_reset_lanes) and
+// its host mirrors.
+void reset_lane_device(LeoHipRuntime* h, const std::vector<Lane*>& lanes, bool set_tick, uint32_t new_tick) {
     for (Lane* l : lanes) clear_reported_error(*l, h->stream);
     stage_descs(h, lanes);
     reset_lanes(h, static_cast<uint32_t>(lanes.size()), set_tick, new_tick);
+}
+void reset_lane_mirrors(const std::vector<Lane*>& lanes, bool set_tick, uint32_t new_tick) {
     for (Lane* l : lanes) {
         if (set_tick) l->tick = new_tick;
         l->plasticity_phase = 0;
         l->persistent_activity = false;
     }
+}
+void reset_lane_objects(LeoHipRuntime* h, const std::vector<Lane*>& lanes, bool set_tick, uint32_t new_tick) {
+    reset_lane_device(h, lanes, set_tick, new_tick);
+    reset_lane_mirrors(lanes, set_tick, new_tick);
 }
 
 // Launch shape of `lanes` lanes: the wanted workgroups per lane, capped by the
@@ -933,22 +943,50 @@ void ensure_schedule(Lane& lane, size_t steps) {
     lane.schedule_capacity = cap;
 }
 
+// The delays whose events a step's tick may deliver at emission: the arrival
+// step is in the same launch and runs no learning trace.
+void mark_early_delivery(std::vector<StepParams>& steps) {
+    for (size_t i = 0; i < steps.size(); ++i) {
+        uint32_t early = 0;
+        for (uint32_t dl = 0; dl < 4; ++dl) {
+            const size_t at = i + (size_t(1) << dl);
+            if (at < steps.size() && !(steps[at].flags & kStepLearnTrace)) early |= 1u << dl;
+        }
+        steps[i].flags = (steps[i].flags & ~static_cast<uint32_t>(kStepEarlyMask)) | (early << kStepEarlyShift);
+    }
+}
+
+void check_tick_range(const LeoHipRuntime* h, uint32_t tick, size_t steps) {
+    const uint64_t end = static_cast<uint64_t>(tick) + steps;
+    if (end + static_cast<uint64_t>(h->cfg.device.refractory_ticks) + 2 >= 0xffffffffULL)
+        throw Error(LEO_ERR_UNSUPPORTED, "lane tick would exceed the 32-bit device tick range");
+}
+
+bool frozen_only_steps(const std::vector<StepParams>& steps) {
+    for (const StepParams& sp : steps)
+        if (!frozen_only_step(sp)) return false;
+    return true;
+}
+
+// The step kernel build: the profiling build, the frozen-only build when
+// every step of the launch is frozen without output (and the lanes select
+// redundantly), else the general one.
+const void* step_kernel(const LeoHipRuntime* h, bool frozen_only, bool redundant_global) {
+    if (h->phase_profile) return reinterpret_cast<const void*>(&leo_lane_steps_profiled);
+    return h->frozen_kernel && redundant_global && frozen_only ? reinterpret_cast<const void*>(&leo_lane_steps_frozen)
+                                                               : reinterpret_cast<const void*>(&leo_lane_steps);
+}
+
 // Queues one launch without waiting for it: uploads through the pinned
 // staging (after the step stream's queued work, which may still read the
 // buffers they replace), the control words' clears and the kernel, then the
 // downloads on the transfer stream. The caller has reserved the staging
 // space of everything it queues before the next drain, and sized the
-// schedule buffers. The lanes' host tick mirrors advance at once. With
-// `deferred_records` (one lane only), the step records go there and nothing
-// is downloaded: the caller downloads the records and fills in the outcome.
-QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent_t start, hipEvent_t stop,
-                           StepRecord* deferred_records = nullptr) {
+// schedule buffers. The lanes' host tick mirrors advance at once.
+QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent_t start, hipEvent_t stop) {
     QueuedLaunch q;
     const uint32_t count = static_cast<uint32_t>(runs.size());
-    uint64_t max_tick = 0;
-    for (auto& r : runs) max_tick = std::max<uint64_t>(max_tick, static_cast<uint64_t>(r.lane->tick) + r.steps.size());
-    if (max_tick + static_cast<uint64_t>(h->cfg.device.refractory_ticks) + 2 >= 0xffffffffULL)
-        throw Error(LEO_ERR_UNSUPPORTED, "lane tick would exceed the 32-bit device tick range");
+    for (auto& r : runs) check_tick_range(h, r.lane->tick, r.steps.size());
     // lanes are padded to a multiple of the XCD count so that each lane's
     // workgroups land on one XCD (see lane_steps)
     q.canonical = count == 1 && runs[0].lane == h->canonical.get();
@@ -958,7 +996,6 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
     h->staging.follow(h->stream);  // the uploads replace what queued work may still read
     // a single lane's kernel arguments and descriptor go up with its schedule
     const bool single = count == 1;
-    if (deferred_records && !single) throw Error(LEO_ERR_INTERNAL, "deferred records of more than one lane");
     for (auto& r : runs) {
         Lane& lane = *r.lane;
         if (r.steps.size() > lane.schedule_capacity) throw Error(LEO_ERR_INTERNAL, "schedule buffer not sized");
@@ -966,26 +1003,15 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
         lane.desc.records = reinterpret_cast<StepRecord*>(
             lane.schedule.base + kScheduleHeader +
             ((static_cast<size_t>(lane.schedule_capacity) * sizeof(StepParams) + 255) & ~size_t(255)));
-        if (deferred_records) lane.desc.records = deferred_records;
         lane.desc.step_count = static_cast<uint32_t>(r.steps.size());
-        // the delays whose events a step's tick may deliver at emission: the
-        // arrival step is in this launch and runs no learning trace
-        for (size_t i = 0; i < r.steps.size(); ++i) {
-            uint32_t early = 0;
-            for (uint32_t dl = 0; dl < 4; ++dl) {
-                const size_t at = i + (size_t(1) << dl);
-                if (at < r.steps.size() && !(r.steps[at].flags & kStepLearnTrace)) early |= 1u << dl;
-            }
-            r.steps[i].flags = (r.steps[i].flags & ~static_cast<uint32_t>(kStepEarlyMask)) | (early << kStepEarlyShift);
-        }
+        mark_early_delivery(r.steps);
         if (!single)
             h->staging.h2d(const_cast<StepParams*>(lane.desc.steps), r.steps.data(), r.steps.size() * sizeof(StepParams));
         // cleared on the transfer stream, after the previous launch's
         // control words have been downloaded there; the error word only once
         // the host has reported its code (a launch queued behind a failed
         // one finds it set and runs nothing)
-        static_assert(offsetof(LaneControl, xcc_mask) == offsetof(LaneControl, barrier) + 8, "cleared together");
-        LEO_HIP_CHECK(hipMemsetAsync(&lane.desc.ctl->barrier, 0, 12, h->staging.active()));  // barrier, abort, xcc_mask
+        LEO_HIP_CHECK(hipMemsetAsync(lane.desc.launch, 0, sizeof(LaunchWords), h->staging.active()));
         clear_reported_error(lane, h->staging.active());
         if (!h->staging.route) h->staging.pending_uploads = true;
     }
@@ -1014,12 +1040,9 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
     }
     h->staging.publish(h->stream);
     void* params[] = {&device_args};
-    bool frozen_only = h->frozen_kernel && a.redundant_global != 0;
-    for (const LaneRun& r : runs)
-        for (const StepParams& sp : r.steps) frozen_only = frozen_only && frozen_only_step(sp);
-    const void* kernel = h->phase_profile ? reinterpret_cast<const void*>(&leo_lane_steps_profiled)
-                         : frozen_only    ? reinterpret_cast<const void*>(&leo_lane_steps_frozen)
-                                          : reinterpret_cast<const void*>(&leo_lane_steps);
+    bool frozen_only = true;
+    for (const LaneRun& r : runs) frozen_only = frozen_only && frozen_only_steps(r.steps);
+    const void* kernel = step_kernel(h, frozen_only, a.redundant_global != 0);
     if (h->phase_profile)
         for (auto& r : runs) LEO_HIP_CHECK(hipMemsetAsync(r.lane->desc.phase_profile, 0, 2 * kPhases * 8, h->stream));
     q.start = start;
@@ -1032,10 +1055,8 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
     q.records.resize(count);
     q.ctl.resize(count);
     for (uint32_t i = 0; i < count; ++i) {
-        if (!deferred_records) {
-            q.records[i] = h->staging.d2h(runs[i].lane->desc.records, runs[i].steps.size() * sizeof(StepRecord));
-            q.ctl[i] = h->staging.d2h(runs[i].lane->desc.ctl, sizeof(LaneControl));
-        }
+        q.records[i] = h->staging.d2h(runs[i].lane->desc.records, runs[i].steps.size() * sizeof(StepRecord));
+        q.ctl[i] = h->staging.d2h(runs[i].lane->desc.ctl, sizeof(LaneControl));
         runs[i].lane->tick += static_cast<uint32_t>(runs[i].steps.size());
         q.end_tick.push_back(runs[i].lane->tick);
     }
@@ -1341,7 +1362,7 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
     }
     // launch cuts and the staging they need, known before anything is queued
     std::vector<std::vector<size_t>> cuts(segments.size());
-    size_t staged = 0, largest = 0, launches = 0;
+    size_t staged = 0, launches = 0;
     for (size_t k = 0; k < segments.size(); ++k) {
         if (segments[k].reset_before) staged += PinnedStaging::rounded(sizeof(LaneDesc));
         size_t chunk = first_canonical_chunk(h);
@@ -1354,7 +1375,6 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
             const size_t n = std::min(chunk, end - at);
             cuts[k].push_back(n);
             staged += launch_staging_bytes(1, {n});
-            largest = std::max(largest, n);
             at += n;
             chunk = std::min<size_t>(4096, chunk * 4);
         }
@@ -1381,65 +1401,120 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
             results_bytes += PinnedStaging::rounded(n * sizeof(StepRecord));
         }
     auto records_end = [&](size_t i) { return i + 1 < launches ? record_at[i + 1] - kSlot : results_bytes; };
+    // Every launch's kernel arguments, lane descriptor, zeroed barrier words
+    // and step parameters go up in one copy before the first launch, so that
+    // the stream holds nothing between two launches of a segment but their
+    // timing events.
+    constexpr size_t kPlanDesc = 512, kPlanWords = 960, kPlanHeader = 1024;
+    static_assert(sizeof(KernelArgs) <= kPlanDesc && kPlanDesc + sizeof(LaneDesc) <= kPlanWords &&
+                      kPlanWords + sizeof(LaunchWords) <= kPlanHeader,
+                  "launch plan header");
+    std::vector<size_t> plan_at;
+    size_t plan_bytes = 0;
+    for (const auto& c : cuts)
+        for (size_t n : c) {
+            plan_at.push_back(plan_bytes);
+            plan_bytes += kPlanHeader + PinnedStaging::rounded(n * sizeof(StepParams));
+        }
     staged += results_bytes + PinnedStaging::rounded(sizeof(LaneControl));
     sync(h->stream);
     if (h->replay_results.bytes < results_bytes) h->replay_results.allocate(results_bytes);
+    if (h->replay_plan.bytes < plan_bytes) h->replay_plan.allocate(plan_bytes);
     const size_t chunks = (launches + kResultChunk - 1) / kResultChunk;
     while (h->chunk_events.size() < chunks) {
         hipEvent_t e;
         LEO_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         h->chunk_events.push_back(e);
     }
-    ensure_schedule(lane, largest);
     h->staging.reserve(staged);
     while (h->launch_events.size() < 2 * launches) {
         hipEvent_t e;
         LEO_HIP_CHECK(hipEventCreate(&e));
         h->launch_events.push_back(e);
     }
+    const LanePlan shape = choose_wgs_per_lane(h, 1, true);
+    const uint32_t P = shape.P, stride = shape.stride;
+    if (P > kMaxLaneWgs) throw Error(LEO_ERR_INTERNAL, "more workgroups per lane than barrier flags");
+    if (static_cast<uint64_t>(shape.grid) > cooperative_capacity(h->cus, h->coop_blocks_per_cu))
+        throw Error(LEO_ERR_INTERNAL, "cooperative launch exceeds the resident workgroup capacity");
+    // the host part, in the executor's order: the lane's mirrors through the
+    // resets and steps, every launch's schedule and header
+    char* results = h->replay_results.base;
+    char* plan = h->replay_plan.base;
+    char* image = h->staging.take(plan_bytes);
     std::vector<QueuedLaunch> queued;
+    std::vector<const void*> kernels;
+    std::vector<const KernelArgs*> device_args;
     queued.reserve(launches);
+    for (size_t k = 0; k < segments.size(); ++k) {
+        const CanonicalSegment& seg = segments[k];
+        if (seg.reset_before) reset_lane_mirrors({&lane}, false, 0);
+        size_t at = 0;
+        for (size_t n : cuts[k]) {
+            const size_t i = queued.size();
+            LaneRun run{&lane, {}, {}};
+            run.steps.reserve(n);
+            check_tick_range(h, lane.tick, n);
+            uint32_t tick = lane.tick;
+            for (size_t j = at; j < at + n; ++j) {
+                run.phase.push_back(lane.plasticity_phase);
+                run.steps.push_back(make_step(h->cfg, lane, seg.steps[j].symbol, seg.steps[j].target,
+                                              seg.permissions[j], tick++, false));
+            }
+            mark_early_delivery(run.steps);
+            char* dev = plan + plan_at[i];
+            LaneDesc desc = lane.desc;
+            desc.steps = reinterpret_cast<const StepParams*>(dev + kPlanHeader);
+            desc.records = reinterpret_cast<StepRecord*>(results + record_at[i]);
+            desc.step_count = static_cast<uint32_t>(n);
+            desc.outcome = i > 0 ? reinterpret_cast<uint32_t*>(results + record_at[i] - kSlot) : nullptr;
+            desc.launch = reinterpret_cast<LaunchWords*>(dev + kPlanWords);
+            KernelArgs a = kernel_args(h, reinterpret_cast<LaneDesc*>(dev + kPlanDesc), 1, P);
+            a.lane_stride = stride;
+            char* img = image + plan_at[i];
+            std::memcpy(img, &a, sizeof(KernelArgs));
+            std::memcpy(img + kPlanDesc, &desc, sizeof(LaneDesc));
+            std::memset(img + kPlanWords, 0, sizeof(LaunchWords));
+            std::memcpy(img + kPlanHeader, run.steps.data(), n * sizeof(StepParams));
+            kernels.push_back(step_kernel(h, frozen_only_steps(run.steps), a.redundant_global != 0));
+            device_args.push_back(reinterpret_cast<const KernelArgs*>(dev));
+            lane.tick += static_cast<uint32_t>(n);
+            QueuedLaunch q;
+            q.runs.push_back(std::move(run));
+            q.records.resize(1);
+            q.ctl.resize(1);
+            q.end_tick.push_back(lane.tick);
+            q.start = h->launch_events[2 * i];
+            q.stop = h->launch_events[2 * i + 1];
+            q.canonical = true;
+            queued.push_back(std::move(q));
+            at += n;
+        }
+    }
+    // the device part: one stream, in queue order (no event handoff between
+    // streams): the upload, then resets, launches and result downloads
     std::vector<size_t> chunk_from;
     std::vector<const char*> chunk_host;
     const char* last_ctl = nullptr;
-    // one lane and one stream: resets, uploads, launches and downloads run in
-    // queue order on the step stream, with no event handoff between streams
     StagingRoute on_step_stream(h->staging, h->stream);
-    struct OutcomeScope {  // later launches of the lane store no outcome
-        Lane& lane;
-        ~OutcomeScope() { lane.desc.outcome = nullptr; }
-    } outcome_scope{lane};
+    LEO_HIP_CHECK(hipMemcpyAsync(plan, image, plan_bytes, hipMemcpyHostToDevice, h->stream));
+    const uint32_t lds = step_lds_bytes(h->cfg.device.neurons_per_block);
+    size_t i = 0;
     for (size_t k = 0; k < segments.size(); ++k) {
-        const CanonicalSegment& seg = segments[k];
-        if (seg.reset_before) {
-            std::vector<Lane*> lanes{&lane};
-            reset_lane_objects(h, lanes, false, 0);
-        }
-        size_t at = 0;
-        for (size_t n : cuts[k]) {
-            LaneRun run{&lane, {}, {}};
-            run.steps.reserve(n);
-            uint32_t tick = lane.tick;
-            for (size_t i = at; i < at + n; ++i) {
-                run.phase.push_back(lane.plasticity_phase);
-                run.steps.push_back(make_step(h->cfg, lane, seg.steps[i].symbol, seg.steps[i].target,
-                                              seg.permissions[i], tick++, false));
-            }
-            std::vector<LaneRun> runs;
-            runs.push_back(std::move(run));
-            const size_t i = queued.size();
-            char* results = h->replay_results.base;
-            lane.desc.outcome = i > 0 ? reinterpret_cast<uint32_t*>(results + record_at[i] - kSlot) : nullptr;
-            queued.push_back(enqueue_lanes(h, std::move(runs), h->launch_events[2 * i], h->launch_events[2 * i + 1],
-                                           reinterpret_cast<StepRecord*>(results + record_at[i])));
+        if (segments[k].reset_before) reset_lane_device(h, {&lane}, false, 0);
+        for (size_t c = 0; c < cuts[k].size(); ++c, ++i) {
+            clear_reported_error(lane, h->stream);
+            void* params[] = {&device_args[i]};
+            LEO_HIP_CHECK(hipEventRecord(queued[i].start, h->stream));
+            LEO_HIP_CHECK(hipLaunchCooperativeKernel(kernels[i], dim3(stride * P), dim3(kThreads), params, lds, h->stream));
+            LEO_HIP_CHECK(hipEventRecord(queued[i].stop, h->stream));
             if ((i + 1) % kResultChunk == 0 || i + 1 == launches) {
                 if (i + 1 == launches) last_ctl = h->staging.d2h(lane.desc.ctl, sizeof(LaneControl));
-                const size_t c = i / kResultChunk, from = record_at[c * kResultChunk] - kSlot;
+                const size_t from = record_at[(i / kResultChunk) * kResultChunk] - kSlot;
                 chunk_from.push_back(from);
                 chunk_host.push_back(h->staging.d2h(results + from, records_end(i) - from));
-                LEO_HIP_CHECK(hipEventRecord(h->chunk_events[c], h->stream));
+                LEO_HIP_CHECK(hipEventRecord(h->chunk_events[i / kResultChunk], h->stream));
             }
-            at += n;
         }
     }
     // where a device offset of the results arrived, once its chunk is in
