@@ -710,12 +710,13 @@ KernelArgs kernel_args(LeoHipRuntime* h, LaneDesc* lanes, uint32_t count, uint32
 }
 
 // Reset transient state of the given lanes (runtime.rs:365-425). Descriptors
-// of these lanes must already be resident at lane_descs[0..count).
-void reset_lanes(LeoHipRuntime* h, uint32_t count, bool set_tick, uint32_t new_tick) {
-    LaneDesc* descs = reinterpret_cast<LaneDesc*>(h->lane_descs.base);
+// of these lanes must already be resident at `descs` (default:
+// lane_descs[0..count)).
+void reset_lanes(LeoHipRuntime* h, uint32_t count, bool set_tick, uint32_t new_tick, LaneDesc* descs = nullptr) {
+    if (!descs) descs = reinterpret_cast<LaneDesc*>(h->lane_descs.base);
     KernelArgs a = kernel_args(h, descs, count, 1);
-    // about four workgroups per CU in all, at least 64 per lane
-    const uint32_t parts = std::max<uint32_t>(64, static_cast<uint32_t>(4 * h->cus) / std::max<uint32_t>(count, 1));
+    // about eight workgroups per CU in all, at least 64 per lane
+    const uint32_t parts = std::max<uint32_t>(64, static_cast<uint32_t>(8 * h->cus) / std::max<uint32_t>(count, 1));
     uint32_t grid = count * parts;
     hipLaunchKernelGGL(leo_reset_lanes, dim3(grid), dim3(kThreads), 0, h->stream, a, set_tick ? 1u : 0u, new_tick);
     LEO_HIP_CHECK(hipGetLastError());
@@ -1501,7 +1502,16 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
     const uint32_t lds = step_lds_bytes(h->cfg.device.neurons_per_block);
     size_t i = 0;
     for (size_t k = 0; k < segments.size(); ++k) {
-        if (segments[k].reset_before) reset_lane_device(h, {&lane}, false, 0);
+        if (segments[k].reset_before) {
+            if (cuts[k].empty()) {
+                reset_lane_device(h, {&lane}, false, 0);
+            } else {
+                // the descriptor in the next launch's header holds the lane's
+                // state as the reset reads it
+                clear_reported_error(lane, h->stream);
+                reset_lanes(h, 1, false, 0, reinterpret_cast<LaneDesc*>(plan + plan_at[i] + kPlanDesc));
+            }
+        }
         for (size_t c = 0; c < cuts[k].size(); ++c, ++i) {
             clear_reported_error(lane, h->stream);
             void* params[] = {&device_args[i]};
