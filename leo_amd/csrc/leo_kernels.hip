@@ -3534,6 +3534,20 @@ __global__ void __launch_bounds__(kThreads) leo_lane_steps_frozen(const KernelAr
     lane_steps<false, true>(*args);
 }
 
+// Each lane's outcome of the launch before this kernel on the stream (error
+// code, error step, bias fail, tick): four words per lane, gathered next to
+// the launch's step records so that one download brings both.
+__global__ void __launch_bounds__(kThreads) leo_lane_outcomes(const KernelArgs* __restrict__ args,
+                                                            uint32_t* __restrict__ out) {
+    const uint32_t l = blockIdx.x * kThreads + threadIdx.x;
+    if (l >= args->lane_count) return;
+    const LaneControl* ctl = args->lanes[l].ctl;
+    out[4 * l + 0] = ctl->error_code;
+    out[4 * l + 1] = ctl->error_step;
+    out[4 * l + 2] = ctl->bias_fail;
+    out[4 * l + 3] = ctl->tick;
+}
+
 // A story group's fork of the canonical parameters (parallel.rs: each worker
 // starts from base.clone()): every 16-byte vector of one canonical tensor is
 // read once and stored to each lane's copy.

@@ -36,6 +36,7 @@ namespace leo {
 __global__ void leo_lane_steps(const KernelArgs* args);
 __global__ void leo_lane_steps_profiled(const KernelArgs* args);
 __global__ void leo_lane_steps_frozen(const KernelArgs* args);
+__global__ void leo_lane_outcomes(const KernelArgs* args, uint32_t* out);
 __global__ void leo_reset_lanes(KernelArgs args, uint32_t set_tick, uint32_t new_tick);
 
 __global__ void leo_merge_fixed(MergeArgs m);
@@ -286,9 +287,9 @@ struct LeoHipRuntime {
     std::vector<std::unique_ptr<leo::Lane>> lanes;
     uint32_t max_lanes = 0;
     leo::Arena lane_descs;     // LaneDesc[max(1,max_lanes)]
-    leo::Arena kernel_args_buf;  // KernelArgs of the step kernel
     leo::Arena replay_results;   // a canonical run's launch outcomes and step records
     leo::Arena replay_plan;      // a canonical run's launch headers and step parameters
+    leo::Arena launch_block;     // a launch of several lanes: arguments, descriptors, schedules, results
     std::vector<hipEvent_t> chunk_events;  // a canonical run's result chunks downloaded
     leo::Arena merge_acc;        // f64 sums + changed flags of the lane-group merge
     leo::Arena merge_list;       // candidate positions of one tensor's merge
@@ -911,6 +912,7 @@ void account_launch(LeoHipRuntime* h, const std::vector<LaneRun>& runs, float ms
 struct QueuedLaunch {
     std::vector<LaneRun> runs;
     std::vector<const char*> records, ctl;
+    const char* outcomes = nullptr;  // instead of ctl: four outcome words per lane
     std::vector<uint32_t> end_tick;
     hipEvent_t start = nullptr, stop = nullptr;
     bool canonical = false;
@@ -995,9 +997,25 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
     const uint32_t P = plan.P, stride = plan.stride;
     if (P > kMaxLaneWgs) throw Error(LEO_ERR_INTERNAL, "more workgroups per lane than barrier flags");
     h->staging.follow(h->stream);  // the uploads replace what queued work may still read
-    // a single lane's kernel arguments and descriptor go up with its schedule
+    if (static_cast<uint64_t>(plan.grid) > cooperative_capacity(h->cus, h->coop_blocks_per_cu))
+        throw Error(LEO_ERR_INTERNAL, "cooperative launch exceeds the resident workgroup capacity");
     const bool single = count == 1;
     for (auto& r : runs) {
+        mark_early_delivery(r.steps);
+        clear_reported_error(*r.lane, h->staging.active());
+    }
+    KernelArgs a;
+    const KernelArgs* device_args = nullptr;
+    // Several lanes share one launch block: kernel arguments, descriptors,
+    // each lane's zeroed barrier words (a 128-byte line each), then the
+    // schedules (one upload), then the step records and the lanes' outcome
+    // words, which leo_lane_outcomes gathers there (one download).
+    size_t block_records = 0, block_outcomes = 0;
+    std::vector<size_t> record_at(count);
+    if (single) {
+        // a single lane's kernel arguments and descriptor go up with its
+        // schedule, in the header of the lane's schedule buffer
+        LaneRun& r = runs[0];
         Lane& lane = *r.lane;
         if (r.steps.size() > lane.schedule_capacity) throw Error(LEO_ERR_INTERNAL, "schedule buffer not sized");
         lane.desc.steps = reinterpret_cast<const StepParams*>(lane.schedule.base + kScheduleHeader);
@@ -1005,40 +1023,56 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
             lane.schedule.base + kScheduleHeader +
             ((static_cast<size_t>(lane.schedule_capacity) * sizeof(StepParams) + 255) & ~size_t(255)));
         lane.desc.step_count = static_cast<uint32_t>(r.steps.size());
-        mark_early_delivery(r.steps);
-        if (!single)
-            h->staging.h2d(const_cast<StepParams*>(lane.desc.steps), r.steps.data(), r.steps.size() * sizeof(StepParams));
-        // cleared on the transfer stream, after the previous launch's
-        // control words have been downloaded there; the error word only once
-        // the host has reported its code (a launch queued behind a failed
-        // one finds it set and runs nothing)
+        // cleared after the previous launch's control words have been
+        // downloaded (a launch queued behind a failed one finds the error
+        // word set and runs nothing)
         LEO_HIP_CHECK(hipMemsetAsync(lane.desc.launch, 0, sizeof(LaunchWords), h->staging.active()));
-        clear_reported_error(lane, h->staging.active());
-        if (!h->staging.route) h->staging.pending_uploads = true;
-    }
-    if (static_cast<uint64_t>(plan.grid) > cooperative_capacity(h->cus, h->coop_blocks_per_cu))
-        throw Error(LEO_ERR_INTERNAL, "cooperative launch exceeds the resident workgroup capacity");
-    KernelArgs a;
-    const KernelArgs* device_args = nullptr;
-    if (single) {
-        const LaneRun& r = runs[0];
-        char* header = r.lane->schedule.base;
+        char* header = lane.schedule.base;
         a = kernel_args(h, reinterpret_cast<LaneDesc*>(header + kHeaderDesc), 1, P);
         a.lane_stride = stride;
         h->staging.h2d_gather(header, {{&a, sizeof(KernelArgs), kHeaderArgs},
-                                       {&r.lane->desc, sizeof(LaneDesc), kHeaderDesc},
+                                       {&lane.desc, sizeof(LaneDesc), kHeaderDesc},
                                        {r.steps.data(), r.steps.size() * sizeof(StepParams), kScheduleHeader}});
         device_args = reinterpret_cast<const KernelArgs*>(header + kHeaderArgs);
     } else {
-        std::vector<Lane*> lanes;
-        for (auto& r : runs) lanes.push_back(r.lane);
-        stage_descs(h, lanes);
-        a = kernel_args(h, reinterpret_cast<LaneDesc*>(h->lane_descs.base), count, P);
+        constexpr size_t kWordsStride = 128;
+        const size_t descs_at = kHeaderDesc;
+        const size_t words_at = PinnedStaging::rounded(descs_at + count * sizeof(LaneDesc));
+        size_t cursor = PinnedStaging::rounded(words_at + count * kWordsStride);
+        std::vector<size_t> steps_at(count);
+        for (uint32_t i = 0; i < count; ++i) {
+            steps_at[i] = cursor;
+            cursor += PinnedStaging::rounded(runs[i].steps.size() * sizeof(StepParams));
+        }
+        const size_t upload = cursor;
+        block_records = cursor;
+        for (uint32_t i = 0; i < count; ++i) {
+            record_at[i] = cursor;
+            cursor += PinnedStaging::rounded(runs[i].steps.size() * sizeof(StepRecord));
+        }
+        block_outcomes = cursor;
+        cursor += PinnedStaging::rounded(count * 4 * sizeof(uint32_t));
+        if (h->launch_block.bytes < cursor) h->launch_block.allocate(cursor);
+        char* block = h->launch_block.base;
+        char* image = h->staging.take(upload);
+        for (uint32_t i = 0; i < count; ++i) {
+            LaneDesc d = runs[i].lane->desc;
+            d.steps = reinterpret_cast<const StepParams*>(block + steps_at[i]);
+            d.records = reinterpret_cast<StepRecord*>(block + record_at[i]);
+            d.step_count = static_cast<uint32_t>(runs[i].steps.size());
+            d.launch = reinterpret_cast<LaunchWords*>(block + words_at + i * kWordsStride);
+            std::memcpy(image + descs_at + i * sizeof(LaneDesc), &d, sizeof(LaneDesc));
+            std::memset(image + words_at + i * kWordsStride, 0, sizeof(LaunchWords));
+            if (!runs[i].steps.empty())
+                std::memcpy(image + steps_at[i], runs[i].steps.data(), runs[i].steps.size() * sizeof(StepParams));
+        }
+        a = kernel_args(h, reinterpret_cast<LaneDesc*>(block + descs_at), count, P);
         a.lane_stride = stride;
-        if (!h->kernel_args_buf.base) h->kernel_args_buf.allocate(sizeof(KernelArgs));
-        h->staging.h2d(h->kernel_args_buf.base, &a, sizeof(KernelArgs));
-        device_args = reinterpret_cast<const KernelArgs*>(h->kernel_args_buf.base);
+        std::memcpy(image, &a, sizeof(KernelArgs));
+        LEO_HIP_CHECK(hipMemcpyAsync(block, image, upload, hipMemcpyHostToDevice, h->staging.active()));
+        device_args = reinterpret_cast<const KernelArgs*>(block);
     }
+    if (!h->staging.route) h->staging.pending_uploads = true;
     h->staging.publish(h->stream);
     void* params[] = {&device_args};
     bool frozen_only = true;
@@ -1052,12 +1086,27 @@ QueuedLaunch enqueue_lanes(LeoHipRuntime* h, std::vector<LaneRun> runs, hipEvent
     LEO_HIP_CHECK(hipLaunchCooperativeKernel(kernel, dim3(stride * P), dim3(kThreads), params,
                                              step_lds_bytes(h->cfg.device.neurons_per_block), h->stream));
     LEO_HIP_CHECK(hipEventRecord(stop, h->stream));
+    if (!single) {
+        char* block = h->launch_block.base;
+        hipLaunchKernelGGL(leo_lane_outcomes, dim3((count + kThreads - 1) / kThreads), dim3(kThreads), 0, h->stream,
+                           device_args, reinterpret_cast<uint32_t*>(block + block_outcomes));
+        LEO_HIP_CHECK(hipGetLastError());
+    }
     h->staging.follow(h->stream);
     q.records.resize(count);
     q.ctl.resize(count);
+    if (!single) {
+        char* block = h->launch_block.base;
+        const size_t end = block_outcomes + PinnedStaging::rounded(count * 4 * sizeof(uint32_t));
+        const char* down = h->staging.d2h(block + block_records, end - block_records);
+        for (uint32_t i = 0; i < count; ++i) q.records[i] = down + (record_at[i] - block_records);
+        q.outcomes = down + (block_outcomes - block_records);
+    }
     for (uint32_t i = 0; i < count; ++i) {
-        q.records[i] = h->staging.d2h(runs[i].lane->desc.records, runs[i].steps.size() * sizeof(StepRecord));
-        q.ctl[i] = h->staging.d2h(runs[i].lane->desc.ctl, sizeof(LaneControl));
+        if (single) {
+            q.records[i] = h->staging.d2h(runs[i].lane->desc.records, runs[i].steps.size() * sizeof(StepRecord));
+            q.ctl[i] = h->staging.d2h(runs[i].lane->desc.ctl, sizeof(LaneControl));
+        }
         runs[i].lane->tick += static_cast<uint32_t>(runs[i].steps.size());
         q.end_tick.push_back(runs[i].lane->tick);
     }
@@ -1087,7 +1136,16 @@ void complete_launch(LeoHipRuntime* h, QueuedLaunch& q) {
     for (uint32_t i = 0; i < count; ++i) {
         q.runs[i].records.resize(q.runs[i].steps.size());
         std::memcpy(q.runs[i].records.data(), q.records[i], q.runs[i].steps.size() * sizeof(StepRecord));
-        std::memcpy(&ctl[i], q.ctl[i], sizeof(LaneControl));
+        if (q.outcomes) {
+            uint32_t w[4];
+            std::memcpy(w, q.outcomes + 4 * sizeof(uint32_t) * i, sizeof(w));
+            ctl[i].error_code = w[0];
+            ctl[i].error_step = w[1];
+            ctl[i].bias_fail = w[2];
+            ctl[i].tick = w[3];
+        } else {
+            std::memcpy(&ctl[i], q.ctl[i], sizeof(LaneControl));
+        }
     }
     float ms = 0.0f;
     LEO_HIP_CHECK(hipEventElapsedTime(&ms, q.start, q.stop));
