@@ -455,6 +455,13 @@ inline DeepSortPlan deep_sort_plan(uint32_t cap, uint32_t fanout, uint32_t synap
     return p;
 }
 
+// Words of a lane's parameter-change bitmaps (ParameterChanges): neurons
+// (threshold and output rows), recurrent synapses, input synapses, context
+// slots.
+struct ChangeWords {
+    uint64_t neurons, recurrent, input, slots;
+};
+
 struct KernelArgs {
     LeoConfig cfg;
     SharedModel m;

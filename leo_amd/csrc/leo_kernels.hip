@@ -3548,6 +3548,27 @@ __global__ void __launch_bounds__(kThreads) leo_lane_outcomes(const KernelArgs* 
     out[4 * l + 3] = ctl->tick;
 }
 
+// Clears the lanes' parameter-change bitmaps and dirty words
+// (enable_parameter_tracking) in one pass for a whole group of lanes.
+__global__ void __launch_bounds__(kThreads) leo_clear_changes(KernelArgs args, ChangeWords w) {
+    const uint32_t L = args.lane_count;
+    const uint32_t lane = blockIdx.x % L;
+    const uint32_t part = blockIdx.x / L, parts = gridDim.x / L;
+    const LaneDesc& d = args.lanes[lane];
+    const uint64_t t0 = static_cast<uint64_t>(part) * kThreads + threadIdx.x, ts = static_cast<uint64_t>(parts) * kThreads;
+    for (uint64_t i = t0; i < w.neurons; i += ts) {
+        d.ch_threshold[i] = 0u;
+        d.ch_out[i] = 0u;
+    }
+    for (uint64_t i = t0; i < w.recurrent; i += ts) d.ch_rec[i] = 0u;
+    for (uint64_t i = t0; i < w.input; i += ts) d.ch_in[i] = 0u;
+    for (uint64_t i = t0; i < w.slots; i += ts) d.ch_ctx[i] = 0u;
+    if (part == 0 && threadIdx.x == 0) {
+        d.ctl->bias_dirty = 0u;
+        d.ctl->ctx_out_dirty = 0u;
+    }
+}
+
 // A story group's fork of the canonical parameters (parallel.rs: each worker
 // starts from base.clone()): every 16-byte vector of one canonical tensor is
 // read once and stored to each lane's copy.

@@ -38,6 +38,7 @@ __global__ void leo_lane_steps_profiled(const KernelArgs* args);
 __global__ void leo_lane_steps_frozen(const KernelArgs* args);
 __global__ void leo_lane_outcomes(const KernelArgs* args, uint32_t* out);
 __global__ void leo_reset_lanes(KernelArgs args, uint32_t set_tick, uint32_t new_tick);
+__global__ void leo_clear_changes(KernelArgs args, ChangeWords w);
 
 __global__ void leo_merge_fixed(MergeArgs m);
 __global__ void leo_merge_candidates(MergeCandidates mc);
@@ -720,6 +721,17 @@ void reset_lanes(LeoHipRuntime* h, uint32_t count, bool set_tick, uint32_t new_t
     const uint32_t parts = std::max<uint32_t>(64, static_cast<uint32_t>(8 * h->cus) / std::max<uint32_t>(count, 1));
     uint32_t grid = count * parts;
     hipLaunchKernelGGL(leo_reset_lanes, dim3(grid), dim3(kThreads), 0, h->stream, a, set_tick ? 1u : 0u, new_tick);
+    LEO_HIP_CHECK(hipGetLastError());
+}
+
+// The change bitmaps of the lanes whose descriptors are resident at
+// lane_descs[0..count), in one kernel for all of them.
+void clear_lane_changes(LeoHipRuntime* h, uint32_t count) {
+    const Sizes& z = h->z;
+    const ChangeWords w{z.words(z.n), z.words(z.ns), z.words(z.ni), z.words(z.slots)};
+    KernelArgs a = kernel_args(h, reinterpret_cast<LaneDesc*>(h->lane_descs.base), count, 1);
+    const uint32_t parts = std::max<uint32_t>(16, static_cast<uint32_t>(8 * h->cus) / std::max<uint32_t>(count, 1));
+    hipLaunchKernelGGL(leo_clear_changes, dim3(count * parts), dim3(kThreads), 0, h->stream, a, w);
     LEO_HIP_CHECK(hipGetLastError());
 }
 
@@ -2249,13 +2261,10 @@ void story_batch(LeoHipRuntime* h, const uint8_t* bytes, const uint64_t* offsets
         auto t0 = std::chrono::steady_clock::now();
         const uint32_t lo = g * per_group, hi = std::min(count, lo + per_group);
         lanes.clear();
-        for (uint32_t i = lo; i < hi; ++i) {
-            Lane& l = story_lane(h, i - lo);
-            clear_changes(l, h->z, h->stream);  // enable_parameter_tracking
-            lanes.push_back(&l);
-        }
+        for (uint32_t i = lo; i < hi; ++i) lanes.push_back(&story_lane(h, i - lo));
         broadcast_params(h, lanes);  // fork(base.clone())
         reset_lane_objects(h, lanes, true, 0);  // Runtime::new (tick 0) + begin_document
+        clear_lane_changes(h, static_cast<uint32_t>(lanes.size()));  // enable_parameter_tracking
         std::vector<LaneRun> runs;
         for (uint32_t i = lo; i < hi; ++i) {
             LaneRun r{lanes[i - lo], {}, {}};
