@@ -487,6 +487,26 @@ struct KernelArgs {
     FastDiv div_synapses;            // synapses_per_neuron
     FastDiv div_block;               // neurons_per_block
     FastDiv div_block_words;         // block_words(neurons_per_block)
+    // A tally launch (the frozen-only build, one lane, host discards the
+    // steps' records): no step records and no per-step work counters; the
+    // launch's totals go here instead (kTally* words), zeroed by the launch.
+    uint32_t LEO_GLOBAL* tally;
+};
+
+// Words of a tally launch's totals: per-wave sums added at the end, then the
+// recording wave's sums as 64-bit words.
+enum : uint32_t {
+    kTEvents = 0,  // folded entries, each tick's input injections included
+    kTTouched,
+    kTInhibitory,
+    kTDeepRegister,
+    kTDeepRadix,
+    kTWaveWords,
+    kTActive = 8,   // 64-bit words from here: sum of active counts,
+    kTCells = 10,   // context cells,
+    kTKeptRec = 12, // eligible recurrent list lengths,
+    kTKeptIn = 14,  // eligible input list lengths
+    kTallyWords = 16
 };
 
 // Batch-end mean of one fixed-parameter tensor (see leo_merge_fixed).

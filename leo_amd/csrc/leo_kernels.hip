@@ -468,6 +468,8 @@ struct alignas(16) StepShared {
     uint32_t ring_early[kRing];
     // each selecting wave's winner count and first 64 winners (phase 2 to 3)
     uint32_t win_count[kWavesPerGroup];
+    uint32_t tally[kWavesPerGroup][kTWaveWords];  // a tally launch's per-wave totals
+    unsigned long long tally_rec[4];               // and the recording wave's (active, cells, kept)
     uint32_t win_n[kWavesPerGroup][kWaveSize];
     float win_act[kWavesPerGroup][kWaveSize];
     // the winner totals a one-barrier step's barrier carries: every wave's,
@@ -495,6 +497,7 @@ struct StepCtx {
     uint32_t dest_epoch;
     bool local;        // workgroups of the lane share one L2 (see lane_barrier)
     bool carried;      // a one-barrier step's barrier carries the waves' winner totals
+    uint32_t* tally;   // a tally launch: this wave's totals in LDS (kTally* words); else null
 };
 
 // This thread's item index when a phase's items are dealt 64 at a time to the
@@ -556,7 +559,13 @@ __device__ __forceinline__ uint32_t LEO_GLOBAL* counter_word(const StepCtx& c, u
 // Adds a wave's count to its workgroup's counter (every lane of the wave calls).
 __device__ __forceinline__ void count_wave(const StepCtx& c, uint32_t kind, uint32_t tick, uint32_t local) {
     const uint32_t total = wave_sum_u32(local);
-    if (__lane_id() == 0 && total) atomicAdd(counter_word(c, c.part, kind, tick), total);
+    if (__lane_id() == 0 && total) {
+        if (c.tally) {
+            if (kind == kCInhibitory) c.tally[kTInhibitory] += total;
+        } else {
+            atomicAdd(counter_word(c, c.part, kind, tick), total);
+        }
+    }
 }
 
 // One counter of `tick` summed over the lane's workgroups by a whole wave, uniform.
@@ -1418,7 +1427,10 @@ __device__ float deep_fold(const StepCtx& c, uint32_t n, float pi, uint32_t set,
         mem = mem + drive;
     }
     if (lane == 0) {
-        atomicAdd(counter_word(c, c.part, kCDeep, tick), cnt <= kDeepRegisterEntries ? 1u : 0x10000u);
+        if (c.tally)
+            c.tally[cnt <= kDeepRegisterEntries ? kTDeepRegister : kTDeepRadix] += 1u;
+        else
+            atomicAdd(counter_word(c, c.part, kCDeep, tick), cnt <= kDeepRegisterEntries ? 1u : 0x10000u);
         if (e > 0) {
             (*nf(d, n, kNFatigue)) = fat;
             (*nf(d, n, kNAdapt0)) = ad0;
@@ -1704,12 +1716,19 @@ __device__ __forceinline__ void phase_fold_select(const StepCtx& c, StepShared& 
     supra = wave_sum_u32(supra);
     entries = wave_sum_u32(entries);
     if (lane == 0) {
-        if (supra) atomicAdd(counter_word(c, c.part, kCSupra, tick), supra);
-        if (entries) atomicAdd(counter_word(c, c.part, kCEvents, tick), entries);
+        if (c.tally) {
+            // no counter atomics mid-step: each would hold up the wave's later
+            // load waits (memory operations retire in order)
+            c.tally[kTEvents] += entries;
+            c.tally[kTTouched] += listed_before;
+        } else {
+            if (supra) atomicAdd(counter_word(c, c.part, kCSupra, tick), supra);
+            if (entries) atomicAdd(counter_word(c, c.part, kCEvents, tick), entries);
+            if (listed_before) atomicAdd(counter_word(c, c.part, kCTouched, tick), listed_before);
+        }
         sh.win_count[wave] = staged;
         wave_totals(d, tick)[wv] = staged;
         d.wave_touched[wv] = listed_before;
-        if (listed_before) atomicAdd(counter_word(c, c.part, kCTouched, tick), listed_before);
     }
 }
 
@@ -1748,7 +1767,7 @@ __device__ __forceinline__ void write_active(const StepCtx& c, const StepParams&
     float pi_old = 0.0f;
     uint32_t supra = 0, rec_n = 0, in_n = 0, cells = 0, probes = 0, applied = 0;
     LateCounters late{};
-    if (rec_wave) {
+    if (rec_wave && !c.tally) {
         if (fuse_post) supra = counter_total(c, kCSupra, c.tick);
         if (step_index > 0 && !late_done) late = load_late_counters(c, c.tick - 1);
     }
@@ -1819,7 +1838,7 @@ __device__ __forceinline__ void write_active(const StepCtx& c, const StepParams&
         // tick-1's record is finished (tick-1 is complete); the recording
         // wave then clears its counters, which tick+1 reuses
         LaneControl LEO_GLOBAL* ctl = c.ctl;
-        if (step_index > 0 && !late_done) store_late_record(d, step_index - 1, late);
+        if (step_index > 0 && !late_done && !c.tally) store_late_record(d, step_index - 1, late);
         ctl->active_count = all;
         ctl->block_selected = all;
         ctl->clipped = 0;
@@ -1830,7 +1849,12 @@ __device__ __forceinline__ void write_active(const StepCtx& c, const StepParams&
         const float pi = clampf(pi_old + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
                                 cfg.population_inhibition_max);
         ctl->population_inhibition = pi;
-        if (fuse_post) {
+        if (fuse_post && c.tally) {
+            sh.tally_rec[0] += all;
+            sh.tally_rec[1] += cells;
+            sh.tally_rec[2] += rec_n;
+            sh.tally_rec[3] += in_n;
+        } else if (fuse_post) {
             // the step record the post phase would write (no readout this step)
             StepRecord LEO_GLOBAL& rec = d.records[step_index];
             rec.p_target = 0.0f;
@@ -1848,7 +1872,7 @@ __device__ __forceinline__ void write_active(const StepCtx& c, const StepParams&
             rec.error_code = 0;
         }
     }
-    if (rec_wave) clear_counters(c, c.tick);  // after its loads of tick-1's counters
+    if (rec_wave && !c.tally) clear_counters(c, c.tick);  // after its loads of tick-1's counters
     if (!fuse_post) return;
     // Post-fire updates of this wave's winners and their emission snapshots
     // (the post phase, runtime.rs:920-938, 1084-1106), folded in here when no
@@ -2107,28 +2131,39 @@ __device__ __forceinline__ float frozen_prologue(const StepCtx& c, StepShared& s
     const float pi = clampf(pi_before + cfg.population_inhibition_rate * (activity - cfg.target_activity), 0.0f,
                             cfg.population_inhibition_max);
     if (c.part == c.P - 1 && wave_index() == 0) {
-        const LateCounters late = load_late_counters(c, prev);
-        const uint32_t supra = counter_total(c, kCSupra, prev);
+        LateCounters late{};
+        uint32_t supra = 0;
+        if (!c.tally) {
+            late = load_late_counters(c, prev);
+            supra = counter_total(c, kCSupra, prev);
+        }
         if (lane == 0) {
             LaneControl LEO_GLOBAL* ctl = c.ctl;
             const uint32_t rec_n = ld(&ctl->rec_count[c.parity]), in_n = ld(&ctl->in_count[c.parity]);
             const uint32_t cells = ld(&ctl->ctx_count), probes = ld(&ctl->ctx_probes);
             const uint32_t applied = ld(&ctl->ctx_applied);
-            StepRecord LEO_GLOBAL& rec = d.records[step_index - 1];
-            rec.p_target = 0.0f;
-            rec.predicted = 0;
-            rec.population_inhibition = pi;
-            rec.active = all;
-            rec.suprathreshold = supra;
-            rec.block_selected = all;
-            rec.clipped = 0;
-            rec.context_cells = cells;
-            rec.context_probes = probes;
-            rec.context_applied = applied;
-            rec.eligible_rec = rec_n;
-            rec.eligible_in = in_n;
-            rec.error_code = 0;
-            store_late_record(d, step_index - 1, late);
+            if (c.tally) {
+                sh.tally_rec[0] += all;
+                sh.tally_rec[1] += cells;
+                sh.tally_rec[2] += rec_n;
+                sh.tally_rec[3] += in_n;
+            } else {
+                StepRecord LEO_GLOBAL& rec = d.records[step_index - 1];
+                rec.p_target = 0.0f;
+                rec.predicted = 0;
+                rec.population_inhibition = pi;
+                rec.active = all;
+                rec.suprathreshold = supra;
+                rec.block_selected = all;
+                rec.clipped = 0;
+                rec.context_cells = cells;
+                rec.context_probes = probes;
+                rec.context_applied = applied;
+                rec.eligible_rec = rec_n;
+                rec.eligible_in = in_n;
+                rec.error_code = 0;
+                store_late_record(d, step_index - 1, late);
+            }
             ctl->active_count = all;
             ctl->block_selected = all;
             ctl->clipped = 0;
@@ -2138,7 +2173,7 @@ __device__ __forceinline__ float frozen_prologue(const StepCtx& c, StepShared& s
             ctl->ring_count[rs] = all;
             ctl->ring_early[rs] = early;
         }
-        clear_counters(c, c.tick);  // after the loads of tick t-1's counters, whose words t+1 reuses
+        if (!c.tally) clear_counters(c, c.tick);  // after the loads of tick t-1's counters, whose words t+1 reuses
     }
     return pi;
 }
@@ -3320,6 +3355,20 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         c.d.outcome[2] = ld(&c.ctl->bias_fail);
         c.d.outcome[3] = ld(&c.ctl->tick);
     }
+    // A tally launch: its totals start at zero (the global words are cleared
+    // by the first workgroup before its first barrier, which every other
+    // workgroup passes only after), and each workgroup clears its own
+    // per-step counter words, which the launch leaves untouched, for the
+    // lane's next launch.
+    c.tally = nullptr;
+    if (kFrozenOnly && args.tally) {
+        c.tally = &sh.tally[wave_index()][0];
+        if (threadIdx.x < kWavesPerGroup * kTWaveWords) (&sh.tally[0][0])[threadIdx.x] = 0u;
+        if (threadIdx.x < 4) sh.tally_rec[threadIdx.x] = 0ull;
+        if (threadIdx.x < 2 * kCounterKinds) c.d.wg_counts[c.part * kFlagWords + threadIdx.x] = 0u;
+        if (c.part == 0 && threadIdx.x < kTallyWords) args.tally[threadIdx.x] = 0u;
+        __syncthreads();
+    }
     // a lane whose guard tripped in an earlier launch runs nothing until the
     // host has read the code (every workgroup reads it before its first
     // barrier, and no step of this launch can set it before then)
@@ -3457,7 +3506,7 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
             // phase would make: that step's record is finished and the
             // counters tick+1 reuses are cleared (a one-barrier step's
             // prologue did both)
-            if (!after_one_barrier && c.part == c.P - 1 && wave_index() == 0) roll_counters(c, s);
+            if (!after_one_barrier && !c.tally && c.part == c.P - 1 && wave_index() == 0) roll_counters(c, s);
             if (!(ok = phase_barrier<kProfile>(c, target, spin, clock, 6, c.carried ? sh.win_count : nullptr,
                                                c.carried ? sh.lane_sums : nullptr)))
                 break;
@@ -3513,8 +3562,21 @@ __device__ __forceinline__ void lane_steps(const KernelArgs& args) {
         after_one_barrier = false;
         c.tick += 1;
     }
-    if (ok && !stopped && c.part == 0 && threadIdx.x < kWaveSize && steps > 0)
+    if (ok && !stopped && !c.tally && c.part == 0 && threadIdx.x < kWaveSize && steps > 0)
         finalize_record(c, steps - 1, c.tick - 1);
+    if (ok && c.tally && __lane_id() == 0) {
+        // each wave's totals; the recording wave's 64-bit sums (it is the
+        // only writer of those words after the launch's first barrier)
+        const uint32_t wave = wave_index();
+#pragma unroll
+        for (uint32_t k = 0; k < kTWaveWords; ++k)
+            if (sh.tally[wave][k]) atomicAdd(&args.tally[k], sh.tally[wave][k]);
+        if (c.part == c.P - 1 && wave == 0) {
+            unsigned long long LEO_GLOBAL* sums = reinterpret_cast<unsigned long long LEO_GLOBAL*>(args.tally + kTActive);
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k) sums[k] = sh.tally_rec[k];
+        }
+    }
     if (ok && c.part == 0 && threadIdx.x == 0) {
         c.ctl->tick = c.tick;
         c.ctl->parity = c.parity;

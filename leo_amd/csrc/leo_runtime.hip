@@ -334,6 +334,9 @@ struct LeoHipRuntime {
     // launches whose steps are all frozen without output run the step kernel
     // built for them (LEO_HIP_FROZEN_KERNEL=0: never)
     bool frozen_kernel = true;
+    // the replay's frozen-only launches keep only their totals, not a record
+    // per step (LEO_HIP_TALLY=0: records)
+    bool tally_launches = true;
     double wall_clock_khz = 0.0;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     std::vector<hipEvent_t> launch_events;  // timing events of queued launches (pairs)
@@ -886,13 +889,49 @@ double step_bytes(const LeoHostConfig& c, const StepParams& sp, const StepRecord
     return b;
 }
 
-void account_launch(LeoHipRuntime* h, const std::vector<LaneRun>& runs, float ms, bool canonical) {
+// `tally`: the totals of a tally launch (one lane of frozen steps without
+// output), which stand for its steps' work counters; step_bytes is linear in
+// them for such steps.
+void account_launch(LeoHipRuntime* h, const std::vector<LaneRun>& runs, float ms, bool canonical,
+                    const char* tally = nullptr) {
     LeoKernelStats& t = h->telemetry;
     const int section = canonical ? 1 : 0;
     t.launches += 1;
     t.kernel_ms += ms;
     t.section_launches[section] += 1;
     t.section_kernel_ms[section] += ms;
+    if (tally) {
+        uint32_t w[kTallyWords];
+        std::memcpy(w, tally, sizeof(w));
+        auto wide = [&](uint32_t at) {
+            uint64_t v;
+            std::memcpy(&v, w + at, sizeof(v));
+            return v;
+        };
+        const double S = h->cfg.device.synapses_per_neuron, F = h->cfg.device.input_fanout;
+        const double E = h->cfg.device.context_embedding_dim;
+        const uint64_t n = runs[0].steps.size(), active = wide(kTActive), cells = wide(kTCells);
+        // the folds counted each tick's F injections with the recurrent events
+        // (a step record counts folded - F)
+        const uint64_t injected = static_cast<uint64_t>(h->cfg.device.input_fanout) * n;
+        const uint64_t events = w[kTEvents] > injected ? w[kTEvents] - injected : 0;
+        const double bytes = 29.0 * static_cast<double>(events) + 17.0 * F * static_cast<double>(n) + 172.0 * w[kTTouched] +
+                             60.0 * static_cast<double>(active) + 8.0 * static_cast<double>(active) * S +
+                             4.0 * static_cast<double>(cells) * E;
+        t.lane_steps += n;
+        t.algorithmic_bytes += bytes;
+        t.section_lane_steps[section] += n;
+        t.section_bytes[section] += bytes;
+        t.events += events;
+        t.touched += w[kTTouched];
+        t.active += active;
+        t.kept_rec += wide(kTKeptRec);
+        t.kept_in += wide(kTKeptIn);
+        t.deep_register_folds += w[kTDeepRegister];
+        t.deep_radix_folds += w[kTDeepRadix];
+        t.active_inhibitory += w[kTInhibitory];
+        return;
+    }
     for (const LaneRun& run : runs) {
         for (size_t i = 0; i < run.steps.size(); ++i) {
             const StepRecord& r = run.records[i];
@@ -925,6 +964,7 @@ struct QueuedLaunch {
     std::vector<LaneRun> runs;
     std::vector<const char*> records, ctl;
     const char* outcomes = nullptr;  // instead of ctl: four outcome words per lane
+    const char* tally = nullptr;     // a tally launch's totals (kTally* words) instead of step records
     std::vector<uint32_t> end_tick;
     hipEvent_t start = nullptr, stop = nullptr;
     bool canonical = false;
@@ -1146,8 +1186,13 @@ void complete_launch(LeoHipRuntime* h, QueuedLaunch& q) {
     const uint32_t count = static_cast<uint32_t>(q.runs.size());
     std::vector<LaneControl> ctl(count);
     for (uint32_t i = 0; i < count; ++i) {
-        q.runs[i].records.resize(q.runs[i].steps.size());
-        std::memcpy(q.runs[i].records.data(), q.records[i], q.runs[i].steps.size() * sizeof(StepRecord));
+        if (q.tally) {
+            // no step records: the steps' metrics are not used, the work counters come from the totals
+            q.runs[i].records.assign(q.runs[i].steps.size(), StepRecord{});
+        } else {
+            q.runs[i].records.resize(q.runs[i].steps.size());
+            std::memcpy(q.runs[i].records.data(), q.records[i], q.runs[i].steps.size() * sizeof(StepRecord));
+        }
         if (q.outcomes) {
             uint32_t w[4];
             std::memcpy(w, q.outcomes + 4 * sizeof(uint32_t) * i, sizeof(w));
@@ -1162,7 +1207,7 @@ void complete_launch(LeoHipRuntime* h, QueuedLaunch& q) {
     float ms = 0.0f;
     LEO_HIP_CHECK(hipEventElapsedTime(&ms, q.start, q.stop));
     h->last_launch_ms = ms;
-    account_launch(h, q.runs, ms, q.canonical);
+    account_launch(h, q.runs, ms, q.canonical, q.tally);
     if (h->phase_profile) {
         // lane 0 of the launch is representative (lanes run the same phase sequence)
         unsigned long long prof[2 * kPhases];
@@ -1462,7 +1507,9 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
     // a chunk's last launch, and the host takes a chunk in while the later
     // launches run (a launch's outcome arrives with its successor's chunk;
     // the last launch's, with the lane's control words).
-    constexpr size_t kSlot = 256;
+    constexpr size_t kSlot = 256, kTallyAt = 64;
+    static_assert(kTallyAt >= 4 * sizeof(uint32_t) && kTallyAt + kTallyWords * sizeof(uint32_t) <= kSlot,
+                  "outcome and totals share a launch's slot");
     std::vector<size_t> record_at;
     size_t results_bytes = 0;
     for (const auto& c : cuts)
@@ -1516,6 +1563,7 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
     std::vector<QueuedLaunch> queued;
     std::vector<const void*> kernels;
     std::vector<const KernelArgs*> device_args;
+    std::vector<bool> tallied;
     queued.reserve(launches);
     for (size_t k = 0; k < segments.size(); ++k) {
         const CanonicalSegment& seg = segments[k];
@@ -1542,12 +1590,17 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
             desc.launch = reinterpret_cast<LaunchWords*>(dev + kPlanWords);
             KernelArgs a = kernel_args(h, reinterpret_cast<LaneDesc*>(dev + kPlanDesc), 1, P);
             a.lane_stride = stride;
+            // the replay discards frozen steps' metrics: a frozen-only launch
+            // keeps only its totals, in its slot after the predecessor's outcome
+            const void* kernel = step_kernel(h, frozen_only_steps(run.steps), a.redundant_global != 0);
+            const bool tally = h->tally_launches && kernel == reinterpret_cast<const void*>(&leo_lane_steps_frozen);
+            if (tally) a.tally = reinterpret_cast<uint32_t*>(results + record_at[i] - kSlot + kTallyAt);
             char* img = image + plan_at[i];
             std::memcpy(img, &a, sizeof(KernelArgs));
             std::memcpy(img + kPlanDesc, &desc, sizeof(LaneDesc));
             std::memset(img + kPlanWords, 0, sizeof(LaunchWords));
             std::memcpy(img + kPlanHeader, run.steps.data(), n * sizeof(StepParams));
-            kernels.push_back(step_kernel(h, frozen_only_steps(run.steps), a.redundant_global != 0));
+            kernels.push_back(kernel);
             device_args.push_back(reinterpret_cast<const KernelArgs*>(dev));
             lane.tick += static_cast<uint32_t>(n);
             QueuedLaunch q;
@@ -1558,6 +1611,7 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
             q.start = h->launch_events[2 * i];
             q.stop = h->launch_events[2 * i + 1];
             q.canonical = true;
+            tallied.push_back(tally);
             queued.push_back(std::move(q));
             at += n;
         }
@@ -1622,6 +1676,7 @@ void run_canonical_segments(LeoHipRuntime* h, const std::vector<CanonicalSegment
             }
             q.records[0] = arrived(i, record_at[i]);
             q.ctl[0] = reinterpret_cast<const char*>(&outcome);
+            if (tallied[i]) q.tally = arrived(i, record_at[i] - kSlot + kTallyAt);
             try {
                 complete_launch(h, q);
             } catch (...) {
@@ -2826,6 +2881,7 @@ int32_t leo_hip_create(const LeoHostConfig* config, const LeoModelView* model, i
         if (const char* env = std::getenv("LEO_HIP_PROFILE_PART"))
             h->profile_part = static_cast<uint32_t>(std::max(0, std::atoi(env)));
         if (const char* env = std::getenv("LEO_HIP_FROZEN_KERNEL")) h->frozen_kernel = std::atoi(env) != 0;
+        if (const char* env = std::getenv("LEO_HIP_TALLY")) h->tally_launches = std::atoi(env) != 0;
         int clock_khz = 0;
         LEO_HIP_CHECK(hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, device));
         h->wall_clock_khz = clock_khz > 0 ? clock_khz : 100000.0;

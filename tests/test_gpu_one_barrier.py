@@ -132,3 +132,44 @@ def test_frozen_only_kernel_matches_oracle_and_general_kernel(require_gpu, oracl
         assert stats[kernel]["touched"] == touched, kernel
     for key in COUNTERS:
         assert stats["1"][key] == stats["0"][key], key
+
+
+@pytest.mark.parametrize("launch_steps", [None, 100])
+def test_replay_tally_launches_match_oracle_and_recorded_launches(require_gpu, oracle, monkeypatch, launch_steps):
+    """The replay's frozen prefixes of 64 steps or more run as tally launches
+    of the frozen-only build (training.rs:1848-1954: the replay keeps no
+    metrics of its frozen steps): no step records and no per-step work
+    counters, the launch's totals summed on the device instead. A batch with
+    replay must leave the oracle's model, and the same work counters and
+    byte-model total as the same launches recording every step
+    (LEO_HIP_TALLY=0); the general kernel (LEO_HIP_FROZEN_KERNEL=0) must leave
+    the same model."""
+    from leo_amd.runtime import HipRuntime
+
+    model = Model.initialize(small_redundant_config())
+    stories = [story(s, 420) for s in (3, 5)]
+    cpu = oracle.OracleRuntime(model)
+    cpu.train_story_batch(stories, oracle.TRAINING, replay=True)
+    want = cpu.model()
+    if launch_steps:
+        monkeypatch.setenv("LEO_HIP_MAX_STEPS_PER_LAUNCH", str(launch_steps))
+    stats = {}
+    for kernel, tally in (("1", "1"), ("1", "0"), ("0", "1")):
+        monkeypatch.setenv("LEO_HIP_FROZEN_KERNEL", kernel)
+        monkeypatch.setenv("LEO_HIP_TALLY", tally)
+        print(f"replay: frozen-only kernel {kernel}, tally {tally}, launches of {launch_steps or 'any'} steps",
+              flush=True)
+        gpu = HipRuntime(model, device=0, max_lanes=len(stories))
+        try:
+            gpu.kernel_stats(reset=True)
+            gpu.train_batch(stories, native.TRAINING, replay=True)
+            assert_models_equal(gpu.model(), want, f"replay, frozen-only kernel {kernel}, tally {tally}")
+            stats[kernel + tally] = gpu.kernel_stats()
+        finally:
+            gpu.close()
+    assert stats["11"]["lane_steps"] > 0
+    for key in COUNTERS:
+        assert stats["11"][key] == stats["10"][key], key
+    assert stats["11"]["algorithmic_bytes"] == pytest.approx(stats["10"]["algorithmic_bytes"], rel=1e-12)
+    print("events: tally", stats["11"]["events"], "recorded", stats["10"]["events"], "general kernel",
+          stats["01"]["events"], flush=True)
